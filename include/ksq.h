@@ -1,0 +1,128 @@
+/*
+ * ksq.h - C ABI of the MI355X (gfx950) quantized GGML matmul library (libksq.so).
+ *
+ * Convention (the reference's quant_gemm operator boundary):
+ *     output[M][N] = activation[M][K] . weight[N][K]^T
+ *   weight      device bytes, [N][K/32] GGML blocks (or [N][K/256] K-quant super-blocks)
+ *   activation  device fp32 [M][K] (the "a32" definitions) or block_q8_1 [M][K/32]
+ *   output      device fp32 [M][N], every element written
+ * All pointers are device pointers owned by the caller.  Shapes are ints as in the
+ * reference signature.  M == 0 or N == 0 is an empty call; K == 0 writes zeros.
+ *
+ * Reference interface each entry replaces:
+ *   extern "C" void <entry_point>(const uint8_t* weight, const <act_t>* activation,
+ *                                 float* output, int M, int N, int K);
+ *   (k_search/tasks/kernelevalplus_prompts.py:38-48; wrapper generated at
+ *    kernelevalplus-main/llm_kernel_test/op_test_handler.py:298-349; a concrete
+ *    instance is kernelevalplus-main/core/operators/quant_gemm/variants/deepseek_v3/
+ *    w8a8c8_q8_0_q8_1/kernel.cu:119-130.)
+ * As in the reference, the void entries launch on the default (null) stream and
+ * return before the work finishes; unlike the reference they validate their
+ * arguments and record failures for ksq_last_error() instead of launching.
+ */
+#ifndef KSQ_H
+#define KSQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "ksq_blocks.h"
+
+#if defined(__GNUC__) || defined(__clang__)
+#define KSQ_API __attribute__((visibility("default")))
+#else
+#define KSQ_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+enum ksq_status {
+    KSQ_OK = 0,
+    KSQ_ERR_NULL = 1,        /* a required pointer is NULL */
+    KSQ_ERR_SHAPE = 2,       /* negative size, K not a multiple of the block size, ... */
+    KSQ_ERR_ALIGN = 3,       /* pointer alignment the kernels cannot honour */
+    KSQ_ERR_TYPE = 4,        /* unknown weight / activation type code */
+    KSQ_ERR_WORKSPACE = 5,   /* caller workspace smaller than ksq_gemm_workspace_size() */
+    KSQ_ERR_HIP = 6,         /* HIP runtime error (launch, allocation, device) */
+};
+
+/* Status of the last ksq call on this host thread, and a message for it. */
+KSQ_API int ksq_last_error(void);
+KSQ_API const char* ksq_last_error_message(void);
+KSQ_API const char* ksq_error_string(int status);
+
+/* Library version string. */
+KSQ_API const char* ksq_version(void);
+
+/* Free the per-device workspace pools the void entries allocate on demand. */
+KSQ_API void ksq_release(void);
+
+/* ---- drop-in entries: the reference's quant_gemm signature --------------- */
+
+/* W4A32C8: Q4_0 weights, fp32 activations quantised to Q8_1 inside the call
+ * (quantize_row_q8_1_ref arithmetic), int8 compute.  Replaces the entry of the
+ * w4a32c8_q4_0_fp32_int8_* definitions (e.g. kernelevalplus-main/definitions/
+ * quant_gemm/llama3_8b/w4a32c8_q4_0_fp32_int8_llama3_8b_att_out_n4096_k4096.json)
+ * and KernelEvalPlus' gemm_w4a8_reference (include/gemm_reference.h:175-222). */
+KSQ_API void gemm_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+
+/* W8A32C8: Q8_0 weights, fp32 activations -> Q8_1, int8 compute (the
+ * w8a32c8_q8_0_fp32_int8_* definitions; gemm_w8a8_reference, gemm_reference.h:233-267). */
+KSQ_API void gemm_w8a32c8_q8_0_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+
+/* K-quant weights (no reference counterpart; named by the reference's naming
+ * scheme, kernelevalplus-main/definitions/NAMING_CONVENTION.md:21-33).  K % 256 == 0. */
+KSQ_API void gemm_w4a32c8_q4_k_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+KSQ_API void gemm_w6a32c8_q6_k_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+
+/* Pre-quantised activations (the harness' uint8_t activation form,
+ * op_test_handler.py:319-323): activation is block_q8_1 [M][K/32]. */
+KSQ_API void ksq_gemm_q4_0_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q8_0_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q4_k_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q6_k_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+
+/* ---- checked, stream-taking entries -------------------------------------- */
+
+/* fp32 [M][K] -> block_q8_1 [M][K/32] (quantize_row_q8_1_ref,
+ * kernelevalplus-main/include/quantize.h:165-193, bit for bit; replaces the launcher
+ * quantize_q8_1_cuda, quantize.h:361-368, whose kernel rounds half-even instead).
+ * x 16-byte aligned, y 4-byte aligned.  stream: hipStream_t or NULL. */
+KSQ_API int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream);
+
+/* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the Q8_1 copy of
+ * fp32 activations, 0 for pre-quantised activations. */
+KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
+
+/* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype.  workspace may be
+ * NULL (then a per-device pool owned by the library is used, which makes the call
+ * allocate on first use and when sizes grow).  Returns a ksq_status. */
+KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,
+             int M, int N, int K, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Debug: per-block integer dot products out[M][N][nblk] (nblk = K/32, or K/16 for
+ * Q6_K) computed by the device block-dot code of the decode kernels. */
+KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
+                         int M, int N, int K, void* stream);
+
+/* Debug: the same per-block integer dots taken from the int8 MFMA tiles of the
+ * prefill GEMM.  Q4_0 / Q8_0 only, K % 256 == 0, weight and act_q8_1 16-byte aligned. */
+KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
+                              int M, int N, int K, void* stream);
+
+/* Path selection for testing and benchmarking: 0 = automatic (default),
+ * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies. */
+KSQ_API int ksq_set_path(int path);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KSQ_H */

@@ -1,0 +1,217 @@
+// ksq_mmq.hip - prefill GEMM on the gfx950 int8 MFMA (the mul_mat_q analogue).
+//
+// Reference path: the tiled GEMMs of kernelevalplus-main/include/gemm_cuda_tiled.cuh:191-262 and
+// gemm_cuda_dp4a.cuh:275-351 (32x32 shared-memory tiles, DP4A on CUDA cores) with the
+// block formula of gemm_w4a8_reference / gemm_w8a8_reference (include/gemm_reference.h:175-267).
+//
+// gfx950 design:
+//  * Workgroup tile 128 activation rows x 128 weight rows, 4 waves each owning a
+//    64 x 64 quadrant = 2 x 2 tiles of v_mfma_i32_32x32x32_i8.  One MFMA contracts
+//    exactly one 32-element Q block, so its i32 result IS the reference's integer
+//    block dot sumi for a 32 x 32 patch of outputs.
+//  * Per K step 8 blocks (256 K) are staged in LDS: Q8_1 quants as int8 rows, Q4_0
+//    weights as packed nibbles (the MFMA lane that holds k = 0..15 takes the low
+//    nibbles, the lane that holds k = 16..31 the high ones, which is exactly the
+//    Q4_0 element order), Q8_0 weights as int8 rows; the fp16 scales are widened to
+//    fp32 once at staging (d_a, -8*s_a per activation row and block, d_w per weight
+//    row and block).
+//  * Epilogue per block: acc += d_w * (d_a * float(sumi) - 8 * s_a) (Q4_0) or
+//    acc += float(sumi) * d_a * d_w (Q8_0), in fp32.
+//  * Row / column tiles past M or N load a clamped in-range row and are not stored.
+#include "ksq_device.h"
+#include "ksq_internal.h"
+
+namespace ksq {
+
+constexpr int kBM = 128, kBN = 128, kKB = 8;
+constexpr int kAPitch = kKB * 32 + 16;  // bytes per staged activation row (conflict-free b128 reads)
+
+typedef uint32_t u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
+
+template <int WT>
+struct MmqShape {
+    static constexpr int WQ = (WT == 0) ? 16 : 32;     // staged weight bytes per block
+    static constexpr int WPitch = kKB * WQ + 16;       // bytes per staged weight row
+    static constexpr int BB = (WT == 0) ? kQ40Bytes : kQ80Bytes;
+    static constexpr int HalfBytes = 4 * BB;           // 72 or 136: half a row's K step
+};
+
+template <int WT, bool DUMP>
+__global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                     float* __restrict__ C, int32_t* __restrict__ dump, int M,
+                                                     int N, int nb) {
+    using S = MmqShape<WT>;
+    __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kAPitch];
+    __shared__ __attribute__((aligned(16))) uint8_t sW[kBN * S::WPitch];
+    __shared__ __attribute__((aligned(16))) float sDa[kKB][kBM];
+    __shared__ __attribute__((aligned(16))) float sSa[kKB][kBM];
+    __shared__ __attribute__((aligned(16))) float sDw[kKB][kBN];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    const int l32 = lane & 31, hi = lane >> 5;
+
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+    // staging assignment: thread t owns row t/2, blocks 4*(t&1) .. 4*(t&1)+3 of the K step
+    const int sr = t >> 1, sh = t & 1;
+    const int am = min(m0 + sr, M - 1);
+    const int wn_row = min(n0 + sr, N - 1);
+    const uint8_t* a_src = A + (size_t)am * nb * kQ81Bytes + (size_t)sh * 4 * kQ81Bytes;
+    const uint8_t* w_src = W + (size_t)wn_row * nb * S::BB + (size_t)sh * S::HalfBytes;
+
+    for (int kb0 = 0; kb0 < nb; kb0 += kKB) {
+        // ---- stage activations: 4 Q8_1 blocks = 144 B = 9 x 16 B
+        {
+            uint32_t v[36];
+            const uint8_t* p = a_src + (size_t)kb0 * kQ81Bytes;
+#pragma unroll
+            for (int i = 0; i < 9; i++) {
+                const u32x4 x = *(const u32x4*)(p + 16 * i);
+                v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int kb = 4 * sh + j;
+                u32x4* dst = (u32x4*)(sA + sr * kAPitch + kb * 32);
+                dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
+                dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
+                sDa[kb][sr] = f16_to_f32(v[9 * j] & 0xFFFFu);
+                sSa[kb][sr] = -8.0f * f16_to_f32(v[9 * j] >> 16);
+            }
+        }
+        // ---- stage weights: 4 blocks = 72 B (Q4_0) / 136 B (Q8_0), 8-byte aligned
+        {
+            constexpr int NW = S::HalfBytes / 4;
+            uint32_t v[NW + 2];
+            const uint8_t* p = w_src + (size_t)kb0 * S::BB;
+#pragma unroll
+            for (int i = 0; i < NW / 2; i++) {
+                const u32x2_a8 x = *(const u32x2_a8*)(p + 8 * i);
+                v[2 * i] = x.x; v[2 * i + 1] = x.y;
+            }
+            v[NW] = 0; v[NW + 1] = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int kb = 4 * sh + j, off = j * S::BB;
+                sDw[kb][sr] = f16_to_f32(half_at(v, off));
+                if constexpr (WT == 0) {
+                    *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
+                        u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
+                } else {
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                    dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
+                    dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
+                }
+            }
+        }
+        __syncthreads();
+
+#pragma unroll 2
+        for (int b = 0; b < kKB; b++) {
+            i32x4 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                af[i] = *(const i32x4*)(sA + (wm * 64 + i * 32 + l32) * kAPitch + b * 32 + 16 * hi);
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                if constexpr (WT == 0) {
+                    const u32x4 x = *(const u32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 16);
+                    const int s4 = 4 * hi;
+                    bf[j] = i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
+                                  (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
+                } else {
+                    bf[j] = *(const i32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const i32x16 zero = {0};
+                    const i32x16 sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
+                    // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
+                    const int col = wn * 64 + j * 32 + l32;
+                    const int rowb = wm * 64 + i * 32 + 4 * hi;
+                    if constexpr (DUMP) {
+                        const int gn = n0 + col;
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int gm = m0 + rowb + 8 * (r >> 2) + (r & 3);
+                            if (gm < M && gn < N) dump[((size_t)gm * N + gn) * nb + kb0 + b] = sumi[r];
+                        }
+                    } else {
+                        const float dw = sDw[b][col];
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            const f32x4 da = *(const f32x4*)&sDa[b][rowb + 8 * q];
+                            if constexpr (WT == 0) {
+                                const f32x4 sa = *(const f32x4*)&sSa[b][rowb + 8 * q];
+#pragma unroll
+                                for (int p = 0; p < 4; p++)
+                                    acc[i][j][4 * q + p] =
+                                        fmaf(dw, fmaf(da[p], (float)sumi[4 * q + p], sa[p]), acc[i][j][4 * q + p]);
+                            } else {
+#pragma unroll
+                                for (int p = 0; p < 4; p++)
+                                    acc[i][j][4 * q + p] = fmaf((float)sumi[4 * q + p] * da[p], dw, acc[i][j][4 * q + p]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    if constexpr (!DUMP) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const int gn = n0 + wn * 64 + j * 32 + l32;
+                const int rowb = m0 + wm * 64 + i * 32 + 4 * hi;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int gm = rowb + 8 * (r >> 2) + (r & 3);
+                    if (gm < M && gn < N) C[(size_t)gm * N + gn] = acc[i][j][r];
+                }
+            }
+    }
+}
+
+bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A) {
+    return (wtype == 0 || wtype == 1) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
+           (((uintptr_t)W & 15u) == 0) && (((uintptr_t)A & 15u) == 0);
+}
+
+hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K, hipStream_t s) {
+    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+    const int nb = K / 32;
+    if (wtype == 0)
+        hipLaunchKernelGGL((mmq_kernel<0, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
+    else
+        hipLaunchKernelGGL((mmq_kernel<1, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,
+                                 hipStream_t s) {
+    if (!mmq_supported(wtype, M, N, K, W, A)) return hipErrorNotSupported;
+    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
+    const int nb = K / 32;
+    if (wtype == 0)
+        hipLaunchKernelGGL((mmq_kernel<0, true>), grid, dim3(256), 0, s, W, A, nullptr, out, M, N, nb);
+    else
+        hipLaunchKernelGGL((mmq_kernel<1, true>), grid, dim3(256), 0, s, W, A, nullptr, out, M, N, nb);
+    return hipGetLastError();
+}
+
+}  // namespace ksq

@@ -1,0 +1,10 @@
+"""ksq - MI355X-native quantized GGML matmul (host side of libksq.so).
+
+The compute path is the HIP library libksq.so (k-search_amd/csrc); this
+package loads it through its C ABI and offers the reference harness's
+forward(weight, activation, M, N, K) convention on torch tensors.
+"""
+from ._lib import A_F32, A_Q8_1, W_Q4_0, W_Q4_K, W_Q6_K, W_Q8_0, KsqError, lib  # noqa: F401
+from .formats import QUANT_TYPES, WTYPE_NAMES, quant_type  # noqa: F401
+from .ops import (ENTRY_POINTS, block_sumi, forward, gemm, quantize_q8_1, release,  # noqa: F401
+                  set_path, workspace_size)

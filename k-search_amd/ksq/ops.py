@@ -1,0 +1,101 @@
+"""Torch-tensor front end of libksq (PyTorch is only the device-memory / stream plumbing).
+
+`forward` mirrors the wrapper the reference harness generates around a
+quant_gemm entry point (kernelevalplus-main/llm_kernel_test/op_test_handler.py:298-349):
+same arguments (weight, activation, M, N, K), same CUDA-tensor checks and
+messages, output allocated as an fp32 [M, N] tensor on the weight's device.
+Calls go through the C ABI on torch's current stream.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import A_F32, A_Q8_1, W_Q4_0, W_Q4_K, W_Q6_K, W_Q8_0, check, lib
+
+# Definition-style entry points of include/ksq.h -> (weight type, activation type)
+ENTRY_POINTS = {
+    "gemm_w4a32c8_q4_0_fp32_int8": (W_Q4_0, A_F32),
+    "gemm_w8a32c8_q8_0_fp32_int8": (W_Q8_0, A_F32),
+    "gemm_w4a32c8_q4_k_fp32_int8": (W_Q4_K, A_F32),
+    "gemm_w6a32c8_q6_k_fp32_int8": (W_Q6_K, A_F32),
+    "ksq_gemm_q4_0_q8_1": (W_Q4_0, A_Q8_1),
+    "ksq_gemm_q8_0_q8_1": (W_Q8_0, A_Q8_1),
+    "ksq_gemm_q4_k_q8_1": (W_Q4_K, A_Q8_1),
+    "ksq_gemm_q6_k_q8_1": (W_Q6_K, A_Q8_1),
+}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def gemm(wtype: int, atype: int, weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
+         out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """output[M, N] = activation[M, K] . weight[N, K]^T through ksq_gemm."""
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=weight.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ksq_gemm(wtype, atype, _ptr(weight), _ptr(activation), _ptr(out), M, N, K,
+                         _ptr(workspace), ws_bytes, _stream()))
+    return out
+
+
+def forward(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
+            entry: str = "gemm_w4a32c8_q4_0_fp32_int8") -> torch.Tensor:
+    """The harness wrapper: forward(weight, activation, M, N, K) -> fp32 [M, N]."""
+    if not weight.is_cuda:
+        raise RuntimeError("Weight must be CUDA tensor")
+    if not activation.is_cuda:
+        raise RuntimeError("Activation must be CUDA tensor")
+    wtype, atype = ENTRY_POINTS[entry]
+    if weight.dtype != torch.uint8:
+        raise RuntimeError(f"expected scalar type Byte for weight but found {weight.dtype}")
+    want = torch.float32 if atype == A_F32 else torch.uint8
+    if activation.dtype != want:
+        raise RuntimeError(f"expected scalar type {want} for activation but found {activation.dtype}")
+    return gemm(wtype, atype, weight, activation, int(M), int(N), int(K))
+
+
+def quantize_q8_1(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [..., K] -> uint8 [..., K/32, 36] (quantize_row_q8_1_ref bit for bit)."""
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise RuntimeError("quantize_q8_1 expects a CUDA float32 tensor")
+    x = x.contiguous()
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if out is None:
+        out = torch.empty((*x.shape[:-1], K // 32, 36), dtype=torch.uint8, device=x.device)
+    check(lib().ksq_quantize_q8_1(_ptr(x), _ptr(out), rows, K, _stream()))
+    return out
+
+
+def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int, N: int, K: int,
+               mfma: bool = False) -> torch.Tensor:
+    """Per-block integer dots [M, N, nblk] from the device block-dot code (debug)."""
+    nblk = K // 16 if wtype == W_Q6_K else K // 32
+    out = torch.empty((M, N, nblk), dtype=torch.int32, device=weight.device)
+    fn = lib().ksq_debug_block_sumi_mfma if mfma else lib().ksq_debug_block_sumi
+    check(fn(wtype, _ptr(weight), _ptr(act_q8_1), _ptr(out), M, N, K, _stream()))
+    return out
+
+
+def set_path(path: int) -> None:
+    """0 automatic, 1 v_dot4 decode kernels only, 2 MFMA GEMM where it applies."""
+    check(lib().ksq_set_path(path))
+
+
+def workspace_size(wtype: int, atype: int, M: int, N: int, K: int) -> int:
+    return lib().ksq_gemm_workspace_size(wtype, atype, M, N, K)
+
+
+def release() -> None:
+    lib().ksq_release()
+
+
+__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "block_sumi", "set_path", "workspace_size",
+           "release", "_lib"]

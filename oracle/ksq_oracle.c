@@ -1,0 +1,609 @@
+/*
+ * ksq_oracle.c - CPU restatement of the reference's quantized-matmul arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker for the HIP path: only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it.
+ * The product library (k-search_amd/) never links or calls it.
+ *
+ * Every function cites the reference lines it restates (paths relative to
+ * /root/reference/kernelevalplus-main).  The reference sources themselves need
+ * cuda_fp16.h / cuda_runtime.h and cannot be compiled in this image, so the
+ * arithmetic is re-stated here in plain C with a hand-written IEEE binary16
+ * converter in place of __float2half / __half2float.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math: the
+ * quantiser and the block formulas must round exactly as written).
+ *
+ * Parity pins (see tests/test_oracle.py):
+ *   fp16 conversion      exhaustive / random check against numpy.float16
+ *   quantize_row_q8_1    closed-form numpy restatement, constructed ties,
+ *                        zero block, amax -> +-127 invariant
+ *   sumi (Q4_0, Q8_0)    brute-force integer dot, known-answer blocks
+ *   gemm (fp32 order)    fp64 block formula (gemm_ref.py:100-153 form) and a
+ *                        dequantise-then-matmul numpy path
+ *   Q4_K / Q6_K          independent encoder (layout written from the public
+ *                        GGML description) -> oracle decoder round trip,
+ *                        integer-sum path vs dequantise-then-fp64-dot path
+ *   MoE                  routing invariants, composition with the dense oracle
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#include "../include/ksq_blocks.h"
+
+#define KSQ_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 <-> binary32 (round to nearest even), the semantics of      */
+/* cuda_fp16's __float2half / __half2float used throughout quant_types.h and */
+/* quantize.h.                                                                */
+/* ------------------------------------------------------------------------ */
+
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+KSQ_API float ksq_ref_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu;
+    uint32_t man = h & 0x3FFu;
+    if (exp == 0) {
+        if (man == 0) return bits_f32(sign);
+        /* subnormal: value = man * 2^-24, exact in binary32 */
+        float v = (float)man * 5.9604644775390625e-08f;
+        return sign ? -v : v;
+    }
+    if (exp == 31) return bits_f32(sign | 0x7F800000u | (man << 13));
+    return bits_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+KSQ_API uint16_t ksq_ref_f32_to_f16(float f) {
+    uint32_t u = f32_bits(f);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t exp = (u >> 23) & 0xFFu;
+    uint32_t man = u & 0x7FFFFFu;
+    if (exp == 0xFF) {                       /* inf / nan (nan keeps a payload bit) */
+        if (man == 0) return sign | 0x7C00u;
+        return sign | 0x7E00u | (uint16_t)(man >> 13);
+    }
+    int32_t e = (int32_t)exp - 127 + 15;     /* rebias */
+    if (e >= 31) return sign | 0x7C00u;      /* overflow -> inf */
+    if (e <= 0) {
+        /* subnormal or zero in binary16: shift the full significand */
+        if (e < -10) return sign;            /* below half the smallest subnormal -> 0 */
+        uint32_t m = man | 0x800000u;        /* implicit bit */
+        uint32_t shift = (uint32_t)(14 - e); /* 24-bit significand -> 10-bit field at exponent 1 */
+        uint32_t q = m >> shift;
+        uint32_t rem = m & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return sign | (uint16_t)q;           /* carry into exponent 1 is the correct encoding */
+    }
+    uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++;  /* may carry into inf: correct */
+    return sign | (uint16_t)q;
+}
+
+/* Round half away from zero then convert to int, as (int)roundf(v) compiles on
+ * x86-64 (the host the reference's CPU path runs on): a value outside the int32
+ * range or a NaN becomes INT32_MIN ("integer indefinite"), which the callers'
+ * clamp then maps to -128. */
+static inline int32_t round_to_i32(float v) {
+    float r = roundf(v);
+    if (!(r >= -2147483648.0f && r < 2147483648.0f)) return INT32_MIN;
+    return (int32_t)r;
+}
+
+static inline float rd_f16(const uint8_t* p) { uint16_t h; memcpy(&h, p, 2); return ksq_ref_f16_to_f32(h); }
+static inline void wr_f16(uint8_t* p, float f) { uint16_t h = ksq_ref_f32_to_f16(f); memcpy(p, &h, 2); }
+
+/* ------------------------------------------------------------------------ */
+/* Quantisers and dequantisers                                              */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_row_q8_1_ref (include/quantize.h:165-193): per 32 floats,
+ * amax = max|x|, sum = sequential fp32 sum, d = amax/127, ds = (half(d), half(sum)),
+ * id = d > 0 ? 1/d : 0 (fp32 d, not the rounded half), q = clamp(roundf(x*id)). */
+KSQ_API void ksq_ref_quantize_row_q8_1(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK8_1;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * KSQ_QK8_1;
+        uint8_t* blk = y + i * 36;
+        float amax = 0.0f, sum = 0.0f;
+        for (int j = 0; j < KSQ_QK8_1; j++) {
+            float a = fabsf(xs[j]);
+            amax = (amax < a) ? a : amax;   /* std::max(amax, std::abs(x)) */
+            sum += xs[j];
+        }
+        const float d = amax / 127.0f;
+        wr_f16(blk + 0, d);
+        wr_f16(blk + 2, sum);
+        const float id = (d > 0) ? 1.0f / d : 0.0f;
+        for (int j = 0; j < KSQ_QK8_1; j++) {
+            int32_t q = round_to_i32(xs[j] * id);
+            q = q < -128 ? -128 : (q > 127 ? 127 : q);
+            blk[4 + j] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
+/* quantize_row_q8_0_ref (include/quantize.h:110-131). */
+KSQ_API void ksq_ref_quantize_row_q8_0(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * KSQ_QK8_0;
+        uint8_t* blk = y + i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < KSQ_QK8_0; j++) { float a = fabsf(xs[j]); amax = (amax < a) ? a : amax; }
+        const float d = amax / 127.0f;
+        wr_f16(blk, d);
+        const float id = (d > 0) ? 1.0f / d : 0.0f;
+        for (int j = 0; j < KSQ_QK8_0; j++) {
+            int32_t q = round_to_i32(xs[j] * id);
+            q = q < -128 ? -128 : (q > 127 ? 127 : q);
+            blk[2 + j] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
+/* quantize_row_q4_0_ref (include/quantize.h:34-68): d = amax/7,
+ * q = clamp(roundf(x/d)+8, 0, 15), low nibble = element j, high = element j+16. */
+KSQ_API void ksq_ref_quantize_row_q4_0(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK4_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * KSQ_QK4_0;
+        uint8_t* blk = y + i * 18;
+        float amax = 0.0f;
+        for (int j = 0; j < KSQ_QK4_0; j++) { float a = fabsf(xs[j]); amax = (amax < a) ? a : amax; }
+        const float d = amax / 7.0f;
+        wr_f16(blk, d);
+        const float id = (d > 0) ? 1.0f / d : 0.0f;
+        for (int j = 0; j < KSQ_QK4_0 / 2; j++) {
+            int32_t q0 = round_to_i32(xs[j] * id);
+            int32_t q1 = round_to_i32(xs[j + 16] * id);
+            q0 = (q0 == INT32_MIN) ? q0 : q0 + 8;
+            q1 = (q1 == INT32_MIN) ? q1 : q1 + 8;
+            q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+            q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+            blk[2 + j] = (uint8_t)((q1 << 4) | (q0 & 0x0F));
+        }
+    }
+}
+
+/* dequantize_row_q4_0 (include/quantize.h:80-100). */
+KSQ_API void ksq_ref_dequantize_row_q4_0(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK4_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* blk = x + i * 18;
+        const float d = rd_f16(blk);
+        for (int j = 0; j < 16; j++) {
+            y[i * 32 + j] = (float)((blk[2 + j] & 0x0F) - 8) * d;
+            y[i * 32 + j + 16] = (float)((blk[2 + j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* dequantize_row_q8_0 (include/quantize.h:136-150). */
+KSQ_API void ksq_ref_dequantize_row_q8_0(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* blk = x + i * 34;
+        const float d = rd_f16(blk);
+        for (int j = 0; j < 32; j++) y[i * 32 + j] = (float)(int8_t)blk[2 + j] * d;
+    }
+}
+
+/* dequantize_row_q8_1 (include/quantize.h:198-211). */
+KSQ_API void ksq_ref_dequantize_row_q8_1(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK8_1;
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* blk = x + i * 36;
+        const float d = rd_f16(blk);
+        for (int j = 0; j < 32; j++) y[i * 32 + j] = (float)(int8_t)blk[4 + j] * d;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Integer block dot products                                               */
+/* ------------------------------------------------------------------------ */
+
+/* Inner loop of gemm_w4a8_reference (include/gemm_reference.h:200-212) and
+ * vec_dot_q4_0_q8_1 (:287-294): sumi = sum_k qa[k]*(qs[k]&15) + qa[k+16]*(qs[k]>>4). */
+KSQ_API int32_t ksq_ref_sumi_q4_0_q8_1(const uint8_t* wblk, const uint8_t* ablk) {
+    int32_t sumi = 0;
+    const int8_t* qa = (const int8_t*)(ablk + 4);
+    for (int k = 0; k < 16; k++) {
+        sumi += (int32_t)qa[k] * (int32_t)(wblk[2 + k] & 0x0F);
+        sumi += (int32_t)qa[k + 16] * (int32_t)(wblk[2 + k] >> 4);
+    }
+    return sumi;
+}
+
+/* Inner loop of gemm_w8a8_reference (include/gemm_reference.h:253-256). */
+KSQ_API int32_t ksq_ref_sumi_q8_0_q8_1(const uint8_t* wblk, const uint8_t* ablk) {
+    int32_t sumi = 0;
+    const int8_t* qa = (const int8_t*)(ablk + 4);
+    const int8_t* qw = (const int8_t*)(wblk + 2);
+    for (int k = 0; k < 32; k++) sumi += (int32_t)qa[k] * (int32_t)qw[k];
+    return sumi;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dense GEMMs, C[M][N] = A[M][K] . W[N][K]^T                               */
+/* ------------------------------------------------------------------------ */
+
+/* gemm_w4a8_reference (include/gemm_reference.h:175-222), fp32 accumulation in
+ * block order: sum += d_w * (d_a * sumi - 8 * s_a).  nthreads > 1 splits the
+ * output rows over OpenMP threads; the per-output arithmetic is unchanged. */
+KSQ_API void ksq_ref_gemm_w4a8(const uint8_t* A, const uint8_t* W, float* C,
+                               int M, int N, int K, int nthreads) {
+    const int nb = K / KSQ_QK4_0;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * 18;
+                const float d_a = rd_f16(ab);
+                const float s_a = rd_f16(ab + 2);
+                const float d_w = rd_f16(wb);
+                const int32_t sumi = ksq_ref_sumi_q4_0_q8_1(wb, ab);
+                sum += d_w * (d_a * (float)sumi - 8.0f * s_a);
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* gemm_w8a8_reference (include/gemm_reference.h:233-267): sum += sumi * d_a * d_w. */
+KSQ_API void ksq_ref_gemm_w8a8(const uint8_t* A, const uint8_t* W, float* C,
+                               int M, int N, int K, int nthreads) {
+    const int nb = K / KSQ_QK8_0;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * 34;
+                const float d_a = rd_f16(ab);
+                const float d_w = rd_f16(wb);
+                const int32_t sumi = ksq_ref_sumi_q8_0_q8_1(wb, ab);
+                sum += (float)sumi * d_a * d_w;
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* The same block formulas accumulated in fp64, the form of the harness oracle
+ * reference_q4_0_q8_1_gemm (llm_kernel_test/reference/gemm_ref.py:100-153).
+ * Used as the tolerance reference for fp32 outputs. wtype: KSQ_W_Q4_0 or KSQ_W_Q8_0. */
+KSQ_API void ksq_ref_gemm_f64(int wtype, const uint8_t* A, const uint8_t* W, double* C,
+                              int M, int N, int K, int nthreads) {
+    const int nb = K / 32;
+    const int wbytes = (wtype == KSQ_W_Q4_0) ? 18 : 34;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            double sum = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * wbytes;
+                const double d_a = rd_f16(ab), s_a = rd_f16(ab + 2), d_w = rd_f16(wb);
+                if (wtype == KSQ_W_Q4_0)
+                    sum += d_w * (d_a * (double)ksq_ref_sumi_q4_0_q8_1(wb, ab) - 8.0 * s_a);
+                else
+                    sum += d_w * d_a * (double)ksq_ref_sumi_q8_0_q8_1(wb, ab);
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* K-quants (absent from the reference).  Layout and arithmetic restate the  */
+/* public GGML k-quant algorithm (llama.cpp ggml-quants.c dequantize_row_q4_K */
+/* / dequantize_row_q6_K and ggml-cuda vecdotq.cuh vec_dot_q4_K_q8_1_impl_mmq */
+/* / vec_dot_q6_K_q8_1_impl_mmq; llama.cpp is not vendored in the reference   */
+/* and no version is pinned there).  Parity for these is pinned only by the   */
+/* closed-form and round-trip checks in tests/test_oracle.py.                 */
+/* ------------------------------------------------------------------------ */
+
+/* 6-bit scale j and min j of a Q4_K super-block (get_scale_min_k4). */
+KSQ_API void ksq_ref_q4_K_scale_min(int j, const uint8_t* q, int* sc, int* m) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Quant value (0..15) of element e (0..255) of a Q4_K super-block: 64-element
+ * group g = e/64 uses qs[32g .. 32g+31], low nibbles for the first 32 elements,
+ * high nibbles for the next 32. */
+static inline int q4_K_q(const uint8_t* qs, int e) {
+    int g = e >> 6, r = e & 63;
+    uint8_t byte = qs[32 * g + (r & 31)];
+    return (r < 32) ? (byte & 0x0F) : (byte >> 4);
+}
+
+/* Quant value (-32..31) of element e of a Q6_K super-block: half n = e/128,
+ * within a half quarter g = (e%128)/32 and lane l = e%32 read
+ * ql[64n + l + 32*(g&1)] (low nibble for g<2, high for g>=2) and
+ * qh[32n + l] bits 2g..2g+1. Sub-block scale index is e/16. */
+static inline int q6_K_q(const uint8_t* blk, int e) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    int n = e >> 7, r = e & 127, g = r >> 5, l = r & 31;
+    uint8_t lb = ql[64 * n + l + 32 * (g & 1)];
+    int lo = (g < 2) ? (lb & 0x0F) : (lb >> 4);
+    int hi = (qh[32 * n + l] >> (2 * g)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+KSQ_API void ksq_ref_dequantize_row_q4_K(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nsb = k / KSQ_QK_K;
+    for (int64_t i = 0; i < nsb; i++) {
+        const uint8_t* blk = x + i * 144;
+        const float d = rd_f16(blk), dmin = rd_f16(blk + 2);
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            ksq_ref_q4_K_scale_min(j, blk + 4, &sc, &m);
+            const float d1 = d * (float)sc, m1 = dmin * (float)m;
+            for (int l = 0; l < 32; l++)
+                y[i * 256 + 32 * j + l] = d1 * (float)q4_K_q(blk + 16, 32 * j + l) - m1;
+        }
+    }
+}
+
+KSQ_API void ksq_ref_dequantize_row_q6_K(const uint8_t* x, float* y, int64_t k) {
+    const int64_t nsb = k / KSQ_QK_K;
+    for (int64_t i = 0; i < nsb; i++) {
+        const uint8_t* blk = x + i * 210;
+        const float d = rd_f16(blk + 208);
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        for (int e = 0; e < 256; e++) y[i * 256 + e] = d * (float)sc[e / 16] * (float)q6_K_q(blk, e);
+    }
+}
+
+/* Integer dot of Q4_K sub-block j (32 elements) with the matching Q8_1 block. */
+KSQ_API int32_t ksq_ref_sumi_q4_K_q8_1(const uint8_t* wsb, int j, const uint8_t* ablk) {
+    const int8_t* qa = (const int8_t*)(ablk + 4);
+    int32_t s = 0;
+    for (int l = 0; l < 32; l++) s += (int32_t)qa[l] * q4_K_q(wsb + 16, 32 * j + l);
+    return s;
+}
+
+/* Integer dot of Q6_K sub-block i (16 elements, quants already offset by -32)
+ * with the matching half of Q8_1 block i/2. */
+KSQ_API int32_t ksq_ref_sumi_q6_K_q8_1(const uint8_t* wsb, int i, const uint8_t* ablk) {
+    const int8_t* qa = (const int8_t*)(ablk + 4);
+    int32_t s = 0;
+    for (int l = 0; l < 16; l++) s += (int32_t)qa[16 * (i & 1) + l] * q6_K_q(wsb, 16 * i + l);
+    return s;
+}
+
+/* Q4_K super-block x 8 Q8_1 blocks (vec_dot_q4_K_q8_1_impl_mmq form):
+ *   sumf_d += d8_j * (float)(sc_j * sumi_j);  sumf_m += s8_j * (float)m_j;
+ *   return d * sumf_d - dmin * sumf_m. */
+static float dot_q4_K_sb(const uint8_t* wsb, const uint8_t* a8) {
+    float sumf_d = 0.0f, sumf_m = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        const uint8_t* ab = a8 + j * 36;
+        int sc, m;
+        ksq_ref_q4_K_scale_min(j, wsb + 4, &sc, &m);
+        const int32_t sumi = ksq_ref_sumi_q4_K_q8_1(wsb, j, ab);
+        sumf_d += rd_f16(ab) * (float)(sc * sumi);
+        sumf_m += rd_f16(ab + 2) * (float)m;
+    }
+    return rd_f16(wsb) * sumf_d - rd_f16(wsb + 2) * sumf_m;
+}
+
+/* Q6_K super-block x 8 Q8_1 blocks (vec_dot_q6_K_q8_1_impl_mmq form):
+ *   sumf += d8_j * (float)(sc[2j]*isum_2j + sc[2j+1]*isum_2j+1);  return d * sumf. */
+static float dot_q6_K_sb(const uint8_t* wsb, const uint8_t* a8) {
+    const int8_t* sc = (const int8_t*)(wsb + 192);
+    float sumf = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        const uint8_t* ab = a8 + j * 36;
+        const int32_t s0 = ksq_ref_sumi_q6_K_q8_1(wsb, 2 * j, ab);
+        const int32_t s1 = ksq_ref_sumi_q6_K_q8_1(wsb, 2 * j + 1, ab);
+        sumf += rd_f16(ab) * (float)(sc[2 * j] * s0 + sc[2 * j + 1] * s1);
+    }
+    return rd_f16(wsb + 208) * sumf;
+}
+
+/* K-quant GEMM in fp32, super-blocks in ascending order. wtype: KSQ_W_Q4_K or KSQ_W_Q6_K. */
+KSQ_API void ksq_ref_gemm_kquant(int wtype, const uint8_t* A, const uint8_t* W, float* C,
+                                 int M, int N, int K, int nthreads) {
+    const int nsb = K / KSQ_QK_K, nb = K / 32;
+    const int sbytes = (wtype == KSQ_W_Q4_K) ? 144 : 210;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int s = 0; s < nsb; s++) {
+                const uint8_t* wsb = W + ((int64_t)j * nsb + s) * sbytes;
+                const uint8_t* a8 = A + ((int64_t)i * nb + 8 * s) * 36;
+                sum += (wtype == KSQ_W_Q4_K) ? dot_q4_K_sb(wsb, a8) : dot_q6_K_sb(wsb, a8);
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* Same formulas in fp64 (tolerance reference for the K-quant outputs). */
+KSQ_API void ksq_ref_gemm_kquant_f64(int wtype, const uint8_t* A, const uint8_t* W, double* C,
+                                     int M, int N, int K, int nthreads) {
+    const int nsb = K / KSQ_QK_K, nb = K / 32;
+    const int sbytes = (wtype == KSQ_W_Q4_K) ? 144 : 210;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            double sum = 0.0;
+            for (int s = 0; s < nsb; s++) {
+                const uint8_t* wsb = W + ((int64_t)j * nsb + s) * sbytes;
+                const uint8_t* a8 = A + ((int64_t)i * nb + 8 * s) * 36;
+                if (wtype == KSQ_W_Q4_K) {
+                    double sd = 0.0, sm = 0.0;
+                    for (int q = 0; q < 8; q++) {
+                        int sc, m;
+                        ksq_ref_q4_K_scale_min(q, wsb + 4, &sc, &m);
+                        sd += (double)rd_f16(a8 + q * 36) * (double)sc * (double)ksq_ref_sumi_q4_K_q8_1(wsb, q, a8 + q * 36);
+                        sm += (double)rd_f16(a8 + q * 36 + 2) * (double)m;
+                    }
+                    sum += (double)rd_f16(wsb) * sd - (double)rd_f16(wsb + 2) * sm;
+                } else {
+                    const int8_t* sc = (const int8_t*)(wsb + 192);
+                    double sd = 0.0;
+                    for (int q = 0; q < 8; q++) {
+                        const uint8_t* ab = a8 + q * 36;
+                        sd += (double)rd_f16(ab) * ((double)sc[2 * q] * ksq_ref_sumi_q6_K_q8_1(wsb, 2 * q, ab) +
+                                                    (double)sc[2 * q + 1] * ksq_ref_sumi_q6_K_q8_1(wsb, 2 * q + 1, ab));
+                    }
+                    sum += (double)rd_f16(wsb + 208) * sd;
+                }
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* Per-block integer dots for every (m, n, block): out[m][n][nblk].  Blocks are
+ * the 32-element Q blocks for Q4_0/Q8_0/Q4_K (nblk = K/32) and the 16-element
+ * sub-blocks for Q6_K (nblk = K/16). */
+KSQ_API void ksq_ref_block_sumi(int wtype, const uint8_t* A, const uint8_t* W, int32_t* out,
+                                int M, int N, int K) {
+    const int nb = K / 32;
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            if (wtype == KSQ_W_Q4_0 || wtype == KSQ_W_Q8_0) {
+                const int wbytes = (wtype == KSQ_W_Q4_0) ? 18 : 34;
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                    const uint8_t* wb = W + ((int64_t)j * nb + b) * wbytes;
+                    out[((int64_t)i * N + j) * nb + b] = (wtype == KSQ_W_Q4_0) ? ksq_ref_sumi_q4_0_q8_1(wb, ab)
+                                                                              : ksq_ref_sumi_q8_0_q8_1(wb, ab);
+                }
+            } else if (wtype == KSQ_W_Q4_K) {
+                const int nsb = K / 256;
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                    const uint8_t* wsb = W + ((int64_t)j * nsb + b / 8) * 144;
+                    out[((int64_t)i * N + j) * nb + b] = ksq_ref_sumi_q4_K_q8_1(wsb, b % 8, ab);
+                }
+            } else {
+                const int nsb = K / 256, nsub = K / 16;
+                for (int u = 0; u < nsub; u++) {
+                    const uint8_t* ab = A + ((int64_t)i * nb + u / 2) * 36;
+                    const uint8_t* wsb = W + ((int64_t)j * nsb + u / 16) * 210;
+                    out[((int64_t)i * N + j) * nsub + u] = ksq_ref_sumi_q6_K_q8_1(wsb, u % 16, ab);
+                }
+            }
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Expert-grouped MoE (absent from the reference for GGML types; structure   */
+/* after results/moe/.../ksearch_best_moe.cu routing -> grouping -> grouped  */
+/* GEMM -> weighted combine).                                                */
+/* ------------------------------------------------------------------------ */
+
+/* Softmax over E logits (fp32, max-subtracted, ascending sum), then top_k by
+ * probability; ties go to the lower expert index.  Selection compares the
+ * logits themselves (softmax is monotonic), so it does not depend on expf.
+ * renorm != 0 divides the chosen probabilities by their sum (Mixtral form);
+ * renorm == 0 keeps the plain softmax probabilities. */
+KSQ_API void ksq_ref_moe_route(const float* logits, int T, int E, int top_k, int renorm,
+                               int32_t* ids, float* w) {
+    float* p = (float*)malloc(sizeof(float) * (size_t)E);
+    unsigned char* used = (unsigned char*)malloc((size_t)E);
+    for (int t = 0; t < T; t++) {
+        const float* l = logits + (int64_t)t * E;
+        float mx = l[0];
+        for (int e = 1; e < E; e++) mx = (l[e] > mx) ? l[e] : mx;
+        float sum = 0.0f;
+        for (int e = 0; e < E; e++) { p[e] = expf(l[e] - mx); sum += p[e]; }
+        for (int e = 0; e < E; e++) { p[e] = p[e] / sum; used[e] = 0; }
+        float wsum = 0.0f;
+        for (int s = 0; s < top_k; s++) {
+            int best = -1;
+            for (int e = 0; e < E; e++) {
+                if (used[e]) continue;
+                if (best < 0 || l[e] > l[best]) best = e;
+            }
+            used[best] = 1;
+            ids[(int64_t)t * top_k + s] = best;
+            w[(int64_t)t * top_k + s] = p[best];
+            wsum += p[best];
+        }
+        if (renorm)
+            for (int s = 0; s < top_k; s++) w[(int64_t)t * top_k + s] /= wsum;
+    }
+    free(p);
+    free(used);
+}
+
+/* MoE Q4_0 up-projection: out[t][n] = sum_s w[t][s] * (A_q8_1[t] . W[ids[t][s]][n]),
+ * each expert product in the gemm_w4a8_reference block formula (fp64 accumulation
+ * here, as the tolerance reference), slots combined in slot order. */
+KSQ_API void ksq_ref_moe_q4_0_f64(const uint8_t* W, const uint8_t* A, const int32_t* ids,
+                                  const float* w, double* out, int T, int N, int K, int top_k,
+                                  int nthreads) {
+    const int nb = K / 32;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int t = 0; t < T; t++) {
+        for (int n = 0; n < N; n++) {
+            double acc = 0.0;
+            for (int s = 0; s < top_k; s++) {
+                const int e = ids[(int64_t)t * top_k + s];
+                const uint8_t* We = W + (int64_t)e * N * nb * 18;
+                double sum = 0.0;
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t* ab = A + ((int64_t)t * nb + b) * 36;
+                    const uint8_t* wb = We + ((int64_t)n * nb + b) * 18;
+                    sum += (double)rd_f16(wb) * ((double)rd_f16(ab) * (double)ksq_ref_sumi_q4_0_q8_1(wb, ab) -
+                                                 8.0 * (double)rd_f16(ab + 2));
+                }
+                acc += (double)w[(int64_t)t * top_k + s] * sum;
+            }
+            out[(int64_t)t * N + n] = acc;
+        }
+    }
+}
+
+KSQ_API int ksq_ref_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

@@ -1,0 +1,186 @@
+"""ctypes front end of the CPU oracle (oracle/ksq_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker.  The product library
+never imports this module.
+
+All buffers are numpy arrays; quantised tensors are flat uint8 byte arrays in
+the reference layouts (block_q4_0 18 B, block_q8_0 34 B, block_q8_1 36 B,
+block_q4_K 144 B, block_q6_K 210 B).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libksq_oracle.so")
+
+W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K = 0, 1, 2, 3
+WBYTES = {W_Q4_0: 18, W_Q8_0: 34, W_Q4_K: 144, W_Q6_K: 210}
+WELEMS = {W_Q4_0: 32, W_Q8_0: 32, W_Q4_K: 256, W_Q6_K: 256}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        P = ctypes.c_void_p
+        i32, i64 = ctypes.c_int, ctypes.c_int64
+        L.ksq_ref_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.ksq_ref_f16_to_f32.restype = ctypes.c_float
+        L.ksq_ref_f32_to_f16.argtypes = [ctypes.c_float]
+        L.ksq_ref_f32_to_f16.restype = ctypes.c_uint16
+        for name in ("quantize_row_q8_1", "quantize_row_q8_0", "quantize_row_q4_0",
+                     "dequantize_row_q4_0", "dequantize_row_q8_0", "dequantize_row_q8_1",
+                     "dequantize_row_q4_K", "dequantize_row_q6_K"):
+            f = getattr(L, "ksq_ref_" + name)
+            f.argtypes = [P, P, i64]
+            f.restype = None
+        for name in ("sumi_q4_0_q8_1", "sumi_q8_0_q8_1"):
+            f = getattr(L, "ksq_ref_" + name)
+            f.argtypes = [P, P]
+            f.restype = ctypes.c_int32
+        L.ksq_ref_q4_K_scale_min.argtypes = [i32, P, P, P]
+        L.ksq_ref_sumi_q4_K_q8_1.argtypes = [P, i32, P]
+        L.ksq_ref_sumi_q4_K_q8_1.restype = ctypes.c_int32
+        L.ksq_ref_sumi_q6_K_q8_1.argtypes = [P, i32, P]
+        L.ksq_ref_sumi_q6_K_q8_1.restype = ctypes.c_int32
+        for name in ("gemm_w4a8", "gemm_w8a8"):
+            getattr(L, "ksq_ref_" + name).argtypes = [P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_f64.argtypes = [i32, P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_kquant.argtypes = [i32, P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_kquant_f64.argtypes = [i32, P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_block_sumi.argtypes = [i32, P, P, P, i32, i32, i32]
+        L.ksq_ref_moe_route.argtypes = [P, i32, i32, i32, i32, P, P]
+        L.ksq_ref_moe_q4_0_f64.argtypes = [P, P, P, P, P, i32, i32, i32, i32, i32]
+        L.ksq_ref_max_threads.restype = i32
+        _lib = L
+    return _lib
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def max_threads() -> int:
+    return lib().ksq_ref_max_threads()
+
+
+def f32_to_f16_bits(x: float) -> int:
+    return lib().ksq_ref_f32_to_f16(x)
+
+
+def f16_bits_to_f32(h: int) -> float:
+    return lib().ksq_ref_f16_to_f32(h)
+
+
+def quantize_q8_1(x: np.ndarray) -> np.ndarray:
+    """fp32 [M, K] -> block_q8_1 bytes [M, K/32, 36] (quantize_row_q8_1_ref per row)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, 36), dtype=np.uint8)
+    lib().ksq_ref_quantize_row_q8_1(_p(x), _p(y), M * K)
+    return y
+
+
+def quantize_q8_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, 34), dtype=np.uint8)
+    lib().ksq_ref_quantize_row_q8_0(_p(x), _p(y), M * K)
+    return y
+
+
+def quantize_q4_0(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, 18), dtype=np.uint8)
+    lib().ksq_ref_quantize_row_q4_0(_p(x), _p(y), M * K)
+    return y
+
+
+def dequantize(wtype_or_name, q: np.ndarray, rows: int, K: int) -> np.ndarray:
+    name = {W_Q4_0: "q4_0", W_Q8_0: "q8_0", W_Q4_K: "q4_K", W_Q6_K: "q6_K"}.get(wtype_or_name, wtype_or_name)
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    y = np.empty((rows, K), dtype=np.float32)
+    getattr(lib(), "ksq_ref_dequantize_row_" + name)(_p(q), _p(y), rows * K)
+    return y
+
+
+def gemm(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 1) -> np.ndarray:
+    """Reference fp32 accumulation order: C[M, N]."""
+    a = np.ascontiguousarray(a_q8_1, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float32)
+    if wtype == W_Q4_0:
+        lib().ksq_ref_gemm_w4a8(_p(a), _p(w), _p(C), M, N, K, nthreads)
+    elif wtype == W_Q8_0:
+        lib().ksq_ref_gemm_w8a8(_p(a), _p(w), _p(C), M, N, K, nthreads)
+    else:
+        lib().ksq_ref_gemm_kquant(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
+    return C
+
+
+def gemm_f64(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 0) -> np.ndarray:
+    """The same block formulas accumulated in fp64 (tolerance reference)."""
+    a = np.ascontiguousarray(a_q8_1, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float64)
+    nthreads = nthreads or max_threads()
+    if wtype in (W_Q4_0, W_Q8_0):
+        lib().ksq_ref_gemm_f64(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
+    else:
+        lib().ksq_ref_gemm_kquant_f64(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
+    return C
+
+
+def block_sumi(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: int) -> np.ndarray:
+    """Integer block dots [M, N, nblk] (nblk = K/16 for Q6_K, else K/32)."""
+    a = np.ascontiguousarray(a_q8_1, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    nblk = K // 16 if wtype == W_Q6_K else K // 32
+    out = np.empty((M, N, nblk), dtype=np.int32)
+    lib().ksq_ref_block_sumi(wtype, _p(a), _p(w), _p(out), M, N, K)
+    return out
+
+
+def q4_K_scale_min(j: int, scales12: np.ndarray) -> tuple[int, int]:
+    s = np.ascontiguousarray(scales12, dtype=np.uint8)
+    sc, m = ctypes.c_int(), ctypes.c_int()
+    lib().ksq_ref_q4_K_scale_min(j, _p(s), ctypes.byref(sc), ctypes.byref(m))
+    return sc.value, m.value
+
+
+def moe_route(logits: np.ndarray, top_k: int, renorm: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    T, E = logits.shape
+    ids = np.empty((T, top_k), dtype=np.int32)
+    w = np.empty((T, top_k), dtype=np.float32)
+    lib().ksq_ref_moe_route(_p(logits), T, E, top_k, int(renorm), _p(ids), _p(w))
+    return ids, w
+
+
+def moe_q4_0_f64(w_experts: np.ndarray, a_q8_1: np.ndarray, ids: np.ndarray, wts: np.ndarray,
+                 T: int, N: int, K: int, nthreads: int = 0) -> np.ndarray:
+    W = np.ascontiguousarray(w_experts, dtype=np.uint8)
+    A = np.ascontiguousarray(a_q8_1, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    wts = np.ascontiguousarray(wts, dtype=np.float32)
+    out = np.empty((T, N), dtype=np.float64)
+    top_k = ids.shape[1]
+    lib().ksq_ref_moe_q4_0_f64(_p(W), _p(A), _p(ids), _p(wts), _p(out), T, N, K, top_k, nthreads or max_threads())
+    return out

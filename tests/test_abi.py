@@ -1,0 +1,109 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol
+include/ksq.h declares, and rejects bad arguments on the host before any launch
+(the reference entries never validate; ksq records a status instead of launching)."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _declared_symbols():
+    txt = open(os.path.join(ROOT, "include", "ksq.h")).read()
+    return re.findall(r"^KSQ_API\s+[\w\s\*]+?\b(\w+)\(", txt, flags=re.M)
+
+
+def test_header_declarations_found():
+    syms = _declared_symbols()
+    assert "gemm_w4a32c8_q4_0_fp32_int8" in syms and "ksq_gemm" in syms
+    assert len(syms) >= 19
+
+
+def test_library_exports_every_declared_symbol():
+    from ksq import _lib
+    L = _lib.lib()
+    for s in _declared_symbols():
+        assert hasattr(L, s), s
+        assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
+
+
+def test_block_layout_header_matches_formats():
+    from ksq.formats import QUANT_TYPES
+    hdr = open(os.path.join(ROOT, "include", "ksq_blocks.h")).read()
+    for name, size in (("q4_0", 18), ("q8_0", 34), ("q8_1", 36), ("q4_K", 144), ("q6_K", 210)):
+        assert f"sizeof(ksq_block_{name}) == {size}" in hdr
+        assert QUANT_TYPES["block_" + name].size_bytes == size
+
+
+def test_version_and_error_strings():
+    from ksq import _lib
+    L = _lib.lib()
+    assert b"gfx950" in L.ksq_version()
+    assert L.ksq_error_string(0) == b"ok"
+    assert L.ksq_error_string(3) == b"misaligned pointer"
+
+
+FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced by the failing paths below
+
+
+@pytest.mark.parametrize("args,status", [
+    ((9, 0, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # unknown weight type
+    ((0, 7, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # unknown activation type
+    ((0, 0, FAKE, FAKE, FAKE, -1, 1, 32), 2),         # negative M
+    ((0, 0, FAKE, FAKE, FAKE, 1, 1, 48), 2),          # K % 32
+    ((2, 0, FAKE, FAKE, FAKE, 1, 1, 288), 2),         # K-quant needs K % 256
+    ((0, 0, None, FAKE, FAKE, 1, 1, 32), 1),          # null weight
+    ((0, 0, FAKE, FAKE, None, 1, 1, 32), 1),          # null output
+    ((0, 0, FAKE + 1, FAKE, FAKE, 1, 1, 32), 3),      # odd weight address
+    ((2, 0, FAKE + 2, FAKE, FAKE, 1, 1, 256), 3),     # K-quant weight not 4-byte aligned
+    ((0, 0, FAKE, FAKE + 4, FAKE, 1, 1, 32), 3),      # fp32 activation not 16-byte aligned
+    ((0, 1, FAKE, FAKE + 2, FAKE, 1, 1, 32), 3),      # Q8_1 activation not 4-byte aligned
+    ((0, 0, FAKE, FAKE, FAKE + 2, 1, 1, 32), 3),      # output not 4-byte aligned
+])
+def test_gemm_rejects_bad_arguments(args, status):
+    from ksq import _lib
+    L = _lib.lib()
+    st = L.ksq_gemm(*args, None, 0, None)
+    assert st == status
+    assert L.ksq_last_error() == status
+    assert L.ksq_last_error_message()
+
+
+def test_empty_calls_are_noops():
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_gemm(0, 0, None, None, None, 0, 5, 64, None, 0, None) == 0
+    assert L.ksq_gemm(0, 0, None, None, None, 5, 0, 64, None, 0, None) == 0
+    assert L.ksq_quantize_q8_1(None, None, 0, 64, None) == 0
+
+
+def test_workspace_size():
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == 2048 * 128 * 36
+    assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == 0
+
+
+def test_void_entry_records_error():
+    """The drop-in void entry validates too (the reference's would launch blindly)."""
+    from ksq import _lib
+    L = _lib.lib()
+    L.gemm_w4a32c8_q4_0_fp32_int8(FAKE, FAKE, FAKE, 1, 1, 33)
+    assert L.ksq_last_error() == 2
+
+
+def test_forward_mirrors_harness_checks():
+    import torch
+    from ksq import forward
+    w = torch.zeros(8, dtype=torch.uint8)
+    a = torch.zeros(32, dtype=torch.float32)
+    with pytest.raises(RuntimeError, match="Weight must be CUDA tensor"):
+        forward(w, a, 1, 1, 32)
+
+
+def test_set_path_validation():
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_set_path(3) == 4
+    assert L.ksq_set_path(0) == 0

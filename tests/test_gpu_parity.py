@@ -1,0 +1,240 @@
+"""Parity of the HIP path (through the C ABI) with the CPU oracle.  GPU only.
+
+Bars: bit-exact for the Q8_1 quantiser and every integer block dot (v_dot4
+decode kernels and int8 MFMA tiles); fp32 outputs within max relative error
+1e-3 of the fp64 oracle (TOL below; per element against |ref| with a floor of
+1e-3 of the row's max |ref| so near-zero outputs do not dominate).  Full
+BASELINE sizes are checked on sampled rows and through size-independent
+properties.
+"""
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    from ksq import _lib
+    _lib.lib()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _rel_err(y, ref):
+    y = np.asarray(y, np.float64)
+    ref = np.asarray(ref, np.float64)
+    floor = 1e-3 * np.abs(ref).max(axis=-1, keepdims=True) + 1e-30
+    return float((np.abs(y - ref) / np.maximum(np.abs(ref), floor)).max())
+
+
+def _gpu_gemm(dev, wtype, w, x, M, N, K, atype=0, path=0):
+    import torch
+    from ksq import ops
+    ops.set_path(path)
+    try:
+        out = ops.gemm(wtype, atype, _t(w, dev), _t(x, dev), M, N, K)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_path(0)
+    return out.cpu().numpy()
+
+
+# ------------------------------------------------------------------ quantiser
+def test_quantize_q8_1_bit_exact(dev, oracle):
+    import torch
+    from ksq import ops
+    g = np.random.default_rng(100)
+    for M, K in ((1, 4096), (3, 1024), (257, 96), (2048, 4096)):
+        x = g.standard_normal((M, K), dtype=np.float32)
+        if M == 3:
+            x[0, :32] = 0.0
+            x[1, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5, 3.49999976]
+            x[1, 8:32] = 0.0
+            x[2, 32:64] *= 3e4
+            x[2, 64:96] *= 1e-30
+        q = ops.quantize_q8_1(_t(x, dev))
+        torch.cuda.synchronize()
+        assert np.array_equal(q.cpu().numpy(), oracle.quantize_q8_1(x)), (M, K)
+
+
+def test_golden_fixture_on_gpu(dev):
+    """The committed fixtures reproduce on the GPU with no CPU oracle in the loop."""
+    import torch
+    from ksq import ops
+    z = np.load(os.path.join(GOLDEN, "q4_0_q8_1_small.npz"), allow_pickle=False)
+    M, K = z["x"].shape
+    N = z["w_q4_0"].shape[0]
+    a = ops.quantize_q8_1(_t(z["x"], dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(a.cpu().numpy(), z["a_q8_1"])
+    s = ops.block_sumi(0, _t(z["w_q4_0"], dev), a, M, N, K).cpu().numpy()
+    assert np.array_equal(s, z["sumi_q4_0"])
+    z2 = np.load(os.path.join(GOLDEN, "all_formats_3x5x256.npz"), allow_pickle=False)
+    M, K = z2["x"].shape
+    for wt, name in ((0, "q4_0"), (1, "q8_0"), (2, "q4_K"), (3, "q6_K")):
+        w = z2["w_" + name]
+        N = w.shape[0]
+        s = ops.block_sumi(wt, _t(w, dev), _t(z2["a_q8_1"], dev), M, N, K).cpu().numpy()
+        assert np.array_equal(s, z2["sumi_" + name]), name
+        y = _gpu_gemm(dev, wt, w, z2["x"], M, N, K)
+        assert _rel_err(y, z2["c64_" + name]) <= TOL, name
+
+
+# ------------------------------------------------------------------ integer block dots
+@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+def test_block_sumi_dot4_bit_exact(dev, oracle, wtype):
+    from ksq import ops, synth
+    g = np.random.default_rng(200 + wtype)
+    M, N, K = 5, 37, 512
+    w = synth.weights(wtype, g, N, K)
+    a = oracle.quantize_q8_1(synth.activations(g, M, K) * 2)
+    got = ops.block_sumi(wtype, _t(w, dev), _t(a, dev), M, N, K).cpu().numpy()
+    assert np.array_equal(got, oracle.block_sumi(wtype, a, w, M, N, K))
+
+
+@pytest.mark.parametrize("wtype", [0, 1])
+def test_block_sumi_mfma_bit_exact(dev, oracle, wtype):
+    from ksq import ops, synth
+    g = np.random.default_rng(300 + wtype)
+    M, N, K = 160, 96, 512          # ragged against the 128 x 128 tile
+    w = synth.weights(wtype, g, N, K)
+    a = oracle.quantize_q8_1(synth.activations(g, M, K))
+    # extreme blocks: all -128 activations against all-15 nibbles / all 127 weights
+    a[0, 0, 4:] = np.uint8(0x80)
+    got = ops.block_sumi(wtype, _t(w, dev), _t(a, dev), M, N, K, mfma=True).cpu().numpy()
+    assert np.array_equal(got, oracle.block_sumi(wtype, a, w, M, N, K))
+
+
+# ------------------------------------------------------------------ fp32 outputs
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8])
+def test_q4_0_gemv_config0(dev, oracle, M):
+    """Config 0 shape (N = K = 4096) at the decode batch sizes of the definitions."""
+    from ksq import synth
+    g = np.random.default_rng(400 + M)
+    N, K = 4096, 4096
+    w = synth.weights(0, g, N, K)
+    x = synth.activations(g, M, K)
+    y = _gpu_gemm(dev, 0, w, x, M, N, K)
+    ref = oracle.gemm_f64(0, oracle.quantize_q8_1(x), w, M, N, K)
+    assert _rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("M", [1, 8, 32])
+def test_q8_0_config1(dev, oracle, M):
+    from ksq import synth
+    g = np.random.default_rng(500 + M)
+    N, K = 4096, 4096
+    w = synth.weights(1, g, N, K)
+    x = synth.activations(g, M, K)
+    y = _gpu_gemm(dev, 1, w, x, M, N, K)
+    ref = oracle.gemm_f64(1, oracle.quantize_q8_1(x), w, M, N, K)
+    assert _rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("wtype,path", [(0, 1), (0, 2), (1, 1), (1, 2)])
+def test_paths_agree_small(dev, oracle, wtype, path):
+    """Both the v_dot4 and the MFMA path on ragged shapes."""
+    from ksq import synth
+    g = np.random.default_rng(600 + 10 * wtype + path)
+    for M, N, K in ((1, 1, 256), (7, 33, 512), (130, 200, 768), (64, 128, 256)):
+        w = synth.weights(wtype, g, N, K)
+        x = synth.activations(g, M, K)
+        y = _gpu_gemm(dev, wtype, w, x, M, N, K, path=path)
+        ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
+        assert _rel_err(y, ref) <= TOL, (M, N, K)
+
+
+def test_q4_0_prefill_config2_sampled(dev, oracle):
+    """Config 2 (M = 2048, N = K = 4096) on the MFMA path; 48 sampled rows against the oracle."""
+    from ksq import synth
+    g = np.random.default_rng(700)
+    M, N, K = 2048, 4096, 4096
+    w = synth.weights(0, g, N, K)
+    x = synth.activations(g, M, K)
+    y = _gpu_gemm(dev, 0, w, x, M, N, K)
+    rows = np.sort(g.choice(M, 48, replace=False))
+    rows[0], rows[-1] = 0, M - 1
+    ref = oracle.gemm_f64(0, oracle.quantize_q8_1(x[rows]), w, len(rows), N, K)
+    assert _rel_err(y[rows], ref) <= TOL
+    assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("wtype", [2, 3])
+def test_kquant_config3_sampled(dev, oracle, wtype):
+    """Config 3 shape (M = 128, N = 14336, K = 4096); 16 sampled rows against the oracle."""
+    from ksq import synth
+    g = np.random.default_rng(800 + wtype)
+    M, N, K = 128, 14336, 4096
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    y = _gpu_gemm(dev, wtype, w, x, M, N, K)
+    rows = np.sort(g.choice(M, 16, replace=False))
+    ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x[rows]), w, len(rows), N, K)
+    assert _rel_err(y[rows], ref) <= TOL
+
+
+@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+def test_prequantized_entry_matches_fp32_entry(dev, oracle, wtype):
+    """ksq_gemm_*_q8_1 on oracle-quantised activations == the fp32 entry (same bits in)."""
+    from ksq import synth
+    g = np.random.default_rng(900 + wtype)
+    M, N, K = 4, 96, 1024
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    y32 = _gpu_gemm(dev, wtype, w, x, M, N, K, atype=0)
+    yq = _gpu_gemm(dev, wtype, w, oracle.quantize_q8_1(x), M, N, K, atype=1)
+    assert np.array_equal(y32, yq)
+
+
+def test_unaligned_weight_uses_generic_path(dev, oracle):
+    """A weight tensor starting 2 bytes into its buffer (blocks are only 2-byte aligned)."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(1000)
+    M, N, K = 3, 50, 512
+    w = synth.weights(0, g, N, K).reshape(-1)
+    buf = torch.zeros(w.size + 16, dtype=torch.uint8, device=dev)
+    buf[2:2 + w.size] = _t(w, dev)
+    x = synth.activations(g, M, K)
+    y = ops.gemm(0, 0, buf[2:2 + w.size], _t(x, dev), M, N, K)
+    torch.cuda.synchronize()
+    ref = oracle.gemm_f64(0, oracle.quantize_q8_1(x), w, M, N, K)
+    assert _rel_err(y.cpu().numpy(), ref) <= TOL
+
+
+def test_k_zero_writes_zeros(dev):
+    import torch
+    from ksq import ops
+    out = torch.full((3, 5), 7.0, device=dev)
+    ops.gemm(0, 0, torch.zeros(1, dtype=torch.uint8, device=dev), torch.zeros(4, device=dev), 3, 5, 0, out=out)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(out).item() == 0
+
+
+def test_forward_harness_convention(dev, oracle):
+    """forward(weight, activation, M, N, K) as the reference harness calls it, plus its NMSE gate."""
+    import torch
+    from ksq import forward, synth
+    g = np.random.default_rng(1100)
+    M, N, K = 8, 4096, 4096
+    w = synth.weights(0, g, N, K)
+    x = synth.activations(g, M, K)
+    y = forward(_t(w, dev), _t(x, dev), M, N, K, entry="gemm_w4a32c8_q4_0_fp32_int8")
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    assert y.shape == (M, N) and y.dtype == np.float32
+    ref_deq = x.astype(np.float64) @ oracle.dequantize(0, w.reshape(N, -1), N, K).astype(np.float64).T
+    nmse = np.mean((y - ref_deq) ** 2) / np.mean(ref_deq ** 2)
+    assert nmse < 0.05           # unified_test_runner.py:411,433-438

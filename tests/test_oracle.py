@@ -1,0 +1,273 @@
+"""Pins for the CPU oracle (oracle/ksq_oracle.c).  CPU only.
+
+The reference ships no golden vectors for this path (its tests grade by NMSE
+only), so the oracle is pinned by exhaustive/closed-form checks, independent
+numpy formulations (tests/npref.py), hand-computed known answers and the
+committed fixtures under tests/golden/.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import npref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- fp16
+def test_f16_to_f32_exhaustive(oracle):
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_bits_to_f32(int(v)) for v in h], dtype=np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_rne(oracle):
+    g = np.random.default_rng(1)
+    # every binary16 exponent range incl. subnormals, overflow and exact ties
+    x = (g.standard_normal(200000) * np.exp2(g.integers(-30, 20, 200000))).astype(np.float32)
+    ties = (np.arange(1, 4000, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -14)
+    special = np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 2.0 ** -24, 2.0 ** -25,
+                        2.0 ** -25 * 1.0000001, 2.0 ** -26, 5.960464477539063e-08, np.inf, -np.inf],
+                       dtype=np.float32)
+    x = np.concatenate([x, ties, -ties, special])
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_f16_bits(float(v)) for v in x], dtype=np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- Q8_1 quantiser
+def test_quantize_q8_1_matches_numpy_restatement(oracle):
+    g = np.random.default_rng(2)
+    x = g.standard_normal((16, 1024), dtype=np.float32)
+    x[3, :32] = 0.0                                   # zero block
+    x[5, 32:64] *= 1e-30                              # tiny but normal amax
+    x[7, 64:96] *= 3e4                                # |sum| beyond 65504: s rounds to +-inf
+    with np.errstate(over="ignore"):
+        assert np.array_equal(oracle.quantize_q8_1(x), npref.quantize_q8_1(x))
+
+
+def test_quantize_q8_1_known_answers(oracle):
+    # amax = 127 -> d = 1, id = 1 exactly: q = roundf(x) and the ties show the rounding mode
+    blk = np.zeros(32, dtype=np.float32)
+    blk[:8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5, 3.49999976]
+    q = oracle.quantize_q8_1(blk[None, :])[0, 0]
+    d = np.frombuffer(q[0:2].tobytes(), np.float16)[0]
+    s = np.frombuffer(q[2:4].tobytes(), np.float16)[0]
+    qs = q[4:].view(np.int8)
+    assert d == np.float16(1.0)
+    assert s == np.float16(np.float32(127 + 2.5 - 2.5 + 0.5 - 0.5 + 1.5 - 126.5 + 3.49999976))
+    # half away from zero (roundf), not half-even (rint / __float2int_rn / np.round)
+    assert list(qs[:8]) == [127, 3, -3, 1, -1, 2, -127, 3]
+    assert np.all(qs[8:] == 0)
+    # zero block: d = 0, s = 0, q = 0 (the C++ rule; the numpy harness quantiser uses d = 1)
+    z = oracle.quantize_q8_1(np.zeros((1, 32), np.float32))[0, 0]
+    assert np.all(z == 0)
+
+
+def test_quantize_q8_1_amax_maps_to_127(oracle):
+    g = np.random.default_rng(3)
+    x = g.standard_normal((64, 256), dtype=np.float32)
+    q = oracle.quantize_q8_1(x).reshape(64 * 8, 36)
+    qs = q[:, 4:].view(np.int8).astype(int)
+    xb = x.reshape(64 * 8, 32)
+    i = np.abs(xb).argmax(axis=1)
+    assert np.all(np.abs(qs[np.arange(len(i)), i]) == 127)
+    assert np.all(np.sign(qs[np.arange(len(i)), i]) == np.sign(xb[np.arange(len(i)), i]))
+
+
+# ---------------------------------------------------------------- integer block dots
+def _q4_0_block(d, qs):
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:] = qs
+    return b
+
+
+def _q8_1_block(d, s, qa):
+    b = np.zeros(36, np.uint8)
+    b[0:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:4] = np.array([s], np.float16).view(np.uint8)
+    b[4:] = np.asarray(qa, np.int8).view(np.uint8)
+    return b
+
+
+def test_sumi_q4_0_known_answers(oracle):
+    L = oracle.lib()
+    p = lambda a: a.ctypes.data  # noqa: E731
+    w15 = _q4_0_block(1.0, np.full(16, 0xFF, np.uint8))
+    assert L.ksq_ref_sumi_q4_0_q8_1(p(w15), p(_q8_1_block(1, 0, [127] * 32))) == 15 * 127 * 32
+    assert L.ksq_ref_sumi_q4_0_q8_1(p(w15), p(_q8_1_block(1, 0, [-128] * 32))) == -61440
+    # qs[i] = i | (15 - i) << 4: element k<16 is k, element k>=16 is 31-k
+    wi = _q4_0_block(1.0, np.array([i | ((15 - i) << 4) for i in range(16)], np.uint8))
+    assert L.ksq_ref_sumi_q4_0_q8_1(p(wi), p(_q8_1_block(1, 0, [1] * 32))) == 240
+    # qa[k] = k: sum_k<16 k*k + sum_k<16 (k+16)*(15-k) = 1240 + 2480 = 3720
+    assert L.ksq_ref_sumi_q4_0_q8_1(p(wi), p(_q8_1_block(1, 0, list(range(32))))) == 3720
+    # qa[k] = k for k < 16 only: 1240 for the low/high split order; the consecutive-pair
+    # nibble order (the bug in gemm_cuda_dp4a.cuh:119-143) would give 932
+    qa = [k if k < 16 else 0 for k in range(32)]
+    assert L.ksq_ref_sumi_q4_0_q8_1(p(wi), p(_q8_1_block(1, 0, qa))) == 1240
+    assert sum(k * ((k // 2) if k % 2 == 0 else 15 - k // 2) for k in range(16)) == 932
+
+
+def test_sumi_matches_bruteforce(oracle):
+    from ksq import synth
+    g = np.random.default_rng(4)
+    for wtype in (0, 1):
+        M, N, K = 3, 5, 256
+        w = synth.weights(wtype, g, N, K)
+        a = oracle.quantize_q8_1(synth.activations(g, M, K) * 3)
+        assert np.array_equal(oracle.block_sumi(wtype, a, w, M, N, K), npref.sumi(wtype, a, w))
+
+
+# ---------------------------------------------------------------- GEMM
+@pytest.mark.parametrize("wtype", [0, 1])
+def test_gemm_matches_fp64_block_formula(oracle, wtype):
+    from ksq import synth
+    g = np.random.default_rng(5 + wtype)
+    M, N, K = 4, 8, 512
+    w = synth.weights(wtype, g, N, K)
+    a = oracle.quantize_q8_1(synth.activations(g, M, K))
+    ref = npref.gemm_f64(wtype, a, w)
+    c32 = oracle.gemm(wtype, a, w, M, N, K)
+    c64 = oracle.gemm_f64(wtype, a, w, M, N, K)
+    assert np.allclose(c64, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+    assert np.abs(c32 - ref).max() <= 1e-5 * np.abs(ref).max()
+    # a transposed product or a dropped s-term would not agree
+    assert not np.allclose(c32.T[:4, :4], ref[:4, :4], rtol=1e-3)
+
+
+def test_gemm_q4_0_near_dequant_matmul(oracle):
+    """The harness' fp32 oracle (dequantise W, fp32 matmul; gemm_ref.py:51-97) agrees to quantisation noise."""
+    from ksq import synth
+    g = np.random.default_rng(7)
+    M, N, K = 4, 64, 1024
+    w = synth.weights(0, g, N, K)
+    x = synth.activations(g, M, K)
+    c = oracle.gemm(0, oracle.quantize_q8_1(x), w, M, N, K)
+    ref = x.astype(np.float64) @ oracle.dequantize(0, w.reshape(N, -1), N, K).astype(np.float64).T
+    nmse = np.mean((c - ref) ** 2) / np.mean(ref ** 2)
+    assert nmse < 1e-3        # the harness threshold is 0.05 (unified_test_runner.py:411)
+
+
+def test_golden_fixtures(oracle):
+    """Committed vectors (tests/golden/make_golden.py) still reproduce."""
+    path = os.path.join(GOLDEN, "q4_0_q8_1_small.npz")
+    z = np.load(path, allow_pickle=False)
+    a = oracle.quantize_q8_1(z["x"])
+    assert np.array_equal(a, z["a_q8_1"])
+    M, K = z["x"].shape
+    N = z["w_q4_0"].shape[0]
+    assert np.array_equal(oracle.block_sumi(0, a, z["w_q4_0"], M, N, K), z["sumi_q4_0"])
+    assert np.array_equal(oracle.gemm(0, a, z["w_q4_0"], M, N, K), z["c_q4_0"])
+    assert np.array_equal(oracle.block_sumi(1, a, z["w_q8_0"], M, N, K), z["sumi_q8_0"])
+    assert np.array_equal(oracle.gemm(1, a, z["w_q8_0"], M, N, K), z["c_q8_0"])
+
+
+# ---------------------------------------------------------------- K-quants
+def test_q4_K_encoder_decoder_round_trip(oracle):
+    g = np.random.default_rng(8)
+    for _ in range(20):
+        sc = g.integers(0, 64, 8)
+        mn = g.integers(0, 64, 8)
+        q = g.integers(0, 16, 256)
+        d, dmin = np.float16(abs(g.standard_normal()) * 0.02), np.float16(abs(g.standard_normal()) * 0.02)
+        blk = npref.encode_q4_K(d, dmin, sc, mn, q)
+        for j in range(8):
+            assert oracle.q4_K_scale_min(j, blk[4:16]) == (sc[j], mn[j])
+        y = oracle.dequantize(2, blk[None, :], 1, 256)[0]
+        d32, m32 = np.float32(d), np.float32(dmin)
+        want = np.array([(d32 * np.float32(sc[e // 32])) * np.float32(q[e]) - m32 * np.float32(mn[e // 32])
+                         for e in range(256)], np.float32)
+        assert np.array_equal(y, want)
+
+
+def test_q6_K_encoder_decoder_round_trip(oracle):
+    g = np.random.default_rng(9)
+    for _ in range(20):
+        sc = g.integers(-128, 128, 16)
+        q = g.integers(0, 64, 256)
+        d = np.float16(abs(g.standard_normal()) * 0.002)
+        blk = npref.encode_q6_K(d, sc, q)
+        y = oracle.dequantize(3, blk[None, :], 1, 256)[0]
+        want = np.array([np.float32(d) * np.float32(sc[e // 16]) * np.float32(q[e] - 32) for e in range(256)],
+                        np.float32)
+        assert np.array_equal(y, want)
+
+
+def test_q4_K_zero_scales_and_single_subblock(oracle):
+    g = np.random.default_rng(10)
+    x = g.standard_normal((1, 256), dtype=np.float32)
+    a = oracle.quantize_q8_1(x)
+    q = g.integers(0, 16, 256)
+    blk = npref.encode_q4_K(0.5, 0.25, np.zeros(8, int), np.zeros(8, int), q)
+    assert oracle.gemm(2, a, blk[None, :], 1, 1, 256)[0, 0] == 0.0
+    sc = np.zeros(8, int); sc[3] = 5
+    mn = np.zeros(8, int); mn[3] = 7
+    blk = npref.encode_q4_K(0.5, 0.25, sc, mn, q)
+    da, sa, qa = npref.unpack_q8_1(a[0])
+    want = 0.5 * da[3] * 5 * int(np.dot(q[96:128], qa[3])) - 0.25 * sa[3] * 7
+    assert abs(oracle.gemm(2, a, blk[None, :], 1, 1, 256)[0, 0] - want) <= 1e-6 * abs(want)
+
+
+@pytest.mark.parametrize("wtype", [2, 3])
+def test_kquant_gemm_vs_encoded_fields(oracle, wtype):
+    """Integer-sum oracle path vs fp64 dot of fields drawn before encoding."""
+    g = np.random.default_rng(11 + wtype)
+    M, N, K = 3, 4, 512
+    nsb = K // 256
+    x = g.standard_normal((M, K), dtype=np.float32)
+    a = oracle.quantize_q8_1(x)
+    da, sa, qa = npref.unpack_q8_1(a)                 # [M, nb], [M, nb], [M, nb, 32]
+    aval = (da[..., None] * qa).reshape(M, K)
+    w = np.zeros((N, nsb, 144 if wtype == 2 else 210), np.uint8)
+    want = np.zeros((M, N))
+    for n in range(N):
+        for s in range(nsb):
+            if wtype == 2:
+                sc, mn, q = g.integers(0, 64, 8), g.integers(0, 64, 8), g.integers(0, 16, 256)
+                d, dmin = np.float16(0.01 + 0.01 * g.random()), np.float16(0.01 + 0.01 * g.random())
+                w[n, s] = npref.encode_q4_K(d, dmin, sc, mn, q)
+                wsc = float(d) * np.repeat(sc, 32) * q                   # scale part per element
+                want[:, n] += aval[:, 256 * s:256 * (s + 1)] @ wsc
+                want[:, n] -= float(dmin) * (sa[:, 8 * s:8 * (s + 1)] @ mn)
+            else:
+                sc, q = g.integers(-128, 128, 16), g.integers(0, 64, 256)
+                d = np.float16(0.001 + 0.001 * g.random())
+                w[n, s] = npref.encode_q6_K(d, sc, q)
+                want[:, n] += aval[:, 256 * s:256 * (s + 1)] @ (float(d) * np.repeat(sc, 16) * (q - 32))
+    c64 = oracle.gemm_f64(wtype, a, w, M, N, K)
+    c32 = oracle.gemm(wtype, a, w, M, N, K)
+    assert np.allclose(c64, want, rtol=1e-10, atol=1e-10 * np.abs(want).max())
+    assert np.abs(c32 - want).max() <= 1e-5 * np.abs(want).max()
+
+
+# ---------------------------------------------------------------- MoE
+def test_moe_route_and_composition(oracle):
+    from ksq import synth
+    g = np.random.default_rng(12)
+    T, E, N, K, k = 16, 4, 32, 256, 2
+    logits = synth.router_logits(g, T, E)
+    logits[0, 1] = logits[0, 2] = 5.0                          # tie -> lower index first
+    ids, wts = oracle.moe_route(logits, k)
+    assert list(ids[0]) == [1, 2]
+    order = np.argsort(-logits, axis=1, kind="stable")[:, :k]
+    assert np.array_equal(ids, order)
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p /= p.sum(1, keepdims=True)
+    assert np.allclose(wts, np.take_along_axis(p, order, 1), rtol=1e-6)
+    _, wren = oracle.moe_route(logits, k, renorm=True)
+    assert np.allclose(wren.sum(1), 1.0, rtol=1e-6)
+    # composition with the dense oracle
+    W = np.stack([synth.weights(0, g, N, K) for _ in range(E)])
+    a = oracle.quantize_q8_1(synth.activations(g, T, K))
+    out = oracle.moe_q4_0_f64(W, a, ids, wts, T, N, K)
+    dense = np.stack([oracle.gemm_f64(0, a, W[e], T, N, K) for e in range(E)])   # [E, T, N]
+    want = sum(wts[:, s, None] * dense[ids[:, s], np.arange(T)] for s in range(k))
+    assert np.allclose(out, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert counts.sum() == T * k
