@@ -5,14 +5,15 @@ Headline (BASELINE.json metric): Q4_0 x Q8_1 GEMM TOPS at M=2048 (N = K = 4096),
 with the decode GEMV's HBM GB/s at M=1 (N = K = 4096) reported beside it.
 
 A "step" is one pass of the hot path over one batch: gemm_w4a32c8_q4_0_fp32_int8
-on fp32 activations [2048, 4096] (quantize_q8_1 + the int8-MFMA GEMM), output
-fp32 [2048, 4096].  Inputs are seeded synthetic tensors resident in HBM before
-timing; the weights and activations rotate over several copies so successive
-steps do not hit the 256 MB MALL on one buffer.
+on fp32 activations [2048, 4096] -> fp32 [2048, 4096], i.e. quantize_q8_1 plus
+the int8-MFMA GEMM.  Inputs are seeded synthetic tensors resident in HBM before
+timing; weights and activations rotate over several copies so successive steps
+do not re-read one buffer from the 256 MB MALL.  Launch sequences are captured
+in HIP graphs and replayed, so host-side launch cost (ctypes) is not timed.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 
-Prints ONE JSON line.
+Prints ONE JSON line on stdout (progress goes to stderr).
 """
 from __future__ import annotations
 
@@ -33,51 +34,70 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def time_events(fn, iters: int) -> float:
-    """Average ms per call of fn() over iters calls, HIP events on torch's current stream."""
+def capture(fn, n: int):
+    """A HIP graph holding fn(0) .. fn(n-1), launched on torch's capture stream."""
+    import torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, replays: int) -> float:
+    """Milliseconds for `replays` replays of graph g (HIP events, torch's current stream)."""
     import torch
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     s.record()
-    for i in range(iters):
-        fn(i)
+    for _ in range(replays):
+        g.replay()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters
+    return s.elapsed_time(e)
 
 
-def cpu_baseline(M: int, N: int, K: int, rows: int, threads: int) -> dict:
-    """The reference CPU path (quantize_row_q8_1_ref + gemm_w4a8_reference order) timed on
-    `rows` activation rows of the workload with `threads` OpenMP threads."""
-    import numpy as np
+def cpu_baseline(M: int, N: int, K: int, budget_s: float = 10.0) -> dict:
+    """The reference CPU path (quantize_row_q8_1_ref + gemm_w4a8_reference's loop and
+    accumulation order, restated in oracle/ksq_oracle.c) on the box's host cores, over
+    a bounded sample of the workload's activation rows."""
     from ksq import synth
     from oracle import oracle
+    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
     g = synth.rng(1)
     w = synth.weights(0, g, N, K)
+    # calibrate on a few rows, then size the sample to ~budget_s
+    probe = max(threads, 8)
+    x = synth.activations(g, probe, K)
+    t0 = time.perf_counter()
+    oracle.gemm(0, oracle.quantize_q8_1(x), w, probe, N, K, nthreads=threads)
+    per_row = (time.perf_counter() - t0) / probe
+    rows = int(max(probe, min(M, budget_s / max(per_row, 1e-9))))
     x = synth.activations(g, rows, K)
     t0 = time.perf_counter()
     a = oracle.quantize_q8_1(x)
     oracle.gemm(0, a, w, rows, N, K, nthreads=threads)
     dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TOPS", "cores": threads,
-            "kind": "port",
-            "sample": f"{rows} of {M} activation rows (N=K={K}), quantize_row_q8_1_ref + gemm_w4a8_reference "
-                      f"order, {dt:.1f} s with {threads} thread(s)"}
+    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {M} activation rows x N=K={K}: quantize_row_q8_1_ref + gemm_w4a8_reference "
+                      f"loop order (oracle/ksq_oracle.c, gcc -O2, OpenMP over outputs), {dt:.2f} s"}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["gemm", "gemv", "step"],
+                    help="profiling mode: launch just that kernel sequence --steps times, eagerly, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build runs the quantized matmul path on a single "
               "MI355X (no collectives); run with --gpus 1", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     import ksq
@@ -87,7 +107,7 @@ def main() -> int:
     M, N, K = 2048, 4096, 4096
     copies = 8
     g = synth.rng(2024)
-    log(f"bench: generating inputs M={M} N={N} K={K} x{copies} copies")
+    log(f"bench: inputs M={M} N={N} K={K}, {copies} rotating copies")
     w_np = synth.weights(ksq.W_Q4_0, g, N, K)
     x_np = synth.activations(g, M, K)
     W = [torch.from_numpy(w_np).to(dev) for _ in range(copies)]
@@ -103,20 +123,33 @@ def main() -> int:
     def gemm_only(i):
         ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, W[i % copies], AQ[i % copies], M, N, K, out=out)
 
+    if args.only in ("gemm", "step"):
+        fn = gemm_only if args.only == "gemm" else step
+        for i in range(args.warmup + args.steps):
+            fn(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": args.only, "launches": args.warmup + args.steps}), flush=True)
+        return 0
+
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
     log(f"bench: timing {args.steps} steps")
+    g_step = capture(step, args.steps)
+    g_step.replay()
     t0 = time.perf_counter()
-    ms = time_events(step, args.steps)
+    ms = time_graph(g_step, 1) / args.steps
     wall = (time.perf_counter() - t0) / args.steps * 1e3
     ops_per_step = 2.0 * M * N * K
     tops = ops_per_step / (ms * 1e-3) / 1e12
 
-    gemm_ms = time_events(gemm_only, args.steps)
+    g_gemm = capture(gemm_only, args.steps)
+    g_gemm.replay()
+    gemm_ms = time_graph(g_gemm, 1) / args.steps
     gemm_tops = ops_per_step / (gemm_ms * 1e-3) / 1e12
+    del g_step, g_gemm
 
-    # ---- decode GEMV, config 0 shape, Q8_1 activations, 64 weight copies (600 MB > MALL)
+    # ---- decode GEMV, config 0 shape: 64 weight copies (604 MB, > 2x the MALL)
     Mv, Nv, Kv = 1, 4096, 4096
     gcopies = 64
     wv_np = synth.weights(ksq.W_Q4_0, g, Nv, Kv)
@@ -124,15 +157,31 @@ def main() -> int:
     xv = torch.from_numpy(synth.activations(g, Mv, Kv)).to(dev)
     aqv = ops.quantize_q8_1(xv)
     outv = torch.empty((Mv, Nv), dtype=torch.float32, device=dev)
+    wsv = torch.empty(ops.workspace_size(0, 0, Mv, Nv, Kv), dtype=torch.uint8, device=dev)
 
     def gemv(i):
         ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, WV[i % gcopies], aqv, Mv, Nv, Kv, out=outv)
 
-    for i in range(gcopies):
-        gemv(i)
-    gemv_ms = time_events(gemv, 4 * gcopies)
+    def gemv_f32(i):
+        ops.gemm(ksq.W_Q4_0, ksq.A_F32, WV[i % gcopies], xv, Mv, Nv, Kv, out=outv, workspace=wsv)
+
+    if args.only == "gemv":
+        for i in range(args.warmup + args.steps):
+            gemv(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "gemv", "launches": args.warmup + args.steps}), flush=True)
+        return 0
+
+    reps = 8
+    g_v = capture(gemv, gcopies)
+    g_v.replay()
+    gemv_ms = time_graph(g_v, reps) / (reps * gcopies)
+    g_vf = capture(gemv_f32, gcopies)
+    g_vf.replay()
+    gemv_f32_ms = time_graph(g_vf, reps) / (reps * gcopies)
     gemv_bytes = Nv * (Kv // 32) * 18 + Mv * (Kv // 32) * 36 + Mv * Nv * 4
     gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    f32_bytes = Nv * (Kv // 32) * 18 + Mv * Kv * 4 + Mv * Nv * 4
 
     result = {
         "metric": "Q4_0×Q8_1 GEMM TOPS at M=2048; GEMV HBM GB/s at M=1 (N=K=4096)",
@@ -146,24 +195,27 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded: Q4_0 nibbles U[0,15], d=|N(0,0.02)|; activations N(0,1))",
-        "config": {"workload": "q4_0_q8_1_prefill_gemm", "M": M, "N": N, "K": K,
-                   "entry": "gemm_w4a32c8_q4_0_fp32_int8 (quantize_q8_1 + int8 MFMA GEMM)",
-                   "rotating_copies": copies, "wall_ms_per_step": round(wall, 4)},
-        "roofline": {"bound": "mfma", "kernel": "mmq_kernel<0> (Q4_0 x Q8_1 int8 MFMA GEMM)",
+        "data": "synthetic, seeded (Q4_0 nibbles U[0,15], d=|N(0,0.02)|; activations N(0,1))",
+        "config": {"workload": "q4_0_q8_1_prefill_gemm (BASELINE config 2)", "M": M, "N": N, "K": K,
+                   "entry": "gemm_w4a32c8_q4_0_fp32_int8: quantize_q8_1 + int8-MFMA GEMM",
+                   "rotating_copies": copies, "host_wall_ms_per_step": round(wall, 5)},
+        "roofline": {"bound": "mfma", "kernel": "mmq_kernel<0> (Q4_0 x Q8_1, v_mfma_i32_32x32x32_i8)",
                      "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                     "avg_kernel_ms": round(gemm_ms, 5)},
+                     "avg_kernel_ms": round(gemm_ms, 5),
+                     "note": "int8 ops = 2*M*N*K per launch over the HIP-event time of graph-replayed launches"},
         "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(gemv_gbs, 1), "unit": "GB/s",
-                    "avg_ms": round(gemv_ms, 5), "algorithmic_bytes": gemv_bytes,
+                    "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6),
+                    "algorithmic_bytes": gemv_bytes,
                     "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+                    "fp32_entry_ms": round(gemv_f32_ms, 6),
+                    "fp32_entry_gbs": round(f32_bytes / (gemv_f32_ms * 1e-3) / 1e9, 1),
                     "weight_copies": gcopies},
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"bench: cpu baseline ({threads} threads)")
-        result["cpu_baseline"] = cpu_baseline(M, N, K, rows=64, threads=threads)
+        log("bench: cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(M, N, K)
     print(json.dumps(result), flush=True)
     return 0
 

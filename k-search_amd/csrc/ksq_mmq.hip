@@ -12,11 +12,20 @@
 //  * Per K step 8 blocks (256 K) are staged in LDS: Q8_1 quants as int8 rows, Q4_0
 //    weights as packed nibbles (the MFMA lane that holds k = 0..15 takes the low
 //    nibbles, the lane that holds k = 16..31 the high ones, which is exactly the
-//    Q4_0 element order), Q8_0 weights as int8 rows; the fp16 scales are widened to
-//    fp32 once at staging (d_a, -8*s_a per activation row and block, d_w per weight
-//    row and block).
-//  * Epilogue per block: acc += d_w * (d_a * float(sumi) - 8 * s_a) (Q4_0) or
-//    acc += float(sumi) * d_a * d_w (Q8_0), in fp32.
+//    Q4_0 element order), Q8_0 weights as int8 rows, plus the per-block scales.
+//  * Epilogue without an int->float conversion: the MFMA accumulates onto the bit
+//    pattern of 12582912.0f (0x4B400000), so the result read as a float is exactly
+//    12582912 + sumi (|sumi| < 2^22).  Then
+//        X   = fma(f, d_a', -12582912 * d_a')    = sumi * d_a'   (one rounding; the
+//              product 12582912 * d_a' is exact because d_a' has 11 significant bits)
+//        acc = fma(d_w, X, acc)
+//    two VALU ops per output per block.  For Q4_0 the -8 * d_w * s_a term of the
+//    reference formula is a rank-(K/32) product of fp16 fields, so it runs on the
+//    f16 MFMA (exact products) straight into the same accumulators; to fold its
+//    factor 8 exactly the main term uses d_a' = d_a / 8 and the result is scaled
+//    by 8 at the end (powers of two: exact).  Q8_0 uses d_a' = d_a and no side term.
+//  * The MFMA for the next tile is issued before the epilogue of the current one,
+//    so matrix and vector pipes overlap within a wave.
 //  * Row / column tiles past M or N load a clamped in-range row and are not stored.
 #include "ksq_device.h"
 #include "ksq_internal.h"
@@ -25,8 +34,11 @@ namespace ksq {
 
 constexpr int kBM = 128, kBN = 128, kKB = 8;
 constexpr int kAPitch = kKB * 32 + 16;  // bytes per staged activation row (conflict-free b128 reads)
+constexpr uint32_t kMagic = 0x4B400000u;  // 12582912.0f
+constexpr float kMagicF = 12582912.0f;
 
 typedef uint32_t u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 template <int WT>
 struct MmqShape {
@@ -43,14 +55,17 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
     using S = MmqShape<WT>;
     __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kAPitch];
     __shared__ __attribute__((aligned(16))) uint8_t sW[kBN * S::WPitch];
-    __shared__ __attribute__((aligned(16))) float sDa[kKB][kBM];
-    __shared__ __attribute__((aligned(16))) float sSa[kKB][kBM];
-    __shared__ __attribute__((aligned(16))) float sDw[kKB][kBN];
+    __shared__ __attribute__((aligned(16))) float sDa[kKB][kBM];     // d_a' (d_a/8 for Q4_0)
+    __shared__ __attribute__((aligned(16))) float sNc[kKB][kBM];     // -12582912 * d_a'
+    __shared__ __attribute__((aligned(16))) float sDw[kKB][kBN];     // d_w
+    __shared__ __attribute__((aligned(16))) uint16_t sSaH[kBM][kKB]; // -s_a, fp16 bits (Q4_0 side term)
+    __shared__ __attribute__((aligned(16))) uint16_t sDwH[kBN][kKB]; //  d_w, fp16 bits
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
     const int l32 = lane & 31, hi = lane >> 5;
+    const float da_scale = (WT == 0) ? 0.125f : 1.0f;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -59,6 +74,9 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
         for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    i32x16 bias;
+#pragma unroll
+    for (int r = 0; r < 16; r++) bias[r] = DUMP ? 0 : (int)kMagic;
 
     // staging assignment: thread t owns row t/2, blocks 4*(t&1) .. 4*(t&1)+3 of the K step
     const int sr = t >> 1, sh = t & 1;
@@ -83,8 +101,10 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
                 u32x4* dst = (u32x4*)(sA + sr * kAPitch + kb * 32);
                 dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
                 dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
-                sDa[kb][sr] = f16_to_f32(v[9 * j] & 0xFFFFu);
-                sSa[kb][sr] = -8.0f * f16_to_f32(v[9 * j] >> 16);
+                const float da = f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
+                sDa[kb][sr] = da;
+                sNc[kb][sr] = -kMagicF * da;
+                sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
             }
         }
         // ---- stage weights: 4 blocks = 72 B (Q4_0) / 136 B (Q8_0), 8-byte aligned
@@ -101,7 +121,9 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int kb = 4 * sh + j, off = j * S::BB;
-                sDw[kb][sr] = f16_to_f32(half_at(v, off));
+                const uint32_t dwb = half_at(v, off);
+                sDw[kb][sr] = f16_to_f32(dwb);
+                sDwH[sr][kb] = (uint16_t)dwb;
                 if constexpr (WT == 0) {
                     *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
                         u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
@@ -114,57 +136,79 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
         }
         __syncthreads();
 
-#pragma unroll 2
-        for (int b = 0; b < kKB; b++) {
-            i32x4 af[2], bf[2];
+        // 32 (block, tile) MFMAs per K step; tile index q = 4*b + 2*i + j.  The MFMA of
+        // step q+1 is issued before the epilogue of step q.
+        auto frag_a = [&](int b, int i) -> i32x4 {
+            return *(const i32x4*)(sA + (wm * 64 + i * 32 + l32) * kAPitch + b * 32 + 16 * hi);
+        };
+        auto frag_b = [&](int b, int j) -> i32x4 {
+            if constexpr (WT == 0) {
+                const u32x4 x = *(const u32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 16);
+                const int s4 = 4 * hi;
+                return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
+                             (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
+            } else {
+                return *(const i32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
+            }
+        };
+        auto epilogue = [&](int b, int i, int j, const i32x16& res) {
+            // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
+            const int col = wn * 64 + j * 32 + l32;
+            const int rowb = wm * 64 + i * 32 + 4 * hi;
+            if constexpr (DUMP) {
+                const int gn = n0 + col;
 #pragma unroll
-            for (int i = 0; i < 2; i++)
-                af[i] = *(const i32x4*)(sA + (wm * 64 + i * 32 + l32) * kAPitch + b * 32 + 16 * hi);
+                for (int r = 0; r < 16; r++) {
+                    const int gm = m0 + rowb + 8 * (r >> 2) + (r & 3);
+                    if (gm < M && gn < N) dump[((size_t)gm * N + gn) * nb + kb0 + b] = res[r];
+                }
+            } else {
+                const float dw = sDw[b][col];
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                if constexpr (WT == 0) {
-                    const u32x4 x = *(const u32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 16);
-                    const int s4 = 4 * hi;
-                    bf[j] = i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
-                                  (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
-                } else {
-                    bf[j] = *(const i32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
+                for (int q = 0; q < 4; q++) {
+                    const f32x4 da = *(const f32x4*)&sDa[b][rowb + 8 * q];
+                    const f32x4 nc = *(const f32x4*)&sNc[b][rowb + 8 * q];
+#pragma unroll
+                    for (int p = 0; p < 4; p++) {
+                        // copy the element out first: bit_cast of an ext-vector element lvalue
+                        // reads element 0 with this compiler
+                        const int e = res[4 * q + p];
+                        const float f = __builtin_bit_cast(float, e);
+                        acc[i][j][4 * q + p] = fmaf(dw, fmaf(f, da[p], nc[p]), acc[i][j][4 * q + p]);
+                    }
                 }
             }
+        };
+
+        i32x4 af[2], bf[2];
+        af[0] = frag_a(0, 0); af[1] = frag_a(0, 1);
+        bf[0] = frag_b(0, 0); bf[1] = frag_b(0, 1);
+        i32x16 cur = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], bias, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 4 * kKB; q++) {
+            const int b = q >> 2, i = (q >> 1) & 1, j = q & 1;
+            i32x16 nxt;
+            if (q + 1 < 4 * kKB) {
+                const int b1 = (q + 1) >> 2, i1 = ((q + 1) >> 1) & 1, j1 = (q + 1) & 1;
+                if (((q + 1) & 3) == 0) {
+                    af[0] = frag_a(b1, 0); af[1] = frag_a(b1, 1);
+                    bf[0] = frag_b(b1, 0); bf[1] = frag_b(b1, 1);
+                }
+                nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i1], bf[j1], bias, 0, 0, 0);
+            }
+            epilogue(b, i, j, cur);
+            cur = nxt;
+        }
+
+        if constexpr (WT == 0 && !DUMP) {
+            // side term: acc += sum_k (-s_a[m][k]) * d_w[n][k] over the 8 blocks (f16 MFMA, exact products)
 #pragma unroll
             for (int i = 0; i < 2; i++) {
+                const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 64 + i * 32 + l32][4 * hi];
 #pragma unroll
                 for (int j = 0; j < 2; j++) {
-                    const i32x16 zero = {0};
-                    const i32x16 sumi = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], zero, 0, 0, 0);
-                    // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
-                    const int col = wn * 64 + j * 32 + l32;
-                    const int rowb = wm * 64 + i * 32 + 4 * hi;
-                    if constexpr (DUMP) {
-                        const int gn = n0 + col;
-#pragma unroll
-                        for (int r = 0; r < 16; r++) {
-                            const int gm = m0 + rowb + 8 * (r >> 2) + (r & 3);
-                            if (gm < M && gn < N) dump[((size_t)gm * N + gn) * nb + kb0 + b] = sumi[r];
-                        }
-                    } else {
-                        const float dw = sDw[b][col];
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            const f32x4 da = *(const f32x4*)&sDa[b][rowb + 8 * q];
-                            if constexpr (WT == 0) {
-                                const f32x4 sa = *(const f32x4*)&sSa[b][rowb + 8 * q];
-#pragma unroll
-                                for (int p = 0; p < 4; p++)
-                                    acc[i][j][4 * q + p] =
-                                        fmaf(dw, fmaf(da[p], (float)sumi[4 * q + p], sa[p]), acc[i][j][4 * q + p]);
-                            } else {
-#pragma unroll
-                                for (int p = 0; p < 4; p++)
-                                    acc[i][j][4 * q + p] = fmaf((float)sumi[4 * q + p] * da[p], dw, acc[i][j][4 * q + p]);
-                            }
-                        }
-                    }
+                    const f16x4 dw4 = *(const f16x4*)&sDwH[wn * 64 + j * 32 + l32][4 * hi];
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dw4, acc[i][j], 0, 0, 0);
                 }
             }
         }
@@ -172,6 +216,7 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
     }
 
     if constexpr (!DUMP) {
+        const float out_scale = (WT == 0) ? 8.0f : 1.0f;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -181,7 +226,7 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int gm = rowb + 8 * (r >> 2) + (r & 3);
-                    if (gm < M && gn < N) C[(size_t)gm * N + gn] = acc[i][j][r];
+                    if (gm < M && gn < N) C[(size_t)gm * N + gn] = out_scale * acc[i][j][r];
                 }
             }
     }
