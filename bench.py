@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import argparse
 import json
+
+import numpy as np
 import os
 import sys
 import time
@@ -84,13 +86,77 @@ def cpu_baseline(M: int, N: int, K: int, budget_s: float = 10.0) -> dict:
                       f"loop order (oracle/ksq_oracle.c, gcc -O2, OpenMP over outputs), {dt:.2f} s"}
 
 
+def graph_ms(fn, n: int, reps: int) -> float:
+    """Average ms per fn(i) call over `reps` replays of a graph of n calls."""
+    g = capture(fn, n)
+    g.replay()
+    return time_graph(g, reps) / (reps * n)
+
+
+def hbm_entry(bytes_, ms, ops=None):
+    gbs = bytes_ / (ms * 1e-3) / 1e9
+    d = {"avg_ms": round(ms, 6), "algorithmic_bytes": int(bytes_), "GB/s": round(gbs, 1),
+         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    if ops is not None:
+        d["TOPS"] = round(ops / (ms * 1e-3) / 1e12, 3)
+    return d
+
+
+def other_configs(g, dev, reps: int) -> dict:
+    """BASELINE configs 1, 3 and 4, each on rotating weight copies (> 256 MB MALL in total)."""
+    import torch
+    import ksq
+    from ksq import ops, synth
+    out = {}
+    # config 1: Q8_0 x Q8_1, M in {1, 8, 32}, N = K = 4096
+    N, K = 4096, 4096
+    w = synth.weights(ksq.W_Q8_0, g, N, K)
+    copies = 32
+    Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
+    for M in (1, 8, 32):
+        aq = ops.quantize_q8_1(torch.from_numpy(synth.activations(g, M, K)).to(dev))
+        o = torch.empty((M, N), dtype=torch.float32, device=dev)
+        ms = graph_ms(lambda i: ops.gemm(ksq.W_Q8_0, ksq.A_Q8_1, Wc[i % copies], aq, M, N, K, out=o), copies, reps)
+        out[f"q8_0_M{M}"] = hbm_entry(N * (K // 32) * 34 + M * (K // 32) * 36 + M * N * 4, ms, 2.0 * M * N * K)
+    del Wc
+    # config 3: K-quants at M = 128, N = 14336, K = 4096
+    M, N, K = 128, 14336, 4096
+    aq = ops.quantize_q8_1(torch.from_numpy(synth.activations(g, M, K)).to(dev))
+    o = torch.empty((M, N), dtype=torch.float32, device=dev)
+    for wt, name, sb in ((ksq.W_Q4_K, "q4_K", 144), (ksq.W_Q6_K, "q6_K", 210)):
+        w = synth.weights(wt, g, N, K)
+        copies = 8
+        Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
+        ms = graph_ms(lambda i: ops.gemm(wt, ksq.A_Q8_1, Wc[i % copies], aq, M, N, K, out=o), copies, reps)
+        out[f"{name}_M128"] = hbm_entry(N * (K // 256) * sb + M * (K // 32) * 36 + M * N * 4, ms, 2.0 * M * N * K)
+        del Wc
+    # config 4: MoE, 512 tokens, 8 experts of 4096 -> 14336 Q4_0, top-2 (whole call: quantize,
+    # route, group, zero-fill, grouped GEMM)
+    T, E, N, K, k = 512, 8, 14336, 4096, 2
+    w = np.stack([synth.weights(ksq.W_Q4_0, g, N, K) for _ in range(E)])
+    copies = 2
+    Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
+    x = torch.from_numpy(synth.activations(g, T, K)).to(dev)
+    lg = torch.from_numpy(synth.router_logits(g, T, E)).to(dev)
+    o = torch.empty((T, N), dtype=torch.float32, device=dev)
+    ws = torch.empty(ops.moe_workspace_size(0, T, N, K, E, k), dtype=torch.uint8, device=dev)
+    ms = graph_ms(lambda i: ops.moe_gemm(ksq.W_Q4_0, Wc[i % copies], x, lg, T, N, K, E, k, out=o, workspace=ws),
+                  copies, reps)
+    moe_bytes = E * N * (K // 32) * 18 + T * K * 4 + T * E * 4 + T * N * 4
+    out["moe_q4_0_T512_E8_top2"] = hbm_entry(moe_bytes, ms, 2.0 * T * k * N * K)
+    del Wc
+    torch.cuda.empty_cache()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemv", "step"],
+    ap.add_argument("--only", choices=["gemm", "gemv", "step", "copy"],
                     help="profiling mode: launch just that kernel sequence --steps times, eagerly, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -104,6 +170,15 @@ def main() -> int:
     from ksq import ops, synth
 
     dev = torch.device("cuda:0")
+    if args.only == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain copy of 256 MiB
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(args.warmup + args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"only": "copy", "bytes": src.numel() * 4, "launches": args.warmup + args.steps}))
+        return 0
     M, N, K = 2048, 4096, 4096
     copies = 8
     g = synth.rng(2024)
@@ -213,6 +288,10 @@ def main() -> int:
                     "fp32_entry_gbs": round(f32_bytes / (gemv_f32_ms * 1e-3) / 1e9, 1),
                     "weight_copies": gcopies},
     }
+    del WV, g_v, g_vf
+    torch.cuda.empty_cache()
+    log("bench: other BASELINE configs")
+    result["configs"] = other_configs(g, dev, reps=4)
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
         result["cpu_baseline"] = cpu_baseline(M, N, K)

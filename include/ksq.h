@@ -117,6 +117,33 @@ KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* a
 KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
                               int M, int N, int K, void* stream);
 
+/* ---- expert-grouped MoE (no reference counterpart for GGML types) ----------
+ * output[t][n] = sum over the top_k experts e chosen for token t of
+ *                w[t][e] * (Q8_1(activation[t]) . weight[e][n]),
+ * weight = E experts, each [N][K/32] blocks (Q4_0 or Q8_0), back to back.
+ * Routing: softmax over router_logits[t][0..E-1] (fp32), the top_k experts by logit
+ * (ties -> lower index); w = the softmax probabilities of the chosen experts, or those
+ * divided by their sum when renorm != 0.  K % 256 == 0, E <= 256, top_k <= E.
+ * For top_k <= 2 every output element receives exactly top_k fp32 additions onto
+ * zero, so the result does not depend on their order.
+ * Structure after the reference's FP8 MoE kernel (results/moe/moe_fp8_block_scale_ds_
+ * routing_topk8_ng8_kg4_e32_h7168_i2048/ksearch_best_moe.cu:44,193-236,525-582). */
+KSQ_API size_t ksq_moe_workspace_size(int wtype, int T, int N, int K, int E, int top_k);
+/* topk_ids_out [T][top_k] / topk_weights_out [T][top_k]: optional device outputs of the routing. */
+KSQ_API int ksq_moe_gemm(int wtype, const void* weights, const float* activation, const float* router_logits,
+                         float* output, int T, int N, int K, int E, int top_k, int renorm,
+                         int32_t* topk_ids_out, float* topk_weights_out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+/* The same with caller-supplied routing (ids in [0, E); other ids contribute nothing). */
+KSQ_API int ksq_moe_gemm_routed(int wtype, const void* weights, const float* activation,
+                                const int32_t* topk_ids, const float* topk_weights, float* output,
+                                int T, int N, int K, int E, int top_k,
+                                void* workspace, size_t workspace_bytes, void* stream);
+/* Drop-in style void entry for the Q4_0 up-projection (default stream, internal workspace). */
+KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* activation,
+                                        const float* router_logits, float* output,
+                                        int T, int N, int K, int E, int top_k);
+
 /* Path selection for testing and benchmarking: 0 = automatic (default),
  * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies. */
 KSQ_API int ksq_set_path(int path);

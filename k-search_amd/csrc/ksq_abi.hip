@@ -220,6 +220,120 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
     return e == hipSuccess ? ok() : hip_error(e, "mfma block_sumi launch");
 }
 
+// ---- expert-grouped MoE --------------------------------------------------------
+namespace {
+constexpr int kMoeTileRows = 128;  // rows per grouped-GEMM tile (the MFMA kernel's BM)
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct MoeLayout {
+    size_t aq, ids, wts, rows, eend, ntiles, texp, trow0, scratch, total;
+    int max_tiles;
+};
+
+MoeLayout moe_layout(int T, int N, int K, int E, int top_k) {
+    MoeLayout L{};
+    const size_t ent = (size_t)T * top_k;
+    L.max_tiles = (int)((ent + kMoeTileRows - 1) / kMoeTileRows) + E;
+    size_t off = 0;
+    L.aq = off; off = align256(off + (size_t)T * (K / 32) * 36);
+    L.ids = off; off = align256(off + ent * 4);
+    L.wts = off; off = align256(off + ent * 4);
+    L.rows = off; off = align256(off + ent * 4);
+    L.eend = off; off = align256(off + (size_t)E * 4);
+    L.ntiles = off; off = align256(off + 4);
+    L.texp = off; off = align256(off + (size_t)L.max_tiles * 4);
+    L.trow0 = off; off = align256(off + (size_t)L.max_tiles * 4);
+    L.scratch = off; off = align256(off + (top_k > 2 ? ent * (size_t)N * 4 : 0));
+    L.total = off;
+    return L;
+}
+
+int moe_run(int wtype, const void* weights, const float* activation, const float* logits, const int32_t* ids_in,
+            const float* wts_in, float* output, int T, int N, int K, int E, int top_k, int renorm, int32_t* ids_out,
+            float* wts_out, void* workspace, size_t ws_bytes, hipStream_t s) {
+    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q8_0)
+        return set_error(KSQ_ERR_TYPE, "MoE GEMM supports Q4_0 and Q8_0 weights");
+    if (T < 0 || N < 0 || K < 0 || E < 1 || E > 256 || top_k < 1 || top_k > E)
+        return set_error(KSQ_ERR_SHAPE, "bad MoE shape T=%d N=%d K=%d E=%d top_k=%d", T, N, K, E, top_k);
+    if (K % 256) return set_error(KSQ_ERR_SHAPE, "MoE GEMM needs K %% 256 == 0 (K=%d)", K);
+    if (T == 0 || N == 0) return ok();
+    if (!weights || !activation || !output || (!logits && (!ids_in || !wts_in)))
+        return set_error(KSQ_ERR_NULL, "null MoE argument");
+    if (((uintptr_t)weights & 15u) || ((uintptr_t)activation & 15u) || ((uintptr_t)output & 3u))
+        return set_error(KSQ_ERR_ALIGN, "MoE weights/activation must be 16-byte aligned, output 4-byte");
+    const MoeLayout L = moe_layout(T, N, K, E, top_k);
+    void* ws = workspace;
+    if (ws) {
+        if (ws_bytes < L.total) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, L.total);
+        if ((uintptr_t)ws & 255u) return set_error(KSQ_ERR_ALIGN, "MoE workspace must be 256-byte aligned");
+    } else {
+        int st = pool_get(L.total, &ws);
+        if (st != KSQ_OK) return st;
+    }
+    uint8_t* base = (uint8_t*)ws;
+    uint8_t* aq = base + L.aq;
+    int32_t* ids = ids_out ? ids_out : (int32_t*)(base + L.ids);
+    float* wts = wts_out ? wts_out : (float*)(base + L.wts);
+    hipError_t e = ksq::launch_quantize_q8_1(activation, aq, T, K, s);
+    if (e != hipSuccess) return hip_error(e, "quantize launch");
+    if (logits) {
+        e = ksq::launch_moe_route(logits, T, E, top_k, renorm, ids, wts, s);
+        if (e != hipSuccess) return hip_error(e, "route launch");
+    } else {
+        ids = (int32_t*)ids_in;
+        wts = (float*)wts_in;
+    }
+    int32_t* rows = (int32_t*)(base + L.rows);
+    int32_t* eend = (int32_t*)(base + L.eend);
+    int32_t* ntiles = (int32_t*)(base + L.ntiles);
+    int32_t* texp = (int32_t*)(base + L.texp);
+    int32_t* trow0 = (int32_t*)(base + L.trow0);
+    e = ksq::launch_moe_group(ids, T, top_k, E, kMoeTileRows, rows, eend, ntiles, texp, trow0, s);
+    if (e != hipSuccess) return hip_error(e, "group launch");
+    float* scratch = top_k > 2 ? (float*)(base + L.scratch) : nullptr;
+    if (!scratch) {
+        e = ksq::launch_fill_zero(output, (int64_t)T * N, s);
+        if (e != hipSuccess) return hip_error(e, "fill launch");
+    }
+    ksq::MoeTilesArgs a{ntiles, texp, trow0, eend, rows, wts, scratch, top_k};
+    e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, a, s);
+    if (e != hipSuccess) return hip_error(e, "grouped gemm launch");
+    if (scratch) {
+        e = ksq::launch_moe_combine(scratch, output, T, N, top_k, s);
+        if (e != hipSuccess) return hip_error(e, "combine launch");
+    }
+    return ok();
+}
+}  // namespace
+
+size_t ksq_moe_workspace_size(int wtype, int T, int N, int K, int E, int top_k) {
+    (void)wtype;
+    if (T <= 0 || N <= 0 || K <= 0 || E <= 0 || top_k <= 0) return 0;
+    return moe_layout(T, N, K, E, top_k).total;
+}
+
+int ksq_moe_gemm(int wtype, const void* weights, const float* activation, const float* router_logits,
+                 float* output, int T, int N, int K, int E, int top_k, int renorm, int32_t* topk_ids_out,
+                 float* topk_weights_out, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!router_logits && T > 0 && N > 0) return set_error(KSQ_ERR_NULL, "router_logits is NULL");
+    return moe_run(wtype, weights, activation, router_logits, nullptr, nullptr, output, T, N, K, E, top_k, renorm,
+                   topk_ids_out, topk_weights_out, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int ksq_moe_gemm_routed(int wtype, const void* weights, const float* activation, const int32_t* topk_ids,
+                        const float* topk_weights, float* output, int T, int N, int K, int E, int top_k,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+    return moe_run(wtype, weights, activation, nullptr, topk_ids, topk_weights, output, T, N, K, E, top_k, 0,
+                   nullptr, nullptr, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* activation, const float* router_logits,
+                                float* output, int T, int N, int K, int E, int top_k) {
+    (void)ksq_moe_gemm(KSQ_W_Q4_0, weight, activation, router_logits, output, T, N, K, E, top_k, 0, nullptr,
+                       nullptr, nullptr, 0, nullptr);
+}
+
 #define KSQ_DROPIN(NAME, WT, AT, ACT_T)                                                              \
     void NAME(const uint8_t* weight, const ACT_T* activation, float* output, int M, int N, int K) { \
         (void)ksq_gemm(WT, AT, weight, activation, output, M, N, K, nullptr, 0, nullptr);             \

@@ -24,6 +24,32 @@ bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A)
 hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       hipStream_t s);
 
+// Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /
+// launch_moe_group; C must be zeroed first when scratch is null (top_k <= 2).
+struct MoeTilesArgs {
+    const int32_t* num_tiles;
+    const int32_t* tile_expert;
+    const int32_t* tile_row0;
+    const int32_t* expert_end;
+    const int32_t* rows;
+    const float* weights;
+    float* scratch;
+    int top_k;
+};
+hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
+                          const MoeTilesArgs& a, hipStream_t s);
+
+// MoE routing: softmax over E logits per token, top_k by logit (ties -> lower expert).
+hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
+                            hipStream_t s);
+// Stable grouping of the T*top_k (token, slot) entries by expert, plus the tile schedule
+// for tiles of `tile_rows` rows.  max_tiles = T*top_k/tile_rows + E bounds num_tiles.
+hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
+                            int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
+                            hipStream_t s);
+// out[t][n] = sum_s scratch[t*top_k + s][n] in slot order (top_k > 2 combine).
+hipError_t launch_moe_combine(const float* scratch, float* out, int T, int N, int top_k, hipStream_t s);
+
 // Per-block integer dots [M][N][nblk] from the same device block-dot code the
 // decode kernels use (debug entry for the bit-exact check).
 hipError_t launch_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N,

@@ -48,10 +48,25 @@ struct MmqShape {
     static constexpr int HalfBytes = 4 * BB;           // 72 or 136: half a row's K step
 };
 
-template <int WT, bool DUMP>
+// Expert-grouped mode (MoE): workgroup tile y is entry blockIdx.x of a tile schedule;
+// its activation rows are gathered through a sorted (token, slot) list and its output is
+// added, weighted by the routing probability, into C[token][n].
+struct MoeTiles {
+    const int32_t* num_tiles;   // [1]
+    const int32_t* tile_expert; // [max_tiles]
+    const int32_t* tile_row0;   // [max_tiles] first entry in `rows` of this tile
+    const int32_t* expert_end;  // [E] one past the expert's last entry in `rows`
+    const int32_t* rows;        // [T*top_k] entry j = token*top_k + slot, grouped by expert
+    const float* weights;       // [T*top_k] routing weight of entry j
+    float* scratch;             // [T*top_k][N] per-entry outputs when top_k > 2, else null
+    int top_k;
+    size_t expert_stride;       // weight bytes per expert
+};
+
+template <int WT, bool DUMP, bool MOE = false>
 __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
                                                      float* __restrict__ C, int32_t* __restrict__ dump, int M,
-                                                     int N, int nb) {
+                                                     int N, int nb, MoeTiles moe = MoeTiles{}) {
     using S = MmqShape<WT>;
     __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kAPitch];
     __shared__ __attribute__((aligned(16))) uint8_t sW[kBN * S::WPitch];
@@ -61,9 +76,23 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
     __shared__ __attribute__((aligned(16))) uint16_t sSaH[kBM][kKB]; // -s_a, fp16 bits (Q4_0 side term)
     __shared__ __attribute__((aligned(16))) uint16_t sDwH[kBN][kKB]; //  d_w, fp16 bits
 
+    __shared__ int32_t sRows[kBM];  // MoE: entry index of each tile row
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * kBM, n0 = blockIdx.x * kBN;
+    int m0 = blockIdx.y * kBM;
+    const int n0 = (MOE ? blockIdx.y : blockIdx.x) * kBN;
+    if constexpr (MOE) {
+        const int tile = blockIdx.x;
+        if (tile >= moe.num_tiles[0]) return;           // surplus workgroups of the worst-case grid
+        const int e = moe.tile_expert[tile];
+        const int r0 = moe.tile_row0[tile];
+        const int rend = moe.expert_end[e];
+        M = min(kBM, rend - r0);                         // valid rows of this tile
+        m0 = 0;
+        W += (size_t)e * moe.expert_stride;
+        if (t < kBM) sRows[t] = moe.rows[r0 + min(t, M - 1)];
+        __syncthreads();
+    }
     const int l32 = lane & 31, hi = lane >> 5;
     const float da_scale = (WT == 0) ? 0.125f : 1.0f;
 
@@ -80,7 +109,7 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
 
     // staging assignment: thread t owns row t/2, blocks 4*(t&1) .. 4*(t&1)+3 of the K step
     const int sr = t >> 1, sh = t & 1;
-    const int am = min(m0 + sr, M - 1);
+    const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
     const int wn_row = min(n0 + sr, N - 1);
     const uint8_t* a_src = A + (size_t)am * nb * kQ81Bytes + (size_t)sh * 4 * kQ81Bytes;
     const uint8_t* w_src = W + (size_t)wn_row * nb * S::BB + (size_t)sh * S::HalfBytes;
@@ -187,7 +216,7 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
 #pragma unroll
         for (int q = 0; q < 4 * kKB; q++) {
             const int b = q >> 2, i = (q >> 1) & 1, j = q & 1;
-            i32x16 nxt;
+            i32x16 nxt = bias;
             if (q + 1 < 4 * kKB) {
                 const int b1 = (q + 1) >> 2, i1 = ((q + 1) >> 1) & 1, j1 = (q + 1) & 1;
                 if (((q + 1) & 3) == 0) {
@@ -226,7 +255,16 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int gm = rowb + 8 * (r >> 2) + (r & 3);
-                    if (gm < M && gn < N) C[(size_t)gm * N + gn] = out_scale * acc[i][j][r];
+                    if (gm < M && gn < N) {
+                        if constexpr (MOE) {
+                            const int ent = sRows[gm];
+                            const float v = out_scale * acc[i][j][r] * moe.weights[ent];
+                            if (moe.scratch) moe.scratch[(size_t)ent * N + gn] = v;
+                            else unsafeAtomicAdd(C + (size_t)(ent / moe.top_k) * N + gn, v);
+                        } else {
+                            C[(size_t)gm * N + gn] = out_scale * acc[i][j][r];
+                        }
+                    }
                 }
             }
     }
@@ -244,6 +282,27 @@ hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, i
         hipLaunchKernelGGL((mmq_kernel<0, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
     else
         hipLaunchKernelGGL((mmq_kernel<1, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
+                          const MoeTilesArgs& a, hipStream_t s) {
+    MoeTiles mt;
+    mt.num_tiles = a.num_tiles;
+    mt.tile_expert = a.tile_expert;
+    mt.tile_row0 = a.tile_row0;
+    mt.expert_end = a.expert_end;
+    mt.rows = a.rows;
+    mt.weights = a.weights;
+    mt.scratch = a.scratch;
+    mt.top_k = a.top_k;
+    const int nb = K / 32;
+    mt.expert_stride = (size_t)N * nb * (wtype == 0 ? kQ40Bytes : kQ80Bytes);
+    const dim3 grid((unsigned)max_tiles, (unsigned)((N + kBN - 1) / kBN));
+    if (wtype == 0)
+        hipLaunchKernelGGL((mmq_kernel<0, false, true>), grid, dim3(256), 0, s, W, Aq, C, nullptr, 0, N, nb, mt);
+    else
+        hipLaunchKernelGGL((mmq_kernel<1, false, true>), grid, dim3(256), 0, s, W, Aq, C, nullptr, 0, N, nb, mt);
     return hipGetLastError();
 }
 

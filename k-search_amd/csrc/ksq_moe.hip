@@ -1,0 +1,135 @@
+// ksq_moe.hip - routing and expert grouping for the expert-grouped quantized GEMM.
+//
+// No GGML-type MoE exists in the reference; the structure follows its FP8 MoE
+// prior art (results/moe/moe_fp8_block_scale_ds_routing_topk8_ng8_kg4_e32_h7168_i2048/
+// ksearch_best_moe.cu:44,193-236,525-582: route, sort/scatter with expert offsets,
+// grouped GEMMs, weighted combine).  Here:
+//   route  one thread per token: softmax over the E logits (fp32, max-subtracted),
+//          top_k chosen by comparing logits (softmax is monotonic, so the choice does
+//          not depend on expf rounding); ties go to the lower expert index
+//   group  one wave walks the T*top_k (token, slot) entries in order and places each
+//          at its expert's cursor (ballot + popcount per expert), i.e. a stable
+//          counting sort; it also writes the per-expert end offsets and the schedule
+//          of row tiles the grouped GEMM launches over
+//   GEMM   mmq_kernel in its gathered mode (ksq_mmq.hip)
+//   combine for top_k > 2 only: per-entry outputs summed in slot order
+#include "ksq_device.h"
+#include "ksq_internal.h"
+
+namespace ksq {
+
+__global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
+                                 int32_t* __restrict__ ids, float* __restrict__ w) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const float* l = logits + (size_t)t * E;
+    float mx = l[0];
+    for (int e = 1; e < E; e++) mx = (l[e] > mx) ? l[e] : mx;
+    float sum = 0.0f;
+    for (int e = 0; e < E; e++) sum += expf(l[e] - mx);
+    // selection: repeatedly take the largest remaining logit (lowest index on ties)
+    uint64_t used[4] = {0, 0, 0, 0};  // E <= 256
+    float wsum = 0.0f;
+    for (int s = 0; s < top_k; s++) {
+        int best = -1;
+        for (int e = 0; e < E; e++) {
+            if ((used[e >> 6] >> (e & 63)) & 1ull) continue;
+            if (best < 0 || l[e] > l[best]) best = e;
+        }
+        used[best >> 6] |= 1ull << (best & 63);
+        const float p = expf(l[best] - mx) / sum;
+        ids[(size_t)t * top_k + s] = best;
+        w[(size_t)t * top_k + s] = p;
+        wsum += p;
+    }
+    if (renorm)
+        for (int s = 0; s < top_k; s++) w[(size_t)t * top_k + s] /= wsum;
+}
+
+hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
+                            hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_route_kernel, dim3((T + 255) / 256), dim3(256), 0, s, logits, T, E, top_k, renorm, ids, w);
+    return hipGetLastError();
+}
+
+// One wave.  cursor[e] counts entries placed so far for expert e.
+__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
+                                                        int tile_rows, int32_t* __restrict__ rows,
+                                                        int32_t* __restrict__ expert_end,
+                                                        int32_t* __restrict__ num_tiles,
+                                                        int32_t* __restrict__ tile_expert,
+                                                        int32_t* __restrict__ tile_row0) {
+    __shared__ int32_t count[256];
+    __shared__ int32_t start[257];
+    const int lane = threadIdx.x;
+    for (int e = lane; e < E; e += 64) count[e] = 0;
+    __syncthreads();
+    // pass 1: counts
+    for (int base = 0; base < total; base += 64) {
+        const int j = base + lane;
+        const int e = (j < total) ? ids[j] : -1;
+        for (int x = 0; x < E; x++) {
+            const uint64_t m = __ballot(e == x);
+            if (lane == 0) count[x] += __popcll(m);
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        int acc = 0, nt = 0;
+        for (int e = 0; e < E; e++) {
+            start[e] = acc;
+            for (int r = 0; r < count[e]; r += tile_rows) {
+                tile_expert[nt] = e;
+                tile_row0[nt] = acc + r;
+                nt++;
+            }
+            acc += count[e];
+            expert_end[e] = acc;
+        }
+        start[E] = acc;
+        num_tiles[0] = nt;
+    }
+    __syncthreads();
+    // pass 2: stable placement
+    for (int base = 0; base < total; base += 64) {
+        const int j = base + lane;
+        const int e = (j < total) ? ids[j] : -1;
+        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        for (int x = 0; x < E; x++) {
+            const uint64_t m = __ballot(e == x);
+            if (e == x) rows[start[x] + __popcll(m & lt)] = j;
+            __syncthreads();
+            if (lane == 0) start[x] += __popcll(m);
+            __syncthreads();
+        }
+    }
+}
+
+hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
+                            int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
+                            hipStream_t s) {
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, s, ids, T * top_k, E, tile_rows, rows, expert_end,
+                       num_tiles, tile_expert, tile_row0);
+    return hipGetLastError();
+}
+
+__global__ void moe_combine_kernel(const float* __restrict__ scratch, float* __restrict__ out, int T, int N,
+                                   int top_k) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)T * N) return;
+    const int64_t t = i / N, n = i - t * N;
+    float acc = 0.0f;
+    for (int s = 0; s < top_k; s++) acc += scratch[((size_t)t * top_k + s) * N + n];
+    out[i] = acc;
+}
+
+hipError_t launch_moe_combine(const float* scratch, float* out, int T, int N, int top_k, hipStream_t s) {
+    const int64_t n = (int64_t)T * N;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, scratch, out, T, N,
+                       top_k);
+    return hipGetLastError();
+}
+
+}  // namespace ksq

@@ -6,5 +6,5 @@ forward(weight, activation, M, N, K) convention on torch tensors.
 """
 from ._lib import A_F32, A_Q8_1, W_Q4_0, W_Q4_K, W_Q6_K, W_Q8_0, KsqError, lib  # noqa: F401
 from .formats import QUANT_TYPES, WTYPE_NAMES, quant_type  # noqa: F401
-from .ops import (ENTRY_POINTS, block_sumi, forward, gemm, quantize_q8_1, release,  # noqa: F401
-                  set_path, workspace_size)
+from .ops import (ENTRY_POINTS, block_sumi, forward, gemm, moe_gemm, moe_gemm_routed,  # noqa: F401
+                  moe_workspace_size, quantize_q8_1, release, set_path, workspace_size)

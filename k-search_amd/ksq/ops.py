@@ -84,6 +84,39 @@ def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int,
     return out
 
 
+def moe_gemm(wtype: int, weights: torch.Tensor, activation: torch.Tensor, router_logits: torch.Tensor,
+             T: int, N: int, K: int, E: int, top_k: int, renorm: bool = False,
+             out: torch.Tensor | None = None, workspace: torch.Tensor | None = None,
+             return_routing: bool = False):
+    """Expert-grouped MoE: fp32 activations [T, K], logits [T, E] -> fp32 [T, N]."""
+    dev = activation.device
+    if out is None:
+        out = torch.empty((T, N), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=dev) if return_routing else None
+    wts = torch.empty((T, top_k), dtype=torch.float32, device=dev) if return_routing else None
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ksq_moe_gemm(wtype, _ptr(weights), _ptr(activation), _ptr(router_logits), _ptr(out), T, N, K, E,
+                             top_k, int(renorm), _ptr(ids), _ptr(wts), _ptr(workspace), ws_bytes, _stream()))
+    return (out, ids, wts) if return_routing else out
+
+
+def moe_gemm_routed(wtype: int, weights: torch.Tensor, activation: torch.Tensor, topk_ids: torch.Tensor,
+                    topk_weights: torch.Tensor, T: int, N: int, K: int, E: int,
+                    out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    dev = activation.device
+    top_k = topk_ids.shape[1]
+    if out is None:
+        out = torch.empty((T, N), dtype=torch.float32, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ksq_moe_gemm_routed(wtype, _ptr(weights), _ptr(activation), _ptr(topk_ids), _ptr(topk_weights),
+                                    _ptr(out), T, N, K, E, top_k, _ptr(workspace), ws_bytes, _stream()))
+    return out
+
+
+def moe_workspace_size(wtype: int, T: int, N: int, K: int, E: int, top_k: int) -> int:
+    return lib().ksq_moe_workspace_size(wtype, T, N, K, E, top_k)
+
+
 def set_path(path: int) -> None:
     """0 automatic, 1 v_dot4 decode kernels only, 2 MFMA GEMM where it applies."""
     check(lib().ksq_set_path(path))
@@ -98,4 +131,4 @@ def release() -> None:
 
 
 __all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "block_sumi", "set_path", "workspace_size",
-           "release", "_lib"]
+           "moe_gemm", "moe_gemm_routed", "moe_workspace_size", "release", "_lib"]

@@ -238,3 +238,66 @@ def test_forward_harness_convention(dev, oracle):
     ref_deq = x.astype(np.float64) @ oracle.dequantize(0, w.reshape(N, -1), N, K).astype(np.float64).T
     nmse = np.mean((y - ref_deq) ** 2) / np.mean(ref_deq ** 2)
     assert nmse < 0.05           # unified_test_runner.py:411,433-438
+
+
+# ------------------------------------------------------------------ expert-grouped MoE
+def _moe_case(dev, oracle, T, E, N, K, top_k, renorm, seed, wtype=0):
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(seed)
+    W = np.stack([synth.weights(wtype, g, N, K) for _ in range(E)])
+    x = synth.activations(g, T, K)
+    logits = synth.router_logits(g, T, E)
+    out, ids, wts = ops.moe_gemm(wtype, _t(W, dev), _t(x, dev), _t(logits, dev), T, N, K, E, top_k, renorm=renorm,
+                                 return_routing=True)
+    torch.cuda.synchronize()
+    ids_ref, wts_ref = oracle.moe_route(logits, top_k, renorm=renorm)
+    assert np.array_equal(ids.cpu().numpy(), ids_ref)
+    assert np.allclose(wts.cpu().numpy(), wts_ref, rtol=1e-6, atol=0)
+    return W, x, logits, out.cpu().numpy(), ids_ref, wts.cpu().numpy()
+
+
+def test_moe_golden_fixture(dev, oracle):
+    import torch
+    from ksq import ops
+    z = np.load(os.path.join(GOLDEN, "moe_16x4.npz"), allow_pickle=False)
+    T, E = z["logits"].shape
+    N, K = z["w"].shape[1], z["w"].shape[2] * 32
+    top_k = z["ids"].shape[1]
+    out, ids, wts = ops.moe_gemm(0, _t(z["w"], dev), _t(z["x"], dev), _t(z["logits"], dev), T, N, K, E, top_k,
+                                 return_routing=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), z["ids"])
+    assert _rel_err(out.cpu().numpy(), z["out64"]) <= TOL
+
+
+@pytest.mark.parametrize("T,E,N,K,top_k,renorm", [(40, 4, 96, 256, 2, False), (37, 8, 160, 512, 3, True),
+                                                  (300, 6, 128, 256, 1, False)])
+def test_moe_small(dev, oracle, T, E, N, K, top_k, renorm):
+    W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, top_k, renorm, 1200 + T)
+    ref = oracle.moe_q4_0_f64(W, oracle.quantize_q8_1(x), ids, wts, T, N, K)
+    assert _rel_err(y, ref) <= TOL
+
+
+def test_moe_routed_matches_routing_entry(dev, oracle):
+    """Caller-supplied routing reproduces the routed entry bit for bit (top_k = 2 sums are order-free)."""
+    import torch
+    from ksq import ops
+    T, E, N, K = 64, 4, 128, 512
+    W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, 2, False, 1300)
+    y2 = ops.moe_gemm_routed(0, _t(W, dev), _t(x, dev), _t(ids, dev), _t(wts, dev), T, N, K, E)
+    torch.cuda.synchronize()
+    assert np.array_equal(y, y2.cpu().numpy())
+
+
+def test_moe_config4_sampled(dev, oracle):
+    """Config 4: 512 tokens, 8 experts of 4096 -> 14336 Q4_0, top-2; 12 sampled tokens checked in full."""
+    T, E, N, K = 512, 8, 14336, 4096
+    W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, 2, False, 1400)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert counts.sum() == T * 2 and (counts > 0).all()
+    g = np.random.default_rng(1401)
+    toks = np.sort(g.choice(T, 12, replace=False))
+    ref = oracle.moe_q4_0_f64(W, oracle.quantize_q8_1(x[toks]), ids[toks], wts[toks], len(toks), N, K)
+    assert _rel_err(y[toks], ref) <= TOL
+    assert np.isfinite(y).all()
