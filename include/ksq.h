@@ -113,7 +113,8 @@ KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* a
                          int M, int N, int K, void* stream);
 
 /* Debug: the same per-block integer dots taken from the int8 MFMA tiles of the
- * prefill GEMM.  Q4_0 / Q8_0 only, K % 256 == 0, weight and act_q8_1 16-byte aligned. */
+ * prefill GEMM (all four weight types).  K % 256 == 0, act_q8_1 16-byte aligned, weight
+ * 16-byte aligned (4-byte for Q6_K). */
 KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
                               int M, int N, int K, void* stream);
 
@@ -147,6 +148,10 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
 /* Path selection for testing and benchmarking: 0 = automatic (default),
  * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies. */
 KSQ_API int ksq_set_path(int path);
+
+/* MFMA tile configuration for tuning: 0 = chosen from (M, N) (default); 1 = 128x128 tile,
+ * K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with K step 4. */
+KSQ_API int ksq_set_mmq_config(int config);
 
 #ifdef __cplusplus
 }

@@ -152,6 +152,11 @@ int ksq_set_path(int path) {
     return ok();
 }
 
+int ksq_set_mmq_config(int config) {
+    if (ksq::mmq_set_config(config) != 0) return set_error(KSQ_ERR_TYPE, "unknown MFMA tile configuration %d", config);
+    return ok();
+}
+
 int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream) {
     if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
     if (M == 0 || K == 0) return ok();

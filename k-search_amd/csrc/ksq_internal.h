@@ -23,6 +23,8 @@ hipError_t launch_gemv(int wtype, const uint8_t* W, const uint8_t* A, float* C, 
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A);
 hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       hipStream_t s);
+// Force one of the MFMA tile configurations (1..4) or automatic choice (0); -1 if out of range.
+int mmq_set_config(int c);
 
 // Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /
 // launch_moe_group; C must be zeroed first when scratch is null (top_k <= 2).

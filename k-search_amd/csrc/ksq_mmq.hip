@@ -5,14 +5,13 @@
 // block formula of gemm_w4a8_reference / gemm_w8a8_reference (include/gemm_reference.h:175-267).
 //
 // gfx950 design:
-//  * Workgroup tile 128 activation rows x 128 weight rows, 4 waves each owning a
-//    64 x 64 quadrant = 2 x 2 tiles of v_mfma_i32_32x32x32_i8.  One MFMA contracts
-//    exactly one 32-element Q block, so its i32 result IS the reference's integer
-//    block dot sumi for a 32 x 32 patch of outputs.
-//  * Per K step 8 blocks (256 K) are staged in LDS: Q8_1 quants as int8 rows, Q4_0
-//    weights as packed nibbles (the MFMA lane that holds k = 0..15 takes the low
-//    nibbles, the lane that holds k = 16..31 the high ones, which is exactly the
-//    Q4_0 element order), Q8_0 weights as int8 rows, plus the per-block scales.
+//  * A BM x BN workgroup tile, 4 waves each owning TM x TN tiles of 32 x 32 computed
+//    with v_mfma_i32_32x32x32_i8.  One MFMA contracts exactly one 32-element Q block,
+//    so its i32 result IS the reference's integer block dot sumi for a 32 x 32 patch.
+//  * Per K step KB blocks are staged in LDS: Q8_1 quants as int8 rows, Q4_0 weights as
+//    packed nibbles (the MFMA lane that holds k = 0..15 takes the low nibbles, the lane
+//    that holds k = 16..31 the high ones, which is exactly the Q4_0 element order),
+//    Q8_0 weights as int8 rows, plus the per-block scales widened once to fp32.
 //  * Epilogue without an int->float conversion: the MFMA accumulates onto the bit
 //    pattern of 12582912.0f (0x4B400000), so the result read as a float is exactly
 //    12582912 + sumi (|sumi| < 2^22).  Then
@@ -27,29 +26,45 @@
 //  * The MFMA for the next tile is issued before the epilogue of the current one,
 //    so matrix and vector pipes overlap within a wave.
 //  * Row / column tiles past M or N load a clamped in-range row and are not stored.
+//  * Tile shapes are template parameters; the host picks one by (M, N) so that small-M
+//    problems still put a workgroup on every CU.
 #include "ksq_device.h"
 #include "ksq_internal.h"
 
 namespace ksq {
 
-constexpr int kBM = 128, kBN = 128, kKB = 8;
-constexpr int kAPitch = kKB * 32 + 16;  // bytes per staged activation row (conflict-free b128 reads)
 constexpr uint32_t kMagic = 0x4B400000u;  // 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
 typedef uint32_t u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int WT>
-struct MmqShape {
-    static constexpr int WQ = (WT == 0) ? 16 : 32;     // staged weight bytes per block
-    static constexpr int WPitch = kKB * WQ + 16;       // bytes per staged weight row
-    static constexpr int BB = (WT == 0) ? kQ40Bytes : kQ80Bytes;
-    static constexpr int HalfBytes = 4 * BB;           // 72 or 136: half a row's K step
+template <int BM_, int BN_, int KB_, int TM_, int TN_, int OCC_>
+struct Tile {
+    static constexpr int BM = BM_, BN = BN_, KB = KB_, TM = TM_, TN = TN_, OCC = OCC_;
+    static constexpr int WN = BN / (32 * TN);          // waves along N
+    static constexpr int WM = BM / (32 * TM);          // waves along M
+    static_assert(WN * WM == 4, "four waves per workgroup");
+    static_assert(KB == 4 || KB == 8, "K step of 4 or 8 blocks");
+    static constexpr int APitch = KB * 32 + 16;        // bytes per staged activation row
 };
 
-// Expert-grouped mode (MoE): workgroup tile y is entry blockIdx.x of a tile schedule;
-// its activation rows are gathered through a sorted (token, slot) list and its output is
+// Staged weight format per type: Q4_0 / Q4_K keep packed nibbles (16 B per 32-element
+// block), Q8_0 / Q6_K int8 values (32 B per block).  SUB = scale groups per 32-element
+// block (2 for Q6_K's 16-element sub-blocks).
+template <int WT, int KB>
+struct WShape {
+    static constexpr int WQ = (WT == 0 || WT == 2) ? 16 : 32;  // staged weight bytes per block
+    static constexpr int WPitch = KB * WQ + 16;                 // bytes per staged weight row
+    static constexpr int BB = (WT == 0) ? kQ40Bytes : kQ80Bytes;
+    static constexpr int Chunk = 4 * BB;                        // 4 blocks: 72 (Q4_0) or 136 (Q8_0) bytes
+    static constexpr int SUB = (WT == 3) ? 2 : 1;
+    static constexpr bool side = (WT == 0 || WT == 2);          // has the s_a side term
+    static constexpr int SB = (WT == 2) ? kQ4KBytes : kQ6KBytes;  // K-quant super-block bytes
+};
+
+// Expert-grouped mode (MoE): workgroup x is entry blockIdx.x of a tile schedule; its
+// activation rows are gathered through a sorted (token, slot) list and its output is
 // added, weighted by the routing probability, into C[token][n].
 struct MoeTiles {
     const int32_t* num_tiles;   // [1]
@@ -63,62 +78,92 @@ struct MoeTiles {
     size_t expert_stride;       // weight bytes per expert
 };
 
-template <int WT, bool DUMP, bool MOE = false>
-__global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
-                                                     float* __restrict__ C, int32_t* __restrict__ dump, int M,
-                                                     int N, int nb, MoeTiles moe = MoeTiles{}) {
-    using S = MmqShape<WT>;
-    __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kAPitch];
-    __shared__ __attribute__((aligned(16))) uint8_t sW[kBN * S::WPitch];
-    __shared__ __attribute__((aligned(16))) float sDa[kKB][kBM];     // d_a' (d_a/8 for Q4_0)
-    __shared__ __attribute__((aligned(16))) float sNc[kKB][kBM];     // -12582912 * d_a'
-    __shared__ __attribute__((aligned(16))) float sDw[kKB][kBN];     // d_w
-    __shared__ __attribute__((aligned(16))) uint16_t sSaH[kBM][kKB]; // -s_a, fp16 bits (Q4_0 side term)
-    __shared__ __attribute__((aligned(16))) uint16_t sDwH[kBN][kKB]; //  d_w, fp16 bits
+// 6-bit scale and min j of a Q4_K super-block (get_scale_min_k4); s3 = the 12 scale bytes.
+__device__ __forceinline__ void q4_K_scale_min_regs(int j, const uint32_t* s3, int& sc, int& m) {
+    auto byte = [&](int k) -> int { return (int)((s3[k >> 2] >> (8 * (k & 3))) & 0xFFu); };
+    if (j < 4) {
+        sc = byte(j) & 63;
+        m = byte(j + 4) & 63;
+    } else {
+        sc = (byte(j + 4) & 0x0F) | ((byte(j - 4) >> 6) << 4);
+        m = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+}
 
-    __shared__ int32_t sRows[kBM];  // MoE: entry index of each tile row
+// NW words starting at the 2-byte aligned global byte pointer p: aligned dword reads
+// re-aligned with v_alignbyte_b32.  The extra dword is read only when p is not 4-byte
+// aligned, so no byte past p + 4*NW is touched.
+template <int NW>
+__device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
+    const int sh = (int)((uintptr_t)p & 3u);
+    const uint32_t* q = (const uint32_t*)(p - sh);
+    uint32_t raw[NW + 1];
+#pragma unroll
+    for (int i = 0; i < NW; i++) raw[i] = q[i];
+    raw[NW] = sh ? q[NW] : 0u;
+#pragma unroll
+    for (int i = 0; i < NW; i++) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+}
+
+template <class T, int WT, bool DUMP, bool MOE>
+__global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
+                                                          const uint8_t* __restrict__ A, float* __restrict__ C,
+                                                          int32_t* __restrict__ dump, int M, int N, int nb,
+                                                          MoeTiles moe) {
+    using S = WShape<WT, T::KB>;
+    constexpr int BM = T::BM, BN = T::BN, KB = T::KB, TM = T::TM, TN = T::TN;
+    __shared__ __attribute__((aligned(16))) uint8_t sA[BM * T::APitch];
+    __shared__ __attribute__((aligned(16))) uint8_t sW[BN * S::WPitch];
+    __shared__ __attribute__((aligned(16))) float sDa[KB][BM];     // d_a' (d_a/8 for Q4_0)
+    __shared__ __attribute__((aligned(16))) float sNc[KB][BM];     // -12582912 * d_a'
+    __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
+    __shared__ __attribute__((aligned(16))) uint16_t sSaH[BM][8];  // -s_a, fp16 bits (side term)
+    __shared__ __attribute__((aligned(16))) uint16_t sDwH[BN][8];  // side-term weight factor, fp16 bits
+    __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == 2 ? BN : 1][8];  // Q4_K: its low part
+    __shared__ int32_t sRows[MOE ? BM : 1];                        // MoE: entry index of each tile row
+
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    int m0 = blockIdx.y * kBM;
-    const int n0 = (MOE ? blockIdx.y : blockIdx.x) * kBN;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+    const int m0 = (MOE ? 0 : (int)blockIdx.y) * BM;
+    const int n0 = (MOE ? (int)blockIdx.y : (int)blockIdx.x) * BN;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const float da_scale = S::side ? 0.125f : 1.0f;
+    static_assert(WT < 2 || KB == 8, "K-quants stage one 256-element super-block per K step");
+
+    if constexpr (KB == 4) {
+        // the f16 side-term MFMA contracts 8 block slots; slots 4..7 stay zero
+        if (t < BM) *(uint4*)&sSaH[t][0] = uint4{0, 0, 0, 0};
+        if (t < BN) *(uint4*)&sDwH[t][0] = uint4{0, 0, 0, 0};
+    }
     if constexpr (MOE) {
         const int tile = blockIdx.x;
         if (tile >= moe.num_tiles[0]) return;           // surplus workgroups of the worst-case grid
         const int e = moe.tile_expert[tile];
         const int r0 = moe.tile_row0[tile];
-        const int rend = moe.expert_end[e];
-        M = min(kBM, rend - r0);                         // valid rows of this tile
-        m0 = 0;
+        M = min(BM, moe.expert_end[e] - r0);             // valid rows of this tile
         W += (size_t)e * moe.expert_stride;
-        if (t < kBM) sRows[t] = moe.rows[r0 + min(t, M - 1)];
-        __syncthreads();
+        if (t < BM) sRows[t] = moe.rows[r0 + min(t, M - 1)];
     }
-    const int l32 = lane & 31, hi = lane >> 5;
-    const float da_scale = (WT == 0) ? 0.125f : 1.0f;
+    __syncthreads();
 
-    f32x16 acc[2][2];
+    f32x16 acc[TM][TN];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < TN; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
     i32x16 bias;
 #pragma unroll
     for (int r = 0; r < 16; r++) bias[r] = DUMP ? 0 : (int)kMagic;
 
-    // staging assignment: thread t owns row t/2, blocks 4*(t&1) .. 4*(t&1)+3 of the K step
-    const int sr = t >> 1, sh = t & 1;
-    const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
-    const int wn_row = min(n0 + sr, N - 1);
-    const uint8_t* a_src = A + (size_t)am * nb * kQ81Bytes + (size_t)sh * 4 * kQ81Bytes;
-    const uint8_t* w_src = W + (size_t)wn_row * nb * S::BB + (size_t)sh * S::HalfBytes;
-
-    for (int kb0 = 0; kb0 < nb; kb0 += kKB) {
-        // ---- stage activations: 4 Q8_1 blocks = 144 B = 9 x 16 B
-        {
+    for (int kb0 = 0; kb0 < nb; kb0 += KB) {
+        // ---- stage activations: chunks of 4 Q8_1 blocks = 144 B = 9 x 16 B
+        for (int c = t; c < BM * (KB / 4); c += 256) {
+            const int sr = c / (KB / 4), g = c % (KB / 4);
+            const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
+            const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * kQ81Bytes;
             uint32_t v[36];
-            const uint8_t* p = a_src + (size_t)kb0 * kQ81Bytes;
 #pragma unroll
             for (int i = 0; i < 9; i++) {
                 const u32x4 x = *(const u32x4*)(p + 16 * i);
@@ -126,8 +171,8 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int kb = 4 * sh + j;
-                u32x4* dst = (u32x4*)(sA + sr * kAPitch + kb * 32);
+                const int kb = 4 * g + j;
+                u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
                 dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
                 dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
                 const float da = f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
@@ -136,63 +181,140 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
                 sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
             }
         }
-        // ---- stage weights: 4 blocks = 72 B (Q4_0) / 136 B (Q8_0), 8-byte aligned
-        {
-            constexpr int NW = S::HalfBytes / 4;
-            uint32_t v[NW + 2];
-            const uint8_t* p = w_src + (size_t)kb0 * S::BB;
-#pragma unroll
-            for (int i = 0; i < NW / 2; i++) {
-                const u32x2_a8 x = *(const u32x2_a8*)(p + 8 * i);
-                v[2 * i] = x.x; v[2 * i + 1] = x.y;
+        if constexpr (WT <= 1) {
+            // ---- stage weights: chunks of 4 blocks = 72 B (Q4_0) / 136 B (Q8_0), 8-byte aligned
+            for (int c = t; c < BN * (KB / 4); c += 256) {
+                const int sr = c / (KB / 4), g = c % (KB / 4);
+                const int wr = min(n0 + sr, N - 1);
+                constexpr int NW = S::Chunk / 4;
+                uint32_t v[NW + 2];
+                const uint8_t* p = W + (size_t)wr * nb * S::BB + (size_t)(kb0 + 4 * g) * S::BB;
+    #pragma unroll
+                for (int i = 0; i < NW / 2; i++) {
+                    const u32x2_a8 x = *(const u32x2_a8*)(p + 8 * i);
+                    v[2 * i] = x.x; v[2 * i + 1] = x.y;
+                }
+                v[NW] = 0; v[NW + 1] = 0;
+    #pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int kb = 4 * g + j, off = j * S::BB;
+                    const uint32_t dwb = half_at(v, off);
+                    sDw[kb][sr] = f16_to_f32(dwb);
+                    sDwH[sr][kb] = (uint16_t)dwb;
+                    if constexpr (WT == 0) {
+                        *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
+                            u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
+                    } else {
+                        u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                        dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
+                        dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
+                    }
+                }
             }
-            v[NW] = 0; v[NW + 1] = 0;
+        } else if constexpr (WT == 2) {
+            // ---- Q4_K: one 144-byte super-block per row and K step (16-byte aligned)
+            const int nsb = nb / 8, s0 = kb0 / 8;
+            for (int sr = t; sr < BN; sr += 256) {
+                const int wr = min(n0 + sr, N - 1);
+                const uint8_t* p = W + ((size_t)wr * nsb + s0) * kQ4KBytes;
+                uint32_t v[36];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int kb = 4 * sh + j, off = j * S::BB;
-                const uint32_t dwb = half_at(v, off);
-                sDw[kb][sr] = f16_to_f32(dwb);
-                sDwH[sr][kb] = (uint16_t)dwb;
-                if constexpr (WT == 0) {
-                    *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
-                        u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
-                } else {
-                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
-                    dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
-                    dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
+                for (int i = 0; i < 9; i++) {
+                    const u32x4 x = *(const u32x4*)(p + 16 * i);
+                    v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+                }
+                const float d = f16_to_f32(v[0] & 0xFFFFu), dmin = f16_to_f32(v[0] >> 16);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    int sc, mn;
+                    q4_K_scale_min_regs(j, v + 1, sc, mn);
+                    sDw[j][sr] = d * (float)sc;                     // exact: 11 x 6 bits
+                    // side factor dmin*m/8 (17 significant bits) as an fp16 hi + lo pair
+                    const float f = dmin * (float)mn * 0.125f;
+                    const _Float16 h = (_Float16)f;
+                    const _Float16 l = (_Float16)(f - (float)h);
+                    sDwH[sr][j] = __builtin_bit_cast(uint16_t, h);
+                    sDwL[sr][j] = __builtin_bit_cast(uint16_t, l);
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    *(u32x4*)(sW + sr * S::WPitch + 16 * i) =
+                        u32x4{v[4 + 4 * i], v[5 + 4 * i], v[6 + 4 * i], v[7 + 4 * i]};
+            }
+        } else {
+            // ---- Q6_K: one 210-byte super-block per row and K step (2-byte aligned); two
+            // threads per row, each unpacking one 128-element half to int8 (q - 32)
+            const int nsb = nb / 8, s0 = kb0 / 8;
+            for (int c = t; c < 2 * BN; c += 256) {
+                const int sr = c >> 1, h = c & 1;
+                const int wr = min(n0 + sr, N - 1);
+                const uint8_t* sb = W + ((size_t)wr * nsb + s0) * kQ6KBytes;
+                uint32_t ql[16], qh[8], scw[2];
+                read_words_g<16>(sb + 64 * h, ql);
+                read_words_g<8>(sb + 128 + 32 * h, qh);
+                read_words_g<2>(sb + 192 + 8 * h, scw);
+                const float d = f16_to_f32(*(const uint16_t*)(sb + 208));
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int sc = (int)(int8_t)((scw[u >> 2] >> (8 * (u & 3))) & 0xFFu);
+                    sDw[8 * h + u][sr] = d * (float)sc;              // exact: 11 x 8 bits
+                }
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    uint32_t o[8];
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const uint32_t lo = (ql[8 * (g & 1) + i] >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
+                        const uint32_t hb = ((qh[i] >> (2 * g)) << 4) & 0x30303030u;
+                        const uint32_t b6 = lo | hb;                 // 6-bit values, one per byte
+                        const uint32_t x = b6 ^ 0x20202020u;         // b - 32 for b >= 32
+                        const uint32_t neg = x & 0x20202020u;        // b < 32: sign-extend
+                        o[i] = x | (neg << 1) | (neg << 2);
+                    }
+                    // elements 128h + 32g .. +31 = block 4h + g of this K step
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + (4 * h + g) * 32);
+                    dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+                    dst[1] = u32x4{o[4], o[5], o[6], o[7]};
                 }
             }
         }
         __syncthreads();
 
-        // 32 (block, tile) MFMAs per K step; tile index q = 4*b + 2*i + j.  The MFMA of
-        // step q+1 is issued before the epilogue of step q.
         auto frag_a = [&](int b, int i) -> i32x4 {
-            return *(const i32x4*)(sA + (wm * 64 + i * 32 + l32) * kAPitch + b * 32 + 16 * hi);
+            return *(const i32x4*)(sA + (wm * 32 * TM + i * 32 + l32) * T::APitch + b * 32 + 16 * hi);
         };
         auto frag_b = [&](int b, int j) -> i32x4 {
-            if constexpr (WT == 0) {
-                const u32x4 x = *(const u32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 16);
+            if constexpr (WT == 2) {
+                // sub-block b: bytes 32*(b/2) + 16*hi .. +15 of the staged qs, low nibbles for
+                // even b, high nibbles for odd b
+                const u32x4 x =
+                    *(const u32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + 32 * (b >> 1) + 16 * hi);
+                const int s4 = 4 * (b & 1);
+                return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
+                             (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
+            } else if constexpr (WT == 0) {
+                const u32x4 x = *(const u32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 16);
                 const int s4 = 4 * hi;
                 return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
                              (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
             } else {
-                return *(const i32x4*)(sW + (wn * 64 + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
+                return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
             }
         };
-        auto epilogue = [&](int b, int i, int j, const i32x16& res) {
+        auto epilogue = [&](int b, int u, int i, int j, const i32x16& res) {
             // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
-            const int col = wn * 64 + j * 32 + l32;
-            const int rowb = wm * 64 + i * 32 + 4 * hi;
+            const int col = wn * 32 * TN + j * 32 + l32;
+            const int rowb = wm * 32 * TM + i * 32 + 4 * hi;
             if constexpr (DUMP) {
                 const int gn = n0 + col;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int gm = m0 + rowb + 8 * (r >> 2) + (r & 3);
-                    if (gm < M && gn < N) dump[((size_t)gm * N + gn) * nb + kb0 + b] = res[r];
+                    if (gm < M && gn < N)
+                        dump[((size_t)gm * N + gn) * nb * S::SUB + (kb0 + b) * S::SUB + (u - b * S::SUB)] = res[r];
                 }
             } else {
-                const float dw = sDw[b][col];
+                const float dw = sDw[u][col];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     const f32x4 da = *(const f32x4*)&sDa[b][rowb + 8 * q];
@@ -209,35 +331,54 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
             }
         };
 
-        i32x4 af[2], bf[2];
-        af[0] = frag_a(0, 0); af[1] = frag_a(0, 1);
-        bf[0] = frag_b(0, 0); bf[1] = frag_b(0, 1);
-        i32x16 cur = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[0], bf[0], bias, 0, 0, 0);
+        // KB*SUB*TM*TN MFMAs per K step; step q = ((b*SUB + h)*TM + i)*TN + j.  For Q6_K the two
+        // 16-element sub-blocks of a block are separate MFMAs whose B fragment keeps only the
+        // lanes holding that half (k = 16*hi ..).  The MFMA of step q+1 is issued before the
+        // epilogue of step q.
+        constexpr int SUBN = S::SUB;
+        constexpr int NQ = KB * SUBN * TM * TN;
+        i32x4 af[TM], bf[TN];
+        auto mfma_step = [&](int q) -> i32x16 {
+            const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
+            const int i = (q / TN) % TM, j = q % TN;
+            if (q % (SUBN * TM * TN) == 0) {
 #pragma unroll
-        for (int q = 0; q < 4 * kKB; q++) {
-            const int b = q >> 2, i = (q >> 1) & 1, j = q & 1;
-            i32x16 nxt = bias;
-            if (q + 1 < 4 * kKB) {
-                const int b1 = (q + 1) >> 2, i1 = ((q + 1) >> 1) & 1, j1 = (q + 1) & 1;
-                if (((q + 1) & 3) == 0) {
-                    af[0] = frag_a(b1, 0); af[1] = frag_a(b1, 1);
-                    bf[0] = frag_b(b1, 0); bf[1] = frag_b(b1, 1);
-                }
-                nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i1], bf[j1], bias, 0, 0, 0);
+                for (int ii = 0; ii < TM; ii++) af[ii] = frag_a(b, ii);
+#pragma unroll
+                for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b(b, jj);
             }
-            epilogue(b, i, j, cur);
+            i32x4 bb = bf[j];
+            if constexpr (SUBN == 2) {
+                if (hi != h) bb = i32x4{0, 0, 0, 0};
+            }
+            return __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bb, bias, 0, 0, 0);
+        };
+        i32x16 cur = mfma_step(0);
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
+            const int i = (q / TN) % TM, j = q % TN;
+            i32x16 nxt = bias;
+            if (q + 1 < NQ) nxt = mfma_step(q + 1);
+            epilogue(b, b * SUBN + h, i, j, cur);
             cur = nxt;
         }
 
-        if constexpr (WT == 0 && !DUMP) {
-            // side term: acc += sum_k (-s_a[m][k]) * d_w[n][k] over the 8 blocks (f16 MFMA, exact products)
+        if constexpr (S::side && !DUMP) {
+            // side term: acc += sum_k (-s_a[m][k]) * f[n][k] over the staged blocks, f = d_w (Q4_0)
+            // or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA over 8 block slots, exact products
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 64 + i * 32 + l32][4 * hi];
+            for (int i = 0; i < TM; i++) {
+                const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 32 * TM + i * 32 + l32][4 * hi];
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const f16x4 dw4 = *(const f16x4*)&sDwH[wn * 64 + j * 32 + l32][4 * hi];
+                for (int j = 0; j < TN; j++) {
+                    const int wrow = wn * 32 * TN + j * 32 + l32;
+                    const f16x4 dw4 = *(const f16x4*)&sDwH[wrow][4 * hi];
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dw4, acc[i][j], 0, 0, 0);
+                    if constexpr (WT == 2) {
+                        const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * hi];
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dl4, acc[i][j], 0, 0, 0);
+                    }
                 }
             }
         }
@@ -245,13 +386,13 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
     }
 
     if constexpr (!DUMP) {
-        const float out_scale = (WT == 0) ? 8.0f : 1.0f;
+        const float out_scale = S::side ? 8.0f : 1.0f;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int gn = n0 + wn * 64 + j * 32 + l32;
-                const int rowb = m0 + wm * 64 + i * 32 + 4 * hi;
+            for (int j = 0; j < TN; j++) {
+                const int gn = n0 + wn * 32 * TN + j * 32 + l32;
+                const int rowb = m0 + wm * 32 * TM + i * 32 + 4 * hi;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const int gm = rowb + 8 * (r >> 2) + (r & 3);
@@ -270,19 +411,75 @@ __global__ __launch_bounds__(256, 2) void mmq_kernel(const uint8_t* __restrict__
     }
 }
 
+// ---- tile configurations ----------------------------------------------------------
+using TileL = Tile<128, 128, 8, 2, 2, 2>;   // large M: 64 x 64 per wave
+using TileN = Tile<128, 64, 8, 2, 1, 2>;    // half the columns per workgroup: twice the workgroups
+using TileS = Tile<64, 64, 8, 1, 1, 3>;     // 32 x 32 per wave, 4x the workgroups of TileL
+using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, more resident workgroups
+
+static int g_mmq_config = 0;  // 0 = automatic
+
+int mmq_set_config(int c) {
+    if (c < 0 || c > 4) return -1;
+    g_mmq_config = c;
+    return 0;
+}
+
+template <class T>
+static int grid_wgs(int M, int N) {
+    return ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
+}
+
+static int pick_config(int wtype, int M, int N) {
+    if (g_mmq_config && !(wtype >= 2 && g_mmq_config == 4)) return g_mmq_config;
+    constexpr int kCUs = 256;
+    if (grid_wgs<TileL>(M, N) >= 2 * kCUs) return 1;
+    if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
+    return 3;
+}
+
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A) {
-    return (wtype == 0 || wtype == 1) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
-           (((uintptr_t)W & 15u) == 0) && (((uintptr_t)A & 15u) == 0);
+    const uintptr_t wal = (wtype == 3) ? 3u : 15u;  // Q6_K rows are read per dword
+    return (wtype >= 0 && wtype <= 3) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
+           (((uintptr_t)W & wal) == 0) && (((uintptr_t)A & 15u) == 0);
+}
+
+template <class T, bool DUMP, bool MOE>
+static hipError_t launch_t(int wtype, dim3 grid, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump,
+                           int M, int N, int nb, const MoeTiles& mt, hipStream_t s) {
+    switch (wtype) {
+        case 0: hipLaunchKernelGGL((mmq_kernel<T, 0, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt); break;
+        case 1: hipLaunchKernelGGL((mmq_kernel<T, 1, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt); break;
+        case 2:
+            if constexpr (T::KB == 8 && !MOE)
+                hipLaunchKernelGGL((mmq_kernel<T, 2, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
+            else return hipErrorNotSupported;
+            break;
+        default:
+            if constexpr (T::KB == 8 && !MOE)
+                hipLaunchKernelGGL((mmq_kernel<T, 3, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
+            else return hipErrorNotSupported;
+            break;
+    }
+    return hipGetLastError();
+}
+
+template <bool DUMP>
+static hipError_t launch_cfg(int cfg, int wtype, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump, int M,
+                             int N, int K, hipStream_t s) {
+    const int nb = K / 32;
+    const MoeTiles mt{};
+    auto grid = [&](int BM, int BN) { return dim3((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM)); };
+    switch (cfg) {
+        case 1: return launch_t<TileL, DUMP, false>(wtype, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 2: return launch_t<TileN, DUMP, false>(wtype, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
+        case 3: return launch_t<TileS, DUMP, false>(wtype, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
+        default: return launch_t<TileK4, DUMP, false>(wtype, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+    }
 }
 
 hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K, hipStream_t s) {
-    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
-    const int nb = K / 32;
-    if (wtype == 0)
-        hipLaunchKernelGGL((mmq_kernel<0, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
-    else
-        hipLaunchKernelGGL((mmq_kernel<1, false>), grid, dim3(256), 0, s, W, A, C, nullptr, M, N, nb);
-    return hipGetLastError();
+    return launch_cfg<false>(pick_config(wtype, M, N), wtype, W, A, C, nullptr, M, N, K, s);
 }
 
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
@@ -298,24 +495,15 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     mt.top_k = a.top_k;
     const int nb = K / 32;
     mt.expert_stride = (size_t)N * nb * (wtype == 0 ? kQ40Bytes : kQ80Bytes);
-    const dim3 grid((unsigned)max_tiles, (unsigned)((N + kBN - 1) / kBN));
-    if (wtype == 0)
-        hipLaunchKernelGGL((mmq_kernel<0, false, true>), grid, dim3(256), 0, s, W, Aq, C, nullptr, 0, N, nb, mt);
-    else
-        hipLaunchKernelGGL((mmq_kernel<1, false, true>), grid, dim3(256), 0, s, W, Aq, C, nullptr, 0, N, nb, mt);
-    return hipGetLastError();
+    // tiles of 128 rows (the grouping schedule's tile_rows) x 128 columns
+    const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileL::BN - 1) / TileL::BN));
+    return launch_t<TileL, false, true>(wtype, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
 }
 
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,
                                  hipStream_t s) {
     if (!mmq_supported(wtype, M, N, K, W, A)) return hipErrorNotSupported;
-    const dim3 grid((unsigned)((N + kBN - 1) / kBN), (unsigned)((M + kBM - 1) / kBM));
-    const int nb = K / 32;
-    if (wtype == 0)
-        hipLaunchKernelGGL((mmq_kernel<0, true>), grid, dim3(256), 0, s, W, A, nullptr, out, M, N, nb);
-    else
-        hipLaunchKernelGGL((mmq_kernel<1, true>), grid, dim3(256), 0, s, W, A, nullptr, out, M, N, nb);
-    return hipGetLastError();
+    return launch_cfg<true>(pick_config(wtype, M, N), wtype, W, A, nullptr, out, M, N, K, s);
 }
 
 }  // namespace ksq

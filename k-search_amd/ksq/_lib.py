@@ -41,6 +41,7 @@ SIGNATURES = {
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi_mfma": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_set_path": ([_I], _I),
+    "ksq_set_mmq_config": ([_I], _I),
     "ksq_moe_workspace_size": ([_I, _I, _I, _I, _I, _I], _SZ),
     "ksq_moe_gemm": ([_I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _SZ, _P], _I),
     "ksq_moe_gemm_routed": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P], _I),

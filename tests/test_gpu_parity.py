@@ -104,7 +104,7 @@ def test_block_sumi_dot4_bit_exact(dev, oracle, wtype):
     assert np.array_equal(got, oracle.block_sumi(wtype, a, w, M, N, K))
 
 
-@pytest.mark.parametrize("wtype", [0, 1])
+@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
 def test_block_sumi_mfma_bit_exact(dev, oracle, wtype):
     from ksq import ops, synth
     g = np.random.default_rng(300 + wtype)
@@ -143,12 +143,12 @@ def test_q8_0_config1(dev, oracle, M):
     assert _rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("wtype,path", [(0, 1), (0, 2), (1, 1), (1, 2)])
+@pytest.mark.parametrize("wtype,path", [(0, 1), (0, 2), (1, 1), (1, 2), (2, 1), (2, 2), (3, 1), (3, 2)])
 def test_paths_agree_small(dev, oracle, wtype, path):
     """Both the v_dot4 and the MFMA path on ragged shapes."""
     from ksq import synth
     g = np.random.default_rng(600 + 10 * wtype + path)
-    for M, N, K in ((1, 1, 256), (7, 33, 512), (130, 200, 768), (64, 128, 256)):
+    for M, N, K in ((1, 1, 256), (7, 33, 512), (130, 200, 768), (64, 128, 256), (200, 96, 1024)):
         w = synth.weights(wtype, g, N, K)
         x = synth.activations(g, M, K)
         y = _gpu_gemm(dev, wtype, w, x, M, N, K, path=path)
@@ -301,3 +301,21 @@ def test_moe_config4_sampled(dev, oracle):
     ref = oracle.moe_q4_0_f64(W, oracle.quantize_q8_1(x[toks]), ids[toks], wts[toks], len(toks), N, K)
     assert _rel_err(y[toks], ref) <= TOL
     assert np.isfinite(y).all()
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+def test_mfma_tile_configs(dev, oracle, cfg, wtype):
+    """Every MFMA tile configuration (K step 4 is Q4_0/Q8_0 only; K-quants fall back to 64x64)."""
+    from ksq import _lib, synth
+    g = np.random.default_rng(1500 + 10 * cfg + wtype)
+    M, N, K = 150, 136, 512
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    _lib.lib().ksq_set_mmq_config(cfg)
+    try:
+        y = _gpu_gemm(dev, wtype, w, x, M, N, K, path=2)
+    finally:
+        _lib.lib().ksq_set_mmq_config(0)
+    ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
+    assert _rel_err(y, ref) <= TOL
