@@ -227,7 +227,7 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
 
 // ---- expert-grouped MoE --------------------------------------------------------
 namespace {
-constexpr int kMoeTileRows = 128;  // rows per grouped-GEMM tile (the MFMA kernel's BM)
+constexpr int kMoeTileRows = 64;  // rows per grouped-GEMM tile (the MFMA kernel's BM for MoE)
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 

@@ -495,9 +495,11 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     mt.top_k = a.top_k;
     const int nb = K / 32;
     mt.expert_stride = (size_t)N * nb * (wtype == 0 ? kQ40Bytes : kQ80Bytes);
-    // tiles of 128 rows (the grouping schedule's tile_rows) x 128 columns
-    const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileL::BN - 1) / TileL::BN));
-    return launch_t<TileL, false, true>(wtype, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
+    // tiles of 64 rows (the grouping schedule's tile_rows) x 64 columns: an expert's few
+    // hundred rows split into several tiles with little padding, and enough workgroups
+    using TileMoe = TileS;
+    const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileMoe::BN - 1) / TileMoe::BN));
+    return launch_t<TileMoe, false, true>(wtype, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
 }
 
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,

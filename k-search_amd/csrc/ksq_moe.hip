@@ -7,10 +7,9 @@
 //   route  one thread per token: softmax over the E logits (fp32, max-subtracted),
 //          top_k chosen by comparing logits (softmax is monotonic, so the choice does
 //          not depend on expf rounding); ties go to the lower expert index
-//   group  one wave walks the T*top_k (token, slot) entries in order and places each
-//          at its expert's cursor (ballot + popcount per expert), i.e. a stable
-//          counting sort; it also writes the per-expert end offsets and the schedule
-//          of row tiles the grouped GEMM launches over
+//   group  one workgroup: a stable counting sort of the T*top_k (token, slot) entries by
+//          expert (ranks from ballot + popcount per expert), plus the per-expert end
+//          offsets and the schedule of row tiles the grouped GEMM launches over
 //   GEMM   mmq_kernel in its gathered mode (ksq_mmq.hip)
 //   combine for top_k > 2 only: per-entry outputs summed in slot order
 #include "ksq_device.h"
@@ -53,32 +52,34 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int re
     return hipGetLastError();
 }
 
-// One wave.  cursor[e] counts entries placed so far for expert e.
-__global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
-                                                        int tile_rows, int32_t* __restrict__ rows,
-                                                        int32_t* __restrict__ expert_end,
-                                                        int32_t* __restrict__ num_tiles,
-                                                        int32_t* __restrict__ tile_expert,
-                                                        int32_t* __restrict__ tile_row0) {
+// One 1024-thread workgroup.  Counts per expert (LDS atomics: order-free), then a
+// stable placement chunk by chunk of 1024 entries: inside a chunk an entry's rank among
+// the same expert's entries is its rank within its wave (ballot + popcount) plus the
+// counts of the waves before it; cursor[e] carries the total across chunks.
+constexpr int kGroupThreads = 1024;
+constexpr int kGroupWaves = kGroupThreads / 64;
+
+__global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
+                                                                  int tile_rows, int32_t* __restrict__ rows,
+                                                                  int32_t* __restrict__ expert_end,
+                                                                  int32_t* __restrict__ num_tiles,
+                                                                  int32_t* __restrict__ tile_expert,
+                                                                  int32_t* __restrict__ tile_row0) {
     __shared__ int32_t count[256];
-    __shared__ int32_t start[257];
-    const int lane = threadIdx.x;
-    for (int e = lane; e < E; e += 64) count[e] = 0;
+    __shared__ int32_t cursor[256];
+    __shared__ int32_t wcnt[kGroupWaves][256];
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    for (int e = t; e < E; e += kGroupThreads) count[e] = 0;
     __syncthreads();
-    // pass 1: counts
-    for (int base = 0; base < total; base += 64) {
-        const int j = base + lane;
-        const int e = (j < total) ? ids[j] : -1;
-        for (int x = 0; x < E; x++) {
-            const uint64_t m = __ballot(e == x);
-            if (lane == 0) count[x] += __popcll(m);
-        }
+    for (int j = t; j < total; j += kGroupThreads) {
+        const int e = ids[j];
+        if (e >= 0 && e < E) atomicAdd(&count[e], 1);
     }
     __syncthreads();
-    if (lane == 0) {
+    if (t == 0) {
         int acc = 0, nt = 0;
         for (int e = 0; e < E; e++) {
-            start[e] = acc;
+            cursor[e] = acc;
             for (int r = 0; r < count[e]; r += tile_rows) {
                 tile_expert[nt] = e;
                 tile_row0[nt] = acc + r;
@@ -87,30 +88,41 @@ __global__ __launch_bounds__(64) void moe_group_kernel(const int32_t* __restrict
             acc += count[e];
             expert_end[e] = acc;
         }
-        start[E] = acc;
         num_tiles[0] = nt;
     }
     __syncthreads();
-    // pass 2: stable placement
-    for (int base = 0; base < total; base += 64) {
-        const int j = base + lane;
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int base = 0; base < total; base += kGroupThreads) {
+        const int j = base + t;
         const int e = (j < total) ? ids[j] : -1;
-        const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const bool valid = e >= 0 && e < E;
+        int rank = 0;
         for (int x = 0; x < E; x++) {
             const uint64_t m = __ballot(e == x);
-            if (e == x) rows[start[x] + __popcll(m & lt)] = j;
-            __syncthreads();
-            if (lane == 0) start[x] += __popcll(m);
-            __syncthreads();
+            if (lane == 0) wcnt[wave][x] = __popcll(m);
+            if (e == x) rank = __popcll(m & lt);
         }
+        __syncthreads();
+        if (valid) {
+            int off = cursor[e] + rank;
+            for (int w = 0; w < wave; w++) off += wcnt[w][e];
+            rows[off] = j;
+        }
+        __syncthreads();
+        for (int x = t; x < E; x += kGroupThreads) {
+            int add = 0;
+            for (int w = 0; w < kGroupWaves; w++) add += wcnt[w][x];
+            cursor[x] += add;
+        }
+        __syncthreads();
     }
 }
 
 hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
                             int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
                             hipStream_t s) {
-    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(64), 0, s, ids, T * top_k, E, tile_rows, rows, expert_end,
-                       num_tiles, tile_expert, tile_row0);
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, ids, T * top_k, E, tile_rows, rows,
+                       expert_end, num_tiles, tile_expert, tile_row0);
     return hipGetLastError();
 }
 
