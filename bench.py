@@ -31,6 +31,12 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "k-search_amd")]
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 
+# HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB per
+# dispatch, mean of 6) over `bench.py --only gemm|gemv`, scaled by the factors a plain
+# 256 MiB copy gives the same counters (reads x2.0, writes x1.0); summaries in profiles/.
+TRAFFIC_MMQ_Q4_0_M2048 = int((41698.03 * 2.0 + 32768.0 * 1.0) * 1024)
+TRAFFIC_GEMV_Q4_0_M1 = int((4650.89 * 2.0 + 32.0 * 1.0) * 1024)
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
@@ -276,14 +282,17 @@ def main() -> int:
                    "rotating_copies": copies, "host_wall_ms_per_step": round(wall, 5)},
         "roofline": {"bound": "mfma", "kernel": "mmq_kernel<0> (Q4_0 x Q8_1, v_mfma_i32_32x32x32_i8)",
                      "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC_MMQ_Q4_0_M2048,
+                     "traffic_unit": "bytes per launch (algorithmic: %d)" % (
+                         N * (K // 32) * 18 + M * (K // 32) * 36 + M * N * 4),
                      "avg_kernel_ms": round(gemm_ms, 5),
                      "note": "int8 ops = 2*M*N*K per launch over the HIP-event time of graph-replayed launches"},
         "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(gemv_gbs, 1), "unit": "GB/s",
                     "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6),
                     "algorithmic_bytes": gemv_bytes,
                     "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
-                                 "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4)},
+                                 "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                                 "traffic": TRAFFIC_GEMV_Q4_0_M1},
                     "fp32_entry_ms": round(gemv_f32_ms, 6),
                     "fp32_entry_gbs": round(f32_bytes / (gemv_f32_ms * 1e-3) / 1e9, 1),
                     "weight_copies": gcopies},

@@ -301,6 +301,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
             }
         };
+        f32x4 eda[4], enc[4];  // row scales of the current (block, row tile), reused across its TN tiles
         auto epilogue = [&](int b, int u, int i, int j, const i32x16& res) {
             // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
             const int col = wn * 32 * TN + j * 32 + l32;
@@ -315,10 +316,17 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 }
             } else {
                 const float dw = sDw[u][col];
+                if (j == 0) {
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        eda[q] = *(const f32x4*)&sDa[b][rowb + 8 * q];
+                        enc[q] = *(const f32x4*)&sNc[b][rowb + 8 * q];
+                    }
+                }
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const f32x4 da = *(const f32x4*)&sDa[b][rowb + 8 * q];
-                    const f32x4 nc = *(const f32x4*)&sNc[b][rowb + 8 * q];
+                    const f32x4 da = eda[q];
+                    const f32x4 nc = enc[q];
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
                         // copy the element out first: bit_cast of an ext-vector element lvalue
