@@ -82,12 +82,40 @@ KSQ_API void gemm_w4a32c8_q4_k_fp32_int8(const uint8_t* weight, const float* act
 KSQ_API void gemm_w6a32c8_q6_k_fp32_int8(const uint8_t* weight, const float* activation, float* output,
                                  int M, int N, int K);
 
+/* W4A32C8 / W5A32C8 with the other legacy GGML blocks of the reference
+ * (kernels/gemm/gemm_quant_formats.cuh:119-267, core/operators/common/types.py:94-140):
+ * Q4_1 replaces the entry of the w4a32c8_q4_1_fp32_int8_* definitions (e.g.
+ * kernelevalplus-main/definitions/quant_gemm/qwen3_4b/
+ * w4a32c8_q4_1_fp32_int8_qwen3_4b_att_out_n2560_k2560.json).  Block contributions:
+ *   Q4_1, Q5_1  d_w*d_a*sumi + m_w*s_a   (the harness oracle gemm_ref.py:274-330; the
+ *               reference's device dot divides the m*s term by 4, gemm_quant_formats.cuh:148,
+ *               :266, which disagrees with that oracle and with the dequantised values)
+ *   Q5_0        d_w*(d_a*sumi - 16*s_a)  (gemm_quant_formats.cuh:207)
+ * No definitions exist for Q5_0 / Q5_1; their names follow NAMING_CONVENTION.md:21-33. */
+KSQ_API void gemm_w4a32c8_q4_1_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+KSQ_API void gemm_w5a32c8_q5_0_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+KSQ_API void gemm_w5a32c8_q5_1_fp32_int8(const uint8_t* weight, const float* activation, float* output,
+                                 int M, int N, int K);
+
+/* The native W8A8C8 operator (kernelevalplus-main/core/operators/quant_gemm/variants/
+ * deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:119-130, same symbol and signature): Q8_0 weights,
+ * fp32 activations re-quantised per 32-element block with an fp32 scale (d = amax/127, 1 when
+ * below 1e-6; q = roundf(x / d) by true division, kernel.cu:66-93), contribution
+ * d_w*d_a*sumi.  Quantised once per activation row here (block_q8s), not once per output. */
+KSQ_API void gemm_w8a8c8_q8_0_q8_1(const uint8_t* weight, const float* activation, float* output,
+                                   int M, int N, int K);
+
 /* Pre-quantised activations (the harness' uint8_t activation form,
  * op_test_handler.py:319-323): activation is block_q8_1 [M][K/32]. */
 KSQ_API void ksq_gemm_q4_0_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
 KSQ_API void ksq_gemm_q8_0_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
 KSQ_API void ksq_gemm_q4_k_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
 KSQ_API void ksq_gemm_q6_k_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q4_1_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q5_0_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
+KSQ_API void ksq_gemm_q5_1_q8_1(const uint8_t* weight, const uint8_t* activation, float* output, int M, int N, int K);
 
 /* ---- checked, stream-taking entries -------------------------------------- */
 
@@ -97,11 +125,17 @@ KSQ_API void ksq_gemm_q6_k_q8_1(const uint8_t* weight, const uint8_t* activation
  * x 16-byte aligned, y 4-byte aligned.  stream: hipStream_t or NULL. */
 KSQ_API int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream);
 
-/* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the Q8_1 copy of
+/* fp32 [M][K] -> block_q8s [M][K/32] by the native W8A8C8 operator's per-block rules
+ * (variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93, bit for bit).  Same alignment
+ * rules as ksq_quantize_q8_1. */
+KSQ_API int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream);
+
+/* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the quantised copy of
  * fp32 activations, 0 for pre-quantised activations. */
 KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
 
-/* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype.  workspace may be
+/* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype (the block_q8s forms pair
+ * with Q8_0 weights only, KSQ_ERR_TYPE otherwise).  workspace may be
  * NULL (then a per-device pool owned by the library is used, which makes the call
  * allocate on first use and when sizes grow).  Returns a ksq_status. */
 KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,
@@ -113,7 +147,7 @@ KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* a
                          int M, int N, int K, void* stream);
 
 /* Debug: the same per-block integer dots taken from the int8 MFMA tiles of the
- * prefill GEMM (all four weight types).  K % 256 == 0, act_q8_1 16-byte aligned, weight
+ * prefill GEMM (all weight types).  K % 256 == 0, act_q8_1 16-byte aligned, weight
  * 16-byte aligned (4-byte for Q6_K). */
 KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
                               int M, int N, int K, void* stream);
@@ -121,7 +155,7 @@ KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8
 /* ---- expert-grouped MoE (no reference counterpart for GGML types) ----------
  * output[t][n] = sum over the top_k experts e chosen for token t of
  *                w[t][e] * (Q8_1(activation[t]) . weight[e][n]),
- * weight = E experts, each [N][K/32] blocks (Q4_0 or Q8_0), back to back.
+ * weight = E experts, each [N][K/32] blocks (Q4_0, Q8_0, Q4_1, Q5_0 or Q5_1), back to back.
  * Routing: softmax over router_logits[t][0..E-1] (fp32), the top_k experts by logit
  * (ties -> lower index); w = the softmax probabilities of the chosen experts, or those
  * divided by their sum when renorm != 0.  K % 256 == 0, E <= 256, top_k <= E.

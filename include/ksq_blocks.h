@@ -11,6 +11,14 @@
  *   block_q8_1  quant_types.h:147-152, types.py:156-169
  *               (ds = half2: d in the low half, s = sum of the source floats
  *                in the high half)
+ *   block_q4_1  quant_types.h:88-95, types.py:94-108
+ *   block_q5_0  types.py:110-123 (used by kernels/gemm/gemm_quant_formats.cuh:162-208)
+ *   block_q5_1  types.py:125-140 (gemm_quant_formats.cuh:222-267)
+ * block_q8s is the activation block of the native W8A8C8 operator
+ * (core/operators/quant_gemm/variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93):
+ * that kernel keeps the per-block scale in fp32 and never stores a sum, so its
+ * quantised activations are {float d; int8 qs[32]}, 36 B with qs at the same
+ * offset as block_q8_1.
  * The K-quant super-blocks are absent from the reference; they follow the
  * public GGML layout (ggml-common.h, QK_K = 256):
  *   block_q4_K  {half d; half dmin; u8 scales[12]; u8 qs[128]}      144 B
@@ -29,6 +37,9 @@
 #define KSQ_QK4_0 32
 #define KSQ_QK8_0 32
 #define KSQ_QK8_1 32
+#define KSQ_QK4_1 32
+#define KSQ_QK5_0 32
+#define KSQ_QK5_1 32
 #define KSQ_QK_K 256
 #define KSQ_K_SCALE_SIZE 12
 
@@ -47,6 +58,30 @@ typedef struct {
     uint16_t s;                 /* fp16 sum of the 32 source floats (high half) */
     int8_t qs[KSQ_QK8_1];
 } ksq_block_q8_1;
+
+typedef struct {
+    uint16_t d;                 /* fp16 scale */
+    uint16_t m;                 /* fp16 offset: value = q * d + m, q in 0..15 */
+    uint8_t qs[KSQ_QK4_1 / 2];  /* nibble order as block_q4_0 */
+} ksq_block_q4_1;
+
+typedef struct {
+    uint16_t d;                 /* fp16 scale: value = (q - 16) * d, q in 0..31 */
+    uint8_t qh[4];              /* bit j of the little-endian word = bit 4 of element j */
+    uint8_t qs[KSQ_QK5_0 / 2];  /* low 4 bits, nibble order as block_q4_0 */
+} ksq_block_q5_0;
+
+typedef struct {
+    uint16_t d;                 /* fp16 scale */
+    uint16_t m;                 /* fp16 offset: value = q * d + m, q in 0..31 */
+    uint8_t qh[4];
+    uint8_t qs[KSQ_QK5_1 / 2];
+} ksq_block_q5_1;
+
+typedef struct {
+    float d;                    /* fp32 scale (amax / 127, or 1 when that is below 1e-6) */
+    int8_t qs[KSQ_QK8_1];
+} ksq_block_q8s;
 
 typedef struct {
     uint16_t d;                          /* super-block scale for the 6-bit sub-block scales */
@@ -75,6 +110,17 @@ KSQ_STATIC_ASSERT(offsetof(ksq_block_q8_0, qs) == 2, "block_q8_0.qs at offset 2"
 KSQ_STATIC_ASSERT(sizeof(ksq_block_q8_1) == 36, "block_q8_1 must be 36 bytes");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q8_1, s) == 2, "block_q8_1.s (high half of ds) at offset 2");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q8_1, qs) == 4, "block_q8_1.qs at offset 4");
+KSQ_STATIC_ASSERT(sizeof(ksq_block_q4_1) == 20, "block_q4_1 must be 20 bytes");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_1, m) == 2, "block_q4_1.m at offset 2");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_1, qs) == 4, "block_q4_1.qs at offset 4");
+KSQ_STATIC_ASSERT(sizeof(ksq_block_q5_0) == 22, "block_q5_0 must be 22 bytes");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_0, qh) == 2, "block_q5_0.qh at offset 2");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_0, qs) == 6, "block_q5_0.qs at offset 6");
+KSQ_STATIC_ASSERT(sizeof(ksq_block_q5_1) == 24, "block_q5_1 must be 24 bytes");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_1, qh) == 4, "block_q5_1.qh at offset 4");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_1, qs) == 8, "block_q5_1.qs at offset 8");
+KSQ_STATIC_ASSERT(sizeof(ksq_block_q8s) == 36, "block_q8s must be 36 bytes");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q8s, qs) == 4, "block_q8s.qs at offset 4, as in block_q8_1");
 KSQ_STATIC_ASSERT(sizeof(ksq_block_q4_K) == 144, "block_q4_K must be 144 bytes");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_K, scales) == 4, "block_q4_K.scales at offset 4");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_K, qs) == 16, "block_q4_K.qs at offset 16");
@@ -89,12 +135,17 @@ enum ksq_wtype {
     KSQ_W_Q8_0 = 1,
     KSQ_W_Q4_K = 2,
     KSQ_W_Q6_K = 3,
+    KSQ_W_Q4_1 = 4,
+    KSQ_W_Q5_0 = 5,
+    KSQ_W_Q5_1 = 6,
 };
 
 /* Activation-type codes. */
 enum ksq_atype {
     KSQ_A_F32 = 0,   /* fp32 [M][K], quantised to Q8_1 inside the call */
     KSQ_A_Q8_1 = 1,  /* pre-quantised block_q8_1 [M][K/32] */
+    KSQ_A_F32_Q8S = 2, /* fp32 [M][K], quantised to block_q8s inside the call (native W8A8C8 rules) */
+    KSQ_A_Q8S = 3,   /* pre-quantised block_q8s [M][K/32] */
 };
 
 #endif /* KSQ_BLOCKS_H */

@@ -77,11 +77,15 @@ int pool_get(size_t bytes, void** out) {
 
 int block_elems(int wtype) { return (wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) ? 256 : 32; }
 
+bool atype_f32(int atype) { return atype == KSQ_A_F32 || atype == KSQ_A_F32_Q8S; }
+int atype_fmt(int atype) { return (atype == KSQ_A_F32_Q8S || atype == KSQ_A_Q8S) ? ksq::kAQ8S : ksq::kAQ81; }
+
 int check_common(int wtype, int atype, const void* weight, const void* activation, const void* output, int M,
                  int N, int K) {
-    if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q6_K) return set_error(KSQ_ERR_TYPE, "unknown weight type %d", wtype);
-    if (atype != KSQ_A_F32 && atype != KSQ_A_Q8_1)
-        return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
+    if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q5_1) return set_error(KSQ_ERR_TYPE, "unknown weight type %d", wtype);
+    if (atype < KSQ_A_F32 || atype > KSQ_A_Q8S) return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
+    if (atype_fmt(atype) == ksq::kAQ8S && wtype != KSQ_W_Q8_0)
+        return set_error(KSQ_ERR_TYPE, "block_q8s activations pair with Q8_0 weights only (weight type %d)", wtype);
     if (M < 0 || N < 0 || K < 0) return set_error(KSQ_ERR_SHAPE, "negative shape M=%d N=%d K=%d", M, N, K);
     const int be = block_elems(wtype);
     if (K % be != 0) return set_error(KSQ_ERR_SHAPE, "K=%d is not a multiple of %d", K, be);
@@ -93,19 +97,20 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
     if (w & 1u) return set_error(KSQ_ERR_ALIGN, "weight must be 2-byte aligned");
     if ((wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) && (w & 3u))
         return set_error(KSQ_ERR_ALIGN, "K-quant weight must be 4-byte aligned");
-    if (atype == KSQ_A_F32 && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "fp32 activation must be 16-byte aligned");
-    if (atype == KSQ_A_Q8_1 && (a & 3u)) return set_error(KSQ_ERR_ALIGN, "Q8_1 activation must be 4-byte aligned");
+    if (atype_f32(atype) && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "fp32 activation must be 16-byte aligned");
+    if (!atype_f32(atype) && (a & 3u)) return set_error(KSQ_ERR_ALIGN, "quantised activation must be 4-byte aligned");
     if (o & 3u) return set_error(KSQ_ERR_ALIGN, "output must be 4-byte aligned");
     return KSQ_OK;
 }
 
-int run_matmul(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int M, int N, int K, hipStream_t s) {
+int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* C, int M, int N, int K,
+               hipStream_t s) {
     hipError_t e;
     const bool use_mmq = (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, Aq) && (g_path == 2 || M > 8);
     if (use_mmq)
-        e = ksq::launch_mmq(wtype, W, Aq, C, M, N, K, s);
+        e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, s);
     else
-        e = ksq::launch_gemv(wtype, W, Aq, C, M, N, K, s);
+        e = ksq::launch_gemv(wtype, afmt, W, Aq, C, M, N, K, s);
     if (e != hipSuccess) return hip_error(e, use_mmq ? "mmq launch" : "gemv launch");
     return KSQ_OK;
 }
@@ -168,10 +173,21 @@ int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream) {
     return ok();
 }
 
+int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
+    if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
+    if (M == 0 || K == 0) return ok();
+    if (!x || !y) return set_error(KSQ_ERR_NULL, "x or y is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 3u))
+        return set_error(KSQ_ERR_ALIGN, "x must be 16-byte and y 4-byte aligned");
+    hipError_t e = ksq::launch_quantize(ksq::kAQ8S, x, y, M, K, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "quantize launch");
+    return ok();
+}
+
 size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
     (void)wtype;
     (void)N;
-    if (atype != KSQ_A_F32 || M <= 0 || K <= 0) return 0;
+    if (!atype_f32(atype) || M <= 0 || K <= 0) return 0;
     return (size_t)M * (size_t)(K / 32) * 36u;
 }
 
@@ -186,7 +202,8 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
         return e == hipSuccess ? ok() : hip_error(e, "fill launch");
     }
     const uint8_t* Aq = (const uint8_t*)activation;
-    if (atype == KSQ_A_F32) {
+    const int afmt = atype_fmt(atype);
+    if (atype_f32(atype)) {
         const size_t need = ksq_gemm_workspace_size(wtype, atype, M, N, K);
         void* ws = workspace;
         if (ws) {
@@ -197,11 +214,11 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
             st = pool_get(need, &ws);
             if (st != KSQ_OK) return st;
         }
-        hipError_t e = ksq::launch_quantize_q8_1((const float*)activation, (uint8_t*)ws, M, K, s);
+        hipError_t e = ksq::launch_quantize(afmt, (const float*)activation, (uint8_t*)ws, M, K, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
         Aq = (const uint8_t*)ws;
     }
-    st = run_matmul(wtype, (const uint8_t*)weight, Aq, output, M, N, K, s);
+    st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, s);
     return st == KSQ_OK ? ok() : st;
 }
 
@@ -220,7 +237,7 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
     if (st != KSQ_OK) return st;
     if (M == 0 || N == 0 || K == 0) return ok();
     if (!ksq::mmq_supported(wtype, M, N, K, weight, act_q8_1))
-        return set_error(KSQ_ERR_SHAPE, "MFMA path needs Q4_0/Q8_0, K %% 256 == 0 and 16-byte aligned operands");
+        return set_error(KSQ_ERR_SHAPE, "MFMA path needs K %% 256 == 0 and 16-byte aligned operands");
     hipError_t e = ksq::launch_mmq_block_sumi(wtype, (const uint8_t*)weight, act_q8_1, out, M, N, K, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_error(e, "mfma block_sumi launch");
 }
@@ -257,8 +274,8 @@ MoeLayout moe_layout(int T, int N, int K, int E, int top_k) {
 int moe_run(int wtype, const void* weights, const float* activation, const float* logits, const int32_t* ids_in,
             const float* wts_in, float* output, int T, int N, int K, int E, int top_k, int renorm, int32_t* ids_out,
             float* wts_out, void* workspace, size_t ws_bytes, hipStream_t s) {
-    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q8_0)
-        return set_error(KSQ_ERR_TYPE, "MoE GEMM supports Q4_0 and Q8_0 weights");
+    if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q5_1 || wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K)
+        return set_error(KSQ_ERR_TYPE, "MoE GEMM supports the 32-element block types (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1)");
     if (T < 0 || N < 0 || K < 0 || E < 1 || E > 256 || top_k < 1 || top_k > E)
         return set_error(KSQ_ERR_SHAPE, "bad MoE shape T=%d N=%d K=%d E=%d top_k=%d", T, N, K, E, top_k);
     if (K % 256) return set_error(KSQ_ERR_SHAPE, "MoE GEMM needs K %% 256 == 0 (K=%d)", K);
@@ -352,5 +369,12 @@ KSQ_DROPIN(ksq_gemm_q4_0_q8_1, KSQ_W_Q4_0, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(ksq_gemm_q8_0_q8_1, KSQ_W_Q8_0, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(ksq_gemm_q4_k_q8_1, KSQ_W_Q4_K, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(ksq_gemm_q6_k_q8_1, KSQ_W_Q6_K, KSQ_A_Q8_1, uint8_t)
+KSQ_DROPIN(gemm_w4a32c8_q4_1_fp32_int8, KSQ_W_Q4_1, KSQ_A_F32, float)
+KSQ_DROPIN(gemm_w5a32c8_q5_0_fp32_int8, KSQ_W_Q5_0, KSQ_A_F32, float)
+KSQ_DROPIN(gemm_w5a32c8_q5_1_fp32_int8, KSQ_W_Q5_1, KSQ_A_F32, float)
+KSQ_DROPIN(ksq_gemm_q4_1_q8_1, KSQ_W_Q4_1, KSQ_A_Q8_1, uint8_t)
+KSQ_DROPIN(ksq_gemm_q5_0_q8_1, KSQ_W_Q5_0, KSQ_A_Q8_1, uint8_t)
+KSQ_DROPIN(ksq_gemm_q5_1_q8_1, KSQ_W_Q5_1, KSQ_A_Q8_1, uint8_t)
+KSQ_DROPIN(gemm_w8a8c8_q8_0_q8_1, KSQ_W_Q8_0, KSQ_A_F32_Q8S, float)
 
 }  // extern "C"

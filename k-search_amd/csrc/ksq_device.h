@@ -22,6 +22,21 @@ constexpr int kQ80Bytes = 34;
 constexpr int kQ81Bytes = 36;
 constexpr int kQ4KBytes = 144;
 constexpr int kQ6KBytes = 210;
+constexpr int kQ41Bytes = 20;
+constexpr int kQ50Bytes = 22;
+constexpr int kQ51Bytes = 24;
+
+// Weight-type codes (enum ksq_wtype of include/ksq_blocks.h).
+constexpr int kWQ40 = 0, kWQ80 = 1, kWQ4K = 2, kWQ6K = 3, kWQ41 = 4, kWQ50 = 5, kWQ51 = 6;
+
+// The K-quant super-block types (256 elements) versus the 32-element block types.
+__host__ __device__ constexpr bool is_kquant(int wt) { return wt == kWQ4K || wt == kWQ6K; }
+
+// Bytes of one 32-element block of a non-K-quant type.
+__host__ __device__ constexpr int block_bytes(int wt) {
+    return wt == kWQ40 ? kQ40Bytes : wt == kWQ80 ? kQ80Bytes : wt == kWQ41 ? kQ41Bytes
+         : wt == kWQ50 ? kQ50Bytes : kQ51Bytes;
+}
 
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
@@ -83,51 +98,36 @@ __device__ __forceinline__ void quantize_block_q8_1(const float* v, uint32_t* ou
     }
 }
 
-// ---------------------------------------------------------------------------
-// Block dot products on register-resident blocks.  `w` holds weight bytes,
-// `a` points at the 9 dwords of one block_q8_1 (ds, then 8 quant words).
-// ---------------------------------------------------------------------------
-
-// Integer part of vec_dot_q4_0_q8_1 (kernelevalplus-main/include/gemm_reference.h:200-212):
-// sumi = sum_k qa[k]*(qs[k]&15) + qa[k+16]*(qs[k]>>4).
-__device__ __forceinline__ int sumi_q4_0(const uint32_t* w, int off, const uint32_t* a) {
-    int sumi = 0;
+// Quantise 32 floats to one block_q8s, the activation block of the native W8A8C8 operator
+// (kernelevalplus-main/core/operators/quant_gemm/variants/deepseek_v3/w8a8c8_q8_0_q8_1/
+// kernel.cu:66-93): amax = fmaxf over |x| from 0, d = amax / 127 in fp32 (1 when below 1e-6,
+// kept in fp32), q = clamp((int)roundf(x / d), -128, 127) with a true division.  That
+// operator's float -> int conversion is the device one (NaN -> 0, saturation); clamping the
+// rounded value before converting gives the same bytes.  out[0] = d bits, out[1..8] = quants.
+__device__ __forceinline__ void quantize_block_q8s(const float* v, uint32_t* out) {
+#pragma clang fp contract(off)
+    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t q = word_at(w, off + 2 + 4 * i);
-        sumi = dot4((int)(q & 0x0F0F0F0Fu), (int)a[1 + i], sumi);
-        sumi = dot4((int)((q >> 4) & 0x0F0F0F0Fu), (int)a[5 + i], sumi);
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(v[j]));
+    float d = amax / 127.0f;
+    if (d < 1e-6f) d = 1.0f;
+    out[0] = __builtin_bit_cast(uint32_t, d);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float r = roundf(v[4 * j + t] / d);
+            const int q = (r != r) ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
+            packed |= ((uint32_t)q & 0xFFu) << (8 * t);
+        }
+        out[1 + j] = packed;
     }
-    return sumi;
 }
 
-// Integer part of vec_dot_q8_0_q8_1 (gemm_reference.h:253-256).
-__device__ __forceinline__ int sumi_q8_0(const uint32_t* w, int off, const uint32_t* a) {
-    int sumi = 0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) sumi = dot4((int)word_at(w, off + 2 + 4 * i), (int)a[1 + i], sumi);
-    return sumi;
-}
-
-// Block contribution d_w * (d_a * sumi - 8 * s_a) (gemm_reference.h:216).
-__device__ __forceinline__ float block_q4_0(const uint32_t* w, int off, const uint32_t* a) {
-    const int sumi = sumi_q4_0(w, off, a);
-    const float dw = f16_to_f32(half_at(w, off));
-    const float da = f16_to_f32(a[0] & 0xFFFFu), sa = f16_to_f32(a[0] >> 16);
-    return dw * (da * (float)sumi - 8.0f * sa);
-}
-
-// Block contribution sumi * d_a * d_w (gemm_reference.h:259).
-__device__ __forceinline__ float block_q8_0(const uint32_t* w, int off, const uint32_t* a) {
-    const int sumi = sumi_q8_0(w, off, a);
-    const float dw = f16_to_f32(half_at(w, off));
-    const float da = f16_to_f32(a[0] & 0xFFFFu);
-    return (float)sumi * da * dw;
-}
-
-template <typename T>
-__device__ __forceinline__ T ldg_nt(const T* p) {
-    return __builtin_nontemporal_load(p);
-}
+// Bits 0..3 of x moved to bit 4 of the four bytes of a word: the fifth bit of four
+// consecutive Q5_0 / Q5_1 quants.  The product places bit k of x at bit 8k (its shifted
+// copies x, x<<7, x<<14, x<<21 do not overlap, so nothing carries).
+__device__ __forceinline__ uint32_t qh_to_bit4(uint32_t x) { return (((x & 0xFu) * 0x00204081u) & 0x01010101u) << 4; }
 
 }  // namespace ksq

@@ -11,11 +11,12 @@
 //    activation rows in LDS once for all four waves.  One-shot reads of a few MB
 //    are fastest as many small, fully coalesced requests spread over the whole
 //    chip, which is what this layout issues.
-//  * Lanes then stride over 32-element units of the row (a Q4_0/Q8_0 block, or one
-//    Q8_1-block-sized slice of a Q4_K/Q6_K super-block), pull the unit's bytes out of
-//    LDS with dword reads re-aligned by v_alignbyte_b32 (blocks are 18/34/144/210 B,
-//    only 2-byte aligned), unpack nibbles in registers and run v_dot4c_i32_i8
-//    against the Q8_1 quants; the per-unit fp32 epilogue is the reference formula.
+//  * Lanes then stride over 32-element units of the row (a Q4_0/Q8_0/Q4_1/Q5_0/Q5_1
+//    block, or one Q8_1-block-sized slice of a Q4_K/Q6_K super-block), pull the unit's
+//    bytes out of LDS with dword reads re-aligned by v_alignbyte_b32 (blocks are
+//    18/34/20/22/24/144/210 B, only 2-byte aligned), unpack nibbles (and Q5 high bits)
+//    in registers and run v_dot4c_i32_i8 against the activation quants; the per-unit
+//    fp32 epilogue is the reference formula.
 //  * The 64 lane partials are combined with xor shuffles; lane 0 stores.
 //  * Rows longer than the LDS tile are walked in K tiles.
 #include "ksq_device.h"
@@ -72,6 +73,47 @@ __device__ __forceinline__ int unit_sumi_q8_0(const uint8_t* blk, const uint32_t
     return s;
 }
 
+// Q4_1 block (gemm_quant_formats.cuh:126-137): the same nibble dot as Q4_0, quants at offset 4.
+__device__ __forceinline__ int unit_sumi_q4_1(const uint8_t* blk, const uint32_t* a) {
+    uint32_t q[4];
+    read_words<4>(blk + 4, q);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        s = dot4((int)(q[i] & 0x0F0F0F0Fu), (int)a[1 + i], s);
+        s = dot4((int)((q[i] >> 4) & 0x0F0F0F0Fu), (int)a[5 + i], s);
+    }
+    return s;
+}
+
+// Q5_0 / Q5_1 block (gemm_quant_formats.cuh:170-200, 230-257): low 4 bits from the nibbles
+// at qs_off, bit 4 of element e from bit e of the qh word at qh_off; quants 0..31.
+template <int QH_OFF, int QS_OFF>
+__device__ __forceinline__ int unit_sumi_q5(const uint8_t* blk, const uint32_t* a) {
+    uint32_t q[4], h[1];
+    read_words<4>(blk + QS_OFF, q);
+    read_words<1>(blk + QH_OFF, h);
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t lo = (q[i] & 0x0F0F0F0Fu) | qh_to_bit4(h[0] >> (4 * i));
+        const uint32_t hi = ((q[i] >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h[0] >> (16 + 4 * i));
+        s = dot4((int)lo, (int)a[1 + i], s);
+        s = dot4((int)hi, (int)a[5 + i], s);
+    }
+    return s;
+}
+
+// Integer block dot of any 32-element block type against the 9-dword activation block a.
+template <int WT>
+__device__ __forceinline__ int unit_sumi_legacy(const uint8_t* blk, const uint32_t* a) {
+    if constexpr (WT == kWQ40) return unit_sumi_q4_0(blk, a);
+    else if constexpr (WT == kWQ80) return unit_sumi_q8_0(blk, a);
+    else if constexpr (WT == kWQ41) return unit_sumi_q4_1(blk, a);
+    else if constexpr (WT == kWQ50) return unit_sumi_q5<2, 6>(blk, a);
+    else return unit_sumi_q5<4, 8>(blk, a);
+}
+
 // Q4_K sub-block j (32 elements) of super-block sb: 64-element group g = j/2 holds its
 // quants in qs[32g .. 32g+31], low nibbles for even j, high nibbles for odd j.
 __device__ __forceinline__ int unit_sumi_q4_K(const uint8_t* sb, int j, const uint32_t* a) {
@@ -120,8 +162,8 @@ __device__ __forceinline__ void unit_sumi_q6_K(const uint8_t* sb, int j, const u
 // ---- the decode kernel -------------------------------------------------------
 template <int WT>
 struct Fmt {
-    // bytes of one 256-element span (8 blocks or one super-block) and units per span
-    static constexpr int span = (WT == 0) ? 144 : (WT == 1) ? 272 : (WT == 2) ? 144 : 210;
+    // bytes of one 256-element span (8 blocks or one super-block)
+    static constexpr int span = (WT == kWQ4K) ? kQ4KBytes : (WT == kWQ6K) ? kQ6KBytes : 8 * block_bytes(WT);
 };
 
 constexpr int kRowsPerWG = 4;
@@ -146,16 +188,17 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
 }
 
 // C[m][row] = sum over the row's units, for m < MR.  KT = blocks per K tile (multiple of 8).
-template <int WT, int MR, bool ALDS>
+// AS: the activations are block_q8s (fp32 scale, no sum) instead of block_q8_1.
+template <int WT, int MR, bool ALDS, bool AS>
 __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
                                                        float* __restrict__ C, int N, int nb, int KT, int ldc,
                                                        int a_vec16) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row = blockIdx.x * kRowsPerWG + wave;
-    const bool kq = (WT >= 2);
-    const size_t RB = kq ? (size_t)(nb / 8) * Fmt<WT>::span : (size_t)nb * (WT == 0 ? kQ40Bytes : kQ80Bytes);
-    const int tile_w = kq ? (KT / 8) * Fmt<WT>::span : KT * (WT == 0 ? kQ40Bytes : kQ80Bytes);
+    constexpr bool kq = is_kquant(WT);
+    const size_t RB = kq ? (size_t)(nb / 8) * Fmt<WT>::span : (size_t)nb * block_bytes(WT);  // row bytes
+    const int tile_w = kq ? (KT / 8) * Fmt<WT>::span : KT * block_bytes(WT);
     const int wpitch = ((tile_w + kTileSlack + 15) & ~15);
     uint8_t* wreg = smem + wave * wpitch;
     uint8_t* areg = smem + kRowsPerWG * wpitch;  // [MR][KT] Q8_1 blocks, 36 B each
@@ -169,8 +212,8 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
         const uint8_t* g = nullptr;
         uint8_t* wt = nullptr;
         if (row < N) {
-            const size_t off = kq ? (size_t)(kt0 / 8) * Fmt<WT>::span : (size_t)kt0 * (WT == 0 ? kQ40Bytes : kQ80Bytes);
-            const int bytes = kq ? (kt / 8) * Fmt<WT>::span : kt * (WT == 0 ? kQ40Bytes : kQ80Bytes);
+            const size_t off = kq ? (size_t)(kt0 / 8) * Fmt<WT>::span : (size_t)kt0 * block_bytes(WT);
+            const int bytes = kq ? (kt / 8) * Fmt<WT>::span : kt * block_bytes(WT);
             g = W + (size_t)row * RB + off;
             wt = wreg + ((uintptr_t)g & 15);
             wave_copy_to_lds(g, wt, bytes, lane);
@@ -197,9 +240,11 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
 
         if (row < N) {
             for (int u = lane; u < kt; u += 64) {   // unit u = 32-element slice, Q8_1 block kt0 + u
-                if constexpr (WT == 0 || WT == 1) {
-                    const uint8_t* blk = wt + u * (WT == 0 ? kQ40Bytes : kQ80Bytes);
+                if constexpr (!kq) {
+                    const uint8_t* blk = wt + u * block_bytes(WT);
                     const float dw = f16_to_f32(read_u16(blk));
+                    float mw = 0.0f;
+                    if constexpr (WT == kWQ41 || WT == kWQ51) mw = f16_to_f32(read_u16(blk + 2));
 #pragma unroll
                     for (int m = 0; m < MR; m++) {
                         const uint32_t* ap = ALDS ? (const uint32_t*)(areg + ((size_t)m * KT + u) * kQ81Bytes)
@@ -207,19 +252,24 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                         uint32_t a[9];
 #pragma unroll
                         for (int i = 0; i < 9; i++) a[i] = ap[i];
-                        const float da = f16_to_f32(a[0] & 0xFFFFu);
-                        if constexpr (WT == 0) {
-                            const int sumi = unit_sumi_q4_0(blk, a);
+                        const float da = AS ? __builtin_bit_cast(float, a[0]) : f16_to_f32(a[0] & 0xFFFFu);
+                        const int sumi = unit_sumi_legacy<WT>(blk, a);
+                        // block formulas of gemm_reference.h:216 / :259 and gemm_quant_formats.cuh:148,
+                        // :207, :266 (the last two without the reference's /4 on the m*s term)
+                        if constexpr (WT == kWQ40) {
                             acc[m] += dw * (da * (float)sumi - 8.0f * f16_to_f32(a[0] >> 16));
+                        } else if constexpr (WT == kWQ80) {
+                            acc[m] += AS ? dw * da * (float)sumi : (float)sumi * da * dw;
+                        } else if constexpr (WT == kWQ50) {
+                            acc[m] += dw * (da * (float)sumi - 16.0f * f16_to_f32(a[0] >> 16));
                         } else {
-                            const int sumi = unit_sumi_q8_0(blk, a);
-                            acc[m] += (float)sumi * da * dw;
+                            acc[m] += dw * da * (float)sumi + mw * f16_to_f32(a[0] >> 16);
                         }
                     }
                 } else {
                     const uint8_t* sb = wt + (u >> 3) * Fmt<WT>::span;
                     const int j = u & 7;
-                    if constexpr (WT == 2) {
+                    if constexpr (WT == kWQ4K) {
                         uint32_t hd[1], sc3[3];
                         read_words<1>(sb, hd);
                         read_words<3>(sb + 4, sc3);
@@ -269,7 +319,9 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
 // ---- host dispatch -------------------------------------------------------------
 constexpr size_t kGemvLdsBudget = 48 * 1024;
 
-static int span_bytes(int wtype) { return wtype == 0 ? 144 : wtype == 1 ? 272 : wtype == 2 ? 144 : 210; }
+static int span_bytes(int wtype) {
+    return wtype == kWQ4K ? kQ4KBytes : wtype == kWQ6K ? kQ6KBytes : 8 * block_bytes(wtype);
+}
 
 // Activation rows are staged in LDS (once per workgroup) for M > 2; for M <= 2 each
 // lane reads its Q8_1 blocks straight from L2, which measured faster at M = 1.
@@ -281,34 +333,35 @@ static size_t gemv_lds_bytes(int wtype, int mr, int KT) {
     return kRowsPerWG * wpitch + (mr >= kActLdsMinRows ? (size_t)mr * KT * kQ81Bytes : 0);
 }
 
-template <int WT, int MR>
+template <int WT, int MR, bool AS>
 static hipError_t row_launch(const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int KT, int ldc, int av16,
                              hipStream_t s) {
     const size_t lds = gemv_lds_bytes(WT, MR, KT);
-    auto k = gemv_row_kernel<WT, MR, (MR >= kActLdsMinRows)>;
+    auto k = gemv_row_kernel<WT, MR, (MR >= kActLdsMinRows), AS>;
     if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     const unsigned grid = (unsigned)((N + kRowsPerWG - 1) / kRowsPerWG);
     hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, W, A, C, N, nb, KT, ldc, av16);
     return hipGetLastError();
 }
 
-template <int WT>
+template <int WT, bool AS = false>
 static hipError_t row_launch_mr(int mr, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int KT, int ldc,
                                 int av16, hipStream_t s) {
     switch (mr) {
-        case 1: return row_launch<WT, 1>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 2: return row_launch<WT, 2>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 3: return row_launch<WT, 3>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 4: return row_launch<WT, 4>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 5: return row_launch<WT, 5>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 6: return row_launch<WT, 6>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 7: return row_launch<WT, 7>(W, A, C, N, nb, KT, ldc, av16, s);
-        default: return row_launch<WT, 8>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 1: return row_launch<WT, 1, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 2: return row_launch<WT, 2, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 3: return row_launch<WT, 3, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 4: return row_launch<WT, 4, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 5: return row_launch<WT, 5, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 6: return row_launch<WT, 6, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        case 7: return row_launch<WT, 7, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+        default: return row_launch<WT, 8, AS>(W, A, C, N, nb, KT, ldc, av16, s);
     }
 }
 
-hipError_t launch_gemv(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s) {
+    if (afmt == kAQ8S && wtype != kWQ80) return hipErrorNotSupported;
     const int nb = K / 32;
     if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
     for (int m0 = 0; m0 < M; m0 += 8) {
@@ -321,10 +374,16 @@ hipError_t launch_gemv(int wtype, const uint8_t* W, const uint8_t* A, float* C, 
         float* Cm = C + (size_t)m0 * N;
         hipError_t e;
         switch (wtype) {
-            case 0: e = row_launch_mr<0>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case 1: e = row_launch_mr<1>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case 2: e = row_launch_mr<2>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            default: e = row_launch_mr<3>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            case kWQ40: e = row_launch_mr<kWQ40>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            case kWQ80:
+                e = (afmt == kAQ8S) ? row_launch_mr<kWQ80, true>(mr, W, Am, Cm, N, nb, KT, N, av16, s)
+                                    : row_launch_mr<kWQ80>(mr, W, Am, Cm, N, nb, KT, N, av16, s);
+                break;
+            case kWQ4K: e = row_launch_mr<kWQ4K>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            case kWQ6K: e = row_launch_mr<kWQ6K>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            case kWQ41: e = row_launch_mr<kWQ41>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            case kWQ50: e = row_launch_mr<kWQ50>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
+            default: e = row_launch_mr<kWQ51>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
         }
         if (e != hipSuccess) return e;
     }
@@ -346,10 +405,10 @@ __global__ void block_sumi_kernel(int wtype, const uint8_t* __restrict__ W, cons
     const int n = (int)(mn % N), m = (int)(mn / N);
     // copy the unit's weight bytes with exact-size 16-bit loads (the unit readers may
     // read a few bytes past a block, which is fine in LDS but not at the end of W)
-    const int ub = (wtype == 0) ? kQ40Bytes : (wtype == 1) ? kQ80Bytes : (wtype == 2) ? kQ4KBytes : kQ6KBytes;
+    const int ub = (wtype == kWQ4K) ? kQ4KBytes : (wtype == kWQ6K) ? kQ6KBytes : block_bytes(wtype);
     const uint8_t* src;
-    if (wtype <= 1) src = W + ((size_t)n * nb + b) * ub;
-    else src = W + ((size_t)n * (K / 256) + (wtype == 3 ? b / 16 : b / 8)) * ub;
+    if (!is_kquant(wtype)) src = W + ((size_t)n * nb + b) * ub;
+    else src = W + ((size_t)n * (K / 256) + (wtype == kWQ6K ? b / 16 : b / 8)) * ub;
     uint32_t buf[56] = {0};
     for (int i = 0; i < ub / 2; i++) {
         const uint32_t h = ((const uint16_t*)src)[i];
@@ -361,9 +420,12 @@ __global__ void block_sumi_kernel(int wtype, const uint8_t* __restrict__ W, cons
     uint32_t a[9];
     for (int i = 0; i < 9; i++) a[i] = ap[i];
     int r;
-    if (wtype == 0) r = unit_sumi_q4_0(blk, a);
-    else if (wtype == 1) r = unit_sumi_q8_0(blk, a);
-    else if (wtype == 2) r = unit_sumi_q4_K(blk, b % 8, a);
+    if (wtype == kWQ40) r = unit_sumi_q4_0(blk, a);
+    else if (wtype == kWQ80) r = unit_sumi_q8_0(blk, a);
+    else if (wtype == kWQ41) r = unit_sumi_q4_1(blk, a);
+    else if (wtype == kWQ50) r = unit_sumi_q5<2, 6>(blk, a);
+    else if (wtype == kWQ51) r = unit_sumi_q5<4, 8>(blk, a);
+    else if (wtype == kWQ4K) r = unit_sumi_q4_K(blk, b % 8, a);
     else {
         int is0, is1;
         unit_sumi_q6_K(blk, (b % 16) >> 1, a, is0, is1);

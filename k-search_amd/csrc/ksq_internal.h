@@ -10,18 +10,23 @@
 
 namespace ksq {
 
-// fp32 [rows][K] -> block_q8_1 [rows][K/32]; x 16-byte aligned, y 4-byte aligned.
+// Quantised-activation formats: block_q8_1 (fp16 d and s) or block_q8s (fp32 d, the native
+// W8A8C8 operator's block; used with Q8_0 weights only).
+constexpr int kAQ81 = 0, kAQ8S = 1;
+
+// fp32 [rows][K] -> [rows][K/32] 36-byte blocks of format afmt; x 16-byte aligned, y 4-byte aligned.
+hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 
-// Decode GEMV/GEMM on v_dot4 (mul_mat_vec_q family), any M; activations are Q8_1.
-// wtype: 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K.
-hipError_t launch_gemv(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+// Decode GEMV/GEMM on v_dot4 (mul_mat_vec_q family), any M.
+// wtype: 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q4_1, 5 Q5_0, 6 Q5_1.
+hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s);
 
 // Prefill GEMM on int8 MFMA (mul_mat_q family); returns hipErrorNotSupported
 // for shapes it does not tile.
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A);
-hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       hipStream_t s);
 // Force one of the MFMA tile configurations (1..4) or automatic choice (0); -1 if out of range.
 int mmq_set_config(int c);

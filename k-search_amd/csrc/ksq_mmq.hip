@@ -8,10 +8,11 @@
 //  * A BM x BN workgroup tile, 4 waves each owning TM x TN tiles of 32 x 32 computed
 //    with v_mfma_i32_32x32x32_i8.  One MFMA contracts exactly one 32-element Q block,
 //    so its i32 result IS the reference's integer block dot sumi for a 32 x 32 patch.
-//  * Per K step KB blocks are staged in LDS: Q8_1 quants as int8 rows, Q4_0 weights as
-//    packed nibbles (the MFMA lane that holds k = 0..15 takes the low nibbles, the lane
-//    that holds k = 16..31 the high ones, which is exactly the Q4_0 element order),
-//    Q8_0 weights as int8 rows, plus the per-block scales widened once to fp32.
+//  * Per K step KB blocks are staged in LDS: Q8_1 quants as int8 rows, Q4_0 / Q4_1
+//    weights as packed nibbles (the MFMA lane that holds k = 0..15 takes the low nibbles,
+//    the lane that holds k = 16..31 the high ones, which is exactly the element order),
+//    Q8_0 weights as int8 rows, Q5_0 / Q5_1 widened to one byte per 5-bit quant, plus the
+//    per-block scales widened once to fp32.
 //  * Epilogue without an int->float conversion: the MFMA accumulates onto the bit
 //    pattern of 12582912.0f (0x4B400000), so the result read as a float is exactly
 //    12582912 + sumi (|sumi| < 2^22).  Then
@@ -22,7 +23,8 @@
 //    reference formula is a rank-(K/32) product of fp16 fields, so it runs on the
 //    f16 MFMA (exact products) straight into the same accumulators; to fold its
 //    factor 8 exactly the main term uses d_a' = d_a / 8 and the result is scaled
-//    by 8 at the end (powers of two: exact).  Q8_0 uses d_a' = d_a and no side term.
+//    by 8 at the end (powers of two: exact).  Q5_0 does the same with 16; Q4_1 and
+//    Q5_1 add m * s_a the same way with factor 1.  Q8_0 uses d_a' = d_a and no side term.
 //  * The MFMA for the next tile is issued before the epilogue of the current one,
 //    so matrix and vector pipes overlap within a wave.
 //  * Row / column tiles past M or N load a clamped in-range row and are not stored.
@@ -49,18 +51,23 @@ struct Tile {
     static constexpr int APitch = KB * 32 + 16;        // bytes per staged activation row
 };
 
-// Staged weight format per type: Q4_0 / Q4_K keep packed nibbles (16 B per 32-element
-// block), Q8_0 / Q6_K int8 values (32 B per block).  SUB = scale groups per 32-element
-// block (2 for Q6_K's 16-element sub-blocks).
+// Staged weight format per type: Q4_0 / Q4_1 / Q4_K keep packed nibbles (16 B per
+// 32-element block); Q8_0 / Q6_K / Q5_0 / Q5_1 int8 values (32 B per block; the 5-bit
+// quants are widened while staging).  SUB = scale groups per 32-element block (2 for
+// Q6_K's 16-element sub-blocks).
 template <int WT, int KB>
 struct WShape {
-    static constexpr int WQ = (WT == 0 || WT == 2) ? 16 : 32;  // staged weight bytes per block
+    static constexpr bool nib = (WT == kWQ40 || WT == kWQ41 || WT == kWQ4K);
+    static constexpr int WQ = nib ? 16 : 32;                    // staged weight bytes per block
     static constexpr int WPitch = KB * WQ + 16;                 // bytes per staged weight row
-    static constexpr int BB = (WT == 0) ? kQ40Bytes : kQ80Bytes;
-    static constexpr int Chunk = 4 * BB;                        // 4 blocks: 72 (Q4_0) or 136 (Q8_0) bytes
-    static constexpr int SUB = (WT == 3) ? 2 : 1;
-    static constexpr bool side = (WT == 0 || WT == 2);          // has the s_a side term
-    static constexpr int SB = (WT == 2) ? kQ4KBytes : kQ6KBytes;  // K-quant super-block bytes
+    static constexpr int BB = is_kquant(WT) ? 0 : block_bytes(WT);
+    static constexpr int Chunk = 4 * BB;                        // 4 blocks: 72 / 136 / 80 / 88 / 96 bytes
+    static constexpr int SUB = (WT == kWQ6K) ? 2 : 1;
+    // the s_a side term: -8 d_w s_a (Q4_0), -dmin m s_a (Q4_K), -16 d_w s_a (Q5_0), +m s_a (Q4_1, Q5_1)
+    static constexpr bool side = !(WT == kWQ80 || WT == kWQ6K);
+    // the main term runs on d_a / out_scale so that the side factor is an fp16 field as stored
+    static constexpr float out_scale = (WT == kWQ40 || WT == kWQ4K) ? 8.0f : (WT == kWQ50) ? 16.0f : 1.0f;
+    static constexpr int SB = (WT == kWQ4K) ? kQ4KBytes : kQ6KBytes;  // K-quant super-block bytes
 };
 
 // Expert-grouped mode (MoE): workgroup x is entry blockIdx.x of a tile schedule; its
@@ -105,7 +112,8 @@ __device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
     for (int i = 0; i < NW; i++) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
 
-template <class T, int WT, bool DUMP, bool MOE>
+// AS: the activations are block_q8s (fp32 scale, no sum; Q8_0 weights only).
+template <class T, int WT, bool DUMP, bool MOE, bool AS>
 __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
                                                           int32_t* __restrict__ dump, int M, int N, int nb,
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
     __shared__ __attribute__((aligned(16))) uint16_t sSaH[BM][8];  // -s_a, fp16 bits (side term)
     __shared__ __attribute__((aligned(16))) uint16_t sDwH[BN][8];  // side-term weight factor, fp16 bits
-    __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == 2 ? BN : 1][8];  // Q4_K: its low part
+    __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == kWQ4K ? BN : 1][8];  // Q4_K: its low part
     __shared__ int32_t sRows[MOE ? BM : 1];                        // MoE: entry index of each tile row
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -127,8 +135,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     const int m0 = (MOE ? 0 : (int)blockIdx.y) * BM;
     const int n0 = (MOE ? (int)blockIdx.y : (int)blockIdx.x) * BN;
     const int l32 = lane & 31, hi = lane >> 5;
-    const float da_scale = S::side ? 0.125f : 1.0f;
-    static_assert(WT < 2 || KB == 8, "K-quants stage one 256-element super-block per K step");
+    constexpr float da_scale = 1.0f / S::out_scale;
+    static_assert(!is_kquant(WT) || KB == 8, "K-quants stage one 256-element super-block per K step");
+    static_assert(!AS || WT == kWQ80, "block_q8s activations pair with Q8_0 weights only");
 
     if constexpr (KB == 4) {
         // the f16 side-term MFMA contracts 8 block slots; slots 4..7 stay zero
@@ -175,14 +184,17 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
                 dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
                 dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
-                const float da = f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
+                // block_q8s: the fp32 scale with its two lowest mantissa bits cleared (22 significant
+                // bits), so that 12582912 * d_a' stays exact (relative change < 2^-21)
+                const float da = AS ? __builtin_bit_cast(float, v[9 * j] & ~3u)
+                                    : f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
                 sDa[kb][sr] = da;
                 sNc[kb][sr] = -kMagicF * da;
                 sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
             }
         }
-        if constexpr (WT <= 1) {
-            // ---- stage weights: chunks of 4 blocks = 72 B (Q4_0) / 136 B (Q8_0), 8-byte aligned
+        if constexpr (!is_kquant(WT)) {
+            // ---- stage weights: chunks of 4 blocks (72 / 136 / 80 / 88 / 96 B), 8-byte aligned
             for (int c = t; c < BN * (KB / 4); c += 256) {
                 const int sr = c / (KB / 4), g = c % (KB / 4);
                 const int wr = min(n0 + sr, N - 1);
@@ -200,18 +212,37 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                     const int kb = 4 * g + j, off = j * S::BB;
                     const uint32_t dwb = half_at(v, off);
                     sDw[kb][sr] = f16_to_f32(dwb);
-                    sDwH[sr][kb] = (uint16_t)dwb;
-                    if constexpr (WT == 0) {
+                    // side factor against -s_a: d_w (Q4_0, Q5_0) or -m (Q4_1, Q5_1)
+                    if constexpr (WT == kWQ41 || WT == kWQ51) sDwH[sr][kb] = (uint16_t)(half_at(v, off + 2) ^ 0x8000u);
+                    else sDwH[sr][kb] = (uint16_t)dwb;
+                    if constexpr (WT == kWQ40 || WT == kWQ41) {
+                        constexpr int q = (WT == kWQ40) ? 2 : 4;  // offset of qs
                         *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
-                            u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
-                    } else {
+                            u32x4{word_at(v, off + q), word_at(v, off + q + 4), word_at(v, off + q + 8),
+                                  word_at(v, off + q + 12)};
+                    } else if constexpr (WT == kWQ80) {
                         u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
                         dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
                         dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
+                    } else {
+                        // Q5_0 / Q5_1: widen to one byte per quant (0..31); element 4i+t takes nibble
+                        // t of word i and qh bit 4i+t, element 16+4i+t the high nibble and bit 16+4i+t
+                        constexpr int qh = (WT == kWQ50) ? 2 : 4, q = qh + 4;
+                        const uint32_t h = word_at(v, off + qh);
+                        uint32_t o[8];
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const uint32_t w4 = word_at(v, off + q + 4 * i);
+                            o[i] = (w4 & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i));
+                            o[4 + i] = ((w4 >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i));
+                        }
+                        u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                        dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+                        dst[1] = u32x4{o[4], o[5], o[6], o[7]};
                     }
                 }
             }
-        } else if constexpr (WT == 2) {
+        } else if constexpr (WT == kWQ4K) {
             // ---- Q4_K: one 144-byte super-block per row and K step (16-byte aligned)
             const int nsb = nb / 8, s0 = kb0 / 8;
             for (int sr = t; sr < BN; sr += 256) {
@@ -284,7 +315,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             return *(const i32x4*)(sA + (wm * 32 * TM + i * 32 + l32) * T::APitch + b * 32 + 16 * hi);
         };
         auto frag_b = [&](int b, int j) -> i32x4 {
-            if constexpr (WT == 2) {
+            if constexpr (WT == kWQ4K) {
                 // sub-block b: bytes 32*(b/2) + 16*hi .. +15 of the staged qs, low nibbles for
                 // even b, high nibbles for odd b
                 const u32x4 x =
@@ -292,7 +323,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 const int s4 = 4 * (b & 1);
                 return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
                              (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
-            } else if constexpr (WT == 0) {
+            } else if constexpr (S::nib) {
                 const u32x4 x = *(const u32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 16);
                 const int s4 = 4 * hi;
                 return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
@@ -373,8 +404,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         }
 
         if constexpr (S::side && !DUMP) {
-            // side term: acc += sum_k (-s_a[m][k]) * f[n][k] over the staged blocks, f = d_w (Q4_0)
-            // or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA over 8 block slots, exact products
+            // side term: acc += sum_k (-s_a[m][k]) * f[n][k] over the staged blocks, f = d_w (Q4_0,
+            // Q5_0), -m (Q4_1, Q5_1) or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA over 8
+            // block slots, exact products
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 32 * TM + i * 32 + l32][4 * hi];
@@ -383,7 +415,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                     const int wrow = wn * 32 * TN + j * 32 + l32;
                     const f16x4 dw4 = *(const f16x4*)&sDwH[wrow][4 * hi];
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dw4, acc[i][j], 0, 0, 0);
-                    if constexpr (WT == 2) {
+                    if constexpr (WT == kWQ4K) {
                         const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * hi];
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dl4, acc[i][j], 0, 0, 0);
                     }
@@ -394,7 +426,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     }
 
     if constexpr (!DUMP) {
-        const float out_scale = S::side ? 8.0f : 1.0f;
+        constexpr float out_scale = S::out_scale;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -439,7 +471,7 @@ static int grid_wgs(int M, int N) {
 }
 
 static int pick_config(int wtype, int M, int N) {
-    if (g_mmq_config && !(wtype >= 2 && g_mmq_config == 4)) return g_mmq_config;
+    if (g_mmq_config && !(is_kquant(wtype) && g_mmq_config == 4)) return g_mmq_config;
     constexpr int kCUs = 256;
     if (grid_wgs<TileL>(M, N) >= 2 * kCUs) return 1;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
@@ -447,47 +479,58 @@ static int pick_config(int wtype, int M, int N) {
 }
 
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A) {
-    const uintptr_t wal = (wtype == 3) ? 3u : 15u;  // Q6_K rows are read per dword
-    return (wtype >= 0 && wtype <= 3) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
+    const uintptr_t wal = (wtype == kWQ6K) ? 3u : 15u;  // Q6_K rows are read per dword
+    return (wtype >= kWQ40 && wtype <= kWQ51) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
            (((uintptr_t)W & wal) == 0) && (((uintptr_t)A & 15u) == 0);
 }
 
-template <class T, bool DUMP, bool MOE>
-static hipError_t launch_t(int wtype, dim3 grid, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump,
-                           int M, int N, int nb, const MoeTiles& mt, hipStream_t s) {
-    switch (wtype) {
-        case 0: hipLaunchKernelGGL((mmq_kernel<T, 0, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt); break;
-        case 1: hipLaunchKernelGGL((mmq_kernel<T, 1, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt); break;
-        case 2:
-            if constexpr (T::KB == 8 && !MOE)
-                hipLaunchKernelGGL((mmq_kernel<T, 2, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
-            else return hipErrorNotSupported;
-            break;
-        default:
-            if constexpr (T::KB == 8 && !MOE)
-                hipLaunchKernelGGL((mmq_kernel<T, 3, DUMP, MOE>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
-            else return hipErrorNotSupported;
-            break;
+template <class T, int WT, bool DUMP, bool MOE, bool AS = false>
+static hipError_t launch_k(dim3 grid, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump, int M, int N,
+                           int nb, const MoeTiles& mt, hipStream_t s) {
+    if constexpr (is_kquant(WT) && (T::KB != 8 || MOE)) {
+        return hipErrorNotSupported;
+    } else {
+        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AS>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
+        return hipGetLastError();
     }
-    return hipGetLastError();
+}
+
+template <class T, bool DUMP, bool MOE>
+static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, const uint8_t* A, float* C,
+                           int32_t* dump, int M, int N, int nb, const MoeTiles& mt, hipStream_t s) {
+    if (afmt == kAQ8S) {
+        if (wtype != kWQ80) return hipErrorNotSupported;
+        return launch_k<T, kWQ80, DUMP, MOE, true>(grid, W, A, C, dump, M, N, nb, mt, s);
+    }
+    switch (wtype) {
+        case kWQ40: return launch_k<T, kWQ40, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ80: return launch_k<T, kWQ80, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ4K: return launch_k<T, kWQ4K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ6K: return launch_k<T, kWQ6K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ41: return launch_k<T, kWQ41, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ50: return launch_k<T, kWQ50, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ51: return launch_k<T, kWQ51, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        default: return hipErrorNotSupported;
+    }
 }
 
 template <bool DUMP>
-static hipError_t launch_cfg(int cfg, int wtype, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump, int M,
-                             int N, int K, hipStream_t s) {
+static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C,
+                             int32_t* dump, int M, int N, int K, hipStream_t s) {
     const int nb = K / 32;
     const MoeTiles mt{};
     auto grid = [&](int BM, int BN) { return dim3((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM)); };
     switch (cfg) {
-        case 1: return launch_t<TileL, DUMP, false>(wtype, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
-        case 2: return launch_t<TileN, DUMP, false>(wtype, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
-        case 3: return launch_t<TileS, DUMP, false>(wtype, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
-        default: return launch_t<TileK4, DUMP, false>(wtype, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 1: return launch_t<TileL, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
+        case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
+        default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
     }
 }
 
-hipError_t launch_mmq(int wtype, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K, hipStream_t s) {
-    return launch_cfg<false>(pick_config(wtype, M, N), wtype, W, A, C, nullptr, M, N, K, s);
+hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+                      hipStream_t s) {
+    return launch_cfg<false>(pick_config(wtype, M, N), wtype, afmt, W, A, C, nullptr, M, N, K, s);
 }
 
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
@@ -502,18 +545,19 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     mt.scratch = a.scratch;
     mt.top_k = a.top_k;
     const int nb = K / 32;
-    mt.expert_stride = (size_t)N * nb * (wtype == 0 ? kQ40Bytes : kQ80Bytes);
+    if (is_kquant(wtype)) return hipErrorNotSupported;
+    mt.expert_stride = (size_t)N * nb * block_bytes(wtype);
     // tiles of 64 rows (the grouping schedule's tile_rows) x 64 columns: an expert's few
     // hundred rows split into several tiles with little padding, and enough workgroups
     using TileMoe = TileS;
     const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileMoe::BN - 1) / TileMoe::BN));
-    return launch_t<TileMoe, false, true>(wtype, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
+    return launch_t<TileMoe, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
 }
 
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,
                                  hipStream_t s) {
     if (!mmq_supported(wtype, M, N, K, W, A)) return hipErrorNotSupported;
-    return launch_cfg<true>(pick_config(wtype, M, N), wtype, W, A, nullptr, out, M, N, K, s);
+    return launch_cfg<true>(pick_config(wtype, M, N), wtype, kAQ81, W, A, nullptr, out, M, N, K, s);
 }
 
 }  // namespace ksq

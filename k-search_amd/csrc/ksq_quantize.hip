@@ -1,4 +1,4 @@
-// ksq_quantize.hip - fp32 activations -> block_q8_1 on gfx950.
+// ksq_quantize.hip - fp32 activations -> block_q8_1 (or block_q8s) on gfx950.
 //
 // Same arithmetic as quantize_row_q8_1_ref (kernelevalplus-main/include/quantize.h:165-193);
 // the reference's own device kernel (quantize.h:302-337) rounds half-even with
@@ -19,6 +19,9 @@ namespace ksq {
 constexpr int kQBlocksPerWG = 256;
 constexpr int kQPitch = 33;  // floats per staged block
 
+// Q8S = false: block_q8_1 (quantize_row_q8_1_ref); true: block_q8s (the native W8A8C8
+// operator's rules).  Both are 36-byte blocks of 9 dwords.
+template <bool Q8S>
 __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restrict__ x,
                                                             uint8_t* __restrict__ y, int64_t nblocks) {
     __shared__ float stage[kQBlocksPerWG * kQPitch];
@@ -47,7 +50,8 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restr
         float v[32];
 #pragma unroll
         for (int j = 0; j < 32; j++) v[j] = stage[t * kQPitch + j];
-        quantize_block_q8_1(v, q);
+        if constexpr (Q8S) quantize_block_q8s(v, q);
+        else quantize_block_q8_1(v, q);
     }
     __syncthreads();
     uint32_t* ostage = (uint32_t*)stage;  // 256 x 9 dwords, odd pitch: conflict free
@@ -64,12 +68,19 @@ __global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restr
     }
 }
 
-hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
+hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
     const int64_t nblocks = rows * (int64_t)(K / 32);
     if (nblocks == 0) return hipSuccess;
     const int64_t grid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
-    hipLaunchKernelGGL(quantize_q8_1_kernel, dim3((unsigned)grid), dim3(256), 0, s, x, y, nblocks);
+    if (afmt == kAQ8S)
+        hipLaunchKernelGGL(quantize_q8_1_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s, x, y, nblocks);
+    else
+        hipLaunchKernelGGL(quantize_q8_1_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s, x, y, nblocks);
     return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
+    return launch_quantize(kAQ81, x, y, rows, K, s);
 }
 
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {

@@ -14,8 +14,8 @@ PKG_ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_ROOT, "libksq.so")
 
 # enum ksq_wtype / ksq_atype / ksq_status (include/ksq_blocks.h, include/ksq.h)
-W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K = 0, 1, 2, 3
-A_F32, A_Q8_1 = 0, 1
+W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
+A_F32, A_Q8_1, A_F32_Q8S, A_Q8S = 0, 1, 2, 3
 STATUS = {0: "KSQ_OK", 1: "KSQ_ERR_NULL", 2: "KSQ_ERR_SHAPE", 3: "KSQ_ERR_ALIGN",
           4: "KSQ_ERR_TYPE", 5: "KSQ_ERR_WORKSPACE", 6: "KSQ_ERR_HIP"}
 
@@ -35,7 +35,15 @@ SIGNATURES = {
     "ksq_gemm_q8_0_q8_1": ([_P, _P, _P, _I, _I, _I], None),
     "ksq_gemm_q4_k_q8_1": ([_P, _P, _P, _I, _I, _I], None),
     "ksq_gemm_q6_k_q8_1": ([_P, _P, _P, _I, _I, _I], None),
+    "gemm_w4a32c8_q4_1_fp32_int8": ([_P, _P, _P, _I, _I, _I], None),
+    "gemm_w5a32c8_q5_0_fp32_int8": ([_P, _P, _P, _I, _I, _I], None),
+    "gemm_w5a32c8_q5_1_fp32_int8": ([_P, _P, _P, _I, _I, _I], None),
+    "ksq_gemm_q4_1_q8_1": ([_P, _P, _P, _I, _I, _I], None),
+    "ksq_gemm_q5_0_q8_1": ([_P, _P, _P, _I, _I, _I], None),
+    "ksq_gemm_q5_1_q8_1": ([_P, _P, _P, _I, _I, _I], None),
+    "gemm_w8a8c8_q8_0_q8_1": ([_P, _P, _P, _I, _I, _I], None),
     "ksq_quantize_q8_1": ([_P, _P, _I, _I, _P], _I),
+    "ksq_quantize_q8s": ([_P, _P, _I, _I, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),

@@ -2,13 +2,14 @@
 
 The table mirrors the reference's quant-type registry
 (kernelevalplus-main/core/operators/common/types.py:78-195) for the formats on
-this path, plus the two K-quant super-blocks the reference lacks.
+this path, plus the two K-quant super-blocks the reference lacks and the
+fp32-scale activation block of the native W8A8C8 operator.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass, field
 
-from ._lib import W_Q4_0, W_Q4_K, W_Q6_K, W_Q8_0
+from ._lib import W_Q4_0, W_Q4_1, W_Q4_K, W_Q5_0, W_Q5_1, W_Q6_K, W_Q8_0
 
 
 @dataclass(frozen=True)
@@ -29,6 +30,14 @@ QUANT_TYPES = {
     "block_q4_0": QuantType("block_q4_0", 18, 32, W_Q4_0, (("d", "half", 0), ("qs", "uint8[16]", 2))),
     "block_q8_0": QuantType("block_q8_0", 34, 32, W_Q8_0, (("d", "half", 0), ("qs", "int8[32]", 2))),
     "block_q8_1": QuantType("block_q8_1", 36, 32, None, (("ds", "half2", 0), ("qs", "int8[32]", 4))),
+    "block_q4_1": QuantType("block_q4_1", 20, 32, W_Q4_1,
+                            (("d", "half", 0), ("m", "half", 2), ("qs", "uint8[16]", 4))),
+    "block_q5_0": QuantType("block_q5_0", 22, 32, W_Q5_0,
+                            (("d", "half", 0), ("qh", "uint8[4]", 2), ("qs", "uint8[16]", 6))),
+    "block_q5_1": QuantType("block_q5_1", 24, 32, W_Q5_1,
+                            (("d", "half", 0), ("m", "half", 2), ("qh", "uint8[4]", 4), ("qs", "uint8[16]", 8))),
+    # activation block of the native W8A8C8 operator: fp32 scale, no sum
+    "block_q8s": QuantType("block_q8s", 36, 32, None, (("d", "float", 0), ("qs", "int8[32]", 4))),
     "block_q4_K": QuantType("block_q4_K", 144, 256, W_Q4_K,
                             (("d", "half", 0), ("dmin", "half", 2), ("scales", "uint8[12]", 4), ("qs", "uint8[128]", 16))),
     "block_q6_K": QuantType("block_q6_K", 210, 256, W_Q6_K,
@@ -36,7 +45,8 @@ QUANT_TYPES = {
 }
 
 # weight-type code -> block type name
-WTYPE_NAMES = {W_Q4_0: "block_q4_0", W_Q8_0: "block_q8_0", W_Q4_K: "block_q4_K", W_Q6_K: "block_q6_K"}
+WTYPE_NAMES = {W_Q4_0: "block_q4_0", W_Q8_0: "block_q8_0", W_Q4_K: "block_q4_K", W_Q6_K: "block_q6_K",
+               W_Q4_1: "block_q4_1", W_Q5_0: "block_q5_0", W_Q5_1: "block_q5_1"}
 
 
 def quant_type(name: str) -> QuantType:

@@ -25,6 +25,11 @@
  *                        GGML description) -> oracle decoder round trip,
  *                        integer-sum path vs dequantise-then-fp64-dot path
  *   MoE                  routing invariants, composition with the dense oracle
+ *   Q4_1 / Q5_0 / Q5_1   numpy restatement of the harness formula
+ *                        (gemm_ref.py:274-330), dequantise-then-fp64-dot,
+ *                        known-answer blocks for the nibble and qh bit order
+ *   native W8A8C8        closed-form quantiser checks (ties, tiny blocks -> d = 1,
+ *                        true division vs reciprocal), per-block composition
  */
 #include <math.h>
 #include <stdint.h>
@@ -288,13 +293,18 @@ KSQ_API void ksq_ref_gemm_w8a8(const uint8_t* A, const uint8_t* W, float* C,
     }
 }
 
-/* The same block formulas accumulated in fp64, the form of the harness oracle
- * reference_q4_0_q8_1_gemm (llm_kernel_test/reference/gemm_ref.py:100-153).
- * Used as the tolerance reference for fp32 outputs. wtype: KSQ_W_Q4_0 or KSQ_W_Q8_0. */
+static int legacy_bytes(int wtype);
+static inline int legacy_q(int wtype, const uint8_t* blk, int e);
+KSQ_API int32_t ksq_ref_sumi_legacy_q8_1(int wtype, const uint8_t* wblk, const uint8_t* ablk);
+
+/* The same block formulas accumulated in fp64, the form of the harness oracles
+ * reference_q4_0_q8_1_gemm (llm_kernel_test/reference/gemm_ref.py:100-153) and
+ * reference_q4_1_q8_1_gemm (:274-330).  Used as the tolerance reference for fp32
+ * outputs.  wtype: any 32-element block type (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1). */
 KSQ_API void ksq_ref_gemm_f64(int wtype, const uint8_t* A, const uint8_t* W, double* C,
                               int M, int N, int K, int nthreads) {
     const int nb = K / 32;
-    const int wbytes = (wtype == KSQ_W_Q4_0) ? 18 : 34;
+    const int wbytes = legacy_bytes(wtype);
     (void)nthreads;
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
@@ -308,8 +318,269 @@ KSQ_API void ksq_ref_gemm_f64(int wtype, const uint8_t* A, const uint8_t* W, dou
                 const double d_a = rd_f16(ab), s_a = rd_f16(ab + 2), d_w = rd_f16(wb);
                 if (wtype == KSQ_W_Q4_0)
                     sum += d_w * (d_a * (double)ksq_ref_sumi_q4_0_q8_1(wb, ab) - 8.0 * s_a);
-                else
+                else if (wtype == KSQ_W_Q8_0)
                     sum += d_w * d_a * (double)ksq_ref_sumi_q8_0_q8_1(wb, ab);
+                else if (wtype == KSQ_W_Q5_0)
+                    sum += d_w * (d_a * (double)ksq_ref_sumi_legacy_q8_1(wtype, wb, ab) - 16.0 * s_a);
+                else
+                    sum += d_w * d_a * (double)ksq_ref_sumi_legacy_q8_1(wtype, wb, ab) + (double)rd_f16(wb + 2) * s_a;
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q4_1 / Q5_0 / Q5_1: the other legacy GGML blocks the reference defines     */
+/* (core/operators/common/types.py:94-140, include/quant_types.h:88-95) with   */
+/* the block dots of kernels/gemm/gemm_quant_formats.cuh:119-267.              */
+/* ------------------------------------------------------------------------ */
+
+static int legacy_bytes(int wtype) {
+    switch (wtype) {
+        case KSQ_W_Q4_0: return 18;
+        case KSQ_W_Q8_0: return 34;
+        case KSQ_W_Q4_1: return 20;
+        case KSQ_W_Q5_0: return 22;
+        default: return 24;  /* KSQ_W_Q5_1 */
+    }
+}
+
+/* Unsigned quant of element e (0..31) of a Q4_1 / Q5_0 / Q5_1 block: the low 4 bits
+ * from qs (element j < 16 in the low nibble of qs[j], j >= 16 in the high nibble of
+ * qs[j-16]; gemm_ref.py:184-187, quantize.py:151-153); for the 5-bit types bit 4 is
+ * bit e of the little-endian qh word (gemm_quant_formats.cuh:180-192). */
+static inline int legacy_q(int wtype, const uint8_t* blk, int e) {
+    const int qs_off = (wtype == KSQ_W_Q4_1) ? 4 : (wtype == KSQ_W_Q5_0) ? 6 : 8;
+    const uint8_t b = blk[qs_off + (e & 15)];
+    int q = (e < 16) ? (b & 0x0F) : (b >> 4);
+    if (wtype != KSQ_W_Q4_1) {
+        const uint8_t* qh = blk + ((wtype == KSQ_W_Q5_0) ? 2 : 4);
+        const uint32_t h = (uint32_t)qh[0] | ((uint32_t)qh[1] << 8) | ((uint32_t)qh[2] << 16) | ((uint32_t)qh[3] << 24);
+        q |= (int)((h >> e) & 1u) << 4;
+    }
+    return q;
+}
+
+static void put_legacy_q(int wtype, uint8_t* blk, int e, int q) {
+    const int qs_off = (wtype == KSQ_W_Q4_1) ? 4 : (wtype == KSQ_W_Q5_0) ? 6 : 8;
+    uint8_t* b = blk + qs_off + (e & 15);
+    if (e < 16) *b = (uint8_t)((*b & 0xF0) | (q & 0x0F));
+    else *b = (uint8_t)((*b & 0x0F) | ((q & 0x0F) << 4));
+    if (wtype != KSQ_W_Q4_1) {
+        uint8_t* qh = blk + ((wtype == KSQ_W_Q5_0) ? 2 : 4);
+        if (q & 0x10) qh[e >> 3] |= (uint8_t)(1u << (e & 7));
+        else qh[e >> 3] &= (uint8_t)~(1u << (e & 7));
+    }
+}
+
+/* quantize_to_q4_1 (llm_kernel_test/reference/quantize.py:105-153), per block of 32:
+ * lo = min, hi = max; scale = (hi - lo) / 15 in fp32, or 1.0 when hi == lo;
+ * q = clip(round_half_even((x - lo) / scale), 0, 15) with the fp32 scale;
+ * d = half(scale), m = half(lo).  (Test-data encoder: weights reach the GEMM
+ * already quantised.) */
+KSQ_API void ksq_ref_quantize_row_q4_1(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK4_1;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * 32;
+        uint8_t* blk = y + i * 20;
+        float lo = xs[0], hi = xs[0];
+        for (int j = 1; j < 32; j++) { lo = xs[j] < lo ? xs[j] : lo; hi = xs[j] > hi ? xs[j] : hi; }
+        const float scale = (hi > lo) ? (hi - lo) / 15.0f : 1.0f;
+        wr_f16(blk, scale);
+        wr_f16(blk + 2, lo);
+        memset(blk + 4, 0, 16);
+        for (int j = 0; j < 32; j++) {
+            float q = rintf((xs[j] - lo) / scale);   /* numpy.round: half to even */
+            q = q < 0.0f ? 0.0f : (q > 15.0f ? 15.0f : q);
+            put_legacy_q(KSQ_W_Q4_1, blk, j, (int)q);
+        }
+    }
+}
+
+/* Q5_0 / Q5_1 test-data encoders.  The reference has no quantiser for these
+ * blocks; these restate the published GGML ones (llama.cpp ggml-quants.c
+ * quantize_row_q5_0_ref / quantize_row_q5_1_ref; llama.cpp is not vendored
+ * and no version is pinned):
+ *   Q5_0: v = the element of largest magnitude, d = v / -16, id = 1/d,
+ *         q = min(31, (int8)(x * id + 16.5))
+ *   Q5_1: d = (max - min) / 31, id = 1/d, m = min, q = (uint8)((x - min) * id + 0.5) */
+KSQ_API void ksq_ref_quantize_row_q5_0(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK5_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * 32;
+        uint8_t* blk = y + i * 22;
+        float amax = 0.0f, vmax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            if (amax < fabsf(xs[j])) { amax = fabsf(xs[j]); vmax = xs[j]; }
+        }
+        const float d = vmax / -16.0f;
+        const float id = d ? 1.0f / d : 0.0f;
+        wr_f16(blk, d);
+        memset(blk + 2, 0, 20);
+        for (int j = 0; j < 32; j++) {
+            int q = (int)(int8_t)(xs[j] * id + 16.5f);
+            q = q > 31 ? 31 : q;
+            put_legacy_q(KSQ_W_Q5_0, blk, j, q);
+        }
+    }
+}
+
+KSQ_API void ksq_ref_quantize_row_q5_1(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK5_1;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * 32;
+        uint8_t* blk = y + i * 24;
+        float lo = xs[0], hi = xs[0];
+        for (int j = 1; j < 32; j++) { lo = xs[j] < lo ? xs[j] : lo; hi = xs[j] > hi ? xs[j] : hi; }
+        const float d = (hi - lo) / 31.0f;
+        const float id = d ? 1.0f / d : 0.0f;
+        wr_f16(blk, d);
+        wr_f16(blk + 2, lo);
+        memset(blk + 4, 0, 20);
+        for (int j = 0; j < 32; j++) put_legacy_q(KSQ_W_Q5_1, blk, j, (int)(uint8_t)((xs[j] - lo) * id + 0.5f));
+    }
+}
+
+/* Dequantisation: Q4_1 / Q5_1 value = q * d + m (gemm_ref.py:189-190), Q5_0 value =
+ * (q - 16) * d (gemm_quant_formats.cuh:158-160). */
+KSQ_API void ksq_ref_dequantize_row_legacy(int wtype, const uint8_t* x, float* y, int64_t k) {
+    const int64_t nb = k / 32;
+    const int bytes = legacy_bytes(wtype);
+    for (int64_t i = 0; i < nb; i++) {
+        const uint8_t* blk = x + i * bytes;
+        const float d = rd_f16(blk);
+        const float m = (wtype == KSQ_W_Q5_0) ? 0.0f : rd_f16(blk + 2);
+        for (int e = 0; e < 32; e++) {
+            const int q = legacy_q(wtype, blk, e);
+            y[i * 32 + e] = (wtype == KSQ_W_Q5_0) ? (float)(q - 16) * d : d * (float)q + m;
+        }
+    }
+}
+
+/* Integer dot of the unsigned quants with the Q8_1 block (the sumi of
+ * gemm_quant_formats.cuh:126-137 / 170-200 / 230-257). */
+KSQ_API int32_t ksq_ref_sumi_legacy_q8_1(int wtype, const uint8_t* wblk, const uint8_t* ablk) {
+    const int8_t* qa = (const int8_t*)(ablk + 4);
+    int32_t s = 0;
+    for (int e = 0; e < 32; e++) s += (int32_t)qa[e] * legacy_q(wtype, wblk, e);
+    return s;
+}
+
+/* One block's contribution in fp32, in the reference's expression order:
+ *   Q4_1  d4*d8*sumi + m4*s8        (gemm_quant_formats.cuh:119-149)
+ *   Q5_0  d5*(d8*sumi - 16*s8)      (:162-208)
+ *   Q5_1  d5*d8*sumi + m5*s8        (:222-267)
+ * The reference divides the m*s8 term of Q4_1 and Q5_1 by 4 (:148, :266), a
+ * leftover of llama.cpp's per-quarter calling convention; its own harness oracles
+ * (llm_kernel_test/reference/gemm_ref.py:156-199 dequantise-then-matmul and
+ * :274-330 d_w*d_a*sumi + m_w*s_a) and the dequantised values q*d + m both give the
+ * term without the division, which is what is restated here. */
+static inline float dot_legacy(int wtype, const uint8_t* wb, const uint8_t* ab) {
+    const float d_w = rd_f16(wb), d_a = rd_f16(ab), s_a = rd_f16(ab + 2);
+    const int32_t sumi = ksq_ref_sumi_legacy_q8_1(wtype, wb, ab);
+    if (wtype == KSQ_W_Q5_0) return d_w * (d_a * (float)sumi - 16.0f * s_a);
+    return d_w * d_a * (float)sumi + rd_f16(wb + 2) * s_a;
+}
+
+/* gemm_quant_kernel (gemm_quant_formats.cuh:313-333): fp32 sum of the block dots in
+ * block order.  wtype: KSQ_W_Q4_1, KSQ_W_Q5_0 or KSQ_W_Q5_1. */
+KSQ_API void ksq_ref_gemm_legacy(int wtype, const uint8_t* A, const uint8_t* W, float* C,
+                                 int M, int N, int K, int nthreads) {
+    const int nb = K / 32, wbytes = legacy_bytes(wtype);
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++)
+                sum += dot_legacy(wtype, W + ((int64_t)j * nb + b) * wbytes, A + ((int64_t)i * nb + b) * 36);
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Native W8A8C8 operator (core/operators/quant_gemm/variants/deepseek_v3/   */
+/* w8a8c8_q8_0_q8_1/kernel.cu:37-130): Q8_0 weights, fp32 activations        */
+/* re-quantised per 32-element block with an fp32 scale.                     */
+/* ------------------------------------------------------------------------ */
+
+/* (int) of a float as the GPU converts it (the reference operator is device code):
+ * NaN -> 0, out-of-range values saturate. */
+static inline int32_t cvt_i32_device(float r) {
+    if (r != r) return 0;
+    if (r >= 2147483648.0f) return INT32_MAX;
+    if (r <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)r;
+}
+
+/* kernel.cu:66-93 for one block: a_max = fmaxf(a_max, fabsf(a)) from 0,
+ * d = a_max / 127.0f, d < 1e-6f -> 1.0f, q = clamp((int)roundf(a / d), -128, 127)
+ * (a true division).  Writes block_q8s {float d; int8 qs[32]}. */
+static void quantize_block_q8s(const float* xs, uint8_t* blk) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(xs[j]));
+    float d = amax / 127.0f;
+    if (d < 1e-6f) d = 1.0f;
+    memcpy(blk, &d, 4);
+    for (int j = 0; j < 32; j++) {
+        int32_t q = cvt_i32_device(roundf(xs[j] / d));
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        blk[4 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+KSQ_API void ksq_ref_quantize_row_q8s(const float* x, uint8_t* y, int64_t k) {
+    for (int64_t i = 0; i < k / 32; i++) quantize_block_q8s(x + i * 32, y + i * 36);
+}
+
+/* The whole operator, kernel.cu:46-117: per output, blocks in order, each activation
+ * block re-quantised as above, sum += d_w * d_a * (float)sumi in fp32
+ * (vec_dot_q8_0_q8_1_impl, :23-35). */
+KSQ_API void ksq_ref_gemm_w8a8c8(const float* X, const uint8_t* W, float* C, int M, int N, int K, int nthreads) {
+    const int nb = K / 32;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            uint8_t ab[36];
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * 34;
+                quantize_block_q8s(X + (int64_t)i * K + 32 * b, ab);
+                float d_a;
+                memcpy(&d_a, ab, 4);
+                const float d_w = rd_f16(wb);
+                sum += d_w * d_a * (float)ksq_ref_sumi_q8_0_q8_1(wb, ab);
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* The same products from pre-quantised block_q8s activations, accumulated in fp64
+ * (tolerance reference). */
+KSQ_API void ksq_ref_gemm_q8_0_q8s_f64(const uint8_t* A, const uint8_t* W, double* C, int M, int N, int K,
+                                       int nthreads) {
+    const int nb = K / 32;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            double sum = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * 34;
+                float d_a;
+                memcpy(&d_a, ab, 4);
+                sum += (double)rd_f16(wb) * (double)d_a * (double)ksq_ref_sumi_q8_0_q8_1(wb, ab);
             }
             C[(int64_t)i * N + j] = sum;
         }
@@ -501,13 +772,14 @@ KSQ_API void ksq_ref_block_sumi(int wtype, const uint8_t* A, const uint8_t* W, i
     const int nb = K / 32;
     for (int i = 0; i < M; i++) {
         for (int j = 0; j < N; j++) {
-            if (wtype == KSQ_W_Q4_0 || wtype == KSQ_W_Q8_0) {
-                const int wbytes = (wtype == KSQ_W_Q4_0) ? 18 : 34;
+            if (wtype != KSQ_W_Q4_K && wtype != KSQ_W_Q6_K) {
+                const int wbytes = legacy_bytes(wtype);
                 for (int b = 0; b < nb; b++) {
                     const uint8_t* ab = A + ((int64_t)i * nb + b) * 36;
                     const uint8_t* wb = W + ((int64_t)j * nb + b) * wbytes;
                     out[((int64_t)i * N + j) * nb + b] = (wtype == KSQ_W_Q4_0) ? ksq_ref_sumi_q4_0_q8_1(wb, ab)
-                                                                              : ksq_ref_sumi_q8_0_q8_1(wb, ab);
+                                                       : (wtype == KSQ_W_Q8_0) ? ksq_ref_sumi_q8_0_q8_1(wb, ab)
+                                                                               : ksq_ref_sumi_legacy_q8_1(wtype, wb, ab);
                 }
             } else if (wtype == KSQ_W_Q4_K) {
                 const int nsb = K / 256;

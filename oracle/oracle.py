@@ -6,7 +6,8 @@ never imports this module.
 
 All buffers are numpy arrays; quantised tensors are flat uint8 byte arrays in
 the reference layouts (block_q4_0 18 B, block_q8_0 34 B, block_q8_1 36 B,
-block_q4_K 144 B, block_q6_K 210 B).
+block_q4_1 20 B, block_q5_0 22 B, block_q5_1 24 B, block_q4_K 144 B, block_q6_K
+210 B) or the native W8A8C8 operator's activation block (block_q8s 36 B).
 """
 from __future__ import annotations
 
@@ -19,9 +20,12 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libksq_oracle.so")
 
-W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K = 0, 1, 2, 3
-WBYTES = {W_Q4_0: 18, W_Q8_0: 34, W_Q4_K: 144, W_Q6_K: 210}
-WELEMS = {W_Q4_0: 32, W_Q8_0: 32, W_Q4_K: 256, W_Q6_K: 256}
+W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
+WBYTES = {W_Q4_0: 18, W_Q8_0: 34, W_Q4_K: 144, W_Q6_K: 210, W_Q4_1: 20, W_Q5_0: 22, W_Q5_1: 24}
+WELEMS = {W_Q4_0: 32, W_Q8_0: 32, W_Q4_K: 256, W_Q6_K: 256, W_Q4_1: 32, W_Q5_0: 32, W_Q5_1: 32}
+LEGACY = (W_Q4_1, W_Q5_0, W_Q5_1)
+NAMES = {W_Q4_0: "q4_0", W_Q8_0: "q8_0", W_Q4_K: "q4_K", W_Q6_K: "q6_K", W_Q4_1: "q4_1", W_Q5_0: "q5_0",
+         W_Q5_1: "q5_1"}
 
 _lib = None
 
@@ -44,6 +48,7 @@ def lib() -> ctypes.CDLL:
         L.ksq_ref_f32_to_f16.argtypes = [ctypes.c_float]
         L.ksq_ref_f32_to_f16.restype = ctypes.c_uint16
         for name in ("quantize_row_q8_1", "quantize_row_q8_0", "quantize_row_q4_0",
+                     "quantize_row_q4_1", "quantize_row_q5_0", "quantize_row_q5_1", "quantize_row_q8s",
                      "dequantize_row_q4_0", "dequantize_row_q8_0", "dequantize_row_q8_1",
                      "dequantize_row_q4_K", "dequantize_row_q6_K"):
             f = getattr(L, "ksq_ref_" + name)
@@ -53,6 +58,12 @@ def lib() -> ctypes.CDLL:
             f = getattr(L, "ksq_ref_" + name)
             f.argtypes = [P, P]
             f.restype = ctypes.c_int32
+        L.ksq_ref_dequantize_row_legacy.argtypes = [i32, P, P, i64]
+        L.ksq_ref_sumi_legacy_q8_1.argtypes = [i32, P, P]
+        L.ksq_ref_sumi_legacy_q8_1.restype = ctypes.c_int32
+        L.ksq_ref_gemm_legacy.argtypes = [i32, P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_w8a8c8.argtypes = [P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_q8_0_q8s_f64.argtypes = [P, P, P, i32, i32, i32, i32]
         L.ksq_ref_q4_K_scale_min.argtypes = [i32, P, P, P]
         L.ksq_ref_sumi_q4_K_q8_1.argtypes = [P, i32, P]
         L.ksq_ref_sumi_q4_K_q8_1.restype = ctypes.c_int32
@@ -113,12 +124,66 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
     return y
 
 
+def _quantize(name: str, x: np.ndarray, bytes_per_block: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, bytes_per_block), dtype=np.uint8)
+    getattr(lib(), "ksq_ref_quantize_row_" + name)(_p(x), _p(y), M * K)
+    return y
+
+
+def quantize_q4_1(x: np.ndarray) -> np.ndarray:
+    """fp32 [N, K] -> block_q4_1 bytes (quantize_to_q4_1 arithmetic)."""
+    return _quantize("q4_1", x, 20)
+
+
+def quantize_q5_0(x: np.ndarray) -> np.ndarray:
+    return _quantize("q5_0", x, 22)
+
+
+def quantize_q5_1(x: np.ndarray) -> np.ndarray:
+    return _quantize("q5_1", x, 24)
+
+
+def quantize_q8s(x: np.ndarray) -> np.ndarray:
+    """fp32 [M, K] -> block_q8s bytes [M, K/32, 36] (the native W8A8C8 operator's rules)."""
+    return _quantize("q8s", x, 36)
+
+
 def dequantize(wtype_or_name, q: np.ndarray, rows: int, K: int) -> np.ndarray:
-    name = {W_Q4_0: "q4_0", W_Q8_0: "q8_0", W_Q4_K: "q4_K", W_Q6_K: "q6_K"}.get(wtype_or_name, wtype_or_name)
+    by_name = {v: k for k, v in NAMES.items()}
+    wt = by_name.get(wtype_or_name, wtype_or_name)
     q = np.ascontiguousarray(q, dtype=np.uint8)
     y = np.empty((rows, K), dtype=np.float32)
-    getattr(lib(), "ksq_ref_dequantize_row_" + name)(_p(q), _p(y), rows * K)
+    if wt in LEGACY:
+        lib().ksq_ref_dequantize_row_legacy(wt, _p(q), _p(y), rows * K)
+    else:
+        getattr(lib(), "ksq_ref_dequantize_row_" + NAMES.get(wt, wt))(_p(q), _p(y), rows * K)
     return y
+
+
+def sumi_legacy(wtype: int, wblk: np.ndarray, ablk: np.ndarray) -> int:
+    w = np.ascontiguousarray(wblk, dtype=np.uint8)
+    a = np.ascontiguousarray(ablk, dtype=np.uint8)
+    return lib().ksq_ref_sumi_legacy_q8_1(wtype, _p(w), _p(a))
+
+
+def gemm_w8a8c8(x: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 1) -> np.ndarray:
+    """The native W8A8C8 operator on fp32 activations (fp32 accumulation order)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float32)
+    lib().ksq_ref_gemm_w8a8c8(_p(x), _p(w), _p(C), M, N, K, nthreads)
+    return C
+
+
+def gemm_q8s_f64(a_q8s: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 0) -> np.ndarray:
+    """Q8_0 weights x block_q8s activations, fp64 accumulation (tolerance reference)."""
+    a = np.ascontiguousarray(a_q8s, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float64)
+    lib().ksq_ref_gemm_q8_0_q8s_f64(_p(a), _p(w), _p(C), M, N, K, nthreads or max_threads())
+    return C
 
 
 def gemm(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 1) -> np.ndarray:
@@ -130,6 +195,8 @@ def gemm(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: int, 
         lib().ksq_ref_gemm_w4a8(_p(a), _p(w), _p(C), M, N, K, nthreads)
     elif wtype == W_Q8_0:
         lib().ksq_ref_gemm_w8a8(_p(a), _p(w), _p(C), M, N, K, nthreads)
+    elif wtype in LEGACY:
+        lib().ksq_ref_gemm_legacy(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
     else:
         lib().ksq_ref_gemm_kquant(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
     return C
@@ -141,7 +208,7 @@ def gemm_f64(wtype: int, a_q8_1: np.ndarray, w: np.ndarray, M: int, N: int, K: i
     w = np.ascontiguousarray(w, dtype=np.uint8)
     C = np.empty((M, N), dtype=np.float64)
     nthreads = nthreads or max_threads()
-    if wtype in (W_Q4_0, W_Q8_0):
+    if wtype in (W_Q4_0, W_Q8_0) + LEGACY:
         lib().ksq_ref_gemm_f64(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)
     else:
         lib().ksq_ref_gemm_kquant_f64(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads)

@@ -3,7 +3,8 @@
     python tests/golden/make_golden.py
 
 Inputs come from a fixed seed (numpy PCG64); expected outputs are the oracle's
-(quantize_row_q8_1_ref, the integer block dots, gemm_w4a8/w8a8_reference order).
+(quantize_row_q8_1_ref, the integer block dots, gemm_w4a8/w8a8_reference order,
+the Q4_1/Q5_0/Q5_1 block formulas and the native W8A8C8 operator).
 The fixtures pin the oracle against regressions and travel to the GPU box,
 where the GPU path is compared against them without rebuilding anything.
 """
@@ -54,6 +55,28 @@ def main():
     a = oracle.quantize_q8_1(x)
     np.savez(os.path.join(HERE, "moe_16x4.npz"), logits=logits, ids=ids, wts=wts, w=W, x=x, a_q8_1=a,
              out64=oracle.moe_q4_0_f64(W, a, ids, wts, T, N, K))
+
+    g = np.random.default_rng(20240602)
+    M, N, K = 3, 5, 256         # Q4_1 / Q5_0 / Q5_1 and the native W8A8C8 operator
+    x = synth.activations(g, M, K)
+    x[2, 0:6] = [127.0, 2.5, -2.5, 0.5, -126.5, 0.0]   # ties under both quantisers (d = 1 exactly)
+    x[2, 6:32] = 0.0
+    x[1, 32:64] *= 1e-5                                 # native rule: d < 1e-6 -> d = 1
+    a = oracle.quantize_q8_1(x)
+    out = {"x": x, "a_q8_1": a}
+    for wt, name in ((4, "q4_1"), (5, "q5_0"), (6, "q5_1")):
+        w = synth.weights(wt, g, N, K)
+        out["w_" + name] = w
+        out["sumi_" + name] = oracle.block_sumi(wt, a, w, M, N, K)
+        out["c_" + name] = oracle.gemm(wt, a, w, M, N, K)
+        out["c64_" + name] = oracle.gemm_f64(wt, a, w, M, N, K)
+    w8 = synth.weights(1, g, N, K)
+    a8s = oracle.quantize_q8s(x)
+    out.update(w_q8_0=w8, a_q8s=a8s, sumi_q8s=oracle.block_sumi(1, a8s, w8, M, N, K),
+               c_w8a8c8=oracle.gemm_w8a8c8(x, w8, M, N, K), c64_w8a8c8=oracle.gemm_q8s_f64(a8s, w8, M, N, K))
+    wf = g.standard_normal((N, K), dtype=np.float32) * np.float32(0.05)
+    out.update(wf=wf, w_q4_1_from_fp32=oracle.quantize_q4_1(wf))    # the harness' quantize_to_q4_1 path
+    np.savez(os.path.join(HERE, "legacy_q8s_3x5x256.npz"), **out)
     print("fixtures written to", HERE)
 
 

@@ -107,3 +107,83 @@ def encode_q6_K(d, sc, q) -> np.ndarray:
     b[192:208] = np.asarray(sc, dtype=np.int8).view(np.uint8)
     b[208:210] = np.array([d], dtype=np.float16).view(np.uint8)
     return b
+
+
+# ---- Q4_1 / Q5_0 / Q5_1 (layouts of core/operators/common/types.py:94-140) ----
+
+LEGACY_LAYOUT = {  # wtype: (bytes, offset of m or None, offset of qh or None, offset of qs)
+    4: (20, 2, None, 4),
+    5: (22, None, 2, 6),
+    6: (24, 2, 4, 8),
+}
+
+
+def unpack_legacy(wtype: int, w: np.ndarray):
+    """[N, nb, bytes] -> (d f64, m f64 or None, q int64 [N, nb, 32] unsigned quants).
+    qh bits via numpy.unpackbits (little bit order), nibbles by shifts."""
+    nbytes, mo, ho, qo = LEGACY_LAYOUT[wtype]
+    d = f16(w[..., 0:2])
+    m = f16(w[..., mo:mo + 2]) if mo is not None else None
+    qs = w[..., qo:qo + 16].astype(np.int64)
+    q = np.concatenate([qs & 0x0F, qs >> 4], axis=-1)
+    if ho is not None:
+        bits = np.unpackbits(np.ascontiguousarray(w[..., ho:ho + 4]), axis=-1, bitorder="little").astype(np.int64)
+        q = q + 16 * bits
+    return d, m, q
+
+
+def encode_legacy(wtype: int, d: float, m, q) -> np.ndarray:
+    """One block from chosen fields (q: 32 unsigned quants)."""
+    nbytes, mo, ho, qo = LEGACY_LAYOUT[wtype]
+    q = np.asarray(q, dtype=np.int64)
+    b = np.zeros(nbytes, dtype=np.uint8)
+    b[0:2] = np.array([d], dtype=np.float16).view(np.uint8)
+    if mo is not None:
+        b[mo:mo + 2] = np.array([m], dtype=np.float16).view(np.uint8)
+    b[qo:qo + 16] = ((q[:16] & 0x0F) | ((q[16:] & 0x0F) << 4)).astype(np.uint8)
+    if ho is not None:
+        h = int(sum(((int(q[e]) >> 4) & 1) << e for e in range(32)))
+        b[ho:ho + 4] = np.array([h], dtype="<u4").view(np.uint8)
+    return b
+
+
+def gemm_legacy_f64(wtype: int, a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """Harness formula in fp64 (gemm_ref.py:274-330 for Q4_1; the same with the 5-bit
+    quants for Q5_1; d_w*(d_a*sumi - 16*s_a) for Q5_0)."""
+    dw, mw, qw = unpack_legacy(wtype, w)
+    da, sa, qa = unpack_q8_1(a)
+    S = np.einsum("mbk,nbk->mnb", qa, qw).astype(np.float64)
+    if wtype == 5:
+        return np.einsum("nb,mnb->mn", dw, da[:, None, :] * S - 16.0 * sa[:, None, :])
+    return np.einsum("nb,mb,mnb->mn", dw, da, S) + np.einsum("nb,mb->mn", mw, sa)
+
+
+def quantize_q4_1(x: np.ndarray) -> np.ndarray:
+    """quantize_to_q4_1 (llm_kernel_test/reference/quantize.py:105-153) vectorised."""
+    x = np.asarray(x, dtype=np.float32)
+    N, K = x.shape
+    xb = x.reshape(N, K // 32, 32)
+    lo, hi = xb.min(axis=-1), xb.max(axis=-1)
+    scale = np.where(hi > lo, (hi - lo) / np.float32(15.0), np.float32(1.0)).astype(np.float32)
+    q = np.clip(np.round((xb - lo[..., None]) / scale[..., None]), 0, 15).astype(np.int64)
+    out = np.zeros((N, K // 32, 20), dtype=np.uint8)
+    out[..., 0:2] = scale.astype(np.float16)[..., None].view(np.uint8)
+    out[..., 2:4] = lo.astype(np.float16)[..., None].view(np.uint8)
+    out[..., 4:] = (q[..., :16] | (q[..., 16:] << 4)).astype(np.uint8)
+    return out
+
+
+def quantize_q8s(x: np.ndarray) -> np.ndarray:
+    """Native W8A8C8 activation quantiser (variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93):
+    d = max|x| / 127 in fp32 (1 when below 1e-6), q = half-away(x / d) by true fp32 division."""
+    x = np.asarray(x, dtype=np.float32)
+    M, K = x.shape
+    xb = x.reshape(M, K // 32, 32)
+    d = (np.abs(xb).max(axis=-1) / np.float32(127.0)).astype(np.float32)
+    d = np.where(d < np.float32(1e-6), np.float32(1.0), d).astype(np.float32)
+    v = (xb / d[..., None]).astype(np.float32).astype(np.float64)
+    q = np.clip(np.sign(v) * np.floor(np.abs(v) + 0.5), -128, 127).astype(np.int8)
+    out = np.empty((M, K // 32, 36), dtype=np.uint8)
+    out[..., 0:4] = d[..., None].view(np.uint8)
+    out[..., 4:] = q.view(np.uint8)
+    return out

@@ -93,7 +93,10 @@ def test_golden_fixture_on_gpu(dev):
 
 
 # ------------------------------------------------------------------ integer block dots
-@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+ALL_WTYPES = [0, 1, 2, 3, 4, 5, 6]      # Q4_0 Q8_0 Q4_K Q6_K Q4_1 Q5_0 Q5_1
+
+
+@pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_block_sumi_dot4_bit_exact(dev, oracle, wtype):
     from ksq import ops, synth
     g = np.random.default_rng(200 + wtype)
@@ -104,7 +107,7 @@ def test_block_sumi_dot4_bit_exact(dev, oracle, wtype):
     assert np.array_equal(got, oracle.block_sumi(wtype, a, w, M, N, K))
 
 
-@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+@pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_block_sumi_mfma_bit_exact(dev, oracle, wtype):
     from ksq import ops, synth
     g = np.random.default_rng(300 + wtype)
@@ -143,7 +146,7 @@ def test_q8_0_config1(dev, oracle, M):
     assert _rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("wtype,path", [(0, 1), (0, 2), (1, 1), (1, 2), (2, 1), (2, 2), (3, 1), (3, 2)])
+@pytest.mark.parametrize("wtype,path", [(w, p) for w in ALL_WTYPES for p in (1, 2)])
 def test_paths_agree_small(dev, oracle, wtype, path):
     """Both the v_dot4 and the MFMA path on ragged shapes."""
     from ksq import synth
@@ -185,7 +188,7 @@ def test_kquant_config3_sampled(dev, oracle, wtype):
     assert _rel_err(y[rows], ref) <= TOL
 
 
-@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+@pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_prequantized_entry_matches_fp32_entry(dev, oracle, wtype):
     """ksq_gemm_*_q8_1 on oracle-quantised activations == the fp32 entry (same bits in)."""
     from ksq import synth
@@ -304,9 +307,9 @@ def test_moe_config4_sampled(dev, oracle):
 
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4])
-@pytest.mark.parametrize("wtype", [0, 1, 2, 3])
+@pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_mfma_tile_configs(dev, oracle, cfg, wtype):
-    """Every MFMA tile configuration (K step 4 is Q4_0/Q8_0 only; K-quants fall back to 64x64)."""
+    """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile)."""
     from ksq import _lib, synth
     g = np.random.default_rng(1500 + 10 * cfg + wtype)
     M, N, K = 150, 136, 512
@@ -319,3 +322,131 @@ def test_mfma_tile_configs(dev, oracle, cfg, wtype):
         _lib.lib().ksq_set_mmq_config(0)
     ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
     assert _rel_err(y, ref) <= TOL
+
+
+# ------------------------------------------------------------------ Q4_1 / Q5_0 / Q5_1
+def test_golden_fixture_legacy_on_gpu(dev):
+    import torch
+    from ksq import ops
+    z = np.load(os.path.join(GOLDEN, "legacy_q8s_3x5x256.npz"), allow_pickle=False)
+    M, K = z["x"].shape
+    for wt, name in ((4, "q4_1"), (5, "q5_0"), (6, "q5_1")):
+        w = z["w_" + name]
+        N = w.shape[0]
+        for mfma in (False, True):
+            s = ops.block_sumi(wt, _t(w, dev), _t(z["a_q8_1"], dev), M, N, K, mfma=mfma).cpu().numpy()
+            assert np.array_equal(s, z["sumi_" + name]), (name, mfma)
+        for path in (1, 2):
+            y = _gpu_gemm(dev, wt, w, z["x"], M, N, K, path=path)
+            assert _rel_err(y, z["c64_" + name]) <= TOL, (name, path)
+    q = ops.quantize_q8s(_t(z["x"], dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(q.cpu().numpy(), z["a_q8s"])
+
+
+ENTRY_OF = {4: "gemm_w4a32c8_q4_1_fp32_int8", 5: "gemm_w5a32c8_q5_0_fp32_int8", 6: "gemm_w5a32c8_q5_1_fp32_int8"}
+
+
+@pytest.mark.parametrize("wtype", [4, 5, 6])
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 64, 512])
+def test_legacy_definition_shapes(dev, oracle, wtype, M):
+    """The Q4_1 definitions' shape family (qwen3_4b att_out N = K = 2560; batch_1 .. batch_512) through
+    the definition entry point, sampled rows against the fp64 oracle."""
+    import torch
+    from ksq import forward, synth
+    g = np.random.default_rng(1600 + 10 * wtype + M)
+    N, K = 2560, 2560
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    y = forward(_t(w, dev), _t(x, dev), M, N, K, entry=ENTRY_OF[wtype])
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    rows = np.arange(M) if M <= 8 else np.sort(g.choice(M, 8, replace=False))
+    ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x[rows]), w, len(rows), N, K)
+    assert _rel_err(y[rows], ref) <= TOL
+
+
+def test_q4_1_harness_flow_nmse(dev, oracle):
+    """The harness flow for a w4a32c8_q4_1 definition: fp32 weights -> quantize_to_q4_1, then the
+    NMSE gate against dequantise-then-fp32-matmul (reference_q4_1_fp32_gemm, gemm_ref.py:156-199)."""
+    import torch
+    from ksq import forward
+    g = np.random.default_rng(1700)
+    M, N, K = 4, 4096, 4096
+    wf = g.standard_normal((N, K), dtype=np.float32)
+    x = g.standard_normal((M, K), dtype=np.float32)
+    w = oracle.quantize_q4_1(wf)
+    y = forward(_t(w, dev), _t(x, dev), M, N, K, entry="gemm_w4a32c8_q4_1_fp32_int8")
+    torch.cuda.synchronize()
+    ref = x.astype(np.float64) @ oracle.dequantize(4, w.reshape(N, -1), N, K).astype(np.float64).T
+    nmse = np.mean((y.cpu().numpy() - ref) ** 2) / np.mean(ref ** 2)
+    assert nmse < 0.05
+
+
+@pytest.mark.parametrize("wtype", [4, 5, 6])
+def test_moe_legacy_types(dev, oracle, wtype):
+    """The grouped MoE GEMM with Q4_1 / Q5_0 / Q5_1 experts: composition of the dense oracle."""
+    T, E, N, K, top_k = 48, 4, 96, 512, 2
+    W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, top_k, False, 1800 + wtype, wtype=wtype)
+    a = oracle.quantize_q8_1(x)
+    dense = np.stack([oracle.gemm_f64(wtype, a, W[e], T, N, K) for e in range(E)])
+    ref = sum(wts[:, s, None] * dense[ids[:, s], np.arange(T)] for s in range(top_k))
+    assert _rel_err(y, ref) <= TOL
+
+
+# ------------------------------------------------------------------ native W8A8C8 operator
+def test_quantize_q8s_bit_exact(dev, oracle):
+    import torch
+    from ksq import ops
+    g = np.random.default_rng(1900)
+    for M, K in ((1, 7168), (5, 1024), (513, 96)):
+        x = g.standard_normal((M, K), dtype=np.float32)
+        if M == 5:
+            x[0, :32] = 0.0
+            x[1, :6] = [127.0, 2.5, -2.5, 0.5, -126.5, 3.49999976]
+            x[1, 6:32] = 0.0
+            x[2, 32:64] *= 1e-5
+            x[3, 64:96] *= 1e4
+        q = ops.quantize_q8s(_t(x, dev))
+        torch.cuda.synchronize()
+        assert np.array_equal(q.cpu().numpy(), oracle.quantize_q8s(x)), (M, K)
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 512])
+def test_w8a8c8_native_spec_configs(dev, oracle, M):
+    """spec.json test_configs of the native operator (M = 1..8, 512; N = K = 7168 defaults) through its
+    own symbol; sampled rows against the fp64 oracle and the operator-order fp32 oracle."""
+    import torch
+    from ksq import forward, synth
+    g = np.random.default_rng(2000 + M)
+    N, K = 7168, 7168
+    w = synth.weights(1, g, N, K)
+    x = synth.activations(g, M, K)
+    y = forward(_t(w, dev), _t(x, dev), M, N, K, entry="gemm_w8a8c8_q8_0_q8_1")
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    rows = np.arange(M) if M <= 8 else np.sort(g.choice(M, 6, replace=False))
+    a = oracle.quantize_q8s(x[rows])
+    ref = oracle.gemm_q8s_f64(a, w, len(rows), N, K)
+    assert _rel_err(y[rows], ref) <= TOL
+    ref32 = oracle.gemm_w8a8c8(x[rows], w, len(rows), N, K, nthreads=oracle.max_threads())
+    assert _rel_err(y[rows], ref32) <= TOL
+
+
+@pytest.mark.parametrize("path", [1, 2])
+def test_w8a8c8_block_dots_and_paths(dev, oracle, path):
+    """Integer block dots of the q8s activations are bit-exact on both engines; outputs of both paths."""
+    import torch
+    from ksq import _lib, ops, synth
+    g = np.random.default_rng(2100 + path)
+    M, N, K = 70, 96, 512
+    w = synth.weights(1, g, N, K)
+    x = synth.activations(g, M, K)
+    x[3, :64] *= 1e-6
+    a = oracle.quantize_q8s(x)
+    s = ops.block_sumi(1, _t(w, dev), _t(a, dev), M, N, K, mfma=(path == 2)).cpu().numpy()
+    assert np.array_equal(s, oracle.block_sumi(1, a, w, M, N, K))
+    y = _gpu_gemm(dev, 1, w, x, M, N, K, atype=_lib.A_F32_Q8S, path=path)
+    assert _rel_err(y, oracle.gemm_q8s_f64(a, w, M, N, K)) <= TOL
+    yq = _gpu_gemm(dev, 1, w, a, M, N, K, atype=_lib.A_Q8S, path=path)
+    assert np.array_equal(y, yq)

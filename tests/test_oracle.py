@@ -168,6 +168,27 @@ def test_golden_fixtures(oracle):
     assert np.array_equal(oracle.gemm(1, a, z["w_q8_0"], M, N, K), z["c_q8_0"])
 
 
+def test_golden_fixtures_legacy_q8s(oracle):
+    z = np.load(os.path.join(GOLDEN, "legacy_q8s_3x5x256.npz"), allow_pickle=False)
+    x = z["x"]
+    M, K = x.shape
+    a = oracle.quantize_q8_1(x)
+    assert np.array_equal(a, z["a_q8_1"])
+    for wt, name in ((4, "q4_1"), (5, "q5_0"), (6, "q5_1")):
+        w = z["w_" + name]
+        N = w.shape[0]
+        assert np.array_equal(oracle.block_sumi(wt, a, w, M, N, K), z["sumi_" + name])
+        assert np.array_equal(oracle.gemm(wt, a, w, M, N, K), z["c_" + name])
+        assert np.allclose(oracle.gemm_f64(wt, a, w, M, N, K), npref.gemm_legacy_f64(wt, a, w), rtol=1e-12)
+    w8 = z["w_q8_0"]
+    N = w8.shape[0]
+    assert np.array_equal(oracle.quantize_q8s(x), z["a_q8s"])
+    assert np.array_equal(npref.quantize_q8s(x), z["a_q8s"])
+    assert np.array_equal(oracle.gemm_w8a8c8(x, w8, M, N, K), z["c_w8a8c8"])
+    assert np.array_equal(oracle.quantize_q4_1(z["wf"]), z["w_q4_1_from_fp32"])
+    assert np.array_equal(npref.quantize_q4_1(z["wf"]), z["w_q4_1_from_fp32"])
+
+
 # ---------------------------------------------------------------- K-quants
 def test_q4_K_encoder_decoder_round_trip(oracle):
     g = np.random.default_rng(8)
@@ -271,3 +292,165 @@ def test_moe_route_and_composition(oracle):
     assert np.allclose(out, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
     counts = np.bincount(ids.ravel(), minlength=E)
     assert counts.sum() == T * k
+
+
+# ---------------------------------------------------------------- Q4_1 / Q5_0 / Q5_1
+LEGACY = (4, 5, 6)
+
+
+@pytest.mark.parametrize("wtype", LEGACY)
+def test_legacy_known_answer_blocks(oracle, wtype):
+    """Blocks encoded from chosen fields (npref.encode_legacy) decode to d*q + m / (q-16)*d, and
+    the integer dot against a ramp is the hand-computable sum."""
+    q = np.array([(7 * e + 3) % (16 if wtype == 4 else 32) for e in range(32)])
+    d, m = 0.125, -1.5
+    blk = npref.encode_legacy(wtype, d, m, q)
+    y = oracle.dequantize(wtype, blk[None, :], 1, 32)[0]
+    want = (q - 16) * d if wtype == 5 else q * d + m
+    assert np.array_equal(y, want.astype(np.float32))
+    qa = np.arange(32) - 16
+    a = _q8_1_block(1.0, 0.0, qa)
+    assert oracle.sumi_legacy(wtype, blk, a) == int(np.dot(q, qa))
+    # element order: a ramp over the first 16 activations only sees the low nibbles / qh bits 0..15
+    a16 = _q8_1_block(1.0, 0.0, [k if k < 16 else 0 for k in range(32)])
+    assert oracle.sumi_legacy(wtype, blk, a16) == int(np.dot(q[:16], np.arange(16)))
+
+
+@pytest.mark.parametrize("wtype", (5, 6))
+def test_legacy_qh_bit_order(oracle, wtype):
+    """Only element e has bit 4 set: the dot with a one-hot activation at e sees 16, elsewhere 0."""
+    for e in (0, 7, 8, 15, 16, 23, 31):
+        q = np.zeros(32, int)
+        q[e] = 16
+        blk = npref.encode_legacy(wtype, 1.0, 0.0, q)
+        for k in (e, (e + 1) % 32, (e + 16) % 32):
+            qa = np.zeros(32, int)
+            qa[k] = 1
+            assert oracle.sumi_legacy(wtype, blk, _q8_1_block(1.0, 0.0, qa)) == (16 if k == e else 0)
+
+
+@pytest.mark.parametrize("wtype", LEGACY)
+def test_legacy_sumi_and_gemm_vs_numpy(oracle, wtype):
+    from ksq import synth
+    g = np.random.default_rng(20 + wtype)
+    M, N, K = 4, 6, 512
+    w = synth.weights(wtype, g, N, K)
+    a = oracle.quantize_q8_1(synth.activations(g, M, K) * 2)
+    _, _, qw = npref.unpack_legacy(wtype, w)
+    _, _, qa = npref.unpack_q8_1(a)
+    assert np.array_equal(oracle.block_sumi(wtype, a, w, M, N, K), np.einsum("mbk,nbk->mnb", qa, qw))
+    ref = npref.gemm_legacy_f64(wtype, a, w)
+    c64 = oracle.gemm_f64(wtype, a, w, M, N, K)
+    c32 = oracle.gemm(wtype, a, w, M, N, K)
+    assert np.allclose(c64, ref, rtol=1e-12, atol=1e-12 * np.abs(ref).max())
+    assert np.abs(c32 - ref).max() <= 1e-5 * np.abs(ref).max()
+    if wtype != 5:
+        # the reference's "m * s8 / 4" (gemm_quant_formats.cuh:148, :266) is not what the harness computes
+        dw, mw, _ = npref.unpack_legacy(wtype, w)
+        _, sa, _ = npref.unpack_q8_1(a)
+        quarter = ref - 0.75 * np.einsum("nb,mb->mn", mw, sa)
+        assert np.abs(c32 - quarter).max() > 1e-2 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("wtype", LEGACY)
+def test_legacy_formula_vs_dequantised_matmul(oracle, wtype):
+    """sum_b (d q + m) . x over the original fp32 x: the s term carries the exact block sums, so the
+    integer formula equals the dequantised product up to the activation quantisation noise."""
+    from ksq import synth
+    g = np.random.default_rng(30 + wtype)
+    M, N, K = 3, 16, 1024
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    c = oracle.gemm(wtype, oracle.quantize_q8_1(x), w, M, N, K)
+    ref = x.astype(np.float64) @ oracle.dequantize(wtype, w.reshape(N, -1), N, K).astype(np.float64).T
+    assert np.mean((c - ref) ** 2) / np.mean(ref ** 2) < 1e-3
+
+
+def test_quantize_q4_1_matches_harness_restatement(oracle):
+    g = np.random.default_rng(40)
+    x = g.standard_normal((8, 512), dtype=np.float32)
+    x[1, :32] = 0.25                                   # constant block: scale 1, all q = 0
+    x[2, 32:64] = np.linspace(-1, 1, 32, dtype=np.float32)
+    assert np.array_equal(oracle.quantize_q4_1(x), npref.quantize_q4_1(x))
+    y = oracle.dequantize(4, oracle.quantize_q4_1(x).reshape(8, -1), 8, 512)
+    xb, yb = x.reshape(-1, 32), y.reshape(-1, 32)
+    span = xb.max(1) - xb.min(1)
+    assert np.all(np.abs(xb - yb).max(1) <= span / 15 * 0.5 + 2e-3 * (np.abs(xb).max(1) + span))
+
+
+@pytest.mark.parametrize("wtype", (5, 6))
+def test_quantize_q5_round_trip(oracle, wtype):
+    g = np.random.default_rng(41 + wtype)
+    x = g.standard_normal((8, 256), dtype=np.float32)
+    q = oracle.quantize_q5_0(x) if wtype == 5 else oracle.quantize_q5_1(x)
+    y = oracle.dequantize(wtype, q.reshape(8, -1), 8, 256).reshape(-1, 32)
+    xb = x.reshape(-1, 32)
+    # Q5_0 covers [-16, 15] steps with the largest magnitude at -16: a value of the opposite
+    # sign and equal magnitude clamps to 15, one full step off; elsewhere half a step
+    step = np.abs(xb).max(1) / 16 if wtype == 5 else (xb.max(1) - xb.min(1)) / 31
+    bound = step * (1.0 if wtype == 5 else 0.5)
+    assert np.all(np.abs(xb - y).max(1) <= bound + 2e-3 * np.abs(xb).max(1) + 1e-6)
+    if wtype == 5:
+        inner = np.abs(xb) < 0.9 * np.abs(xb).max(1, keepdims=True)
+        assert np.all(np.where(inner, np.abs(xb - y), 0).max(1) <= step * 0.5 + 2e-3 * np.abs(xb).max(1) + 1e-6)
+
+
+# ---------------------------------------------------------------- native W8A8C8 operator
+def test_quantize_q8s_matches_numpy_restatement(oracle):
+    g = np.random.default_rng(50)
+    x = g.standard_normal((16, 512), dtype=np.float32)
+    x[3, :32] = 0.0                                    # zero block -> d = 1, q = 0
+    x[4, 32:64] *= 1e-5                                # amax/127 < 1e-6 -> d = 1, q = round(x) = 0
+    x[5, 64:96] *= 1e4
+    assert np.array_equal(oracle.quantize_q8s(x), npref.quantize_q8s(x))
+
+
+def test_quantize_q8s_known_answers(oracle):
+    blk = np.zeros(32, np.float32)
+    blk[:6] = [127.0, 2.5, -2.5, 0.5, -126.5, 3.49999976]      # d = 1 exactly: ties round away from zero
+    q = oracle.quantize_q8s(blk[None, :])[0, 0]
+    assert q[0:4].view(np.float32)[0] == np.float32(1.0)
+    assert list(q[4:10].view(np.int8)) == [127, 3, -3, 1, -127, 3]
+    tiny = np.full((1, 32), 1e-5, np.float32)
+    t = oracle.quantize_q8s(tiny)[0, 0]
+    assert t[0:4].view(np.float32)[0] == np.float32(1.0) and np.all(t[4:] == 0)
+    # true division: find x where x / d and x * (1/d) round to different integers
+    g = np.random.default_rng(51)
+    found = 0
+    for _ in range(20000):
+        amax = np.float32(g.uniform(0.5, 2.0))
+        d = np.float32(amax / np.float32(127))
+        k = int(g.integers(1, 127))
+        x = np.float32((k + 0.5) * d)
+        for cand in (x, np.nextafter(x, np.float32(0)), np.nextafter(x, np.float32(9))):
+            by_div = np.float64(np.float32(cand / d))
+            by_mul = np.float64(np.float32(cand * np.float32(np.float32(1) / d)))
+            if np.floor(by_div + 0.5) != np.floor(by_mul + 0.5):
+                b = np.zeros((1, 32), np.float32)
+                b[0, 0], b[0, 1] = amax, cand
+                got = int(oracle.quantize_q8s(b)[0, 0, 5].view(np.int8))
+                assert got == int(np.floor(by_div + 0.5))
+                found += 1
+    assert found > 0
+
+
+def test_gemm_w8a8c8_composition(oracle):
+    """The whole operator (per-output re-quantisation) equals quantise-once then the block formula."""
+    from ksq import synth
+    g = np.random.default_rng(52)
+    M, N, K = 5, 7, 512
+    w = synth.weights(1, g, N, K)
+    x = synth.activations(g, M, K)
+    x[1, :64] *= 1e-6
+    c = oracle.gemm_w8a8c8(x, w, M, N, K)
+    a = oracle.quantize_q8s(x)
+    c64 = oracle.gemm_q8s_f64(a, w, M, N, K)
+    d_a = a[..., 0:4].copy().view(np.float32)[..., 0].astype(np.float64)
+    dw, qw = npref.unpack_q8_0(w)
+    qa = a[..., 4:].view(np.int8).astype(np.int64)
+    want = np.einsum("nb,mb,mnb->mn", dw, d_a, np.einsum("mbk,nbk->mnb", qa, qw).astype(np.float64))
+    assert np.allclose(c64, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+    assert np.abs(c - want).max() <= 1e-5 * np.abs(want).max()
+    # a Q8_1 (fp16 scale) activation path is a different operator: it differs at the fp16 level
+    q81 = oracle.gemm(1, oracle.quantize_q8_1(x), w, M, N, K)
+    assert np.abs(q81 - want).max() > 1e-7 * np.abs(want).max()
