@@ -93,7 +93,11 @@ def cpu_baseline(M: int, N: int, K: int, budget_s: float = 10.0) -> dict:
 
 
 def graph_ms(fn, n: int, reps: int) -> float:
-    """Average ms per fn(i) call over `reps` replays of a graph of n calls."""
+    """Average ms per fn(i) call over `reps` replays of a graph of n calls.  One eager call
+    first, so the library's workspace pool is sized before capture (no hipMalloc inside)."""
+    import torch
+    fn(0)
+    torch.cuda.synchronize()
     g = capture(fn, n)
     g.replay()
     return time_graph(g, reps) / (reps * n)

@@ -44,7 +44,8 @@ int hip_error(hipError_t e, const char* where) {
     return set_error(KSQ_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
 }
 
-// Per-device scratch for the Q8_1 copy of fp32 activations.
+// Per-device scratch: the quantised copy of fp32 activations, split-K partial sums and the
+// MoE routing tables when the caller passes no workspace.
 struct Pool {
     void* ptr = nullptr;
     size_t size = 0;
@@ -103,15 +104,40 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
     return KSQ_OK;
 }
 
+// The MFMA GEMM above 8 rows (or when forced), the v_dot4 decode kernels otherwise.
+bool use_mmq(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
+    return (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, a_aligned16) && (g_path == 2 || M > 8);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Workspace of one ksq_gemm call: [quantised activations][split-K partial sums], each part
+// 256-byte aligned.  `mmq` is whether the MFMA path runs (alignment permitting).
+struct GemmWs {
+    size_t q, p, total;
+};
+
+GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
+    GemmWs w{};
+    w.q = atype_f32(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
+    const int splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
+    w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
+    w.total = w.q + w.p;
+    return w;
+}
+
 int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* C, int M, int N, int K,
-               hipStream_t s) {
+               float* partials, hipStream_t s) {
     hipError_t e;
-    const bool use_mmq = (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, Aq) && (g_path == 2 || M > 8);
-    if (use_mmq)
-        e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, s);
+    const bool mmq = use_mmq(wtype, M, N, K, W, aligned16(Aq));
+    if (mmq)
+        e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, partials, s);
     else
         e = ksq::launch_gemv(wtype, afmt, W, Aq, C, M, N, K, s);
-    if (e != hipSuccess) return hip_error(e, use_mmq ? "mmq launch" : "gemv launch");
+    if (e != hipSuccess) return hip_error(e, mmq ? "mmq launch" : "gemv launch");
     return KSQ_OK;
 }
 
@@ -185,10 +211,9 @@ int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
 }
 
 size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
-    (void)wtype;
-    (void)N;
-    if (!atype_f32(atype) || M <= 0 || K <= 0) return 0;
-    return (size_t)M * (size_t)(K / 32) * 36u;
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const bool mmq_possible = (g_path != 1) && (g_path == 2 || M > 8) && (K % 256) == 0;
+    return gemm_ws(wtype, atype, M, N, K, mmq_possible).total;
 }
 
 int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output, int M, int N,
@@ -203,22 +228,36 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     const uint8_t* Aq = (const uint8_t*)activation;
     const int afmt = atype_fmt(atype);
-    if (atype_f32(atype)) {
-        const size_t need = ksq_gemm_workspace_size(wtype, atype, M, N, K);
-        void* ws = workspace;
+    if (atype_f32(atype) && ksq::gemv_fused_profitable(M, N, K) && !use_mmq(wtype, M, N, K, weight, true)) {
+        hipError_t e = ksq::launch_gemv_f32(wtype, afmt, (const uint8_t*)weight, (const float*)activation, output, M,
+                                            N, K, s);
+        return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
+    }
+    // fp32 activations are quantised to the start of the (16-byte aligned) workspace, which is
+    // what the MFMA path then reads
+    const bool f32 = atype_f32(atype);
+    const bool mmq = use_mmq(wtype, M, N, K, weight, f32 || aligned16(activation));
+    const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq);
+    uint8_t* ws = (uint8_t*)workspace;
+    if (L.total) {
         if (ws) {
-            if (workspace_bytes < need)
-                return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+            if (workspace_bytes < L.total)
+                return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, L.total);
             if ((uintptr_t)ws & 15u) return set_error(KSQ_ERR_ALIGN, "workspace must be 16-byte aligned");
         } else {
-            st = pool_get(need, &ws);
+            void* p = nullptr;
+            st = pool_get(L.total, &p);
             if (st != KSQ_OK) return st;
+            ws = (uint8_t*)p;
         }
-        hipError_t e = ksq::launch_quantize(afmt, (const float*)activation, (uint8_t*)ws, M, K, s);
-        if (e != hipSuccess) return hip_error(e, "quantize launch");
-        Aq = (const uint8_t*)ws;
     }
-    st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, s);
+    if (f32) {
+        hipError_t e = ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+        Aq = ws;
+    }
+    float* partials = L.p ? (float*)(ws + L.q) : nullptr;
+    st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, partials, s);
     return st == KSQ_OK ? ok() : st;
 }
 
@@ -236,7 +275,7 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
     int st = check_common(wtype, KSQ_A_Q8_1, weight, act_q8_1, out, M, N, K);
     if (st != KSQ_OK) return st;
     if (M == 0 || N == 0 || K == 0) return ok();
-    if (!ksq::mmq_supported(wtype, M, N, K, weight, act_q8_1))
+    if (!ksq::mmq_supported(wtype, M, N, K, weight, aligned16(act_q8_1)))
         return set_error(KSQ_ERR_SHAPE, "MFMA path needs K %% 256 == 0 and 16-byte aligned operands");
     hipError_t e = ksq::launch_mmq_block_sumi(wtype, (const uint8_t*)weight, act_q8_1, out, M, N, K, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_error(e, "mfma block_sumi launch");
@@ -245,8 +284,6 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
 // ---- expert-grouped MoE --------------------------------------------------------
 namespace {
 constexpr int kMoeTileRows = 64;  // rows per grouped-GEMM tile (the MFMA kernel's BM for MoE)
-
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct MoeLayout {
     size_t aq, ids, wts, rows, eend, ntiles, texp, trow0, scratch, total;

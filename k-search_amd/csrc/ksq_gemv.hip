@@ -4,13 +4,16 @@
 // (one warp per weight row, lanes striding K-blocks, DP4A, shuffle reduce) and the
 // CPU dots vec_dot_q4_0_q8_1 / vec_dot_q8_0_q8_1 (include/gemm_reference.h:276-336).
 //
-// gfx950 design (one weight row per wave):
-//  * A 256-thread workgroup owns 4 consecutive weight rows, one per wave.  Each wave
-//    copies its row (a contiguous byte range) into LDS with global_load_lds_dwordx4
-//    (1 KiB per wave instruction, no VGPRs), and the workgroup stages the Q8_1
-//    activation rows in LDS once for all four waves.  One-shot reads of a few MB
-//    are fastest as many small, fully coalesced requests spread over the whole
+// gfx950 design (weight rows streamed into LDS by DMA):
+//  * A 256-thread workgroup owns 4, 2 or 1 consecutive weight rows (fewer rows when N is
+//    small, so the grid still covers the chip; the waves of a row then split it).  Each
+//    wave copies its row or row part (a contiguous byte range) into LDS with
+//    global_load_lds_dwordx4 (1 KiB per wave instruction, no VGPRs).  One-shot reads of
+//    a few MB are fastest as many small, fully coalesced requests spread over the whole
 //    chip, which is what this layout issues.
+//  * Activations: 1-2 rows are read by each lane straight from L2; 3-8 rows are DMA'd
+//    into LDS once per workgroup beside the weights; fp32 activations of 1-2 rows can be
+//    quantised inside every workgroup (see kAFQ), saving the quantise launch.
 //  * Lanes then stride over 32-element units of the row (a Q4_0/Q8_0/Q4_1/Q5_0/Q5_1
 //    block, or one Q8_1-block-sized slice of a Q4_K/Q6_K super-block), pull the unit's
 //    bytes out of LDS with dword reads re-aligned by v_alignbyte_b32 (blocks are
@@ -166,7 +169,6 @@ struct Fmt {
     static constexpr int span = (WT == kWQ4K) ? kQ4KBytes : (WT == kWQ6K) ? kQ6KBytes : 8 * block_bytes(WT);
 };
 
-constexpr int kRowsPerWG = 4;
 constexpr int kTileSlack = 32;  // bytes after each staged row: head offset + read-ahead of read_words
 
 // Copy `bytes` from global g (2-byte aligned) into LDS at dst = region + (g & 15), one wave:
@@ -187,21 +189,59 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
     }
 }
 
+// Activation staging modes of the decode kernel.
+//   kAL2   each lane reads its activation blocks from global memory (L2) after the weight wait
+//          (1 or 2 activation rows: the fewest bytes moved)
+//   kADMA  the activation rows of the K tile are copied into LDS by DMA, issued together with
+//          the weight DMA, so one wait covers both (3 or more rows, read once per workgroup)
+//   kAFQ   the activations arrive as fp32 and every workgroup quantises the K tile's blocks
+//          itself into LDS while its weight DMA is in flight (the same device quantiser as
+//          ksq_quantize.hip, so the blocks are bit-identical); no separate quantise launch
+constexpr int kAL2 = 0, kADMA = 1, kAFQ = 2;
+constexpr int kMaxL2Rows = 2, kMaxFusedRows = 2;
+
+// Part `part` of `nparts` of a copy of `bytes` from g into LDS at dst (dst = g mod 16): the
+// parts split at 16-byte boundaries of g, so each is a valid wave_copy_to_lds.
+__device__ __forceinline__ void wave_copy_part(const uint8_t* g, uint8_t* dst, int bytes, int part, int nparts,
+                                               int lane) {
+    if (nparts == 1) {
+        wave_copy_to_lds(g, dst, bytes, lane);
+        return;
+    }
+    const int sh = (int)((uintptr_t)g & 15);
+    auto cut = [&](int k) -> int {   // offset of the k-th split point, 16-byte aligned in g
+        if (k <= 0) return 0;
+        if (k >= nparts) return bytes;
+        const int c = ((sh + (int)(((int64_t)bytes * k) / nparts) + 15) & ~15) - sh;
+        return c < 0 ? 0 : (c > bytes ? bytes : c);
+    };
+    const int b0 = cut(part), b1 = cut(part + 1);
+    if (b1 > b0) wave_copy_to_lds(g + b0, dst + b0, b1 - b0, lane);
+}
+
 // C[m][row] = sum over the row's units, for m < MR.  KT = blocks per K tile (multiple of 8).
+// RPW weight rows per workgroup; the 4 / RPW waves of a row split its units (and its
+// weight copy) and add their partial sums through LDS at the end.
 // AS: the activations are block_q8s (fp32 scale, no sum) instead of block_q8_1.
-template <int WT, int MR, bool ALDS, bool AS>
-__global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
-                                                       float* __restrict__ C, int N, int nb, int KT, int ldc,
-                                                       int a_vec16) {
+// Ain: block_q8_1 / block_q8s bytes [MR][nb] (kAL2, kADMA) or fp32 [MR][32 nb] (kAFQ).
+template <int WT, int MR, int AMODE, bool AS, int RPW>
+__global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
+                                                       float* __restrict__ C, int N, int nb, int KT, int ldc) {
+    static_assert(RPW == 1 || RPW == 2 || RPW == 4, "1, 2 or 4 rows per workgroup");
+    constexpr int WPR = 4 / RPW;  // waves per row
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float red[4][MR];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int row = blockIdx.x * kRowsPerWG + wave;
+    const int rloc = wave / WPR, part = wave % WPR;
+    const int row = blockIdx.x * RPW + rloc;
     constexpr bool kq = is_kquant(WT);
+    const uint8_t* A = (const uint8_t*)Ain;
     const size_t RB = kq ? (size_t)(nb / 8) * Fmt<WT>::span : (size_t)nb * block_bytes(WT);  // row bytes
     const int tile_w = kq ? (KT / 8) * Fmt<WT>::span : KT * block_bytes(WT);
     const int wpitch = ((tile_w + kTileSlack + 15) & ~15);
-    uint8_t* wreg = smem + wave * wpitch;
-    uint8_t* areg = smem + kRowsPerWG * wpitch;  // [MR][KT] Q8_1 blocks, 36 B each
+    const int apitch = ((KT * kQ81Bytes + 16 + 15) & ~15);
+    uint8_t* wreg = smem + rloc * wpitch;
+    uint8_t* areg = smem + RPW * wpitch;  // [MR][apitch]: the K tile's activation blocks, 36 B each
 
     float acc[MR];
 #pragma unroll
@@ -209,37 +249,55 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
 
     for (int kt0 = 0; kt0 < nb; kt0 += KT) {
         const int kt = (nb - kt0) < KT ? (nb - kt0) : KT;
-        const uint8_t* g = nullptr;
         uint8_t* wt = nullptr;
         if (row < N) {
             const size_t off = kq ? (size_t)(kt0 / 8) * Fmt<WT>::span : (size_t)kt0 * block_bytes(WT);
             const int bytes = kq ? (kt / 8) * Fmt<WT>::span : kt * block_bytes(WT);
-            g = W + (size_t)row * RB + off;
+            const uint8_t* g = W + (size_t)row * RB + off;
             wt = wreg + ((uintptr_t)g & 15);
-            wave_copy_to_lds(g, wt, bytes, lane);
+            wave_copy_part(g, wt, bytes, part, WPR, lane);
         }
-        // activations: MR rows x kt blocks, 36 B each (staged in LDS only when ALDS)
-        if (!ALDS) {
-        } else if (a_vec16) {
-            const int nv = kt * 36 / 16;  // per activation row (kt % 4 == 0 here)
-            for (int v = threadIdx.x; v < MR * nv; v += 256) {
-                const int m = v / nv, j = v - m * nv;
-                const u32x4 x = *(const u32x4*)(A + ((size_t)m * nb + kt0) * kQ81Bytes + 16 * j);
-                *(u32x4*)(areg + (size_t)m * KT * kQ81Bytes + 16 * j) = x;
+        // per activation row, the byte offset of its first staged block inside its LDS region
+        int ashift[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) ashift[m] = 0;
+        if constexpr (AMODE == kADMA) {
+            // activation row m is copied by wave m % 4
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const uint8_t* g = A + ((size_t)m * nb + kt0) * kQ81Bytes;
+                ashift[m] = (int)((uintptr_t)g & 15);
+                if ((m & 3) == wave) wave_copy_to_lds(g, areg + m * apitch + ashift[m], kt * kQ81Bytes, lane);
             }
-        } else {
-            const int nv = kt * 9;
-            for (int v = threadIdx.x; v < MR * nv; v += 256) {
-                const int m = v / nv, j = v - m * nv;
-                ((uint32_t*)(areg + (size_t)m * KT * kQ81Bytes))[j] =
-                    ((const uint32_t*)(A + ((size_t)m * nb + kt0) * kQ81Bytes))[j];
+        } else if constexpr (AMODE == kAFQ) {
+            const float* X = (const float*)Ain;
+            const int K = nb * 32;
+            for (int v = threadIdx.x; v < MR * kt; v += 256) {
+                const int m = v / kt, u = v - m * kt;
+                const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)(kt0 + u) * 32);
+                float x[32];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const f32x4 q = src[i];
+                    x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+                }
+                uint32_t blk[9];
+                if constexpr (AS) quantize_block_q8s(x, blk);
+                else quantize_block_q8_1(x, blk);
+                uint32_t* dst = (uint32_t*)(areg + m * apitch + u * kQ81Bytes);
+#pragma unroll
+                for (int i = 0; i < 9; i++) dst[i] = blk[i];
             }
         }
         wait_vmem();
         __syncthreads();
 
         if (row < N) {
-            for (int u = lane; u < kt; u += 64) {   // unit u = 32-element slice, Q8_1 block kt0 + u
+            auto act = [&](int m, int u) -> const uint32_t* {
+                if constexpr (AMODE == kAL2) return (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes);
+                else return (const uint32_t*)(areg + m * apitch + ashift[m] + u * kQ81Bytes);
+            };
+            for (int u = part * 64 + lane; u < kt; u += 64 * WPR) {   // unit u: activation block kt0 + u
                 if constexpr (!kq) {
                     const uint8_t* blk = wt + u * block_bytes(WT);
                     const float dw = f16_to_f32(read_u16(blk));
@@ -247,8 +305,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                     if constexpr (WT == kWQ41 || WT == kWQ51) mw = f16_to_f32(read_u16(blk + 2));
 #pragma unroll
                     for (int m = 0; m < MR; m++) {
-                        const uint32_t* ap = ALDS ? (const uint32_t*)(areg + ((size_t)m * KT + u) * kQ81Bytes)
-                                             : (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes);
+                        const uint32_t* ap = act(m, u);
                         uint32_t a[9];
 #pragma unroll
                         for (int i = 0; i < 9; i++) a[i] = ap[i];
@@ -278,8 +335,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                         const float d = f16_to_f32(hd[0] & 0xFFFFu), dmin = f16_to_f32(hd[0] >> 16);
 #pragma unroll
                         for (int m = 0; m < MR; m++) {
-                            const uint32_t* ap = ALDS ? (const uint32_t*)(areg + ((size_t)m * KT + u) * kQ81Bytes)
-                                             : (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes);
+                            const uint32_t* ap = act(m, u);
                             uint32_t a[9];
 #pragma unroll
                             for (int i = 0; i < 9; i++) a[i] = ap[i];
@@ -293,8 +349,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                         const float d = f16_to_f32(read_u16(sb + 208));
 #pragma unroll
                         for (int m = 0; m < MR; m++) {
-                            const uint32_t* ap = ALDS ? (const uint32_t*)(areg + ((size_t)m * KT + u) * kQ81Bytes)
-                                             : (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes);
+                            const uint32_t* ap = act(m, u);
                             uint32_t a[9];
 #pragma unroll
                             for (int i = 0; i < 9; i++) a[i] = ap[i];
@@ -310,7 +365,19 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
     }
 #pragma unroll
     for (int m = 0; m < MR; m++) acc[m] = wave_sum(acc[m]);
-    if (row < N && lane == 0) {
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                for (int p = 1; p < WPR; p++) acc[m] += red[wave + p][m];
+        }
+    }
+    if (row < N && part == 0 && lane == 0) {
 #pragma unroll
         for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row] = acc[m];
     }
@@ -323,71 +390,133 @@ static int span_bytes(int wtype) {
     return wtype == kWQ4K ? kQ4KBytes : wtype == kWQ6K ? kQ6KBytes : 8 * block_bytes(wtype);
 }
 
-// Activation rows are staged in LDS (once per workgroup) for M > 2; for M <= 2 each
-// lane reads its Q8_1 blocks straight from L2, which measured faster at M = 1.
-constexpr int kActLdsMinRows = 3;
-
-static size_t gemv_lds_bytes(int wtype, int mr, int KT) {
+static size_t gemv_lds_bytes(int wtype, int mr, int KT, int amode, int rpw) {
     const int tile_w = (KT / 8) * span_bytes(wtype);
     const size_t wpitch = (size_t)((tile_w + kTileSlack + 15) & ~15);
-    return kRowsPerWG * wpitch + (mr >= kActLdsMinRows ? (size_t)mr * KT * kQ81Bytes : 0);
+    const size_t apitch = (size_t)((KT * kQ81Bytes + 16 + 15) & ~15);
+    return rpw * wpitch + (amode == kAL2 ? 0 : (size_t)mr * apitch);
 }
 
-template <int WT, int MR, bool AS>
-static hipError_t row_launch(const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int KT, int ldc, int av16,
+// Rows per workgroup: 4 while that still gives at least kGemvMinWGs workgroups, else 2 or 1
+// (the waves of a row then split its K range), so small-N matrices still cover the chip.
+#ifndef KSQ_GEMV_MIN_WGS
+#define KSQ_GEMV_MIN_WGS 256
+#endif
+constexpr int kGemvMinWGs = KSQ_GEMV_MIN_WGS;
+
+static int pick_rpw(int N) {
+    if ((N + 3) / 4 >= kGemvMinWGs) return 4;
+    if ((N + 1) / 2 >= kGemvMinWGs) return 2;
+    return 1;
+}
+
+template <int WT, int MR, int AMODE, bool AS, int RPW>
+static hipError_t row_launch(const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
                              hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(WT, MR, KT);
-    auto k = gemv_row_kernel<WT, MR, (MR >= kActLdsMinRows), AS>;
-    if (lds > 65536) (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    const unsigned grid = (unsigned)((N + kRowsPerWG - 1) / kRowsPerWG);
-    hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, W, A, C, N, nb, KT, ldc, av16);
-    return hipGetLastError();
+    if constexpr ((AMODE == kAL2 && MR > kMaxL2Rows) || (AMODE == kADMA && MR <= kMaxL2Rows) ||
+                  (AMODE == kAFQ && MR > kMaxFusedRows)) {
+        return hipErrorNotSupported;  // combinations the dispatcher never asks for are not compiled
+    } else {
+        const size_t lds = gemv_lds_bytes(WT, MR, KT, AMODE, RPW);
+        auto k = gemv_row_kernel<WT, MR, AMODE, AS, RPW>;
+        if (lds > 65536)
+            (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const unsigned grid = (unsigned)((N + RPW - 1) / RPW);
+        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, W, A, C, N, nb, KT, ldc);
+        return hipGetLastError();
+    }
 }
 
-template <int WT, bool AS = false>
-static hipError_t row_launch_mr(int mr, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int KT, int ldc,
-                                int av16, hipStream_t s) {
-    switch (mr) {
-        case 1: return row_launch<WT, 1, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 2: return row_launch<WT, 2, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 3: return row_launch<WT, 3, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 4: return row_launch<WT, 4, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 5: return row_launch<WT, 5, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 6: return row_launch<WT, 6, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        case 7: return row_launch<WT, 7, AS>(W, A, C, N, nb, KT, ldc, av16, s);
-        default: return row_launch<WT, 8, AS>(W, A, C, N, nb, KT, ldc, av16, s);
+template <int WT, int MR, int AMODE, bool AS>
+static hipError_t row_launch_rpw(int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
+                                 hipStream_t s) {
+    switch (rpw) {
+        case 4: return row_launch<WT, MR, AMODE, AS, 4>(W, A, C, N, nb, KT, ldc, s);
+        case 2: return row_launch<WT, MR, AMODE, AS, 2>(W, A, C, N, nb, KT, ldc, s);
+        default: return row_launch<WT, MR, AMODE, AS, 1>(W, A, C, N, nb, KT, ldc, s);
     }
+}
+
+template <int WT, int AMODE, bool AS>
+static hipError_t row_launch_mr(int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int KT,
+                                int ldc, hipStream_t s) {
+    switch (mr) {
+        case 1: return row_launch_rpw<WT, 1, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 2: return row_launch_rpw<WT, 2, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 3: return row_launch_rpw<WT, 3, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 4: return row_launch_rpw<WT, 4, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 5: return row_launch_rpw<WT, 5, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 6: return row_launch_rpw<WT, 6, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 7: return row_launch_rpw<WT, 7, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        default: return row_launch_rpw<WT, 8, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+    }
+}
+
+// QUANT: the activations are already quantised (kAL2 / kADMA by row count), else fp32 (kAFQ).
+template <int AMODE>
+static hipError_t gemv_dispatch_mode(int wtype, int afmt, int mr, const uint8_t* W, const void* Am, float* Cm,
+                                     int N, int nb, int KT, int rpw, hipStream_t s) {
+    switch (wtype) {
+        case kWQ40: return row_launch_mr<kWQ40, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ80:
+            return (afmt == kAQ8S) ? row_launch_mr<kWQ80, AMODE, true>(mr, rpw, W, Am, Cm, N, nb, KT, N, s)
+                                   : row_launch_mr<kWQ80, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ4K: return row_launch_mr<kWQ4K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ6K: return row_launch_mr<kWQ6K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ41: return row_launch_mr<kWQ41, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ50: return row_launch_mr<kWQ50, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        default: return row_launch_mr<kWQ51, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+    }
+}
+
+template <bool QUANT>
+static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const void* A, float* C, int M, int N, int K,
+                                hipStream_t s) {
+    if (afmt == kAQ8S && wtype != kWQ80) return hipErrorNotSupported;
+    const int nb = K / 32;
+    if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
+    const int chunk = QUANT ? 8 : kMaxFusedRows;
+    for (int m0 = 0; m0 < M; m0 += chunk) {
+        const int mr = (M - m0) < chunk ? (M - m0) : chunk;
+        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows ? kAL2 : kADMA);
+        // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
+        const int rpw = pick_rpw(N);
+        int KT = (nb + 7) & ~7;
+        while (KT > 64 && gemv_lds_bytes(wtype, mr, KT, AMODE, rpw) > kGemvLdsBudget) KT = ((KT / 2) + 63) & ~63;
+        const void* Am = QUANT ? (const void*)((const uint8_t*)A + (size_t)m0 * nb * kQ81Bytes)
+                               : (const void*)((const float*)A + (size_t)m0 * K);
+        float* Cm = C + (size_t)m0 * N;
+        hipError_t e;
+        if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s) {
-    if (afmt == kAQ8S && wtype != kWQ80) return hipErrorNotSupported;
-    const int nb = K / 32;
-    if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
-    for (int m0 = 0; m0 < M; m0 += 8) {
-        const int mr = (M - m0) < 8 ? (M - m0) : 8;
-        // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
-        int KT = (nb + 7) & ~7;
-        while (KT > 64 && gemv_lds_bytes(wtype, mr, KT) > kGemvLdsBudget) KT = ((KT / 2) + 63) & ~63;
-        const uint8_t* Am = A + (size_t)m0 * nb * kQ81Bytes;
-        const int av16 = ((((uintptr_t)Am) & 15u) == 0) && (nb % 4 == 0) && (KT % 4 == 0);
-        float* Cm = C + (size_t)m0 * N;
-        hipError_t e;
-        switch (wtype) {
-            case kWQ40: e = row_launch_mr<kWQ40>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case kWQ80:
-                e = (afmt == kAQ8S) ? row_launch_mr<kWQ80, true>(mr, W, Am, Cm, N, nb, KT, N, av16, s)
-                                    : row_launch_mr<kWQ80>(mr, W, Am, Cm, N, nb, KT, N, av16, s);
-                break;
-            case kWQ4K: e = row_launch_mr<kWQ4K>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case kWQ6K: e = row_launch_mr<kWQ6K>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case kWQ41: e = row_launch_mr<kWQ41>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            case kWQ50: e = row_launch_mr<kWQ50>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-            default: e = row_launch_mr<kWQ51>(mr, W, Am, Cm, N, nb, KT, N, av16, s); break;
-        }
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
+    return gemv_dispatch<true>(wtype, afmt, W, A, C, M, N, K, s);
+}
+
+// The in-workgroup quantisation is repeated by every workgroup; it beats the separate quantise
+// launch while that repeated work stays small (measured crossover: between 4.0e5 and 4.6e5
+// block quantisations, e.g. N = K = 7168 fused is faster, N = 14336, K = 4096 is not).
+#ifndef KSQ_GEMV_FUSED_MAX_WORK
+#define KSQ_GEMV_FUSED_MAX_WORK 420000ll
+#endif
+
+bool gemv_fused_profitable(int M, int N, int K) {
+    if (M < 1 || M > kMaxFusedRows) return false;
+    const int rpw = pick_rpw(N);
+    const long long wgs = (N + rpw - 1) / rpw;
+    return (long long)M * wgs * (K / 32) <= KSQ_GEMV_FUSED_MAX_WORK;
+}
+
+hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X, float* C, int M, int N, int K,
+                           hipStream_t s) {
+    return gemv_dispatch<false>(wtype, afmt, W, X, C, M, N, K, s);
 }
 
 // ---------------------------------------------------------------------------

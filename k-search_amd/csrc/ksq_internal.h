@@ -23,11 +23,24 @@ hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K,
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s);
 
+// The same decode kernels on fp32 activations [M][K] (16-byte aligned): every workgroup
+// quantises the activation blocks it needs (block_q8_1, or block_q8s for afmt kAQ8S) into
+// LDS while its weight loads are in flight, so no quantise launch or workspace is needed.
+hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X, float* C, int M, int N, int K,
+                           hipStream_t s);
+// Whether launch_gemv_f32 beats quantise + launch_gemv for this shape (M <= 2 and a bounded
+// amount of repeated quantisation).
+bool gemv_fused_profitable(int M, int N, int K);
+
 // Prefill GEMM on int8 MFMA (mul_mat_q family); returns hipErrorNotSupported
 // for shapes it does not tile.
-bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A);
+// a_aligned16: the quantised activations the GEMM will read are 16-byte aligned.
+bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16);
+// Number of K splits launch_mmq uses for this shape (1: none).  With splits > 1 it needs
+// `partials`, splits * M * N floats of device scratch.
+int mmq_splits(int wtype, int M, int N, int K);
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
-                      hipStream_t s);
+                      float* partials, hipStream_t s);
 // Force one of the MFMA tile configurations (1..4) or automatic choice (0); -1 if out of range.
 int mmq_set_config(int c);
 

@@ -166,7 +166,12 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) bias[r] = DUMP ? 0 : (int)kMagic;
 
-    for (int kb0 = 0; kb0 < nb; kb0 += KB) {
+    // split-K: workgroup z of gridDim.z covers K steps [z*steps/Z, (z+1)*steps/Z) and writes its
+    // partial sums to C + z*M*N (the caller adds the partials)
+    const int nsteps = nb / KB, Z = (int)gridDim.z, z = (int)blockIdx.z;
+    const int kb_lo = (int)((long long)nsteps * z / Z) * KB, kb_hi = (int)((long long)nsteps * (z + 1) / Z) * KB;
+    if constexpr (!MOE) C += (size_t)z * (size_t)M * (size_t)N;
+    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += KB) {
         // ---- stage activations: chunks of 4 Q8_1 blocks = 144 B = 9 x 16 B
         for (int c = t; c < BM * (KB / 4); c += 256) {
             const int sr = c / (KB / 4), g = c % (KB / 4);
@@ -478,10 +483,34 @@ static int pick_config(int wtype, int M, int N) {
     return 3;
 }
 
-bool mmq_supported(int wtype, int M, int N, int K, const void* W, const void* A) {
+bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
     const uintptr_t wal = (wtype == kWQ6K) ? 3u : 15u;  // Q6_K rows are read per dword
     return (wtype >= kWQ40 && wtype <= kWQ51) && M > 0 && N > 0 && K > 0 && (K % 256) == 0 &&
-           (((uintptr_t)W & wal) == 0) && (((uintptr_t)A & 15u) == 0);
+           (((uintptr_t)W & wal) == 0) && a_aligned16;
+}
+
+// Split-K factor for a (tile, M, N, K): grids of fewer than kSplitMinWGs workgroups are split
+// along K (at least kSplitMinSteps K steps per split) so that small-M problems still occupy
+// the chip; the partial sums go to a workspace and splitk_reduce_kernel adds them in order.
+constexpr int kSplitMinWGs = 256, kSplitTargetWGs = 512, kSplitMinSteps = 2, kSplitMax = 16;
+
+template <class T>
+static int split_for(int M, int N, int K) {
+    const int wgs = ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
+    const int steps = (K / 32) / T::KB;
+    if (wgs >= kSplitMinWGs) return 1;
+    int sp = (kSplitTargetWGs + wgs - 1) / wgs;
+    sp = sp < steps / kSplitMinSteps ? sp : steps / kSplitMinSteps;
+    sp = sp < kSplitMax ? sp : kSplitMax;
+    return sp < 1 ? 1 : sp;
+}
+
+__global__ void splitk_reduce_kernel(const float* __restrict__ P, float* __restrict__ C, int64_t mn, int splits) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= mn) return;
+    float acc = P[i];
+    for (int z = 1; z < splits; z++) acc += P[(size_t)z * (size_t)mn + (size_t)i];
+    C[i] = acc;
 }
 
 template <class T, int WT, bool DUMP, bool MOE, bool AS = false>
@@ -514,12 +543,24 @@ static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, con
     }
 }
 
+static int split_cfg(int cfg, int M, int N, int K) {
+    switch (cfg) {
+        case 1: return split_for<TileL>(M, N, K);
+        case 2: return split_for<TileN>(M, N, K);
+        case 3: return split_for<TileS>(M, N, K);
+        default: return split_for<TileK4>(M, N, K);
+    }
+}
+
+// splits > 1: C receives splits partial [M][N] results back to back.
 template <bool DUMP>
 static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C,
-                             int32_t* dump, int M, int N, int K, hipStream_t s) {
+                             int32_t* dump, int M, int N, int K, int splits, hipStream_t s) {
     const int nb = K / 32;
     const MoeTiles mt{};
-    auto grid = [&](int BM, int BN) { return dim3((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM)); };
+    auto grid = [&](int BM, int BN) {
+        return dim3((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
+    };
     switch (cfg) {
         case 1: return launch_t<TileL, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
         case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
@@ -528,9 +569,23 @@ static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, con
     }
 }
 
+int mmq_splits(int wtype, int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 1;
+    return split_cfg(pick_config(wtype, M, N), M, N, K);
+}
+
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
-                      hipStream_t s) {
-    return launch_cfg<false>(pick_config(wtype, M, N), wtype, afmt, W, A, C, nullptr, M, N, K, s);
+                      float* partials, hipStream_t s) {
+    const int cfg = pick_config(wtype, M, N);
+    const int splits = split_cfg(cfg, M, N, K);
+    if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s);
+    if (!partials) return hipErrorInvalidValue;
+    hipError_t e = launch_cfg<false>(cfg, wtype, afmt, W, A, partials, nullptr, M, N, K, splits, s);
+    if (e != hipSuccess) return e;
+    const int64_t mn = (int64_t)M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, partials, C, mn,
+                       splits);
+    return hipGetLastError();
 }
 
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
@@ -556,8 +611,8 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
 
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,
                                  hipStream_t s) {
-    if (!mmq_supported(wtype, M, N, K, W, A)) return hipErrorNotSupported;
-    return launch_cfg<true>(pick_config(wtype, M, N), wtype, kAQ81, W, A, nullptr, out, M, N, K, s);
+    if (!mmq_supported(wtype, M, N, K, W, ((uintptr_t)A & 15u) == 0)) return hipErrorNotSupported;
+    return launch_cfg<true>(pick_config(wtype, M, N), wtype, kAQ81, W, A, nullptr, out, M, N, K, 1, s);
 }
 
 }  // namespace ksq

@@ -450,3 +450,69 @@ def test_w8a8c8_block_dots_and_paths(dev, oracle, path):
     assert _rel_err(y, oracle.gemm_q8s_f64(a, w, M, N, K)) <= TOL
     yq = _gpu_gemm(dev, 1, w, a, M, N, K, atype=_lib.A_Q8S, path=path)
     assert np.array_equal(y, yq)
+
+
+# ------------------------------------------------------------------ definition runner
+@pytest.mark.parametrize("name", ["w4a32c8_q4_0_fp32_int8_qwen3_4b_att_out_n2560_k2560",
+                                  "w4a32c8_q4_1_fp32_int8_qwen3_4b_att_out_n2560_k2560",
+                                  "w8a32c8_q8_0_fp32_int8_qwen3_4b_att_out_n2560_k2560"])
+def test_runner_definition_end_to_end(dev, tmp_path, name):
+    """One definition through ksq.runner: compilation (entry resolved), NMSE gate, exact checks,
+    timing, GGML comparison and test_results.json in the reference schema."""
+    import json
+    from ksq import runner
+    d = next(t for t in runner.definitions_table() if t["name"] == name)
+    r = runner.DefinitionRunner(warmup=1, iterations=3, log=lambda s: None).run(runner.spec_from_table(d),
+                                                                                  str(tmp_path))
+    assert r["compilation"]["success"]
+    assert r["correctness"]["passed"], r["correctness"]
+    for c in r["correctness"]["test_cases"]:
+        assert c["exact"]["quantize_bit_exact"] and c["exact"]["block_dots_bit_exact"]
+        assert c["exact"]["max_rel_err_vs_fp64"] <= TOL and c["nmse"] < 0.05
+    assert [b["config"] for b in r["performance"]["benchmarks"]] == ["single_token", "small_batch", "large_batch"]
+    assert all(b["tflops"] > 0 and "ggml" in b for b in r["performance"]["benchmarks"])
+    saved = json.load(open(tmp_path / "test_results.json"))
+    assert set(saved) >= {"attempt_id", "variant", "op_type", "tested_at", "spec", "compilation", "correctness",
+                          "performance"}
+
+
+def test_runner_native_spec(dev, tmp_path):
+    """The native W8A8C8 operator's spec.json form (kernel.entry_point, params defaults N = K = 7168)."""
+    from ksq import runner
+    spec = {"name": "w8a8c8_q8_0_q8_1", "kernel": {"file": "kernel.cu", "entry_point": "forward"},
+            "inputs": {"weight": {"dtype": "block_q8_0"}, "activation": {"dtype": "float32"}},
+            "params": {"M": {"type": "int"}, "N": {"default": 7168}, "K": {"default": 7168}},
+            "accuracy": {"metric": "nmse", "threshold": 0.05}}
+    r = runner.DefinitionRunner(warmup=1, iterations=2, log=lambda s: None).run(spec, str(tmp_path))
+    assert r["compilation"]["entry_point"] == "gemm_w8a8c8_q8_0_q8_1"
+    assert r["correctness"]["passed"], r["correctness"]
+
+
+# ------------------------------------------------------------------ split-K MFMA path
+@pytest.mark.parametrize("wtype,M,N,K", [(1, 32, 4096, 4096), (0, 16, 512, 7168), (4, 24, 1536, 5120),
+                                         (3, 40, 640, 2048), (5, 9, 300, 4096)])
+def test_mfma_split_k(dev, oracle, wtype, M, N, K):
+    """Small-M grids split along K (partials in the workspace, reduced in split order): the result
+    matches the oracle, repeats bit for bit, and is the same with a caller workspace of
+    ksq_gemm_workspace_size bytes as with the library pool."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(2200 + M)
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    wt, xt = _t(w, dev), _t(x, dev)
+    ops.set_path(2)
+    try:
+        y1 = ops.gemm(wtype, 0, wt, xt, M, N, K)
+        y2 = ops.gemm(wtype, 0, wt, xt, M, N, K)
+        nbytes = ops.workspace_size(wtype, 0, M, N, K)
+        assert nbytes >= M * (K // 32) * 36
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        y3 = ops.gemm(wtype, 0, wt, xt, M, N, K, workspace=ws)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_path(0)
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)
+    rows = np.arange(M) if M <= 16 else np.sort(g.choice(M, 12, replace=False))
+    ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x[rows]), w, len(rows), N, K)
+    assert _rel_err(y1.cpu().numpy()[rows], ref) <= TOL
