@@ -220,42 +220,50 @@ __device__ __forceinline__ void wave_copy_part(const uint8_t* g, uint8_t* dst, i
 }
 
 // C[m][row] = sum over the row's units, for m < MR.  KT = blocks per K tile (multiple of 8).
-// RPW weight rows per workgroup; the 4 / RPW waves of a row split its units (and its
-// weight copy) and add their partial sums through LDS at the end.
+// RPW weight rows per workgroup: with 1 or 2 the 4 / RPW waves of a row split its units
+// (and its weight copy) and add their partial sums through LDS at the end; with 8 every
+// wave owns 2 rows, so each activation block it reads serves both.
 // AS: the activations are block_q8s (fp32 scale, no sum) instead of block_q8_1.
 // Ain: block_q8_1 / block_q8s bytes [MR][nb] (kAL2, kADMA) or fp32 [MR][32 nb] (kAFQ).
 template <int WT, int MR, int AMODE, bool AS, int RPW>
 __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
                                                        float* __restrict__ C, int N, int nb, int KT, int ldc) {
-    static_assert(RPW == 1 || RPW == 2 || RPW == 4, "1, 2 or 4 rows per workgroup");
-    constexpr int WPR = 4 / RPW;  // waves per row
+    static_assert(RPW == 1 || RPW == 2 || RPW == 4 || RPW == 8, "1, 2, 4 or 8 rows per workgroup");
+    constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
+    constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ float red[4][MR];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int rloc = wave / WPR, part = wave % WPR;
-    const int row = blockIdx.x * RPW + rloc;
+    const int row0 = blockIdx.x * RPW + rloc * VR;   // this wave's rows: row0 .. row0 + VR - 1
     constexpr bool kq = is_kquant(WT);
     const uint8_t* A = (const uint8_t*)Ain;
     const size_t RB = kq ? (size_t)(nb / 8) * Fmt<WT>::span : (size_t)nb * block_bytes(WT);  // row bytes
     const int tile_w = kq ? (KT / 8) * Fmt<WT>::span : KT * block_bytes(WT);
     const int wpitch = ((tile_w + kTileSlack + 15) & ~15);
     const int apitch = ((KT * kQ81Bytes + 16 + 15) & ~15);
-    uint8_t* wreg = smem + rloc * wpitch;
+    uint8_t* wreg = smem + rloc * VR * wpitch;
     uint8_t* areg = smem + RPW * wpitch;  // [MR][apitch]: the K tile's activation blocks, 36 B each
 
-    float acc[MR];
+    float acc[VR][MR];
 #pragma unroll
-    for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = 0.0f;
 
     for (int kt0 = 0; kt0 < nb; kt0 += KT) {
         const int kt = (nb - kt0) < KT ? (nb - kt0) : KT;
-        uint8_t* wt = nullptr;
-        if (row < N) {
-            const size_t off = kq ? (size_t)(kt0 / 8) * Fmt<WT>::span : (size_t)kt0 * block_bytes(WT);
-            const int bytes = kq ? (kt / 8) * Fmt<WT>::span : kt * block_bytes(WT);
-            const uint8_t* g = W + (size_t)row * RB + off;
-            wt = wreg + ((uintptr_t)g & 15);
-            wave_copy_part(g, wt, bytes, part, WPR, lane);
+        uint8_t* wt[VR];
+#pragma unroll
+        for (int v = 0; v < VR; v++) {
+            wt[v] = nullptr;
+            if (row0 + v < N) {
+                const size_t off = kq ? (size_t)(kt0 / 8) * Fmt<WT>::span : (size_t)kt0 * block_bytes(WT);
+                const int bytes = kq ? (kt / 8) * Fmt<WT>::span : kt * block_bytes(WT);
+                const uint8_t* g = W + (size_t)(row0 + v) * RB + off;
+                wt[v] = wreg + v * wpitch + ((uintptr_t)g & 15);
+                wave_copy_part(g, wt[v], bytes, part, WPR, lane);
+            }
         }
         // per activation row, the byte offset of its first staged block inside its LDS region
         int ashift[MR];
@@ -289,97 +297,113 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                 for (int i = 0; i < 9; i++) dst[i] = blk[i];
             }
         }
+        const int ustep = 64 * WPR, u0 = part * 64 + lane;
+        auto load_act = [&](int u, uint32_t (&av)[MR][9]) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const uint32_t* ap = (AMODE == kAL2) ? (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes)
+                                                     : (const uint32_t*)(areg + m * apitch + ashift[m] + u * kQ81Bytes);
+#pragma unroll
+                for (int i = 0; i < 9; i++) av[m][i] = ap[i];
+            }
+        };
+        // LDS written by other waves (shared activations, or a row split over waves) needs the
+        // workgroup barrier; a wave that reads only the row it copied itself just waits for its
+        // own loads
+        constexpr bool shared_lds = (AMODE != kAL2) || (WPR > 1);
         wait_vmem();
-        __syncthreads();
+        if constexpr (shared_lds) __syncthreads();
 
-        if (row < N) {
-            auto act = [&](int m, int u) -> const uint32_t* {
-                if constexpr (AMODE == kAL2) return (const uint32_t*)(A + ((size_t)m * nb + kt0 + u) * kQ81Bytes);
-                else return (const uint32_t*)(areg + m * apitch + ashift[m] + u * kQ81Bytes);
-            };
-            for (int u = part * 64 + lane; u < kt; u += 64 * WPR) {   // unit u: activation block kt0 + u
-                if constexpr (!kq) {
-                    const uint8_t* blk = wt + u * block_bytes(WT);
-                    const float dw = f16_to_f32(read_u16(blk));
-                    float mw = 0.0f;
-                    if constexpr (WT == kWQ41 || WT == kWQ51) mw = f16_to_f32(read_u16(blk + 2));
+        // one unit u (activation block kt0 + u) of weight row row0 + v for all MR activation rows
+        auto unit = [&](int v, int u, const uint32_t (&av)[MR][9]) {
+            if constexpr (!kq) {
+                const uint8_t* blk = wt[v] + u * block_bytes(WT);
+                const float dw = f16_to_f32(read_u16(blk));
+                float mw = 0.0f;
+                if constexpr (WT == kWQ41 || WT == kWQ51) mw = f16_to_f32(read_u16(blk + 2));
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const uint32_t* a = av[m];
+                    const float da = AS ? __builtin_bit_cast(float, a[0]) : f16_to_f32(a[0] & 0xFFFFu);
+                    const int sumi = unit_sumi_legacy<WT>(blk, a);
+                    // block formulas of gemm_reference.h:216 / :259 and gemm_quant_formats.cuh:148,
+                    // :207, :266 (the last two without the reference's /4 on the m*s term)
+                    if constexpr (WT == kWQ40) {
+                        acc[v][m] += dw * (da * (float)sumi - 8.0f * f16_to_f32(a[0] >> 16));
+                    } else if constexpr (WT == kWQ80) {
+                        acc[v][m] += AS ? dw * da * (float)sumi : (float)sumi * da * dw;
+                    } else if constexpr (WT == kWQ50) {
+                        acc[v][m] += dw * (da * (float)sumi - 16.0f * f16_to_f32(a[0] >> 16));
+                    } else {
+                        acc[v][m] += dw * da * (float)sumi + mw * f16_to_f32(a[0] >> 16);
+                    }
+                }
+            } else {
+                const uint8_t* sb = wt[v] + (u >> 3) * Fmt<WT>::span;
+                const int j = u & 7;
+                if constexpr (WT == kWQ4K) {
+                    uint32_t hd[1], sc3[3];
+                    read_words<1>(sb, hd);
+                    read_words<3>(sb + 4, sc3);
+                    int sc, mn;
+                    q4_K_scale_min(j, sc3, sc, mn);
+                    const float d = f16_to_f32(hd[0] & 0xFFFFu), dmin = f16_to_f32(hd[0] >> 16);
 #pragma unroll
                     for (int m = 0; m < MR; m++) {
-                        const uint32_t* ap = act(m, u);
-                        uint32_t a[9];
-#pragma unroll
-                        for (int i = 0; i < 9; i++) a[i] = ap[i];
-                        const float da = AS ? __builtin_bit_cast(float, a[0]) : f16_to_f32(a[0] & 0xFFFFu);
-                        const int sumi = unit_sumi_legacy<WT>(blk, a);
-                        // block formulas of gemm_reference.h:216 / :259 and gemm_quant_formats.cuh:148,
-                        // :207, :266 (the last two without the reference's /4 on the m*s term)
-                        if constexpr (WT == kWQ40) {
-                            acc[m] += dw * (da * (float)sumi - 8.0f * f16_to_f32(a[0] >> 16));
-                        } else if constexpr (WT == kWQ80) {
-                            acc[m] += AS ? dw * da * (float)sumi : (float)sumi * da * dw;
-                        } else if constexpr (WT == kWQ50) {
-                            acc[m] += dw * (da * (float)sumi - 16.0f * f16_to_f32(a[0] >> 16));
-                        } else {
-                            acc[m] += dw * da * (float)sumi + mw * f16_to_f32(a[0] >> 16);
-                        }
+                        const uint32_t* a = av[m];
+                        const int sumi = unit_sumi_q4_K(sb, j, a);
+                        acc[v][m] += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc * sumi)) -
+                                  dmin * (f16_to_f32(a[0] >> 16) * (float)mn);
                     }
                 } else {
-                    const uint8_t* sb = wt + (u >> 3) * Fmt<WT>::span;
-                    const int j = u & 7;
-                    if constexpr (WT == kWQ4K) {
-                        uint32_t hd[1], sc3[3];
-                        read_words<1>(sb, hd);
-                        read_words<3>(sb + 4, sc3);
-                        int sc, mn;
-                        q4_K_scale_min(j, sc3, sc, mn);
-                        const float d = f16_to_f32(hd[0] & 0xFFFFu), dmin = f16_to_f32(hd[0] >> 16);
+                    const uint32_t scw = read_u16(sb + 192 + 2 * j);
+                    const int sc0 = (int)(int8_t)(scw & 0xFFu), sc1 = (int)(int8_t)(scw >> 8);
+                    const float d = f16_to_f32(read_u16(sb + 208));
 #pragma unroll
-                        for (int m = 0; m < MR; m++) {
-                            const uint32_t* ap = act(m, u);
-                            uint32_t a[9];
-#pragma unroll
-                            for (int i = 0; i < 9; i++) a[i] = ap[i];
-                            const int sumi = unit_sumi_q4_K(sb, j, a);
-                            acc[m] += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc * sumi)) -
-                                      dmin * (f16_to_f32(a[0] >> 16) * (float)mn);
-                        }
-                    } else {
-                        const uint32_t scw = read_u16(sb + 192 + 2 * j);
-                        const int sc0 = (int)(int8_t)(scw & 0xFFu), sc1 = (int)(int8_t)(scw >> 8);
-                        const float d = f16_to_f32(read_u16(sb + 208));
-#pragma unroll
-                        for (int m = 0; m < MR; m++) {
-                            const uint32_t* ap = act(m, u);
-                            uint32_t a[9];
-#pragma unroll
-                            for (int i = 0; i < 9; i++) a[i] = ap[i];
-                            int is0, is1;
-                            unit_sumi_q6_K(sb, j, a, is0, is1);
-                            acc[m] += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc0 * is0 + sc1 * is1));
-                        }
+                    for (int m = 0; m < MR; m++) {
+                        const uint32_t* a = av[m];
+                        int is0, is1;
+                        unit_sumi_q6_K(sb, j, a, is0, is1);
+                        acc[v][m] += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc0 * is0 + sc1 * is1));
                     }
                 }
             }
+        };
+
+        if (row0 < N) {
+            for (int u = u0; u < kt; u += ustep) {
+                uint32_t av[MR][9];
+                load_act(u, av);
+#pragma unroll
+                for (int v = 0; v < VR; v++)
+                    if (row0 + v < N) unit(v, u, av);
+            }
         }
-        if (kt0 + KT < nb) __syncthreads();  // the next tile overwrites LDS
+        if (shared_lds && kt0 + KT < nb) __syncthreads();  // the next tile overwrites LDS
     }
 #pragma unroll
-    for (int m = 0; m < MR; m++) acc[m] = wave_sum(acc[m]);
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = wave_sum(acc[v][m]);
     if constexpr (WPR > 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int m = 0; m < MR; m++) red[wave][m] = acc[m];
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[0][m];
         }
         __syncthreads();
         if (part == 0) {
 #pragma unroll
             for (int m = 0; m < MR; m++)
-                for (int p = 1; p < WPR; p++) acc[m] += red[wave + p][m];
+                for (int p = 1; p < WPR; p++) acc[0][m] += red[wave + p][m];
         }
     }
-    if (row < N && part == 0 && lane == 0) {
+    if (part == 0 && lane == 0) {
 #pragma unroll
-        for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row] = acc[m];
+        for (int v = 0; v < VR; v++)
+            if (row0 + v < N) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+            }
     }
 }
 
@@ -404,7 +428,16 @@ static size_t gemv_lds_bytes(int wtype, int mr, int KT, int amode, int rpw) {
 #endif
 constexpr int kGemvMinWGs = KSQ_GEMV_MIN_WGS;
 
-static int pick_rpw(int N) {
+// Staging modes (bit AMODE) that use 8 rows per workgroup (2 rows per wave) when N allows.
+// Only the fused mode does: it halves the quantisation every workgroup repeats.  For the DMA
+// mode the halved activation traffic did not pay for the halved grid (measured over the 87
+// definitions: neutral at N = 4096, 8-24% slower at N >= 9728 with 8 activation rows).
+#ifndef KSQ_GEMV_RPW8_MODES
+#define KSQ_GEMV_RPW8_MODES 0x4
+#endif
+
+static int pick_rpw(int N, int amode) {
+    if (((KSQ_GEMV_RPW8_MODES >> amode) & 1) && (N + 7) / 8 >= kGemvMinWGs) return 8;
     if ((N + 3) / 4 >= kGemvMinWGs) return 4;
     if ((N + 1) / 2 >= kGemvMinWGs) return 2;
     return 1;
@@ -431,6 +464,9 @@ template <int WT, int MR, int AMODE, bool AS>
 static hipError_t row_launch_rpw(int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
                                  hipStream_t s) {
     switch (rpw) {
+        case 8:
+            if constexpr ((KSQ_GEMV_RPW8_MODES >> AMODE) & 1) return row_launch<WT, MR, AMODE, AS, 8>(W, A, C, N, nb, KT, ldc, s);
+            else return hipErrorNotSupported;
         case 4: return row_launch<WT, MR, AMODE, AS, 4>(W, A, C, N, nb, KT, ldc, s);
         case 2: return row_launch<WT, MR, AMODE, AS, 2>(W, A, C, N, nb, KT, ldc, s);
         default: return row_launch<WT, MR, AMODE, AS, 1>(W, A, C, N, nb, KT, ldc, s);
@@ -480,7 +516,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
         const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows ? kAL2 : kADMA);
         // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
-        const int rpw = pick_rpw(N);
+        const int rpw = pick_rpw(N, AMODE);
         int KT = (nb + 7) & ~7;
         while (KT > 64 && gemv_lds_bytes(wtype, mr, KT, AMODE, rpw) > kGemvLdsBudget) KT = ((KT / 2) + 63) & ~63;
         const void* Am = QUANT ? (const void*)((const uint8_t*)A + (size_t)m0 * nb * kQ81Bytes)
@@ -507,11 +543,14 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 #define KSQ_GEMV_FUSED_MAX_WORK 420000ll
 #endif
 
-bool gemv_fused_profitable(int M, int N, int K) {
+bool gemv_fused_profitable(int wtype, int M, int N, int K) {
     if (M < 1 || M > kMaxFusedRows) return false;
-    const int rpw = pick_rpw(N);
+    const int rpw = pick_rpw(N, kAFQ);
+    const int nb = K / 32, KT = (nb + 7) & ~7;
+    // one K tile only: with several, each tile's quantisation would wait for the previous tile
+    if (gemv_lds_bytes(wtype, M, KT, kAFQ, rpw) > kGemvLdsBudget) return false;
     const long long wgs = (N + rpw - 1) / rpw;
-    return (long long)M * wgs * (K / 32) <= KSQ_GEMV_FUSED_MAX_WORK;
+    return (long long)M * wgs * nb <= KSQ_GEMV_FUSED_MAX_WORK;
 }
 
 hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X, float* C, int M, int N, int K,

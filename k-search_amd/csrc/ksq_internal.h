@@ -30,7 +30,7 @@ hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X
                            hipStream_t s);
 // Whether launch_gemv_f32 beats quantise + launch_gemv for this shape (M <= 2 and a bounded
 // amount of repeated quantisation).
-bool gemv_fused_profitable(int M, int N, int K);
+bool gemv_fused_profitable(int wtype, int M, int N, int K);
 
 // Prefill GEMM on int8 MFMA (mul_mat_q family); returns hipErrorNotSupported
 // for shapes it does not tile.
