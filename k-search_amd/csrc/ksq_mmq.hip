@@ -337,46 +337,44 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
             }
         };
-        f32x4 eda[4], enc[4];  // row scales of the current (block, row tile), reused across its TN tiles
+        // The MFMA computes the transposed tile D[n][m] (A operand = weight fragment, B operand =
+        // activation fragment): lane l holds activation row m = l % 32 and the 16 weight rows
+        // n = 8*(r/4) + 4*(l/32) + r%4, so its activation scales are two scalars and its weight
+        // scales 16 floats that stay in registers across the TM row tiles of a block.
+        f32x4 edw[4];
         auto epilogue = [&](int b, int u, int i, int j, const i32x16& res) {
-            // 32x32 accumulator layout: column = lane % 32, row = 8*(r/4) + 4*(lane/32) + r%4
-            const int col = wn * 32 * TN + j * 32 + l32;
-            const int rowb = wm * 32 * TM + i * 32 + 4 * hi;
+            const int lm = wm * 32 * TM + i * 32 + l32;          // local activation row
+            const int nbase = wn * 32 * TN + j * 32 + 4 * hi;    // local weight row of r = 0
             if constexpr (DUMP) {
-                const int gn = n0 + col;
+                const int gm = m0 + lm;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
-                    const int gm = m0 + rowb + 8 * (r >> 2) + (r & 3);
+                    const int gn = n0 + nbase + 8 * (r >> 2) + (r & 3);
                     if (gm < M && gn < N)
                         dump[((size_t)gm * N + gn) * nb * S::SUB + (kb0 + b) * S::SUB + (u - b * S::SUB)] = res[r];
                 }
             } else {
-                const float dw = sDw[u][col];
-                if (j == 0) {
+                if (i == 0) {
 #pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        eda[q] = *(const f32x4*)&sDa[b][rowb + 8 * q];
-                        enc[q] = *(const f32x4*)&sNc[b][rowb + 8 * q];
-                    }
+                    for (int q = 0; q < 4; q++) edw[q] = *(const f32x4*)&sDw[u][nbase + 8 * q];
                 }
+                const float da = sDa[b][lm], nc = sNc[b][lm];
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const f32x4 da = eda[q];
-                    const f32x4 nc = enc[q];
 #pragma unroll
                     for (int p = 0; p < 4; p++) {
                         // copy the element out first: bit_cast of an ext-vector element lvalue
                         // reads element 0 with this compiler
                         const int e = res[4 * q + p];
                         const float f = __builtin_bit_cast(float, e);
-                        acc[i][j][4 * q + p] = fmaf(dw, fmaf(f, da[p], nc[p]), acc[i][j][4 * q + p]);
+                        acc[i][j][4 * q + p] = fmaf(edw[q][p], fmaf(f, da, nc), acc[i][j][4 * q + p]);
                     }
                 }
             }
         };
 
-        // KB*SUB*TM*TN MFMAs per K step; step q = ((b*SUB + h)*TM + i)*TN + j.  For Q6_K the two
-        // 16-element sub-blocks of a block are separate MFMAs whose B fragment keeps only the
+        // KB*SUB*TN*TM MFMAs per K step; step q = ((b*SUB + h)*TN + j)*TM + i.  For Q6_K the two
+        // 16-element sub-blocks of a block are separate MFMAs whose weight fragment keeps only the
         // lanes holding that half (k = 16*hi ..).  The MFMA of step q+1 is issued before the
         // epilogue of step q.
         constexpr int SUBN = S::SUB;
@@ -384,7 +382,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         i32x4 af[TM], bf[TN];
         auto mfma_step = [&](int q) -> i32x16 {
             const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
-            const int i = (q / TN) % TM, j = q % TN;
+            const int j = (q / TM) % TN, i = q % TM;
             if (q % (SUBN * TM * TN) == 0) {
 #pragma unroll
                 for (int ii = 0; ii < TM; ii++) af[ii] = frag_a(b, ii);
@@ -395,13 +393,13 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             if constexpr (SUBN == 2) {
                 if (hi != h) bb = i32x4{0, 0, 0, 0};
             }
-            return __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bb, bias, 0, 0, 0);
+            return __builtin_amdgcn_mfma_i32_32x32x32_i8(bb, af[i], bias, 0, 0, 0);
         };
         i32x16 cur = mfma_step(0);
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
             const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
-            const int i = (q / TN) % TM, j = q % TN;
+            const int j = (q / TM) % TN, i = q % TM;
             i32x16 nxt = bias;
             if (q + 1 < NQ) nxt = mfma_step(q + 1);
             epilogue(b, b * SUBN + h, i, j, cur);
@@ -409,9 +407,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         }
 
         if constexpr (S::side && !DUMP) {
-            // side term: acc += sum_k (-s_a[m][k]) * f[n][k] over the staged blocks, f = d_w (Q4_0,
-            // Q5_0), -m (Q4_1, Q5_1) or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA over 8
-            // block slots, exact products
+            // side term: acc[n][m] += sum_k f[n][k] * (-s_a[m][k]) over the staged blocks, f = d_w
+            // (Q4_0, Q5_0), -m (Q4_1, Q5_1) or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA
+            // over 8 block slots, exact products
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 32 * TM + i * 32 + l32][4 * hi];
@@ -419,10 +417,10 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 for (int j = 0; j < TN; j++) {
                     const int wrow = wn * 32 * TN + j * 32 + l32;
                     const f16x4 dw4 = *(const f16x4*)&sDwH[wrow][4 * hi];
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dw4, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(dw4, sa4, acc[i][j], 0, 0, 0);
                     if constexpr (WT == kWQ4K) {
                         const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * hi];
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(sa4, dl4, acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(dl4, sa4, acc[i][j], 0, 0, 0);
                     }
                 }
             }
@@ -430,26 +428,57 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         __syncthreads();
     }
 
-    if constexpr (!DUMP) {
+    if constexpr (MOE) {
+        // Gathered rows scatter-add into out[token][n]: route each wave's tile through LDS (the
+        // staging buffer is free after the last K step's barrier) so that the atomics of one
+        // instruction cover 32 consecutive columns of one token instead of 32 tokens.
+        constexpr int kTP = 33;   // padded row pitch (floats) of the [32 m][32 n] transpose
+        static_assert(4 * 32 * kTP * 4 <= BM * T::APitch, "transpose scratch fits the activation tile");
+        float* tp = (float*)sA + wave * 32 * kTP;
         constexpr float out_scale = S::out_scale;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
-                const int gn = n0 + wn * 32 * TN + j * 32 + l32;
-                const int rowb = m0 + wm * 32 * TM + i * 32 + 4 * hi;
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int gm = rowb + 8 * (r >> 2) + (r & 3);
-                    if (gm < M && gn < N) {
-                        if constexpr (MOE) {
-                            const int ent = sRows[gm];
-                            const float v = out_scale * acc[i][j][r] * moe.weights[ent];
-                            if (moe.scratch) moe.scratch[(size_t)ent * N + gn] = v;
-                            else unsafeAtomicAdd(C + (size_t)(ent / moe.top_k) * N + gn, v);
-                        } else {
-                            C[(size_t)gm * N + gn] = out_scale * acc[i][j][r];
-                        }
+                for (int r = 0; r < 16; r++) tp[l32 * kTP + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[i][j][r];
+                __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes done
+                __builtin_amdgcn_wave_barrier();
+                const int gn = n0 + wn * 32 * TN + j * 32 + l32;
+#pragma unroll
+                for (int p = 0; p < 16; p++) {
+                    const int lm = wm * 32 * TM + i * 32 + 2 * p + hi;   // local activation row
+                    if (lm < M && gn < N) {
+                        const int ent = sRows[lm];
+                        const float v = out_scale * tp[(2 * p + hi) * kTP + l32] * moe.weights[ent];
+                        if (moe.scratch) moe.scratch[(size_t)ent * N + gn] = v;
+                        else unsafeAtomicAdd(C + (size_t)(ent / moe.top_k) * N + gn, v);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+    } else if constexpr (!DUMP) {
+        constexpr float out_scale = S::out_scale;
+        const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int lm = wm * 32 * TM + i * 32 + l32;
+                const int gm = m0 + lm;
+                if (gm >= M) continue;
+                const int nbase = n0 + wn * 32 * TN + j * 32 + 4 * hi;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int gn = nbase + 8 * q;   // this lane's 4 consecutive outputs gn .. gn + 3
+                    if (vec_ok && gn + 3 < N) {
+                        *(f32x4*)(C + (size_t)gm * N + gn) =
+                            f32x4{out_scale * acc[i][j][4 * q], out_scale * acc[i][j][4 * q + 1],
+                                  out_scale * acc[i][j][4 * q + 2], out_scale * acc[i][j][4 * q + 3]};
+                    } else {
+#pragma unroll
+                        for (int p = 0; p < 4; p++)
+                            if (gn + p < N) C[(size_t)gm * N + gn + p] = out_scale * acc[i][j][4 * q + p];
                     }
                 }
             }
@@ -475,10 +504,14 @@ static int grid_wgs(int M, int N) {
     return ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
 }
 
+// Measured on MI355X (M = 32 .. 2048, N = 4096 / 14336, K = 4096): the 128 x 128 tile is
+// best for the nibble-staged Q4_0 / Q4_1 from M = 256 on (split along K when its grid is
+// small); the byte-staged types (Q8_0, Q5_x, Q6_K) need 86 KB of LDS for it, one workgroup
+// per CU, and like Q4_K run best on 128 x 64 while that grid covers the CUs, else 64 x 64.
 static int pick_config(int wtype, int M, int N) {
     if (g_mmq_config && !(is_kquant(wtype) && g_mmq_config == 4)) return g_mmq_config;
     constexpr int kCUs = 256;
-    if (grid_wgs<TileL>(M, N) >= 2 * kCUs) return 1;
+    if ((wtype == kWQ40 || wtype == kWQ41) && M >= 256) return 1;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     return 3;
 }
