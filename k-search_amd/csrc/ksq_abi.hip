@@ -106,7 +106,8 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
 
 // The MFMA GEMM above 8 rows (or when forced), the v_dot4 decode kernels otherwise.
 bool use_mmq(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
-    return (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, a_aligned16) && (g_path == 2 || M > 8);
+    return (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, a_aligned16) &&
+           (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K));
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -212,7 +213,8 @@ int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
 
 size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const bool mmq_possible = (g_path != 1) && (g_path == 2 || M > 8) && (K % 256) == 0;
+    const bool mmq_possible =
+        (g_path != 1) && (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K)) && (K % 256) == 0;
     return gemm_ws(wtype, atype, M, N, K, mmq_possible).total;
 }
 

@@ -77,24 +77,55 @@ __device__ __forceinline__ uint32_t clamp_i8(int32_t q) {
 // (kernelevalplus-main/include/quantize.h:165-193): sequential fp32 sum,
 // IEEE d = amax/127, id = 1/d (fp32 d), q = clamp(roundf(x*id)), ds = half2(d, sum).
 // out[0] = ds word, out[1..8] = the 32 quants.
+//
+// Two paths with identical results.  When the sum is finite every input is finite, so
+// max|x| is a plain v_max3 reduction; when 1/d is finite as well, |x * id| <= 127 * (1 + 2^-22),
+// and roundf(y) = trunc(y + copysign(0.49999997f, y)) there (0.49999997f = the float below
+// 0.5: the sum is exact or rounds away from the next integer, checked exhaustively on the
+// CPU over every float in [0.25, 128]), so each quant is mul, bfi, add, cvt with no clamp
+// (|q| <= 127).  Blocks holding inf / NaN, or so small that 1/d overflows, take the general
+// path: the reference's comparison-based max and roundf with out-of-range -> INT32_MIN.
 __device__ __forceinline__ void quantize_block_q8_1(const float* v, uint32_t* out) {
 #pragma clang fp contract(off)
-    float amax = 0.0f, sum = 0.0f;
+    float sum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-        const float a = fabsf(v[j]);
-        amax = (amax < a) ? a : amax;
-        sum += v[j];
+    for (int j = 0; j < 32; j++) sum += v[j];
+    const bool finite = __builtin_isfinite(sum);
+    float amax = 0.0f;
+    if (finite) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) amax = __builtin_fmaxf(amax, fabsf(v[j]));
+    } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float a = fabsf(v[j]);
+            amax = (amax < a) ? a : amax;
+        }
     }
     const float d = amax / 127.0f;
     const float id = (d > 0.0f) ? 1.0f / d : 0.0f;
     out[0] = f32_to_f16(d) | (f32_to_f16(sum) << 16);
+    if (finite && __builtin_isfinite(id)) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        uint32_t packed = 0;
+        for (int j = 0; j < 8; j++) {
+            int q[4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) packed |= clamp_i8(round_to_i32(v[4 * j + t] * id)) << (8 * t);
-        out[1 + j] = packed;
+            for (int t = 0; t < 4; t++) {
+                const float y = v[4 * j + t] * id;
+                q[t] = (int)(y + __builtin_copysignf(0.49999997f, y));
+            }
+            const uint32_t lo = (uint32_t)__builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
+            const uint32_t hi = (uint32_t)__builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
+            out[1 + j] = __builtin_amdgcn_perm(hi, lo, 0x06040200u);  // bytes 0, 2 of lo, then of hi
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) packed |= clamp_i8(round_to_i32(v[4 * j + t] * id)) << (8 * t);
+            out[1 + j] = packed;
+        }
     }
 }
 

@@ -36,12 +36,15 @@ bool gemv_fused_profitable(int wtype, int M, int N, int K);
 // for shapes it does not tile.
 // a_aligned16: the quantised activations the GEMM will read are 16-byte aligned.
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16);
+// Whether the MFMA kernel is expected to beat the decode kernel for this shape (M > 8, or
+// a large matrix with M >= 5 .. 7 by the measured crossovers).
+bool mmq_preferred(int wtype, int M, int N, int K);
 // Number of K splits launch_mmq uses for this shape (1: none).  With splits > 1 it needs
 // `partials`, splits * M * N floats of device scratch.
 int mmq_splits(int wtype, int M, int N, int K);
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       float* partials, hipStream_t s);
-// Force one of the MFMA tile configurations (1..4) or automatic choice (0); -1 if out of range.
+// Force one of the MFMA tile configurations (1..5) or automatic choice (0); -1 if out of range.
 int mmq_set_config(int c);
 
 // Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /

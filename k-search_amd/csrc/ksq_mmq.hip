@@ -490,11 +490,12 @@ using TileL = Tile<128, 128, 8, 2, 2, 2>;   // large M: 64 x 64 per wave
 using TileN = Tile<128, 64, 8, 2, 1, 2>;    // half the columns per workgroup: twice the workgroups
 using TileS = Tile<64, 64, 8, 1, 1, 3>;     // 32 x 32 per wave, 4x the workgroups of TileL
 using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, more resident workgroups
+using TileT = Tile<32, 128, 8, 1, 1, 3>;    // skinny: M <= 32, the four waves side by side along N
 
 static int g_mmq_config = 0;  // 0 = automatic
 
 int mmq_set_config(int c) {
-    if (c < 0 || c > 4) return -1;
+    if (c < 0 || c > 5) return -1;
     g_mmq_config = c;
     return 0;
 }
@@ -504,16 +505,35 @@ static int grid_wgs(int M, int N) {
     return ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
 }
 
-// Measured on MI355X (M = 32 .. 2048, N = 4096 / 14336, K = 4096): the 128 x 128 tile is
-// best for the nibble-staged Q4_0 / Q4_1 from M = 256 on (split along K when its grid is
+// Measured on MI355X (M = 3 .. 2048, N = 512 .. 18944, K = 2560 .. 7168): the 128 x 128 tile
+// is best for the nibble-staged Q4_0 / Q4_1 from M = 256 on (split along K when its grid is
 // small); the byte-staged types (Q8_0, Q5_x, Q6_K) need 86 KB of LDS for it, one workgroup
 // per CU, and like Q4_K run best on 128 x 64 while that grid covers the CUs, else 64 x 64.
+// Nibble types with M <= 32 run best on 32 x 128 (e.g. Q4_0 N = 14336, K = 4096: 21.1 vs
+// 25.2 us at M = 8, 23.7 vs 26.1 us at M = 32); Q8_0 does not gain from it.
 static int pick_config(int wtype, int M, int N) {
     if (g_mmq_config && !(is_kquant(wtype) && g_mmq_config == 4)) return g_mmq_config;
     constexpr int kCUs = 256;
-    if ((wtype == kWQ40 || wtype == kWQ41) && M >= 256) return 1;
+    const bool nib = (wtype == kWQ40 || wtype == kWQ41);
+    if (nib && M >= 256) return 1;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
+    if (nib && M <= 32) return 5;
     return 3;
+}
+
+// Below M = 9 the decode kernel usually wins; its time grows with M * N * K while the
+// MFMA kernel's stays near its ~12 us floor, so for large matrices the MFMA kernel takes
+// over earlier.  Crossovers measured on MI355X with block_q8_1 activations (GEMV vs
+// 32 x 128 tile, us): Q4_0 N = 8192 K = 4096 at M = 7 (17.7 vs 14.5), N = 11008 / 14336
+// K = 4096 and Q4_1 N = 18944 K = 3584 at M = 5 (17.3 vs 16.8, 21.7 vs 20.5, 25.2 vs 20.6),
+// but not Q4_0 N = K = 4096 at M = 8 (11.1 vs 12.0); Q8_0 N = 14336 K = 4096 at M = 7
+// (37.9 vs 28.6, 64 x 64 tile).
+bool mmq_preferred(int wtype, int M, int N, int K) {
+    if (M > 8) return true;
+    const double nk = (double)N * (double)K;
+    if (wtype == kWQ40 || wtype == kWQ41) return (M >= 7 && nk >= 3.0e7) || (M >= 5 && nk >= 4.4e7);
+    if (wtype == kWQ80) return M >= 7 && nk >= 5.0e7;
+    return false;
 }
 
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
@@ -581,6 +601,7 @@ static int split_cfg(int cfg, int M, int N, int K) {
         case 1: return split_for<TileL>(M, N, K);
         case 2: return split_for<TileN>(M, N, K);
         case 3: return split_for<TileS>(M, N, K);
+        case 5: return split_for<TileT>(M, N, K);
         default: return split_for<TileK4>(M, N, K);
     }
 }
@@ -598,6 +619,7 @@ static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, con
         case 1: return launch_t<TileL, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
         case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
         case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
+        case 5: return launch_t<TileT, DUMP, false>(wtype, afmt, grid(32, 128), W, A, C, dump, M, N, nb, mt, s);
         default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
     }
 }

@@ -5,65 +5,81 @@
 // __float2int_rn, the CPU reference rounds half away from zero with roundf, and
 // this kernel follows the CPU reference bit for bit.
 //
-// Layout of the work: one thread per 32-float block, 256 blocks (32 KiB of
-// input) per workgroup.  Input is read with coalesced 16-byte loads into LDS
-// (33-float row pitch, so the per-thread block reads below are conflict free),
-// each thread quantises its block from LDS (the sum must be the sequential
-// left-to-right fp32 sum, so one lane owns a whole block), and the 36-byte
-// results go back out through LDS as coalesced dword stores.
+// Layout of the work: one lane per 32-float block; each wave owns 64 consecutive blocks
+// (8 KiB of input) and works alone (no workgroup barrier, so the waves of a workgroup do
+// not wait for each other's loads).  The wave reads its input with coalesced 16-byte
+// loads into its own LDS region (33-float row pitch, so the per-lane block reads below
+// are conflict free), each lane quantises its block from LDS (the sum must be the
+// sequential left-to-right fp32 sum, so one lane owns a whole block), and the 36-byte
+// results go back out through the same LDS region as coalesced dword stores.
 #include "ksq_device.h"
 #include "ksq_internal.h"
 
 namespace ksq {
 
-constexpr int kQBlocksPerWG = 256;
+constexpr int kQWaves = 4;                       // waves per workgroup
+constexpr int kQBlocksPerWG = 64 * kQWaves;
 constexpr int kQPitch = 33;  // floats per staged block
+
+// LDS written and read back by lanes of the same wave: wait for this wave's LDS
+// operations, then keep the compiler from moving LDS accesses across the point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+}
 
 // Q8S = false: block_q8_1 (quantize_row_q8_1_ref); true: block_q8s (the native W8A8C8
 // operator's rules).  Both are 36-byte blocks of 9 dwords.
 template <bool Q8S>
-__global__ __launch_bounds__(256) void quantize_q8_1_kernel(const float* __restrict__ x,
-                                                            uint8_t* __restrict__ y, int64_t nblocks) {
-    __shared__ float stage[kQBlocksPerWG * kQPitch];
-    const int t = threadIdx.x;
-    const int64_t blk0 = (int64_t)blockIdx.x * kQBlocksPerWG;
-    const int nblk = (int)((nblocks - blk0) < kQBlocksPerWG ? (nblocks - blk0) : kQBlocksPerWG);
+__global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float* __restrict__ x,
+                                                                     uint8_t* __restrict__ y, int64_t nblocks) {
+    __shared__ float stage_all[kQWaves][64 * kQPitch];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float* stage = stage_all[w];
+    const int64_t blk0 = ((int64_t)blockIdx.x * kQWaves + w) * 64;
+    if (blk0 >= nblocks) return;
+    const int nblk = (int)((nblocks - blk0) < 64 ? (nblocks - blk0) : 64);
 
-    // 256 blocks x 8 float4 = 2048 float4; thread t moves float4 t + 256*j.
+    // 64 blocks x 8 float4 = 512 float4; lane l moves float4 l + 64*j.
     const f32x4* src = (const f32x4*)(x + blk0 * 32);
+    f32x4 in[8];
 #pragma unroll
     for (int j = 0; j < 8; j++) {
-        const int idx = t + 256 * j;
+        const int idx = lane + 64 * j;
+        if (idx < nblk * 8) in[j] = __builtin_nontemporal_load(src + idx);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int idx = lane + 64 * j;
         if (idx < nblk * 8) {
-            const f32x4 v = __builtin_nontemporal_load(src + idx);
             float* dst = stage + (idx >> 3) * kQPitch + (idx & 7) * 4;
-            dst[0] = v.x;
-            dst[1] = v.y;
-            dst[2] = v.z;
-            dst[3] = v.w;
+            dst[0] = in[j].x;
+            dst[1] = in[j].y;
+            dst[2] = in[j].z;
+            dst[3] = in[j].w;
         }
     }
-    __syncthreads();
+    wave_lds_sync();
 
     uint32_t q[9];
-    if (t < nblk) {
+    if (lane < nblk) {
         float v[32];
 #pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = stage[t * kQPitch + j];
+        for (int j = 0; j < 32; j++) v[j] = stage[lane * kQPitch + j];
         if constexpr (Q8S) quantize_block_q8s(v, q);
         else quantize_block_q8_1(v, q);
     }
-    __syncthreads();
-    uint32_t* ostage = (uint32_t*)stage;  // 256 x 9 dwords, odd pitch: conflict free
-    if (t < nblk) {
+    wave_lds_sync();
+    uint32_t* ostage = (uint32_t*)stage;  // 64 x 9 dwords, odd pitch: conflict free
+    if (lane < nblk) {
 #pragma unroll
-        for (int j = 0; j < 9; j++) ostage[t * 9 + j] = q[j];
+        for (int j = 0; j < 9; j++) ostage[lane * 9 + j] = q[j];
     }
-    __syncthreads();
+    wave_lds_sync();
     uint32_t* dst = (uint32_t*)(y + blk0 * 36);
 #pragma unroll
     for (int j = 0; j < 9; j++) {
-        const int idx = t + 256 * j;
+        const int idx = lane + 64 * j;
         if (idx < nblk * 9) dst[idx] = ostage[idx];
     }
 }
@@ -73,9 +89,9 @@ hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, i
     if (nblocks == 0) return hipSuccess;
     const int64_t grid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
     if (afmt == kAQ8S)
-        hipLaunchKernelGGL(quantize_q8_1_kernel<true>, dim3((unsigned)grid), dim3(256), 0, s, x, y, nblocks);
+        hipLaunchKernelGGL(quantize_q8_1_kernel<true>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y, nblocks);
     else
-        hipLaunchKernelGGL(quantize_q8_1_kernel<false>, dim3((unsigned)grid), dim3(256), 0, s, x, y, nblocks);
+        hipLaunchKernelGGL(quantize_q8_1_kernel<false>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y, nblocks);
     return hipGetLastError();
 }
 

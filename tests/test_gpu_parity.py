@@ -64,6 +64,9 @@ def test_quantize_q8_1_bit_exact(dev, oracle):
             x[1, 8:32] = 0.0
             x[2, 32:64] *= 3e4
             x[2, 64:96] *= 1e-30
+            # the general path: an infinite input, and a block so small that 1/d overflows
+            x[0, 64] = np.inf
+            x[0, 96:128] *= 1e-39
         q = ops.quantize_q8_1(_t(x, dev))
         torch.cuda.synchronize()
         assert np.array_equal(q.cpu().numpy(), oracle.quantize_q8_1(x)), (M, K)
@@ -306,7 +309,7 @@ def test_moe_config4_sampled(dev, oracle):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
 @pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_mfma_tile_configs(dev, oracle, cfg, wtype):
     """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile)."""
@@ -322,6 +325,27 @@ def test_mfma_tile_configs(dev, oracle, cfg, wtype):
         _lib.lib().ksq_set_mmq_config(0)
     ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
     assert _rel_err(y, ref) <= TOL
+
+
+@pytest.mark.parametrize("wtype,M,N,K", [(0, 6, 11008, 4096), (4, 5, 18944, 3584), (1, 7, 14336, 4096),
+                                         (0, 8, 4096, 4096)])
+def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
+    """M = 5..8 on large matrices takes the MFMA kernel by default (the measured crossover), small
+    ones the decode kernel; either way the fp32 entry matches the oracle, with the library pool
+    and with a caller workspace of exactly ksq_gemm_workspace_size bytes."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(2300 + M)
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    wt, xt = _t(w, dev), _t(x, dev)
+    y1 = ops.gemm(wtype, 0, wt, xt, M, N, K)
+    ws = torch.empty(max(ops.workspace_size(wtype, 0, M, N, K), 1), dtype=torch.uint8, device=dev)
+    y2 = ops.gemm(wtype, 0, wt, xt, M, N, K, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+    ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
+    assert _rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
 # ------------------------------------------------------------------ Q4_1 / Q5_0 / Q5_1
