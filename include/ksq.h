@@ -180,7 +180,8 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
                                         int T, int N, int K, int E, int top_k);
 
 /* Path selection for testing and benchmarking: 0 = automatic (default),
- * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies. */
+ * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies,
+ * 3 = the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies. */
 KSQ_API int ksq_set_path(int path);
 
 /* MFMA tile configuration for tuning: 0 = chosen from (M, N) (default); 1 = 128x128 tile,

@@ -104,13 +104,23 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
     return KSQ_OK;
 }
 
-// The MFMA GEMM above 8 rows (or when forced), the v_dot4 decode kernels otherwise.
+// The MFMA GEMM above 8 rows or past the measured small-M crossovers (or when forced), the
+// small-batch or v_dot4 decode kernels otherwise.
 bool use_mmq(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
-    return (g_path != 1) && ksq::mmq_supported(wtype, M, N, K, W, a_aligned16) &&
-           (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K));
+    if (g_path == 1 || !ksq::mmq_supported(wtype, M, N, K, W, a_aligned16)) return false;
+    if (g_path == 2) return true;
+    if (g_path == 3) return M > 8;
+    return ksq::mmq_preferred(wtype, M, N, K);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The 4x4x4-MFMA small-batch kernel where it beats the decode kernel (path 3 forces it where it
+// applies).  Checked after use_mmq.
+bool use_skinny(int wtype, int afmt, int M, int N, int K, const void* W, const void* A) {
+    if (!ksq::skinny_supported(wtype, afmt, M, N, K, W, A)) return false;
+    return g_path == 3 || (g_path == 0 && ksq::skinny_preferred(wtype, M, N, K));
+}
 
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -134,11 +144,16 @@ int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* 
                float* partials, hipStream_t s) {
     hipError_t e;
     const bool mmq = use_mmq(wtype, M, N, K, W, aligned16(Aq));
-    if (mmq)
+    if (mmq) {
         e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, partials, s);
-    else
+        if (e != hipSuccess) return hip_error(e, "mmq launch");
+    } else if (use_skinny(wtype, afmt, M, N, K, W, Aq)) {
+        e = ksq::launch_skinny(wtype, afmt, W, Aq, C, M, N, K, s);
+        if (e != hipSuccess) return hip_error(e, "skinny launch");
+    } else {
         e = ksq::launch_gemv(wtype, afmt, W, Aq, C, M, N, K, s);
-    if (e != hipSuccess) return hip_error(e, mmq ? "mmq launch" : "gemv launch");
+        if (e != hipSuccess) return hip_error(e, "gemv launch");
+    }
     return KSQ_OK;
 }
 
@@ -179,7 +194,7 @@ void ksq_release(void) {
 }
 
 int ksq_set_path(int path) {
-    if (path < 0 || path > 2) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
+    if (path < 0 || path > 3) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
     g_path = path;
     return ok();
 }
@@ -230,7 +245,8 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     const uint8_t* Aq = (const uint8_t*)activation;
     const int afmt = atype_fmt(atype);
-    if (atype_f32(atype) && ksq::gemv_fused_profitable(wtype, M, N, K) && !use_mmq(wtype, M, N, K, weight, true)) {
+    if (atype_f32(atype) && ksq::gemv_fused_profitable(wtype, M, N, K) && !use_mmq(wtype, M, N, K, weight, true) &&
+        g_path != 3) {
         hipError_t e = ksq::launch_gemv_f32(wtype, afmt, (const uint8_t*)weight, (const float*)activation, output, M,
                                             N, K, s);
         return e == hipSuccess ? ok() : hip_error(e, "gemv launch");

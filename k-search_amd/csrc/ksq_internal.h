@@ -32,6 +32,14 @@ hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X
 // amount of repeated quantisation).
 bool gemv_fused_profitable(int wtype, int M, int N, int K);
 
+// Small-batch GEMM (1 <= M <= 8) on the 4x4x4 int8 MFMA for the 32-element block types
+// (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1; block_q8s activations with Q8_0).  W and A 4-byte aligned.
+bool skinny_supported(int wtype, int afmt, int M, int N, int K, const void* W, const void* A);
+// Whether it is expected to beat the decode kernel (measured crossovers by type, M and N).
+bool skinny_preferred(int wtype, int M, int N, int K);
+hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+                         hipStream_t s);
+
 // Prefill GEMM on int8 MFMA (mul_mat_q family); returns hipErrorNotSupported
 // for shapes it does not tile.
 // a_aligned16: the quantised activations the GEMM will read are 16-byte aligned.

@@ -516,8 +516,8 @@ static int pick_config(int wtype, int M, int N) {
     constexpr int kCUs = 256;
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
     if (nib && M >= 256) return 1;
-    if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     if (nib && M <= 32) return 5;
+    if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     return 3;
 }
 

@@ -1,0 +1,330 @@
+// ksq_skinny.hip - small-batch GEMM (M <= 8 activation rows) on the 4x4x4 int8 MFMA.
+//
+// Reference path: the decode GEMVs of kernelevalplus-main/kernels/gemm/gemm_warp_optimized.cuh:108-1212
+// run with batch > 1 (one warp per weight row, DP4A per activation row) and the block formulas of
+// include/gemm_reference.h:200-259 and include/gemm_quant_formats.cuh:126-266.
+//
+// gfx950 design:
+//  * v_mfma_i32_4x4x4_16b_i8 computes 16 independent 4 x 4 x 4 int8 products.  Lane
+//    l = 16 g + 4 kb + q: product (g, kb) is weight rows 4g .. 4g+3 x activation rows q of block
+//    kb of the current K step; the lane supplies weight row 4g + q and activation row q of that
+//    block.  Eight instructions (k = 0..31) leave the reference's integer block dot sumi of
+//    4 weight rows x 4 activation rows in every lane's four result registers, for 16 rows x
+//    4 blocks per wave and step; activation rows 4..7 take a second set of eight.  The
+//    activation fragment is used by all 16 rows, so the integer work per (row, block, column)
+//    is 1/16 of an MFMA issue slot instead of the 8 v_dot4 of the decode kernel.
+//  * A workgroup owns 16 weight rows and its waves split the K steps (4 blocks each).  Lanes
+//    load their weight block and activation block straight from global memory into registers
+//    kSkPD steps ahead of the MFMAs (the 16 rows x 4 blocks of one step are 16 contiguous runs
+//    of 4 blocks), so each wave keeps several KB in flight with no LDS staging and no barrier
+//    in the K loop.  The loads are bounds-checked buffer loads: blocks past K and activation
+//    rows past M read zeros without branches.
+//  * Per-block epilogue as the MFMA GEMM: the MFMA accumulates onto the bit pattern of
+//    12582912.0f, X = fma(f, d_a, -12582912 d_a) = d_a * sumi with one rounding; the four weight
+//    rows' scales come from the lanes of the quad by DPP broadcast.
+//  * The 4 blocks of a step are summed over lanes by DPP row rotation once at the end, the
+//    waves' K ranges through LDS.
+#include "ksq_device.h"
+#include "ksq_internal.h"
+
+namespace ksq {
+
+namespace {
+
+constexpr uint32_t kSkMagic = 0x4B400000u;  // 12582912.0f
+constexpr float kSkMagicF = 12582912.0f;
+constexpr int kSkRows = 16;                 // weight rows per workgroup
+constexpr int kSkPD = 4;                    // K steps in flight per wave
+
+// Per-lane weight registers of one block: the WD dwords from the 4-byte aligned address at or
+// below the block start (Q4_0 18 B, Q8_0 34 B and Q5_0 22 B blocks are only 2-byte aligned; the
+// window covers the block wherever it starts).  NP payload dwords follow the fp16 scale(s).
+template <int WT>
+struct SkFmt {
+    static constexpr bool al4 = (WT == kWQ41 || WT == kWQ51);
+    static constexpr int BB = block_bytes(WT);
+    static constexpr int WD = (BB + (al4 ? 3 : 5)) / 4;
+    static constexpr int NP = (WT == kWQ80) ? 8 : (WT == kWQ50 || WT == kWQ51) ? 5 : 4;  // payload dwords
+};
+
+constexpr uint32_t kOOB = 0x80000000u;  // buffer offset past every buffer this kernel reads: loads give 0
+
+// ND consecutive dwords at byte offset off of the buffer (dword aligned), as 16-byte loads
+// plus one 4-, 8- or 12-byte load.
+template <int ND>
+__device__ __forceinline__ void buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* out) {
+#pragma unroll
+    for (int i = 0; i + 4 <= ND; i += 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 4 * i, 0, 0);
+        out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+    }
+    constexpr int R = ND & 3, B = ND - R;
+    if constexpr (R == 1) {
+        out[B] = __builtin_amdgcn_raw_buffer_load_b32(r, off + 4 * B, 0, 0);
+    } else if constexpr (R == 2) {
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 4 * B, 0, 0);
+        out[B] = v.x; out[B + 1] = v.y;
+    } else if constexpr (R == 3) {
+        typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+        const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off + 4 * B, 0, 0);
+        out[B] = v.x; out[B + 1] = v.y; out[B + 2] = v.z;
+    }
+}
+
+__device__ __forceinline__ float dpp_quad_bcast(float v, int r) {
+    const int x = __builtin_bit_cast(int, v);
+    int y;
+    switch (r) {
+        case 0: y = __builtin_amdgcn_mov_dpp(x, 0x00, 0xF, 0xF, false); break;
+        case 1: y = __builtin_amdgcn_mov_dpp(x, 0x55, 0xF, 0xF, false); break;
+        case 2: y = __builtin_amdgcn_mov_dpp(x, 0xAA, 0xF, 0xF, false); break;
+        default: y = __builtin_amdgcn_mov_dpp(x, 0xFF, 0xF, 0xF, false); break;
+    }
+    return __builtin_bit_cast(float, y);
+}
+
+__device__ __forceinline__ float dpp_row_ror(float v, int n) {
+    const int x = __builtin_bit_cast(int, v);
+    const int y = (n == 4) ? __builtin_amdgcn_mov_dpp(x, 0x124, 0xF, 0xF, false)
+                           : __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);
+    return __builtin_bit_cast(float, y);
+}
+
+// C[m][n] = sum over blocks of the reference block formula, m < M <= 4*MP, for the 16 rows
+// n0 .. n0+15 of this workgroup.  NWV waves split the K steps.  AS: block_q8s activations
+// (Q8_0 weights only).  wbytes / abytes: readable bytes of W and A (W's rounded up to a dword:
+// the last dword of the weights is read whole).  Loads are buffer loads: a block past K or an
+// activation row past M reads at an offset beyond the buffer and gets zeros.
+template <int WT, int MP, bool AS, int NWV>
+__global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                          float* __restrict__ C, int M, int N, int nb, int ldc,
+                                                          uint32_t wbytes, uint32_t abytes) {
+    using F = SkFmt<WT>;
+    constexpr int BB = F::BB;
+    __shared__ float red[NWV][kSkRows][4 * MP];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, kb = (lane >> 2) & 3, q = lane & 3;
+    const int n0 = blockIdx.x * kSkRows;
+    const int wrow = min(n0 + 4 * g + q, N - 1);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)abytes, 0x00020000);
+    // this lane's block starts at row offset + (4 s + kb) * BB; its offset mod 4 is the same at
+    // every step, since a step advances 4 blocks
+    const uint32_t wrow_off = (uint32_t)wrow * (uint32_t)nb * (uint32_t)BB + (uint32_t)kb * BB;
+    const int sh = (int)(((uintptr_t)W + wrow_off) & 3u);   // block start within its dword (0 or 2)
+    uint32_t aoff0[MP];
+#pragma unroll
+    for (int pp = 0; pp < MP; pp++) {
+        const int m = q + 4 * pp;
+        aoff0[pp] = m < M ? ((uint32_t)m * (uint32_t)nb + (uint32_t)kb) * (uint32_t)kQ81Bytes : kOOB;
+    }
+
+    const int S = (nb + 3) >> 2;
+    const int s_lo = (int)((long long)S * wave / NWV), s_hi = (int)((long long)S * (wave + 1) / NWV);
+
+    i32x4 bias;
+#pragma unroll
+    for (int r = 0; r < 4; r++) bias[r] = (int)kSkMagic;
+    float acc[MP][4];
+#pragma unroll
+    for (int p = 0; p < MP; p++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[p][r] = 0.0f;
+
+    struct Step {
+        uint32_t w[F::WD];
+        uint32_t a[MP][9];
+    };
+    auto load = [&](int s, Step& st) {
+        const bool bok = 4 * s + kb < nb;
+        const uint32_t woff = bok ? wrow_off + (uint32_t)(4 * s) * BB - (uint32_t)sh : kOOB;
+        buf_load<F::WD>(rw, woff, st.w);
+#pragma unroll
+        for (int pp = 0; pp < MP; pp++) {
+            const uint32_t aoff = bok ? aoff0[pp] + (uint32_t)(4 * s) * kQ81Bytes : kOOB;
+            buf_load<9>(ra, aoff, st.a[pp]);
+        }
+    };
+
+    auto compute = [&](const Step& st) {
+        // weight scale(s) and the 8 A-operand dwords (elements 4j .. 4j+3)
+        float dw, mw = 0.0f;
+        uint32_t pay[F::NP];
+        if constexpr (F::al4) {
+            dw = f16_to_f32(st.w[0] & 0xFFFFu);
+            mw = f16_to_f32(st.w[0] >> 16);
+#pragma unroll
+            for (int i = 0; i < F::NP; i++) pay[i] = st.w[1 + i];
+        } else {
+            // d at byte sh of the window, the payload from byte sh + 2 (2 or 4)
+            dw = f16_to_f32((st.w[0] >> (8 * sh)) & 0xFFFFu);
+#pragma unroll
+            for (int i = 0; i < F::NP; i++)
+                pay[i] = sh ? st.w[i + 1] : __builtin_amdgcn_alignbyte(st.w[i + 1], st.w[i], 2);
+        }
+        uint32_t a8[8];
+        if constexpr (WT == kWQ80) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) a8[j] = pay[j];
+        } else if constexpr (WT == kWQ40 || WT == kWQ41) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a8[j] = pay[j] & 0x0F0F0F0Fu;
+                a8[4 + j] = (pay[j] >> 4) & 0x0F0F0F0Fu;
+            }
+        } else {
+            const uint32_t h = pay[0];  // qh: bit e = bit 4 of element e
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a8[j] = (pay[1 + j] & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * j));
+                a8[4 + j] = ((pay[1 + j] >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * j));
+            }
+        }
+        float dwr[4], mwr[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            dwr[r] = dpp_quad_bcast(dw, r);
+            if constexpr (WT == kWQ41 || WT == kWQ51) mwr[r] = dpp_quad_bcast(mw, r);
+        }
+#pragma unroll
+        for (int pp = 0; pp < MP; pp++) {
+            if (pp * 4 >= M) break;  // uniform: no activation rows in this pass
+            i32x4 d = bias;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                d = __builtin_amdgcn_mfma_i32_4x4x4i8((int)a8[j], (int)st.a[pp][1 + j], d, 0, 0, 0);
+            const uint32_t ds = st.a[pp][0];
+            // block_q8s: fp32 scale with its two lowest mantissa bits cleared so that
+            // 12582912 * d_a stays exact (relative change < 2^-21)
+            const float da = AS ? __builtin_bit_cast(float, ds & ~3u) : f16_to_f32(ds & 0xFFFFu);
+            const float sa = AS ? 0.0f : f16_to_f32(ds >> 16);
+            const float nc = -kSkMagicF * da;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int e = d[r];
+                const float X = fmaf(__builtin_bit_cast(float, e), da, nc);  // d_a * sumi
+                if constexpr (WT == kWQ40) acc[pp][r] = fmaf(dwr[r], fmaf(-8.0f, sa, X), acc[pp][r]);
+                else if constexpr (WT == kWQ50) acc[pp][r] = fmaf(dwr[r], fmaf(-16.0f, sa, X), acc[pp][r]);
+                else if constexpr (WT == kWQ80) acc[pp][r] = fmaf(dwr[r], X, acc[pp][r]);
+                else acc[pp][r] = fmaf(mwr[r], sa, fmaf(dwr[r], X, acc[pp][r]));
+            }
+        }
+    };
+
+    // kSkPD steps in flight (wave-uniform branches only)
+    Step buf[kSkPD];
+#pragma unroll
+    for (int d = 0; d < kSkPD; d++)
+        if (s_lo + d < s_hi) load(s_lo + d, buf[d]);
+    for (int s0 = s_lo; s0 < s_hi; s0 += kSkPD) {
+#pragma unroll
+        for (int d = 0; d < kSkPD; d++) {
+            if (s0 + d < s_hi) {
+                compute(buf[d]);
+                if (s0 + d + kSkPD < s_hi) load(s0 + d + kSkPD, buf[d]);
+            }
+        }
+    }
+
+    // sum the 4 blocks of a step (lanes kb = 0..3 of a 16-lane row), then the waves
+#pragma unroll
+    for (int pp = 0; pp < MP; pp++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float v = acc[pp][r];
+            v += dpp_row_ror(v, 4);
+            v += dpp_row_ror(v, 8);
+            acc[pp][r] = v;
+        }
+    if (kb == 0) {
+#pragma unroll
+        for (int pp = 0; pp < MP; pp++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][4 * g + r][q + 4 * pp] = acc[pp][r];
+    }
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < kSkRows * 4 * MP) {
+        const int row = t % kSkRows, m = t / kSkRows;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) v += red[w][row][m];
+        if (m < M && n0 + row < N) C[(size_t)m * ldc + n0 + row] = v;
+    }
+}
+
+template <int WT, int MP, bool AS>
+hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
+                             hipStream_t s) {
+    const uint32_t wbytes = (uint32_t)(((uint64_t)N * nb * block_bytes(WT) + 3) & ~(uint64_t)3);
+    const uint32_t abytes = (uint32_t)((uint64_t)M * nb * kQ81Bytes);
+    const dim3 grid((unsigned)((N + kSkRows - 1) / kSkRows));
+    if constexpr (MP == 1) {  // 16 waves leave 128 VGPRs per lane: enough for one activation pass only
+        if (nwv == 16) {
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+            return hipGetLastError();
+        }
+    }
+    if (nwv >= 8)
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    return hipGetLastError();
+}
+
+template <int WT, bool AS>
+hipError_t skinny_launch_mp(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
+                            hipStream_t s) {
+    return M <= 4 ? skinny_launch_nwv<WT, 1, AS>(nwv, W, A, C, M, N, nb, s)
+                  : skinny_launch_nwv<WT, 2, AS>(nwv, W, A, C, M, N, nb, s);
+}
+
+}  // namespace
+
+bool skinny_supported(int wtype, int afmt, int M, int N, int K, const void* W, const void* A) {
+    const bool type_ok = wtype == kWQ40 || wtype == kWQ80 || wtype == kWQ41 || wtype == kWQ50 || wtype == kWQ51;
+    if (!type_ok || !(afmt == kAQ81 || (afmt == kAQ8S && wtype == kWQ80)) || M < 1 || M > 8 || N < 1 || K < 32 ||
+        (K % 32) != 0 || (((uintptr_t)W | (uintptr_t)A) & 3u) != 0)
+        return false;
+    // buffer offsets are 32-bit and kOOB (2^31) must lie past both buffers
+    const uint64_t wbytes = (uint64_t)N * (K / 32) * block_bytes(wtype) + 4, abytes = (uint64_t)M * (K / 32) * kQ81Bytes;
+    return wbytes < (1ull << 31) && abytes < (1ull << 31);
+}
+
+// Measured on MI355X against the decode kernel (block_q8_1 activations, us): the 4-byte aligned
+// Q4_1 blocks load without re-alignment and win from M = 3 (N = K = 2560: 3.8 vs 4.6 at M = 3,
+// 4.8 vs 7.5 at M = 8; N = 18944, K = 3584: 15.8 vs 17.4 at M = 3); the 2-byte aligned types
+// win at M = 8 (Q4_0 N = K = 4096: 9.2 vs 10.8; Q8_0: 10.3 vs 11.1) and lose below
+// (Q4_0 M = 3: 7.4 vs 6.3).  Below N = 2048 the 16-row workgroups do not fill the chip
+// (N = 512, K = 7168, M = 8: 10.9 vs 7.2).
+bool skinny_preferred(int wtype, int M, int N, int K) {
+    (void)K;
+    if (N < 2048) return false;
+    if (wtype == kWQ41 || wtype == kWQ51) return M >= 3;
+    return M >= 8;
+}
+
+hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
+                         hipStream_t s) {
+    if (!skinny_supported(wtype, afmt, M, N, K, W, A)) return hipErrorNotSupported;
+    const int nb = K / 32;
+    // waves per workgroup: enough workgroups x waves to put ~4 waves on every CU, but at least
+    // one K step (4 blocks) per wave
+    const int wgs = (N + kSkRows - 1) / kSkRows;
+    const int steps = (nb + 3) / 4;
+    const int max_nwv = M <= 4 ? 16 : 8;
+    int nwv = 4;
+    while (nwv < max_nwv && (long long)wgs * nwv < 1024 && steps >= 2 * nwv) nwv *= 2;
+    switch (wtype) {
+        case kWQ40: return skinny_launch_mp<kWQ40, false>(nwv, W, A, C, M, N, nb, s);
+        case kWQ80:
+            return afmt == kAQ8S ? skinny_launch_mp<kWQ80, true>(nwv, W, A, C, M, N, nb, s)
+                                 : skinny_launch_mp<kWQ80, false>(nwv, W, A, C, M, N, nb, s);
+        case kWQ41: return skinny_launch_mp<kWQ41, false>(nwv, W, A, C, M, N, nb, s);
+        case kWQ50: return skinny_launch_mp<kWQ50, false>(nwv, W, A, C, M, N, nb, s);
+        default: return skinny_launch_mp<kWQ51, false>(nwv, W, A, C, M, N, nb, s);
+    }
+}
+
+}  // namespace ksq

@@ -140,7 +140,8 @@ def moe_workspace_size(wtype: int, T: int, N: int, K: int, E: int, top_k: int) -
 
 
 def set_path(path: int) -> None:
-    """0 automatic, 1 v_dot4 decode kernels only, 2 MFMA GEMM where it applies."""
+    """0 automatic, 1 v_dot4 decode kernels only, 2 MFMA GEMM where it applies,
+    3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies."""
     check(lib().ksq_set_path(path))
 
 

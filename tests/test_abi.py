@@ -105,5 +105,7 @@ def test_forward_mirrors_harness_checks():
 def test_set_path_validation():
     from ksq import _lib
     L = _lib.lib()
-    assert L.ksq_set_path(3) == 4
+    assert L.ksq_set_path(4) == 4
+    assert L.ksq_set_path(-1) == 4
+    assert L.ksq_set_path(3) == 0
     assert L.ksq_set_path(0) == 0

@@ -327,12 +327,45 @@ def test_mfma_tile_configs(dev, oracle, cfg, wtype):
     assert _rel_err(y, ref) <= TOL
 
 
+SKINNY_WTYPES = [0, 1, 4, 5, 6]          # the 32-element block types of the 4x4x4-MFMA kernel
+
+
+@pytest.mark.parametrize("wtype", SKINNY_WTYPES)
+def test_skinny_small_batch(dev, oracle, wtype):
+    """The 4x4x4-MFMA small-batch kernel (path 3) for M = 1..8 on ragged shapes: N not a multiple
+    of the 16-row workgroup, K steps with a partial last step (K/32 not a multiple of 4), one K
+    step in all, and enough steps for every wave count (4, 8, 16 waves per workgroup)."""
+    from ksq import synth
+    g = np.random.default_rng(2400 + wtype)
+    for M, N, K in ((1, 37, 96), (2, 100, 544), (3, 16, 32), (4, 4096, 4096), (5, 75, 1056), (7, 260, 2048),
+                    (8, 1536, 5120), (6, 4100, 4096)):
+        w = synth.weights(wtype, g, N, K)
+        x = synth.activations(g, M, K)
+        y = _gpu_gemm(dev, wtype, w, x, M, N, K, path=3)
+        ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x), w, M, N, K)
+        assert _rel_err(y, ref) <= TOL, (M, N, K)
+
+
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_skinny_q8s_native(dev, oracle, M):
+    """Q8_0 weights with block_q8s activations (the native W8A8C8 operator's blocks) on path 3."""
+    from ksq import synth
+    g = np.random.default_rng(2500 + M)
+    N, K = 530, 2048
+    w = synth.weights(1, g, N, K)
+    x = synth.activations(g, M, K)
+    y = _gpu_gemm(dev, 1, w, x, M, N, K, atype=2, path=3)
+    ref = oracle.gemm_q8s_f64(oracle.quantize_q8s(x), w, M, N, K)
+    assert _rel_err(y, ref) <= TOL
+
+
 @pytest.mark.parametrize("wtype,M,N,K", [(0, 6, 11008, 4096), (4, 5, 18944, 3584), (1, 7, 14336, 4096),
-                                         (0, 8, 4096, 4096)])
+                                         (0, 8, 4096, 4096), (4, 3, 2560, 2560), (0, 3, 4096, 4096)])
 def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
-    """M = 5..8 on large matrices takes the MFMA kernel by default (the measured crossover), small
-    ones the decode kernel; either way the fp32 entry matches the oracle, with the library pool
-    and with a caller workspace of exactly ksq_gemm_workspace_size bytes."""
+    """M = 3..8 by default: large matrices take the MFMA GEMM (the measured crossover), Q4_1 from
+    M = 3 and the other types at M = 8 the 4x4x4-MFMA small-batch kernel, the rest the decode
+    kernel; each way the fp32 entry matches the oracle, with the library pool and with a caller
+    workspace of exactly ksq_gemm_workspace_size bytes."""
     import torch
     from ksq import ops, synth
     g = np.random.default_rng(2300 + M)
