@@ -152,6 +152,16 @@ KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* a
 KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
                               int M, int N, int K, void* stream);
 
+/* Debug: fp32 [M][K] -> the q8h activation layout of the f16-MFMA GEMM: qh [M][K] fp16 holding
+ * q/8 and ds [M][K/32] the block_q8_1 ds words, with the quants and ds of ksq_quantize_q8_1.
+ * x and qh 16-byte aligned, ds 4-byte aligned. */
+KSQ_API int ksq_debug_quantize_q8h(const float* x, void* qh, uint32_t* ds, int M, int K, void* stream);
+
+/* Debug: the same per-block integer dots from the f16-MFMA prefill GEMM of Q4_0 weights
+ * (the activations converted to its fp16 q/8 layout first).  K % 64 == 0. */
+KSQ_API int ksq_debug_block_sumi_f16mfma(const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N,
+                                         int K, void* stream);
+
 /* ---- expert-grouped MoE (no reference counterpart for GGML types) ----------
  * output[t][n] = sum over the top_k experts e chosen for token t of
  *                w[t][e] * (Q8_1(activation[t]) . weight[e][n]),
@@ -180,8 +190,9 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
                                         int T, int N, int K, int E, int top_k);
 
 /* Path selection for testing and benchmarking: 0 = automatic (default),
- * 1 = always the v_dot4 decode kernels, 2 = always the MFMA GEMM where it applies,
- * 3 = the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies. */
+ * 1 = always the v_dot4 decode kernels, 2 = always the int8 MFMA GEMM where it applies,
+ * 3 = the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies,
+ * 4 = the f16-MFMA GEMM for Q4_0 where it applies. */
 KSQ_API int ksq_set_path(int path);
 
 /* MFMA tile configuration for tuning: 0 = chosen from (M, N) (default); 1 = 128x128 tile,

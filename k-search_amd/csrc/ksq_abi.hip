@@ -123,18 +123,33 @@ bool use_skinny(int wtype, int afmt, int M, int N, int K, const void* W, const v
 }
 
 
+// The f16-MFMA GEMM (Q4_0) on path 4 only: measured slower than the int8 MFMA GEMM at every
+// shape tried (M = 2048, N = K = 4096: 138 vs 113 us), so the automatic path does not take it.
+bool use_mmqh(int wtype, int M, int N, int K, const void* W) {
+    return g_path == 4 && ksq::mmqh_supported(wtype, M, N, K, W);
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace of one ksq_gemm call: [quantised activations][split-K partial sums], each part
-// 256-byte aligned.  `mmq` is whether the MFMA path runs (alignment permitting).
+// 256-byte aligned.  `mmq` is whether the int8 MFMA path runs (alignment permitting), `mmqh`
+// whether the f16-MFMA path does: its activations are the q8h layout [qh: M*K fp16][ds: M*K/32
+// words], for quantised input too (converted from block_q8_1).
 struct GemmWs {
-    size_t q, p, total;
+    size_t q, qds, p, total;
 };
 
-GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
+GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq, bool mmqh) {
     GemmWs w{};
-    w.q = atype_f32(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
-    const int splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
+    int splits = 1;
+    if (mmqh) {
+        w.qds = align256((size_t)M * (size_t)K * 2u);
+        w.q = w.qds + align256((size_t)M * (size_t)(K / 32) * 4u);
+        splits = ksq::mmqh_splits(M, N, K);
+    } else {
+        w.q = atype_f32(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
+        splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
+    }
     w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
     w.total = w.q + w.p;
     return w;
@@ -194,7 +209,7 @@ void ksq_release(void) {
 }
 
 int ksq_set_path(int path) {
-    if (path < 0 || path > 3) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
+    if (path < 0 || path > 4) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
     g_path = path;
     return ok();
 }
@@ -230,7 +245,11 @@ size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const bool mmq_possible =
         (g_path != 1) && (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K)) && (K % 256) == 0;
-    return gemm_ws(wtype, atype, M, N, K, mmq_possible).total;
+    const size_t a = gemm_ws(wtype, atype, M, N, K, mmq_possible, false).total;
+    const size_t b = (wtype == KSQ_W_Q4_0 && g_path == 4 && (K % 64) == 0)
+                         ? gemm_ws(wtype, atype, M, N, K, false, true).total
+                         : 0;
+    return a > b ? a : b;
 }
 
 int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output, int M, int N,
@@ -254,8 +273,9 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     // fp32 activations are quantised to the start of the (16-byte aligned) workspace, which is
     // what the MFMA path then reads
     const bool f32 = atype_f32(atype);
-    const bool mmq = use_mmq(wtype, M, N, K, weight, f32 || aligned16(activation));
-    const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq);
+    const bool mmqh = afmt == ksq::kAQ81 && use_mmqh(wtype, M, N, K, weight);
+    const bool mmq = !mmqh && use_mmq(wtype, M, N, K, weight, f32 || aligned16(activation));
+    const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq, mmqh);
     uint8_t* ws = (uint8_t*)workspace;
     if (L.total) {
         if (ws) {
@@ -269,12 +289,21 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
             ws = (uint8_t*)p;
         }
     }
+    float* partials = L.p ? (float*)(ws + L.q) : nullptr;
+    if (mmqh) {
+        _Float16* qh = (_Float16*)ws;
+        uint32_t* ds = (uint32_t*)(ws + L.qds);
+        hipError_t e = f32 ? ksq::launch_quantize_q8h((const float*)activation, qh, ds, M, K, s)
+                           : ksq::launch_q8_1_to_q8h(Aq, qh, ds, M, K, s);
+        if (e != hipSuccess) return hip_error(e, f32 ? "quantize launch" : "q8h conversion launch");
+        e = ksq::launch_mmqh((const uint8_t*)weight, qh, ds, output, M, N, K, partials, s);
+        return e == hipSuccess ? ok() : hip_error(e, "f16 mfma launch");
+    }
     if (f32) {
         hipError_t e = ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
         Aq = ws;
     }
-    float* partials = L.p ? (float*)(ws + L.q) : nullptr;
     st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, partials, s);
     return st == KSQ_OK ? ok() : st;
 }
@@ -297,6 +326,34 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
         return set_error(KSQ_ERR_SHAPE, "MFMA path needs K %% 256 == 0 and 16-byte aligned operands");
     hipError_t e = ksq::launch_mmq_block_sumi(wtype, (const uint8_t*)weight, act_q8_1, out, M, N, K, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_error(e, "mfma block_sumi launch");
+}
+
+int ksq_debug_quantize_q8h(const float* x, void* qh, uint32_t* ds, int M, int K, void* stream) {
+    if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
+    if (M == 0 || K == 0) return ok();
+    if (!x || !qh || !ds) return set_error(KSQ_ERR_NULL, "x, qh or ds is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)qh & 15u) || ((uintptr_t)ds & 3u))
+        return set_error(KSQ_ERR_ALIGN, "x and qh must be 16-byte and ds 4-byte aligned");
+    hipError_t e = ksq::launch_quantize_q8h(x, (_Float16*)qh, ds, M, K, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_error(e, "quantize launch");
+}
+
+int ksq_debug_block_sumi_f16mfma(const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N, int K,
+                                 void* stream) {
+    int st = check_common(KSQ_W_Q4_0, KSQ_A_Q8_1, weight, act_q8_1, out, M, N, K);
+    if (st != KSQ_OK) return st;
+    if (M == 0 || N == 0 || K == 0) return ok();
+    if (!ksq::mmqh_supported(KSQ_W_Q4_0, M, N, K, weight)) return set_error(KSQ_ERR_SHAPE, "f16 MFMA path needs K %% 64 == 0");
+    void* p = nullptr;
+    const size_t qb = align256((size_t)M * K * 2);
+    st = pool_get(qb + align256((size_t)M * (K / 32) * 4), &p);
+    if (st != KSQ_OK) return st;
+    _Float16* qh = (_Float16*)p;
+    uint32_t* ds = (uint32_t*)((uint8_t*)p + qb);
+    hipError_t e = ksq::launch_q8_1_to_q8h(act_q8_1, qh, ds, M, K, (hipStream_t)stream);
+    if (e == hipSuccess)
+        e = ksq::launch_mmqh_block_sumi((const uint8_t*)weight, qh, ds, out, M, N, K, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_error(e, "f16 mfma block_sumi launch");
 }
 
 // ---- expert-grouped MoE --------------------------------------------------------

@@ -17,6 +17,11 @@ constexpr int kAQ81 = 0, kAQ8S = 1;
 // fp32 [rows][K] -> [rows][K/32] 36-byte blocks of format afmt; x 16-byte aligned, y 4-byte aligned.
 hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
+// The q8h activation layout of the f16-MFMA GEMM: the block_q8_1 quants of [rows][K] as fp16 q/8
+// (qh, [rows][K], 16-byte aligned) and the block ds words (ds, [rows][K/32]); from fp32 (the same
+// quants and ds as block_q8_1, bit for bit) or converted from block_q8_1 blocks.
+hipError_t launch_quantize_q8h(const float* x, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s);
+hipError_t launch_q8_1_to_q8h(const uint8_t* a, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s);
 
 // Decode GEMV/GEMM on v_dot4 (mul_mat_vec_q family), any M.
 // wtype: 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q4_1, 5 Q5_0, 6 Q5_1.
@@ -52,6 +57,20 @@ bool mmq_preferred(int wtype, int M, int N, int K);
 int mmq_splits(int wtype, int M, int N, int K);
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       float* partials, hipStream_t s);
+// In-order sum of `splits` partial [M][N] results (P) into C.
+hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits, hipStream_t s);
+
+// Prefill GEMM for Q4_0 weights on the f16 MFMA (exact integer block dots, one FMA per output
+// and block) over q8h activations; K % 64 == 0.  Splits along K for small grids like launch_mmq
+// (mmqh_splits; partials of splits * M * N floats).
+bool mmqh_supported(int wtype, int M, int N, int K, const void* W);
+int mmqh_splits(int M, int N, int K);
+hipError_t launch_mmqh(const uint8_t* W, const _Float16* QH, const uint32_t* DS, float* C, int M, int N, int K,
+                       float* partials, hipStream_t s);
+// Its integer block dots (sumi) as [M][N][K/32] (debug entry for the bit-exact check).
+hipError_t launch_mmqh_block_sumi(const uint8_t* W, const _Float16* QH, const uint32_t* DS, int32_t* out, int M,
+                                  int N, int K, hipStream_t s);
+
 // Force one of the MFMA tile configurations (1..5) or automatic choice (0); -1 if out of range.
 int mmq_set_config(int c);
 

@@ -624,6 +624,11 @@ static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, con
     }
 }
 
+hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits, hipStream_t s) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, P, C, mn, splits);
+    return hipGetLastError();
+}
+
 int mmq_splits(int wtype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 1;
     return split_cfg(pick_config(wtype, M, N), M, N, K);

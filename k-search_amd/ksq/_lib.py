@@ -48,6 +48,8 @@ SIGNATURES = {
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi_mfma": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
+    "ksq_debug_block_sumi_f16mfma": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "ksq_debug_quantize_q8h": ([_P, _P, _P, _I, _I, _P], _I),
     "ksq_set_path": ([_I], _I),
     "ksq_set_mmq_config": ([_I], _I),
     "ksq_moe_workspace_size": ([_I, _I, _I, _I, _I, _I], _SZ),

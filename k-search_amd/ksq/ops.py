@@ -96,11 +96,28 @@ def quantize_q8s(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tens
     return out
 
 
+def quantize_q8h(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 [M, K] -> the f16-MFMA GEMM's activation layout: (qh fp16 [M, K] = q/8, ds int32
+    [M, K/32] = the block_q8_1 ds words) with the quants of quantize_q8_1 (debug)."""
+    x = x.contiguous()
+    M, K = x.shape
+    qh = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    ds = torch.empty((M, K // 32), dtype=torch.int32, device=x.device)
+    check(lib().ksq_debug_quantize_q8h(_ptr(x), _ptr(qh), _ptr(ds), M, K, _stream()))
+    return qh, ds
+
+
 def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int, N: int, K: int,
-               mfma: bool = False) -> torch.Tensor:
-    """Per-block integer dots [M, N, nblk] from the device block-dot code (debug)."""
+               mfma: bool | str = False) -> torch.Tensor:
+    """Per-block integer dots [M, N, nblk] from the device block-dot code (debug): the v_dot4
+    decode kernels, the int8 MFMA GEMM (mfma=True) or the f16-MFMA GEMM of Q4_0 (mfma="f16")."""
     nblk = K // 16 if wtype == W_Q6_K else K // 32
     out = torch.empty((M, N, nblk), dtype=torch.int32, device=weight.device)
+    if mfma == "f16":
+        if wtype != W_Q4_0:
+            raise ValueError("the f16-MFMA GEMM takes Q4_0 weights")
+        check(lib().ksq_debug_block_sumi_f16mfma(_ptr(weight), _ptr(act_q8_1), _ptr(out), M, N, K, _stream()))
+        return out
     fn = lib().ksq_debug_block_sumi_mfma if mfma else lib().ksq_debug_block_sumi
     check(fn(wtype, _ptr(weight), _ptr(act_q8_1), _ptr(out), M, N, K, _stream()))
     return out
@@ -140,8 +157,9 @@ def moe_workspace_size(wtype: int, T: int, N: int, K: int, E: int, top_k: int) -
 
 
 def set_path(path: int) -> None:
-    """0 automatic, 1 v_dot4 decode kernels only, 2 MFMA GEMM where it applies,
-    3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies."""
+    """0 automatic, 1 v_dot4 decode kernels only, 2 int8 MFMA GEMM where it applies,
+    3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies, 4 the f16-MFMA GEMM for
+    Q4_0 where it applies."""
     check(lib().ksq_set_path(path))
 
 
@@ -153,5 +171,5 @@ def release() -> None:
     lib().ksq_release()
 
 
-__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "block_sumi", "set_path",
+__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "quantize_q8h", "block_sumi", "set_path",
            "workspace_size", "moe_gemm", "moe_gemm_routed", "moe_workspace_size", "release", "_lib"]

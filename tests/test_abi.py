@@ -79,10 +79,20 @@ def test_empty_calls_are_noops():
 
 
 def test_workspace_size():
+    """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K); on
+    path 4 (the f16-MFMA GEMM of Q4_0) the q8h activations (fp16 quants + ds words) for both."""
     from ksq import _lib
     L = _lib.lib()
     assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == 2048 * 128 * 36
     assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == 0
+    assert L.ksq_gemm_workspace_size(1, 0, 2048, 4096, 4096) == 2048 * 128 * 36
+    q8h = 2048 * 4096 * 2 + 2048 * 128 * 4
+    assert L.ksq_set_path(4) == 0
+    try:
+        assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == q8h
+        assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == q8h
+    finally:
+        L.ksq_set_path(0)
 
 
 def test_void_entry_records_error():
@@ -105,7 +115,8 @@ def test_forward_mirrors_harness_checks():
 def test_set_path_validation():
     from ksq import _lib
     L = _lib.lib()
-    assert L.ksq_set_path(4) == 4
+    assert L.ksq_set_path(5) == 4
     assert L.ksq_set_path(-1) == 4
     assert L.ksq_set_path(3) == 0
+    assert L.ksq_set_path(4) == 0
     assert L.ksq_set_path(0) == 0
