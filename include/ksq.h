@@ -196,7 +196,8 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
 KSQ_API int ksq_set_path(int path);
 
 /* MFMA tile configuration for tuning: 0 = chosen from (M, N) (default); 1 = 128x128 tile,
- * K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with K step 4; 5 = 32x128. */
+ * K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with K step 4; 5 = 32x128; 6 = 128x128 with
+ * K step 4 and the next step's loads prefetched into registers. */
 KSQ_API int ksq_set_mmq_config(int config);
 
 #ifdef __cplusplus

@@ -71,7 +71,7 @@ hipError_t launch_mmqh(const uint8_t* W, const _Float16* QH, const uint32_t* DS,
 hipError_t launch_mmqh_block_sumi(const uint8_t* W, const _Float16* QH, const uint32_t* DS, int32_t* out, int M,
                                   int N, int K, hipStream_t s);
 
-// Force one of the MFMA tile configurations (1..5) or automatic choice (0); -1 if out of range.
+// Force one of the MFMA tile configurations (1..6) or automatic choice (0); -1 if out of range.
 int mmq_set_config(int c);
 
 // Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /

@@ -41,9 +41,10 @@ constexpr float kMagicF = 12582912.0f;
 typedef uint32_t u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-template <int BM_, int BN_, int KB_, int TM_, int TN_, int OCC_>
+template <int BM_, int BN_, int KB_, int TM_, int TN_, int OCC_, bool PIPE_ = false>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, KB = KB_, TM = TM_, TN = TN_, OCC = OCC_;
+    static constexpr bool PIPE = PIPE_;   // staging loads of the next K step prefetched into registers
     static constexpr int WN = BN / (32 * TN);          // waves along N
     static constexpr int WM = BM / (32 * TM);          // waves along M
     static_assert(WN * WM == 4, "four waves per workgroup");
@@ -113,6 +114,9 @@ __device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
 }
 
 // AS: the activations are block_q8s (fp32 scale, no sum; Q8_0 weights only).
+// T::PIPE (tiles of 128 x 128 with K steps of 4 blocks; 32-element block types, no MoE): the
+// global loads of K step k+1 are issued into registers before step k computes (threads 0..127
+// hold an activation chunk, 128..255 a weight chunk), so their latency hides behind the MFMAs.
 template <class T, int WT, bool DUMP, bool MOE, bool AS>
 __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
@@ -171,81 +175,122 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     const int nsteps = nb / KB, Z = (int)gridDim.z, z = (int)blockIdx.z;
     const int kb_lo = (int)((long long)nsteps * z / Z) * KB, kb_hi = (int)((long long)nsteps * (z + 1) / Z) * KB;
     if constexpr (!MOE) C += (size_t)z * (size_t)M * (size_t)N;
-    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += KB) {
-        // ---- stage activations: chunks of 4 Q8_1 blocks = 144 B = 9 x 16 B
-        for (int c = t; c < BM * (KB / 4); c += 256) {
-            const int sr = c / (KB / 4), g = c % (KB / 4);
-            const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
-            const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * kQ81Bytes;
-            uint32_t v[36];
+    // ---- staging of 32-element blocks, split into the global loads and the LDS writes
+    // activation chunk g (4 Q8_1 blocks = 144 B = 9 x 16 B) of staged row sr
+    auto load_act = [&](int sr, int g, int kb0, uint32_t* v) {
+        const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
+        const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * kQ81Bytes;
 #pragma unroll
-            for (int i = 0; i < 9; i++) {
-                const u32x4 x = *(const u32x4*)(p + 16 * i);
-                v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+        for (int i = 0; i < 9; i++) {
+            const u32x4 x = *(const u32x4*)(p + 16 * i);
+            v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+        }
+    };
+    auto store_act = [&](int sr, int g, const uint32_t* v) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int kb = 4 * g + j;
+            u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
+            dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
+            dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
+            // block_q8s: the fp32 scale with its two lowest mantissa bits cleared (22 significant
+            // bits), so that 12582912 * d_a' stays exact (relative change < 2^-21)
+            const float da = AS ? __builtin_bit_cast(float, v[9 * j] & ~3u)
+                                : f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
+            sDa[kb][sr] = da;
+            sNc[kb][sr] = -kMagicF * da;
+            sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
+        }
+    };
+    // weight chunk g (4 blocks: 72 / 136 / 80 / 88 / 96 B, 8-byte aligned) of staged row sr
+    constexpr int WNW = is_kquant(WT) ? 2 : S::Chunk / 4;
+    auto load_w = [&](int sr, int g, int kb0, uint32_t* v) {
+        if constexpr (!is_kquant(WT)) {
+            const int wr = min(n0 + sr, N - 1);
+            const uint8_t* p = W + (size_t)wr * nb * S::BB + (size_t)(kb0 + 4 * g) * S::BB;
+#pragma unroll
+            for (int i = 0; i < WNW / 2; i++) {
+                const u32x2_a8 x = *(const u32x2_a8*)(p + 8 * i);
+                v[2 * i] = x.x; v[2 * i + 1] = x.y;
             }
+            v[WNW] = 0; v[WNW + 1] = 0;
+        }
+    };
+    auto store_w = [&](int sr, int g, const uint32_t* v) {
+        if constexpr (!is_kquant(WT)) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int kb = 4 * g + j;
-                u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
-                dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
-                dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
-                // block_q8s: the fp32 scale with its two lowest mantissa bits cleared (22 significant
-                // bits), so that 12582912 * d_a' stays exact (relative change < 2^-21)
-                const float da = AS ? __builtin_bit_cast(float, v[9 * j] & ~3u)
-                                    : f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
-                sDa[kb][sr] = da;
-                sNc[kb][sr] = -kMagicF * da;
-                sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
+                const int kb = 4 * g + j, off = j * S::BB;
+                const uint32_t dwb = half_at(v, off);
+                sDw[kb][sr] = f16_to_f32(dwb);
+                // side factor against -s_a: d_w (Q4_0, Q5_0) or -m (Q4_1, Q5_1)
+                if constexpr (WT == kWQ41 || WT == kWQ51) sDwH[sr][kb] = (uint16_t)(half_at(v, off + 2) ^ 0x8000u);
+                else sDwH[sr][kb] = (uint16_t)dwb;
+                if constexpr (WT == kWQ40 || WT == kWQ41) {
+                    constexpr int q = (WT == kWQ40) ? 2 : 4;  // offset of qs
+                    *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
+                        u32x4{word_at(v, off + q), word_at(v, off + q + 4), word_at(v, off + q + 8),
+                              word_at(v, off + q + 12)};
+                } else if constexpr (WT == kWQ80) {
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                    dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
+                    dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
+                } else {
+                    // Q5_0 / Q5_1: widen to one byte per quant (0..31); element 4i+t takes nibble
+                    // t of word i and qh bit 4i+t, element 16+4i+t the high nibble and bit 16+4i+t
+                    constexpr int qh = (WT == kWQ50) ? 2 : 4, q = qh + 4;
+                    const uint32_t h = word_at(v, off + qh);
+                    uint32_t o[8];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const uint32_t w4 = word_at(v, off + q + 4 * i);
+                        o[i] = (w4 & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i));
+                        o[4 + i] = ((w4 >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i));
+                    }
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                    dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+                    dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+                }
             }
         }
+    };
+    constexpr bool PIPE = T::PIPE && !MOE && !is_kquant(WT);
+    static_assert(!PIPE || (KB == 4 && BM == 128 && BN == 128),
+                  "the pipelined staging covers 128 x 128 tiles with 4-block K steps");
+    // PIPE: one chunk per thread and K step; threads 0..127 activation row t, 128..255 weight row t-128
+    uint32_t pre[PIPE ? 36 : 1];
+    const bool pre_act = t < 128;
+    auto pre_load = [&](int kb0) {
+        if constexpr (PIPE) {
+            if (pre_act) load_act(t, 0, kb0, pre);
+            else load_w(t - 128, 0, kb0, pre);
+        }
+    };
+    if constexpr (PIPE) {
+        if (kb_lo < kb_hi) pre_load(kb_lo);
+    }
+
+    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += KB) {
+        if constexpr (PIPE) {
+            if (pre_act) store_act(t, 0, pre);
+            else store_w(t - 128, 0, pre);
+            __syncthreads();
+            if (kb0 + KB < kb_hi) pre_load(kb0 + KB);
+        } else {
+        // ---- stage activations
+        for (int c = t; c < BM * (KB / 4); c += 256) {
+            const int sr = c / (KB / 4), g = c % (KB / 4);
+            uint32_t v[36];
+            load_act(sr, g, kb0, v);
+            store_act(sr, g, v);
+        }
         if constexpr (!is_kquant(WT)) {
-            // ---- stage weights: chunks of 4 blocks (72 / 136 / 80 / 88 / 96 B), 8-byte aligned
+            // ---- stage weights
             for (int c = t; c < BN * (KB / 4); c += 256) {
                 const int sr = c / (KB / 4), g = c % (KB / 4);
-                const int wr = min(n0 + sr, N - 1);
-                constexpr int NW = S::Chunk / 4;
-                uint32_t v[NW + 2];
-                const uint8_t* p = W + (size_t)wr * nb * S::BB + (size_t)(kb0 + 4 * g) * S::BB;
-    #pragma unroll
-                for (int i = 0; i < NW / 2; i++) {
-                    const u32x2_a8 x = *(const u32x2_a8*)(p + 8 * i);
-                    v[2 * i] = x.x; v[2 * i + 1] = x.y;
-                }
-                v[NW] = 0; v[NW + 1] = 0;
-    #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int kb = 4 * g + j, off = j * S::BB;
-                    const uint32_t dwb = half_at(v, off);
-                    sDw[kb][sr] = f16_to_f32(dwb);
-                    // side factor against -s_a: d_w (Q4_0, Q5_0) or -m (Q4_1, Q5_1)
-                    if constexpr (WT == kWQ41 || WT == kWQ51) sDwH[sr][kb] = (uint16_t)(half_at(v, off + 2) ^ 0x8000u);
-                    else sDwH[sr][kb] = (uint16_t)dwb;
-                    if constexpr (WT == kWQ40 || WT == kWQ41) {
-                        constexpr int q = (WT == kWQ40) ? 2 : 4;  // offset of qs
-                        *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
-                            u32x4{word_at(v, off + q), word_at(v, off + q + 4), word_at(v, off + q + 8),
-                                  word_at(v, off + q + 12)};
-                    } else if constexpr (WT == kWQ80) {
-                        u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
-                        dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
-                        dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
-                    } else {
-                        // Q5_0 / Q5_1: widen to one byte per quant (0..31); element 4i+t takes nibble
-                        // t of word i and qh bit 4i+t, element 16+4i+t the high nibble and bit 16+4i+t
-                        constexpr int qh = (WT == kWQ50) ? 2 : 4, q = qh + 4;
-                        const uint32_t h = word_at(v, off + qh);
-                        uint32_t o[8];
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const uint32_t w4 = word_at(v, off + q + 4 * i);
-                            o[i] = (w4 & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i));
-                            o[4 + i] = ((w4 >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i));
-                        }
-                        u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
-                        dst[0] = u32x4{o[0], o[1], o[2], o[3]};
-                        dst[1] = u32x4{o[4], o[5], o[6], o[7]};
-                    }
-                }
+                uint32_t v[WNW + 2];
+                load_w(sr, g, kb0, v);
+                store_w(sr, g, v);
             }
         } else if constexpr (WT == kWQ4K) {
             // ---- Q4_K: one 144-byte super-block per row and K step (16-byte aligned)
@@ -315,6 +360,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             }
         }
         __syncthreads();
+        }  // staging without prefetch
 
         auto frag_a = [&](int b, int i) -> i32x4 {
             return *(const i32x4*)(sA + (wm * 32 * TM + i * 32 + l32) * T::APitch + b * 32 + 16 * hi);
@@ -491,11 +537,12 @@ using TileN = Tile<128, 64, 8, 2, 1, 2>;    // half the columns per workgroup: t
 using TileS = Tile<64, 64, 8, 1, 1, 3>;     // 32 x 32 per wave, 4x the workgroups of TileL
 using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, more resident workgroups
 using TileT = Tile<32, 128, 8, 1, 1, 3>;    // skinny: M <= 32, the four waves side by side along N
+using TileP = Tile<128, 128, 4, 2, 2, 2, true>;  // 128 x 128, K step 4, next step's loads prefetched
 
 static int g_mmq_config = 0;  // 0 = automatic
 
 int mmq_set_config(int c) {
-    if (c < 0 || c > 5) return -1;
+    if (c < 0 || c > 6) return -1;
     g_mmq_config = c;
     return 0;
 }
@@ -505,18 +552,24 @@ static int grid_wgs(int M, int N) {
     return ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
 }
 
-// Measured on MI355X (M = 3 .. 2048, N = 512 .. 18944, K = 2560 .. 7168): the 128 x 128 tile
-// is best for the nibble-staged Q4_0 / Q4_1 from M = 256 on (split along K when its grid is
-// small); the byte-staged types (Q8_0, Q5_x, Q6_K) need 86 KB of LDS for it, one workgroup
-// per CU, and like Q4_K run best on 128 x 64 while that grid covers the CUs, else 64 x 64.
-// Nibble types with M <= 32 run best on 32 x 128 (e.g. Q4_0 N = 14336, K = 4096: 21.1 vs
-// 25.2 us at M = 8, 23.7 vs 26.1 us at M = 32); Q8_0 does not gain from it.
+// Measured on MI355X (M = 3 .. 2048, N = 512 .. 18944, K = 2560 .. 7168, block_q8_1 input, us):
+//  * nibble-staged Q4_0 / Q4_1: the 128 x 128 tile from M = 256 on while it covers the CUs
+//    (Q4_0 M = 2048, N = K = 4096: 114; N = 14336: 343 vs 396 prefetched K-step-4), else
+//    64 x 64 (Q4_1 M = 512, N = K = 4096: 42.5 vs 46.5); 32 x 128 at M <= 32 (Q4_0 N = 14336,
+//    K = 4096: 21.1 vs 25.2 at M = 8, 23.7 vs 26.1 at M = 32);
+//  * byte-staged Q8_0 / Q5_0 / Q5_1 need 86 KB of LDS for the 128 x 128 K-step-8 tile (one
+//    workgroup per CU); its K-step-4 form with prefetched loads wins on large grids (Q8_0
+//    M = 2048, N = K = 4096: 113 vs 128 for 128 x 64 and 187 for K-step 8; Q5_1 M = 512,
+//    N = 14336: 111 vs 123), 64 x 64 below (Q8_0 M = 512, N = K = 4096: 40.7 vs 46.3 and 55.3);
+//  * Q4_K / Q6_K stage one super-block per K step: 128 x 64 while that grid covers the CUs,
+//    else 64 x 64.
 static int pick_config(int wtype, int M, int N) {
-    if (g_mmq_config && !(is_kquant(wtype) && g_mmq_config == 4)) return g_mmq_config;
+    if (g_mmq_config && !(is_kquant(wtype) && (g_mmq_config == 4 || g_mmq_config == 6))) return g_mmq_config;
     constexpr int kCUs = 256;
-    const bool nib = (wtype == kWQ40 || wtype == kWQ41);
-    if (nib && M >= 256) return 1;
+    const bool nib = (wtype == kWQ40 || wtype == kWQ41), kq = is_kquant(wtype);
     if (nib && M <= 32) return 5;
+    if (nib && M >= 256) return grid_wgs<TileL>(M, N) >= kCUs ? 1 : 3;
+    if (!nib && !kq) return grid_wgs<TileP>(M, N) >= 384 ? 6 : 3;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     return 3;
 }
@@ -602,6 +655,7 @@ static int split_cfg(int cfg, int M, int N, int K) {
         case 2: return split_for<TileN>(M, N, K);
         case 3: return split_for<TileS>(M, N, K);
         case 5: return split_for<TileT>(M, N, K);
+        case 6: return split_for<TileP>(M, N, K);
         default: return split_for<TileK4>(M, N, K);
     }
 }
@@ -620,6 +674,7 @@ static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, con
         case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
         case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
         case 5: return launch_t<TileT, DUMP, false>(wtype, afmt, grid(32, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 6: return launch_t<TileP, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
         default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
     }
 }

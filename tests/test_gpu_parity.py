@@ -309,7 +309,7 @@ def test_moe_config4_sampled(dev, oracle):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6])
 @pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_mfma_tile_configs(dev, oracle, cfg, wtype):
     """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile)."""
