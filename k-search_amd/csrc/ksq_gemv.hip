@@ -191,14 +191,21 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
 
 // Activation staging modes of the decode kernel.
 //   kAL2   each lane reads its activation blocks from global memory (L2) after the weight wait
-//          (1 or 2 activation rows: the fewest bytes moved)
+//          (1 or 2 activation rows of fewer than kGemvDmaMinBlocks blocks: no barrier)
 //   kADMA  the activation rows of the K tile are copied into LDS by DMA, issued together with
-//          the weight DMA, so one wait covers both (3 or more rows, read once per workgroup)
+//          the weight DMA, so one wait covers both (3 or more rows, or long rows; read once
+//          per workgroup)
 //   kAFQ   the activations arrive as fp32 and every workgroup quantises the K tile's blocks
 //          itself into LDS while its weight DMA is in flight (the same device quantiser as
 //          ksq_quantize.hip, so the blocks are bit-identical); no separate quantise launch
 constexpr int kAL2 = 0, kADMA = 1, kAFQ = 2;
 constexpr int kMaxL2Rows = 2, kMaxFusedRows = 2;
+// With 1-2 activation rows kAL2 reads each row once per wave, i.e. 4x the activation bytes of
+// kADMA, as many bytes again as the weights for M = 1.  Short rows are latency-bound and kAL2
+// (no workgroup barrier) wins; from 256 blocks (K = 8192) on the L2 traffic dominates and kADMA
+// wins (measured on MI355X, M = 1: Q4_1 N = 3584, K = 18944 12.7 vs 15.3 us; Q4_0
+// N = K = 4096 4.99 vs 4.76 us the other way).
+constexpr int kGemvDmaMinBlocks = 256;
 
 // Part `part` of `nparts` of a copy of `bytes` from g into LDS at dst (dst = g mod 16): the
 // parts split at 16-byte boundaries of g, so each is a valid wave_copy_to_lds.
@@ -446,7 +453,7 @@ static int pick_rpw(int N, int amode) {
 template <int WT, int MR, int AMODE, bool AS, int RPW>
 static hipError_t row_launch(const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
                              hipStream_t s) {
-    if constexpr ((AMODE == kAL2 && MR > kMaxL2Rows) || (AMODE == kADMA && MR <= kMaxL2Rows) ||
+    if constexpr ((AMODE == kAL2 && MR > kMaxL2Rows) ||
                   (AMODE == kAFQ && MR > kMaxFusedRows)) {
         return hipErrorNotSupported;  // combinations the dispatcher never asks for are not compiled
     } else {
@@ -488,7 +495,7 @@ static hipError_t row_launch_mr(int mr, int rpw, const uint8_t* W, const void* A
     }
 }
 
-// QUANT: the activations are already quantised (kAL2 / kADMA by row count), else fp32 (kAFQ).
+// QUANT: the activations are already quantised (kAL2 / kADMA by row count and length), else fp32 (kAFQ).
 template <int AMODE>
 static hipError_t gemv_dispatch_mode(int wtype, int afmt, int mr, const uint8_t* W, const void* Am, float* Cm,
                                      int N, int nb, int KT, int rpw, hipStream_t s) {
@@ -514,7 +521,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
     const int chunk = QUANT ? 8 : kMaxFusedRows;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
-        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows ? kAL2 : kADMA);
+        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows && nb < kGemvDmaMinBlocks ? kAL2 : kADMA);
         // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
         const int rpw = pick_rpw(N, AMODE);
         int KT = (nb + 7) & ~7;

@@ -438,6 +438,26 @@ def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
     assert _rel_err(y1.cpu().numpy(), ref) <= TOL
 
 
+@pytest.mark.parametrize("wtype,M,N,K", [(4, 1, 3584, 18944), (0, 2, 520, 8192), (2, 1, 264, 8192),
+                                         (3, 2, 136, 16384), (1, 1, 300, 8704), (5, 2, 200, 8192),
+                                         (6, 1, 96, 12288)])
+def test_long_row_decode(dev, oracle, wtype, M, N, K):
+    """M = 1, 2 with rows of 256 blocks or more: the decode kernel stages the activation rows in
+    LDS once per workgroup instead of reading them per wave; fp32 and pre-quantised entries
+    against the oracle."""
+    from ksq import ops, synth
+    g = np.random.default_rng(2400 + K + M)
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    wt, xt = _t(w, dev), _t(x, dev)
+    q = oracle.quantize_q8_1(x)
+    ref = oracle.gemm_f64(wtype, q, w, M, N, K)
+    y = ops.gemm(wtype, 0, wt, xt, M, N, K).cpu().numpy()
+    assert _rel_err(y, ref) <= TOL
+    yq = ops.gemm(wtype, 1, wt, _t(q, dev), M, N, K).cpu().numpy()
+    assert _rel_err(yq, ref) <= TOL
+
+
 # ------------------------------------------------------------------ Q4_1 / Q5_0 / Q5_1
 def test_golden_fixture_legacy_on_gpu(dev):
     import torch
