@@ -598,13 +598,29 @@ bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned
 // Split-K factor for a (tile, M, N, K): grids of fewer than kSplitMinWGs workgroups are split
 // along K (at least kSplitMinSteps K steps per split) so that small-M problems still occupy
 // the chip; the partial sums go to a workspace and splitk_reduce_kernel adds them in order.
+// Larger grids that still leave most CUs below the tile's residency (at most 2/3 of
+// 256 x OCC workgroups for the nibble types, 1/2 for the others) are split too when K >= 4096,
+// up to that residency with at least 8 K steps per split.  Measured on MI355X against the
+// unsplit grid (us, Q4_0 / Q8_0): M = 256, N = 4096, K = 14336 on 64 x 64 tiles 129 -> 77 /
+// 130 -> 85; M = 512, N = 2048, K = 7168 64 -> 44 / 59 -> 44; M = 1024, N = 4096, K = 14336 on
+// 128 x 128 tiles 254 -> 194.  Past those fractions the reduction costs more than the fuller
+// chip gains (Q8_0 M = 512, N = 4096, K = 14336 with 512 of 768: 145 -> 162).
 constexpr int kSplitMinWGs = 256, kSplitTargetWGs = 512, kSplitMinSteps = 2, kSplitMax = 16;
+constexpr int kCUCount = 256;
 
 template <class T>
-static int split_for(int M, int N, int K) {
+static int split_for(int wtype, int M, int N, int K) {
     const int wgs = ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
     const int steps = (K / 32) / T::KB;
-    if (wgs >= kSplitMinWGs) return 1;
+    if (wgs >= kSplitMinWGs) {
+        const int target = kCUCount * T::OCC;
+        const bool nib = (wtype == kWQ40 || wtype == kWQ41);
+        const int limit = nib ? (2 * target) / 3 : target / 2;
+        if (wgs > limit || K < 4096) return 1;
+        int sp = (target + wgs - 1) / wgs;
+        sp = sp < steps / 8 ? sp : steps / 8;
+        return sp < 1 ? 1 : sp;
+    }
     int sp = (kSplitTargetWGs + wgs - 1) / wgs;
     sp = sp < steps / kSplitMinSteps ? sp : steps / kSplitMinSteps;
     sp = sp < kSplitMax ? sp : kSplitMax;
@@ -649,14 +665,14 @@ static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, con
     }
 }
 
-static int split_cfg(int cfg, int M, int N, int K) {
+static int split_cfg(int cfg, int wtype, int M, int N, int K) {
     switch (cfg) {
-        case 1: return split_for<TileL>(M, N, K);
-        case 2: return split_for<TileN>(M, N, K);
-        case 3: return split_for<TileS>(M, N, K);
-        case 5: return split_for<TileT>(M, N, K);
-        case 6: return split_for<TileP>(M, N, K);
-        default: return split_for<TileK4>(M, N, K);
+        case 1: return split_for<TileL>(wtype, M, N, K);
+        case 2: return split_for<TileN>(wtype, M, N, K);
+        case 3: return split_for<TileS>(wtype, M, N, K);
+        case 5: return split_for<TileT>(wtype, M, N, K);
+        case 6: return split_for<TileP>(wtype, M, N, K);
+        default: return split_for<TileK4>(wtype, M, N, K);
     }
 }
 
@@ -686,13 +702,13 @@ hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits
 
 int mmq_splits(int wtype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 1;
-    return split_cfg(pick_config(wtype, M, N), M, N, K);
+    return split_cfg(pick_config(wtype, M, N), wtype, M, N, K);
 }
 
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       float* partials, hipStream_t s) {
     const int cfg = pick_config(wtype, M, N);
-    const int splits = split_cfg(cfg, M, N, K);
+    const int splits = split_cfg(cfg, wtype, M, N, K);
     if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s);
     if (!partials) return hipErrorInvalidValue;
     hipError_t e = launch_cfg<false>(cfg, wtype, afmt, W, A, partials, nullptr, M, N, K, splits, s);
