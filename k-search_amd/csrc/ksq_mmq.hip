@@ -552,24 +552,37 @@ static int grid_wgs(int M, int N) {
     return ((N + T::BN - 1) / T::BN) * ((M + T::BM - 1) / T::BM);
 }
 
-// Measured on MI355X (M = 3 .. 2048, N = 512 .. 18944, K = 2560 .. 7168, block_q8_1 input, us):
+// Measured on MI355X (M = 3 .. 2048, N = 512 .. 18944, K = 2560 .. 18944, block_q8_1 input, us):
 //  * nibble-staged Q4_0 / Q4_1: the 128 x 128 tile from M = 256 on while it covers the CUs
-//    (Q4_0 M = 2048, N = K = 4096: 114; N = 14336: 343 vs 396 prefetched K-step-4), else
-//    64 x 64 (Q4_1 M = 512, N = K = 4096: 42.5 vs 46.5); 32 x 128 at M <= 32 (Q4_0 N = 14336,
-//    K = 4096: 21.1 vs 25.2 at M = 8, 23.7 vs 26.1 at M = 32);
+//    (Q4_0 M = 2048, N = K = 4096: 103 vs 113 prefetched K-step-4), or with long rows (K >= 9728)
+//    when the 64 x 64 grid has 512 workgroups or more (M = 512, N = 4096, K = 14336: 103 vs
+//    117; M = 1024, N = 3584, K = 18944: 243 vs 273), else 64 x 64 (M = 512, N = K = 4096: 42.5
+//    vs 46.5); 32 x 128 at M <= 32 (N = 14336, K = 4096: 21.1 vs 25.2 at M = 8) and for larger
+//    grids below M = 256 (M = 64, N = 18944, K = 3584: 37.2 vs 53.7 for 128 x 64);
 //  * byte-staged Q8_0 / Q5_0 / Q5_1 need 86 KB of LDS for the 128 x 128 K-step-8 tile (one
 //    workgroup per CU); its K-step-4 form with prefetched loads wins on large grids (Q8_0
-//    M = 2048, N = K = 4096: 113 vs 128 for 128 x 64 and 187 for K-step 8; Q5_1 M = 512,
-//    N = 14336: 111 vs 123), 64 x 64 below (Q8_0 M = 512, N = K = 4096: 40.7 vs 46.3 and 55.3);
+//    M = 2048, N = K = 4096: 113 vs 128 for 128 x 64 and 187 for K-step 8), 128 x 64 when its
+//    grid of 416 .. 512 workgroups fills the CUs in one round (Q8_0 M = 512, N = K = 7168:
+//    104 vs 131; M = 1024, N = K = 4096: 71 vs 84), else 64 x 64 (M = 512, N = K = 4096: 41.6
+//    vs 46.2 and 46.6);
 //  * Q4_K / Q6_K stage one super-block per K step: 128 x 64 while that grid covers the CUs,
 //    else 64 x 64.
-static int pick_config(int wtype, int M, int N) {
+static int pick_config(int wtype, int M, int N, int K) {
     if (g_mmq_config && !(is_kquant(wtype) && (g_mmq_config == 4 || g_mmq_config == 6))) return g_mmq_config;
     constexpr int kCUs = 256;
     const bool nib = (wtype == kWQ40 || wtype == kWQ41), kq = is_kquant(wtype);
     if (nib && M <= 32) return 5;
-    if (nib && M >= 256) return grid_wgs<TileL>(M, N) >= kCUs ? 1 : 3;
-    if (!nib && !kq) return grid_wgs<TileP>(M, N) >= 384 ? 6 : 3;
+    if (nib && M >= 256) {
+        if (grid_wgs<TileL>(M, N) >= kCUs) return 1;
+        if (K >= 9728 && grid_wgs<TileS>(M, N) >= 2 * kCUs) return 1;
+        return 3;
+    }
+    if (nib) return grid_wgs<TileN>(M, N) >= kCUs ? 5 : 3;
+    if (!kq) {
+        if (grid_wgs<TileP>(M, N) >= 384) return 6;
+        const int gn = grid_wgs<TileN>(M, N);
+        return (gn >= 416 && gn <= 2 * kCUs) ? 2 : 3;
+    }
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     return 3;
 }
@@ -702,12 +715,12 @@ hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits
 
 int mmq_splits(int wtype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 1;
-    return split_cfg(pick_config(wtype, M, N), wtype, M, N, K);
+    return split_cfg(pick_config(wtype, M, N, K), wtype, M, N, K);
 }
 
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                       float* partials, hipStream_t s) {
-    const int cfg = pick_config(wtype, M, N);
+    const int cfg = pick_config(wtype, M, N, K);
     const int splits = split_cfg(cfg, wtype, M, N, K);
     if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s);
     if (!partials) return hipErrorInvalidValue;
@@ -743,7 +756,7 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,
                                  hipStream_t s) {
     if (!mmq_supported(wtype, M, N, K, W, ((uintptr_t)A & 15u) == 0)) return hipErrorNotSupported;
-    return launch_cfg<true>(pick_config(wtype, M, N), wtype, kAQ81, W, A, nullptr, out, M, N, K, 1, s);
+    return launch_cfg<true>(pick_config(wtype, M, N, K), wtype, kAQ81, W, A, nullptr, out, M, N, K, 1, s);
 }
 
 }  // namespace ksq
