@@ -587,19 +587,26 @@ static int pick_config(int wtype, int M, int N, int K) {
     return 3;
 }
 
-// Below M = 9 the decode kernel usually wins; its time grows with M * N * K while the
-// MFMA kernel's stays near its ~12 us floor, so for large matrices the MFMA kernel takes
-// over earlier.  Crossovers measured on MI355X with block_q8_1 activations (GEMV vs
-// 32 x 128 tile, us): Q4_0 N = 8192 K = 4096 at M = 7 (17.7 vs 14.5), N = 11008 / 14336
-// K = 4096 and Q4_1 N = 18944 K = 3584 at M = 5 (17.3 vs 16.8, 21.7 vs 20.5, 25.2 vs 20.6),
-// but not Q4_0 N = K = 4096 at M = 8 (11.1 vs 12.0); Q8_0 N = 14336 K = 4096 at M = 7
-// (37.9 vs 28.6, 64 x 64 tile).
+// Below M = 9 the decode and small-batch kernels usually win; their time grows with M * N * K
+// while the MFMA kernel's stays near its ~10 us floor, so for large matrices the MFMA kernel
+// takes over.  Fitted to measurements over the quant_gemm definition shapes (M = 5 .. 8,
+// block_q8_1 activations, us): the nibble types from M = 7 once N * K >= 2e7 (Q4_0 N = K = 5120,
+// M = 8: 12.7 vs 17.9 decode, 15.5 small-batch) and at M = 5, 6 from N * K >= 6e7 (N = 3584,
+// K = 18944: 21.6 vs 27.4 decode); Q8_0 from M = 7 once N * K >= 2e7 (N = K = 7168, M = 8: 26.1
+// vs 30.7 decode), never at M = 5, 6 (N = 18944, K = 3584: 36.7 vs 27.1 decode).  Where the small-batch
+// kernel also applies it keeps rows of up to 3584 elements (Q8_0 N = 18944, K = 3584, M = 8:
+// 26.4 vs 36.5).
 bool mmq_preferred(int wtype, int M, int N, int K) {
     if (M > 8) return true;
+    const bool nib = (wtype == kWQ40 || wtype == kWQ41);
+    if (!nib && wtype != kWQ80) return false;
     const double nk = (double)N * (double)K;
-    if (wtype == kWQ40 || wtype == kWQ41) return (M >= 7 && nk >= 3.0e7) || (M >= 5 && nk >= 4.4e7);
-    if (wtype == kWQ80) return M >= 7 && nk >= 5.0e7;
-    return false;
+    bool pref;
+    if (M >= 7) pref = nk >= 2.0e7;
+    else if (M >= 5) pref = nib && nk >= 6.0e7;
+    else pref = false;
+    if (pref && K <= 3584 && skinny_preferred(wtype, M, N, K)) return false;
+    return pref;
 }
 
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {

@@ -292,30 +292,38 @@ bool skinny_supported(int wtype, int afmt, int M, int N, int K, const void* W, c
     return wbytes < (1ull << 31) && abytes < (1ull << 31);
 }
 
-// Measured on MI355X against the decode kernel (block_q8_1 activations, us): the 4-byte aligned
-// Q4_1 blocks load without re-alignment and win from M = 3 (N = K = 2560: 3.8 vs 4.6 at M = 3,
-// 4.8 vs 7.5 at M = 8; N = 18944, K = 3584: 15.8 vs 17.4 at M = 3); the 2-byte aligned types
-// win at M = 8 (Q4_0 N = K = 4096: 9.2 vs 10.8; Q8_0: 10.3 vs 11.1) and lose below
-// (Q4_0 M = 3: 7.4 vs 6.3).  Below N = 2048 the 16-row workgroups do not fill the chip
-// (N = 512, K = 7168, M = 8: 10.9 vs 7.2).
+// Measured on MI355X against the decode kernel over the quant_gemm definition shapes (block_q8_1
+// activations, M = 1 .. 8, us): with ~16 waves per CU the small-batch kernel wins from M = 2 on
+// rows of up to 4096 elements once N >= 2048 gives enough 16-row workgroups (Q4_0 N = 9728,
+// K = 2560: 7.4 vs 9.2 at M = 3, 7.6 vs 10.9 at M = 4; N = 7168, K = 512: 2.8 vs 5.9 at M = 3),
+// on rows up to 8192 elements only for N >= 7168 (Q4_0 N = 12288, K = 5120: 15.2 vs 17.3 at
+// M = 4; N = 5120, K = 5120: 11.0 vs 9.6 the other way), at M = 1 only on very short rows
+// (N = 7168, K = 512: 2.7 vs 3.7); below N = 2048 (N = 512, K = 7168: 5.8 vs 3.4 at M = 2) and on
+// long rows (N = 5120, K = 12288: 19.8 vs 11.1 at M = 2) the decode kernel wins.
 bool skinny_preferred(int wtype, int M, int N, int K) {
-    (void)K;
+    (void)wtype;
+    if (M == 1) return K <= 1024 && N >= 4096;
     if (N < 2048) return false;
-    if (wtype == kWQ41 || wtype == kWQ51) return M >= 3;
-    return M >= 8;
+    if (K <= 4096) return true;
+    if (K <= 8192) return N >= 7168;
+    return false;
 }
 
 hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                          hipStream_t s) {
     if (!skinny_supported(wtype, afmt, M, N, K, W, A)) return hipErrorNotSupported;
     const int nb = K / 32;
-    // waves per workgroup: enough workgroups x waves to put ~4 waves on every CU, but at least
-    // one K step (4 blocks) per wave
+    // waves per workgroup: enough workgroups x waves to put ~16 waves on every CU for M <= 4
+    // (~4 for 5-8 rows, whose waves hold twice the accumulators), but at least two K steps
+    // (4 blocks each) per wave.  Measured (us, M = 2 / 4): Q4_0 N = 4096, K = 14336 20.2 / 20.9
+    // with ~4 waves per CU, 13.4 / 15.8 with ~16; at M = 8 ~16 waves per CU lose (Q4_0
+    // N = 14336, K = 4096: 29.3 vs 24.4).
     const int wgs = (N + kSkRows - 1) / kSkRows;
     const int steps = (nb + 3) / 4;
     const int max_nwv = M <= 4 ? 16 : 8;
+    const long long wave_target = M <= 4 ? 4096 : 1024;
     int nwv = 4;
-    while (nwv < max_nwv && (long long)wgs * nwv < 1024 && steps >= 2 * nwv) nwv *= 2;
+    while (nwv < max_nwv && (long long)wgs * nwv < wave_target && steps >= 2 * nwv) nwv *= 2;
     switch (wtype) {
         case kWQ40: return skinny_launch_mp<kWQ40, false>(nwv, W, A, C, M, N, nb, s);
         case kWQ80:

@@ -417,12 +417,14 @@ def test_skinny_q8s_native(dev, oracle, M):
 
 
 @pytest.mark.parametrize("wtype,M,N,K", [(0, 6, 11008, 4096), (4, 5, 18944, 3584), (1, 7, 14336, 4096),
-                                         (0, 8, 4096, 4096), (4, 3, 2560, 2560), (0, 3, 4096, 4096)])
+                                         (0, 8, 4096, 4096), (4, 3, 2560, 2560), (0, 3, 4096, 4096),
+                                         (0, 2, 7168, 512), (1, 4, 9728, 2560), (4, 8, 18944, 3584),
+                                         (0, 5, 3584, 18944), (1, 8, 7168, 7168), (5, 4, 12288, 5120)])
 def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
-    """M = 3..8 by default: large matrices take the MFMA GEMM (the measured crossover), Q4_1 from
-    M = 3 and the other types at M = 8 the 4x4x4-MFMA small-batch kernel, the rest the decode
-    kernel; each way the fp32 entry matches the oracle, with the library pool and with a caller
-    workspace of exactly ksq_gemm_workspace_size bytes."""
+    """M = 2..8 by default: large matrices take the MFMA GEMM (the measured crossovers), short
+    rows on wide matrices the 4x4x4-MFMA small-batch kernel, the rest the decode kernel; each way
+    the fp32 entry matches the oracle, with the library pool and with a caller workspace of
+    exactly ksq_gemm_workspace_size bytes."""
     import torch
     from ksq import ops, synth
     g = np.random.default_rng(2300 + M)
@@ -456,6 +458,21 @@ def test_long_row_decode(dev, oracle, wtype, M, N, K):
     assert _rel_err(y, ref) <= TOL
     yq = ops.gemm(wtype, 1, wt, _t(q, dev), M, N, K).cpu().numpy()
     assert _rel_err(yq, ref) <= TOL
+
+
+@pytest.mark.parametrize("wtype,M,N,K", [(0, 1, 7168, 512), (1, 2, 9728, 2560), (4, 3, 4096, 4096),
+                                         (6, 4, 2560, 2560), (0, 8, 18944, 3584)])
+def test_prequantized_small_m_routing(dev, oracle, wtype, M, N, K):
+    """block_q8_1 input at M = 1..8 through the default routing (the small-batch kernel from
+    M = 1 on short rows) against the oracle."""
+    from ksq import ops, synth
+    g = np.random.default_rng(2600 + M)
+    w = synth.weights(wtype, g, N, K)
+    x = synth.activations(g, M, K)
+    q = oracle.quantize_q8_1(x)
+    y = ops.gemm(wtype, 1, _t(w, dev), _t(q, dev), M, N, K).cpu().numpy()
+    ref = oracle.gemm_f64(wtype, q, w, M, N, K)
+    assert _rel_err(y, ref) <= TOL
 
 
 # ------------------------------------------------------------------ Q4_1 / Q5_0 / Q5_1
