@@ -191,7 +191,7 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
 
 // Activation staging modes of the decode kernel.
 //   kAL2   each lane reads its activation blocks from global memory (L2) after the weight wait
-//          (1 or 2 activation rows of fewer than kGemvDmaMinBlocks blocks: no barrier)
+//          (1 or 2 activation rows short of kGemvDmaMinBlocks1/2 blocks: no barrier)
 //   kADMA  the activation rows of the K tile are copied into LDS by DMA, issued together with
 //          the weight DMA, so one wait covers both (3 or more rows, or long rows; read once
 //          per workgroup)
@@ -201,11 +201,13 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
 constexpr int kAL2 = 0, kADMA = 1, kAFQ = 2;
 constexpr int kMaxL2Rows = 2, kMaxFusedRows = 2;
 // With 1-2 activation rows kAL2 reads each row once per wave, i.e. 4x the activation bytes of
-// kADMA, as many bytes again as the weights for M = 1.  Short rows are latency-bound and kAL2
-// (no workgroup barrier) wins; from 256 blocks (K = 8192) on the L2 traffic dominates and kADMA
-// wins (measured on MI355X, M = 1: Q4_1 N = 3584, K = 18944 12.7 vs 15.3 us; Q4_0
-// N = K = 4096 4.99 vs 4.76 us the other way).
-constexpr int kGemvDmaMinBlocks = 256;
+// kADMA, as many bytes again as the weights for M = 1.  Shorter rows are latency-bound and kAL2
+// (no workgroup barrier) wins; on the longest rows the L2 traffic dominates and kADMA wins
+// (measured on MI355X, us, weights streamed from HBM): M = 1 from 576 blocks (Q4_1 N = 3584,
+// K = 18944: 13.1 vs 15.7; Q8_0 N = 7168, K = 18432: 29.6 vs 36.4; but Q4_0 N = 4096,
+// K = 14336: 12.2 vs 10.7 the other way), M = 2 from 256 blocks (Q4_0 N = 4096, K = 14336: 11.6
+// vs 13.8).
+constexpr int kGemvDmaMinBlocks1 = 576, kGemvDmaMinBlocks2 = 256;
 
 // Part `part` of `nparts` of a copy of `bytes` from g into LDS at dst (dst = g mod 16): the
 // parts split at 16-byte boundaries of g, so each is a valid wave_copy_to_lds.
@@ -521,7 +523,8 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
     const int chunk = QUANT ? 8 : kMaxFusedRows;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
-        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows && nb < kGemvDmaMinBlocks ? kAL2 : kADMA);
+        const int dma_min = mr == 1 ? kGemvDmaMinBlocks1 : kGemvDmaMinBlocks2;
+        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows && nb < dma_min ? kAL2 : kADMA);
         // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
         const int rpw = pick_rpw(N, AMODE);
         int KT = (nb + 7) & ~7;

@@ -442,11 +442,11 @@ def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
 
 @pytest.mark.parametrize("wtype,M,N,K", [(4, 1, 3584, 18944), (0, 2, 520, 8192), (2, 1, 264, 8192),
                                          (3, 2, 136, 16384), (1, 1, 300, 8704), (5, 2, 200, 8192),
-                                         (6, 1, 96, 12288)])
+                                         (6, 1, 96, 12288), (1, 1, 100, 18432)])
 def test_long_row_decode(dev, oracle, wtype, M, N, K):
-    """M = 1, 2 with rows of 256 blocks or more: the decode kernel stages the activation rows in
-    LDS once per workgroup instead of reading them per wave; fp32 and pre-quantised entries
-    against the oracle."""
+    """M = 1, 2 on long rows: from 576 blocks (M = 1) or 256 blocks (M = 2) the decode kernel
+    stages the activation rows in LDS once per workgroup instead of reading them per wave, below
+    that per wave from L2; fp32 and pre-quantised entries against the oracle."""
     from ksq import ops, synth
     g = np.random.default_rng(2400 + K + M)
     w = synth.weights(wtype, g, N, K)
