@@ -9,7 +9,9 @@ on fp32 activations [2048, 4096] -> fp32 [2048, 4096], i.e. quantize_q8_1 plus
 the int8-MFMA GEMM.  Inputs are seeded synthetic tensors resident in HBM before
 timing; weights and activations rotate over several copies so successive steps
 do not re-read one buffer from the 256 MB MALL.  Launch sequences are captured
-in HIP graphs and replayed, so host-side launch cost (ctypes) is not timed.
+in HIP graphs and replayed, so host-side launch cost (ctypes) is not timed.  The W
+untimed warm-up steps (default 256: two eager, the rest replays of the captured
+step graph) bring the GPU clocks to their steady state before the K timed steps.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 
@@ -164,7 +166,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64)
-    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--warmup", type=int, default=256,
+                    help="untimed steps before the timed ones (the first two eager, the rest as replays of "
+                         "the captured step graph): brings the GPU clocks to their steady state")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["gemm", "gemv", "step", "copy"],
                     help="profiling mode: launch just that kernel sequence --steps times, eagerly, and exit")
@@ -216,12 +220,15 @@ def main() -> int:
         print(json.dumps({"only": args.only, "launches": args.warmup + args.steps}), flush=True)
         return 0
 
-    for i in range(args.warmup):
+    n_eager = min(args.warmup, 2)            # sizes the library's workspace pool before capture
+    for i in range(n_eager):
         step(i)
     torch.cuda.synchronize()
-    log(f"bench: timing {args.steps} steps")
     g_step = capture(step, args.steps)
-    g_step.replay()
+    for _ in range(max(1, -(-(args.warmup - n_eager) // args.steps))):
+        g_step.replay()
+    torch.cuda.synchronize()
+    log(f"bench: timing {args.steps} steps")
     t0 = time.perf_counter()
     ms = time_graph(g_step, 1) / args.steps
     wall = (time.perf_counter() - t0) / args.steps * 1e3
