@@ -565,8 +565,12 @@ static int grid_wgs(int M, int N) {
 //    grid of 416 .. 512 workgroups fills the CUs in one round (Q8_0 M = 512, N = K = 7168:
 //    104 vs 131; M = 1024, N = K = 4096: 71 vs 84), else 64 x 64 (M = 512, N = K = 4096: 41.6
 //    vs 46.2 and 46.6);
-//  * Q4_K / Q6_K stage one super-block per K step: 128 x 64 while that grid covers the CUs,
-//    else 64 x 64.
+//  * Q4_K / Q6_K stage one super-block per K step: 128 x 64 while that grid covers the CUs or
+//    for long rows below M = 256 (Q6_K M = 128, N = 4096, K = 14336: 58.8 vs 70.0 for 64 x 64),
+//    else 64 x 64; Q4_K (nibble-staged) like Q4_0 takes 32 x 128 at M <= 32 (N = 14336,
+//    K = 4096, M = 16: 20.5 vs 26.7) and on grids of 384+ workgroups below M = 256 (M = 128: 45.3
+//    vs 49.3), 128 x 128 from M = 256 while it covers the CUs (M = 2048, N = K = 4096: 114.5 vs
+//    131.9).
 static int pick_config(int wtype, int M, int N, int K) {
     if (g_mmq_config && !(is_kquant(wtype) && (g_mmq_config == 4 || g_mmq_config == 6))) return g_mmq_config;
     constexpr int kCUs = 256;
@@ -583,6 +587,12 @@ static int pick_config(int wtype, int M, int N, int K) {
         const int gn = grid_wgs<TileN>(M, N);
         return (gn >= 416 && gn <= 2 * kCUs) ? 2 : 3;
     }
+    if (wtype == kWQ4K) {
+        if (M <= 32) return 5;
+        if (M >= 256 && grid_wgs<TileL>(M, N) >= kCUs) return 1;
+        if (M < 256 && grid_wgs<TileT>(M, N) >= 384) return 5;
+    }
+    if (M < 256 && K >= 9728) return 2;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;
     return 3;
 }
