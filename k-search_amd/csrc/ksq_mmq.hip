@@ -606,11 +606,17 @@ static int pick_config(int wtype, int M, int N, int K) {
 // vs 30.7 decode), never at M = 5, 6 (N = 18944, K = 3584: 36.7 vs 27.1 decode).  Where the small-batch
 // kernel also applies it keeps rows of up to 3584 elements (Q8_0 N = 18944, K = 3584, M = 8:
 // 26.4 vs 36.5).
+// K-quants (decode kernel vs MFMA GEMM only): Q4_K from M = 7 once N * K >= 1.2e7 (N = K = 4096,
+// M = 8: 1.08x) and at M = 5, 6 from 5e7 (N = 7168, K = 7168, M = 5: 1.20x); Q6_K from M = 7 on
+// rows of up to 7168 elements once N * K >= 1.5e7 (N = 12288, K = 5120, M = 8: 1.30x; with
+// K = 14336 the decode kernel stays 1.15x faster).
 bool mmq_preferred(int wtype, int M, int N, int K) {
     if (M > 8) return true;
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
-    if (!nib && wtype != kWQ80) return false;
     const double nk = (double)N * (double)K;
+    if (wtype == kWQ4K) return (M >= 7 && nk >= 1.2e7) || (M >= 5 && nk >= 5.0e7);
+    if (wtype == kWQ6K) return M >= 7 && K <= 7168 && nk >= 1.5e7;
+    if (!nib && wtype != kWQ80) return false;
     bool pref;
     if (M >= 7) pref = nk >= 2.0e7;
     else if (M >= 5) pref = nib && nk >= 6.0e7;
