@@ -358,17 +358,17 @@ int ksq_debug_block_sumi_f16mfma(const void* weight, const uint8_t* act_q8_1, in
 
 // ---- expert-grouped MoE --------------------------------------------------------
 namespace {
-constexpr int kMoeTileRows = 64;  // rows per grouped-GEMM tile (the MFMA kernel's BM for MoE)
 
 struct MoeLayout {
     size_t aq, ids, wts, rows, eend, ntiles, texp, trow0, scratch, total;
     int max_tiles;
 };
 
-MoeLayout moe_layout(int T, int N, int K, int E, int top_k) {
+MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
     MoeLayout L{};
     const size_t ent = (size_t)T * top_k;
-    L.max_tiles = (int)((ent + kMoeTileRows - 1) / kMoeTileRows) + E;
+    const int tile_rows = ksq::mmq_moe_tile_rows(wtype, T, E, top_k);
+    L.max_tiles = (int)((ent + tile_rows - 1) / tile_rows) + E;
     size_t off = 0;
     L.aq = off; off = align256(off + (size_t)T * (K / 32) * 36);
     L.ids = off; off = align256(off + ent * 4);
@@ -396,7 +396,8 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
         return set_error(KSQ_ERR_NULL, "null MoE argument");
     if (((uintptr_t)weights & 15u) || ((uintptr_t)activation & 15u) || ((uintptr_t)output & 3u))
         return set_error(KSQ_ERR_ALIGN, "MoE weights/activation must be 16-byte aligned, output 4-byte");
-    const MoeLayout L = moe_layout(T, N, K, E, top_k);
+    const MoeLayout L = moe_layout(wtype, T, N, K, E, top_k);
+    const int tile_rows = ksq::mmq_moe_tile_rows(wtype, T, E, top_k);
     void* ws = workspace;
     if (ws) {
         if (ws_bytes < L.total) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, L.total);
@@ -423,7 +424,7 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     int32_t* ntiles = (int32_t*)(base + L.ntiles);
     int32_t* texp = (int32_t*)(base + L.texp);
     int32_t* trow0 = (int32_t*)(base + L.trow0);
-    e = ksq::launch_moe_group(ids, T, top_k, E, kMoeTileRows, rows, eend, ntiles, texp, trow0, s);
+    e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
     if (e != hipSuccess) return hip_error(e, "group launch");
     float* scratch = top_k > 2 ? (float*)(base + L.scratch) : nullptr;
     if (!scratch) {
@@ -431,7 +432,7 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
         if (e != hipSuccess) return hip_error(e, "fill launch");
     }
     ksq::MoeTilesArgs a{ntiles, texp, trow0, eend, rows, wts, scratch, top_k};
-    e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, a, s);
+    e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, tile_rows, a, s);
     if (e != hipSuccess) return hip_error(e, "grouped gemm launch");
     if (scratch) {
         e = ksq::launch_moe_combine(scratch, output, T, N, top_k, s);
@@ -442,9 +443,8 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
 }  // namespace
 
 size_t ksq_moe_workspace_size(int wtype, int T, int N, int K, int E, int top_k) {
-    (void)wtype;
     if (T <= 0 || N <= 0 || K <= 0 || E <= 0 || top_k <= 0) return 0;
-    return moe_layout(T, N, K, E, top_k).total;
+    return moe_layout(wtype, T, N, K, E, top_k).total;
 }
 
 int ksq_moe_gemm(int wtype, const void* weights, const float* activation, const float* router_logits,

@@ -86,8 +86,10 @@ struct MoeTilesArgs {
     float* scratch;
     int top_k;
 };
+// Rows per grouped-GEMM tile (the MoE tile schedule's granularity) for a routing shape.
+int mmq_moe_tile_rows(int wtype, int T, int E, int top_k);
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
-                          const MoeTilesArgs& a, hipStream_t s);
+                          int tile_rows, const MoeTilesArgs& a, hipStream_t s);
 
 // MoE routing: softmax over E logits per token, top_k by logit (ties -> lower expert).
 hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,

@@ -278,8 +278,12 @@ def test_moe_golden_fixture(dev, oracle):
 
 
 @pytest.mark.parametrize("T,E,N,K,top_k,renorm", [(40, 4, 96, 256, 2, False), (37, 8, 160, 512, 3, True),
-                                                  (300, 6, 128, 256, 1, False)])
+                                                  (300, 6, 128, 256, 1, False), (400, 2, 300, 512, 2, False),
+                                                  (500, 3, 136, 256, 3, True)])
 def test_moe_small(dev, oracle, T, E, N, K, top_k, renorm):
+    """Small routed MoE cases against the oracle; the last two average 384+ rows per expert, so the
+    grouped GEMM runs on 128-row tiles (top_k = 2 by atomics, top_k = 3 through the per-entry
+    scratch)."""
     W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, top_k, renorm, 1200 + T)
     ref = oracle.moe_q4_0_f64(W, oracle.quantize_q8_1(x), ids, wts, T, N, K)
     assert _rel_err(y, ref) <= TOL
