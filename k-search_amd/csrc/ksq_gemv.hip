@@ -22,6 +22,8 @@
 //    fp32 epilogue is the reference formula.
 //  * The 64 lane partials are combined with xor shuffles; lane 0 stores.
 //  * Rows longer than the LDS tile are walked in K tiles.
+//  * 1-2 quantised activation rows on 32-element block types take gemv_direct_kernel instead:
+//    lanes load 4-byte-aligned block pairs straight into VGPRs (no LDS round trip).
 #include "ksq_device.h"
 #include "ksq_internal.h"
 
@@ -416,6 +418,129 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
     }
 }
 
+// ---- the register-direct decode kernel ------------------------------------------
+// For 32-element block types with 1-2 activation rows read from L2 (kAL2), every lane owns
+// pairs of adjacent blocks: a pair is 36/40/44/48/68 bytes, 4-byte aligned whenever the row
+// start is (even block count, 4-byte aligned W), so the lane pulls it with dwordx4 loads
+// straight into VGPRs: no LDS round trip, no barrier, no wait for other lanes.  Measured on
+// MI355X against gemv_row_kernel (weights streamed from HBM, us): Q4_0 M = 1 N = K = 4096
+// 4.78 -> 4.14, N = 14336 K = 4096 11.2 -> 8.7, N = 512 K = 7168 3.11 -> 2.57; Q8_0
+// N = K = 4096 6.1 -> 5.4; Q5_1 N = 4096 K = 14336 14.3 -> 11.0.  Issuing two pairs' loads
+// ahead was mixed (-5% to +3%); long rows that stage activations by DMA keep gemv_row_kernel.
+
+// NW dwords from p (4-byte aligned) by 16-, 8- and 4-byte loads.
+template <int NW>
+__device__ __forceinline__ void load_dwords(const uint32_t* __restrict__ p, uint32_t* w) {
+#pragma unroll
+    for (int i = 0; i + 4 <= NW; i += 4) {
+        const u32x4a4 v = *(const u32x4a4*)(p + i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+    }
+    constexpr int r0 = NW & ~3;
+    if constexpr (NW - r0 >= 2) {
+        const u32x2a4 v = *(const u32x2a4*)(p + r0);
+        w[r0] = v.x; w[r0 + 1] = v.y;
+    }
+    if constexpr ((NW - r0) & 1) w[NW - 1] = p[NW - 1];
+}
+
+// Little-endian word i / 16-bit field of the byte string at compile-time offset OFF of raw.
+template <int OFF>
+__device__ __forceinline__ uint32_t word_at(const uint32_t* raw, int i) {
+    constexpr int q = OFF / 4, r = OFF % 4;
+    if constexpr (r == 0) return raw[q + i];
+    else return __builtin_amdgcn_alignbyte(raw[q + i + 1], raw[q + i], r);
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t half_at(const uint32_t* raw) {
+    return (raw[OFF / 4] >> (8 * (OFF % 4))) & 0xFFFFu;
+}
+
+// The block at byte OFF of raw dotted with activation block a[9]: the same integer dots and
+// fp32 block formulas as unit_sumi_legacy and gemv_row_kernel's epilogue.
+template <int WT, bool AS, int OFF>
+__device__ __forceinline__ float reg_block_dot(const uint32_t* raw, const uint32_t* a) {
+    int s = 0;
+    if constexpr (WT == kWQ40 || WT == kWQ41) {
+        constexpr int QO = OFF + (WT == kWQ40 ? 2 : 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = word_at<QO>(raw, i);
+            s = dot4((int)(q & 0x0F0F0F0Fu), (int)a[1 + i], s);
+            s = dot4((int)((q >> 4) & 0x0F0F0F0Fu), (int)a[5 + i], s);
+        }
+    } else if constexpr (WT == kWQ80) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s = dot4((int)word_at<OFF + 2>(raw, i), (int)a[1 + i], s);
+    } else {
+        constexpr int QH = OFF + (WT == kWQ50 ? 2 : 4), QS = OFF + (WT == kWQ50 ? 6 : 8);
+        const uint32_t h = word_at<QH>(raw, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = word_at<QS>(raw, i);
+            s = dot4((int)((q & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i))), (int)a[1 + i], s);
+            s = dot4((int)(((q >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i))), (int)a[5 + i], s);
+        }
+    }
+    const float dw = f16_to_f32(half_at<OFF>(raw));
+    const float da = AS ? __builtin_bit_cast(float, a[0]) : f16_to_f32(a[0] & 0xFFFFu);
+    if constexpr (WT == kWQ40) return dw * (da * (float)s - 8.0f * f16_to_f32(a[0] >> 16));
+    else if constexpr (WT == kWQ80) return AS ? dw * da * (float)s : (float)s * da * dw;
+    else if constexpr (WT == kWQ50) return dw * (da * (float)s - 16.0f * f16_to_f32(a[0] >> 16));
+    else return dw * da * (float)s + f16_to_f32(half_at<OFF + 2>(raw)) * f16_to_f32(a[0] >> 16);
+}
+
+// C[m][row] for m < MR (1 or 2); RPW rows per 256-thread workgroup, 4 / RPW waves per row
+// (their partial sums meet in LDS).  A: block_q8_1 (or block_q8s when AS) [MR][nb], nb even.
+template <int WT, int MR, bool AS, int RPW>
+__global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                          float* __restrict__ C, int N, int nb, int ldc) {
+    static_assert(!is_kquant(WT) && (MR == 1 || MR == 2), "32-element block types, 1-2 activation rows");
+    constexpr int WPR = 4 / RPW;
+    constexpr int BB = block_bytes(WT), PW = BB / 2;  // dwords per block pair
+    __shared__ float red[4][MR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int part = wave % WPR;
+    const int row = blockIdx.x * RPW + wave / WPR;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+    if (row < N) {
+        const uint32_t* wrow = (const uint32_t*)(W + (size_t)row * nb * BB);
+        const int np = nb >> 1;
+        for (int p = part * 64 + lane; p < np; p += 64 * WPR) {
+            uint32_t w[PW], a[MR][18];
+            load_dwords<PW>(wrow + (size_t)p * PW, w);
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                load_dwords<18>((const uint32_t*)(A + ((size_t)m * nb + 2 * p) * kQ81Bytes), a[m]);
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                acc[m] += reg_block_dot<WT, AS, 0>(w, a[m]);
+                acc[m] += reg_block_dot<WT, AS, BB>(w, a[m] + 9);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = wave_sum(acc[m]);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                for (int q = 1; q < WPR; q++) acc[m] += red[wave + q][m];
+        }
+    }
+    if (part == 0 && lane == 0 && row < N) {
+#pragma unroll
+        for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row] = acc[m];
+    }
+}
+
 // ---- host dispatch -------------------------------------------------------------
 constexpr size_t kGemvLdsBudget = 48 * 1024;
 
@@ -497,6 +622,45 @@ static hipError_t row_launch_mr(int mr, int rpw, const uint8_t* W, const void* A
     }
 }
 
+template <int WT, bool AS, int MR>
+static hipError_t direct_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
+                                    hipStream_t s) {
+    const dim3 blk(256);
+    switch (rpw) {
+        case 4: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, 0, s, W, A, C, N, nb, ldc); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, 0, s, W, A, C, N, nb, ldc); break;
+        default: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 1>), dim3(N), blk, 0, s, W, A, C, N, nb, ldc); break;
+    }
+    return hipGetLastError();
+}
+
+template <int WT, bool AS>
+static hipError_t direct_launch(int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
+                                hipStream_t s) {
+    return mr == 1 ? direct_launch_rpw<WT, AS, 1>(rpw, W, A, C, N, nb, ldc, s)
+                   : direct_launch_rpw<WT, AS, 2>(rpw, W, A, C, N, nb, ldc, s);
+}
+
+// The register-direct kernel takes 1-2 quantised activation rows read from L2 for 32-element
+// block types when every block pair is 4-byte aligned.
+static bool direct_eligible(int wtype, int amode, int mr, int nb, const void* W, const void* A) {
+    return amode == kAL2 && !is_kquant(wtype) && mr <= 2 && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 &&
+           ((uintptr_t)A & 3) == 0;
+}
+
+static hipError_t direct_dispatch(int wtype, int afmt, int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C,
+                                  int N, int nb, hipStream_t s) {
+    switch (wtype) {
+        case kWQ40: return direct_launch<kWQ40, false>(mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ80:
+            return afmt == kAQ8S ? direct_launch<kWQ80, true>(mr, rpw, W, A, C, N, nb, N, s)
+                                 : direct_launch<kWQ80, false>(mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ41: return direct_launch<kWQ41, false>(mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ50: return direct_launch<kWQ50, false>(mr, rpw, W, A, C, N, nb, N, s);
+        default: return direct_launch<kWQ51, false>(mr, rpw, W, A, C, N, nb, N, s);
+    }
+}
+
 // QUANT: the activations are already quantised (kAL2 / kADMA by row count and length), else fp32 (kAFQ).
 template <int AMODE>
 static hipError_t gemv_dispatch_mode(int wtype, int afmt, int mr, const uint8_t* W, const void* Am, float* Cm,
@@ -533,7 +697,9 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
                                : (const void*)((const float*)A + (size_t)m0 * K);
         float* Cm = C + (size_t)m0 * N;
         hipError_t e;
-        if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        if (direct_eligible(wtype, AMODE, mr, nb, W, Am))
+            e = direct_dispatch(wtype, afmt, mr, rpw, W, (const uint8_t*)Am, Cm, N, nb, s);
+        else if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         if (e != hipSuccess) return e;
