@@ -541,6 +541,101 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restr
     }
 }
 
+// The same with fp32 activations quantised inside every workgroup (the kAFQ idea): each lane
+// first issues the loads of its first weight pair, the workgroup then quantises the MR
+// activation rows into LDS (hiding the weight latency), and after one barrier the lanes walk
+// their pairs with the activation blocks read from LDS.  RPW 8: two rows per wave, halving
+// the quantisation each row costs.
+template <int WT, int MR, bool AS, int RPW>
+__global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                             float* __restrict__ C, int N, int nb, int ldc) {
+    static_assert(!is_kquant(WT) && (MR == 1 || MR == 2), "32-element block types, 1-2 activation rows");
+    constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
+    constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
+    constexpr int BB = block_bytes(WT), PW = BB / 2;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [MR][nb] activation blocks
+    __shared__ float red[4][MR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int part = wave % WPR;
+    const int row0 = blockIdx.x * RPW + (wave / WPR) * VR;
+    const int np = nb >> 1;
+    int p = part * 64 + lane;
+    uint32_t w[VR][PW];
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+        if (p < np && row0 + v < N) load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+    const int K = nb * 32;
+    for (int t = threadIdx.x; t < MR * nb; t += 256) {
+        const int m = t / nb, u = t - m * nb;
+        const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)u * 32);
+        float x[32];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f32x4 q = src[i];
+            x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+        }
+        uint32_t blk[9];
+        if constexpr (AS) quantize_block_q8s(x, blk);
+        else quantize_block_q8_1(x, blk);
+        uint32_t* dst = (uint32_t*)(smem + (size_t)t * kQ81Bytes);
+#pragma unroll
+        for (int i = 0; i < 9; i++) dst[i] = blk[i];
+    }
+    __syncthreads();
+    float acc[VR][MR];
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = 0.0f;
+    if (row0 < N) {
+        for (bool first = true; p < np; p += 64 * WPR, first = false) {
+            if (!first) {
+#pragma unroll
+                for (int v = 0; v < VR; v++)
+                    if (row0 + v < N)
+                        load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+            }
+            uint32_t a[MR][18];
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                load_dwords<18>((const uint32_t*)(smem + ((size_t)m * nb + 2 * p) * kQ81Bytes), a[m]);
+#pragma unroll
+            for (int v = 0; v < VR; v++)
+                if (row0 + v < N) {
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a[m]);
+                        acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a[m] + 9);
+                    }
+                }
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = wave_sum(acc[v][m]);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[0][m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                for (int q = 1; q < WPR; q++) acc[0][m] += red[wave + q][m];
+        }
+    }
+    if (part == 0 && lane == 0) {
+#pragma unroll
+        for (int v = 0; v < VR; v++)
+            if (row0 + v < N) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+            }
+    }
+}
+
 // ---- host dispatch -------------------------------------------------------------
 constexpr size_t kGemvLdsBudget = 48 * 1024;
 
@@ -634,30 +729,53 @@ static hipError_t direct_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A,
     return hipGetLastError();
 }
 
+template <int WT, bool AS, int MR>
+static hipError_t direct_fq_launch_rpw(int rpw, const uint8_t* W, const float* X, float* C, int N, int nb, int ldc,
+                                       hipStream_t s) {
+    const dim3 blk(256);
+    const size_t lds = (size_t)MR * nb * kQ81Bytes;
+    switch (rpw) {
+        case 8: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 8>), dim3((N + 7) / 8), blk, lds, s, W, X, C, N, nb, ldc); break;
+        case 4: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, lds, s, W, X, C, N, nb, ldc); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, lds, s, W, X, C, N, nb, ldc); break;
+        default: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 1>), dim3(N), blk, lds, s, W, X, C, N, nb, ldc); break;
+    }
+    return hipGetLastError();
+}
+
+// QUANT: pre-quantised activations (gemv_direct_kernel), else fp32 (gemv_direct_fq_kernel).
 template <int WT, bool AS>
-static hipError_t direct_launch(int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
-                                hipStream_t s) {
-    return mr == 1 ? direct_launch_rpw<WT, AS, 1>(rpw, W, A, C, N, nb, ldc, s)
-                   : direct_launch_rpw<WT, AS, 2>(rpw, W, A, C, N, nb, ldc, s);
+static hipError_t direct_launch(bool quant, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb,
+                                int ldc, hipStream_t s) {
+    if (!quant)
+        return mr == 1 ? direct_fq_launch_rpw<WT, AS, 1>(rpw, W, (const float*)A, C, N, nb, ldc, s)
+                       : direct_fq_launch_rpw<WT, AS, 2>(rpw, W, (const float*)A, C, N, nb, ldc, s);
+    return mr == 1 ? direct_launch_rpw<WT, AS, 1>(rpw, W, (const uint8_t*)A, C, N, nb, ldc, s)
+                   : direct_launch_rpw<WT, AS, 2>(rpw, W, (const uint8_t*)A, C, N, nb, ldc, s);
 }
 
-// The register-direct kernel takes 1-2 quantised activation rows read from L2 for 32-element
-// block types when every block pair is 4-byte aligned.
+// The register-direct kernels take 1-2 activation rows (quantised ones read from L2, or fp32
+// ones quantised per workgroup) for 32-element block types when every block pair is 4-byte
+// aligned; the fp32 form also needs the quantised rows to fit the LDS budget.
+#ifndef KSQ_GEMV_DIRECT_FQ
+#define KSQ_GEMV_DIRECT_FQ 1
+#endif
 static bool direct_eligible(int wtype, int amode, int mr, int nb, const void* W, const void* A) {
-    return amode == kAL2 && !is_kquant(wtype) && mr <= 2 && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 &&
-           ((uintptr_t)A & 3) == 0;
+    if (is_kquant(wtype) || mr > 2 || (nb & 1) || ((uintptr_t)W & 3) || ((uintptr_t)A & 3)) return false;
+    if (amode == kAFQ) return KSQ_GEMV_DIRECT_FQ && (size_t)mr * nb * kQ81Bytes <= kGemvLdsBudget;
+    return amode == kAL2;
 }
 
-static hipError_t direct_dispatch(int wtype, int afmt, int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C,
-                                  int N, int nb, hipStream_t s) {
+static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int rpw, const uint8_t* W, const void* A,
+                                  float* C, int N, int nb, hipStream_t s) {
     switch (wtype) {
-        case kWQ40: return direct_launch<kWQ40, false>(mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ40: return direct_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
         case kWQ80:
-            return afmt == kAQ8S ? direct_launch<kWQ80, true>(mr, rpw, W, A, C, N, nb, N, s)
-                                 : direct_launch<kWQ80, false>(mr, rpw, W, A, C, N, nb, N, s);
-        case kWQ41: return direct_launch<kWQ41, false>(mr, rpw, W, A, C, N, nb, N, s);
-        case kWQ50: return direct_launch<kWQ50, false>(mr, rpw, W, A, C, N, nb, N, s);
-        default: return direct_launch<kWQ51, false>(mr, rpw, W, A, C, N, nb, N, s);
+            return afmt == kAQ8S ? direct_launch<kWQ80, true>(quant, mr, rpw, W, A, C, N, nb, N, s)
+                                 : direct_launch<kWQ80, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ41: return direct_launch<kWQ41, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ50: return direct_launch<kWQ50, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+        default: return direct_launch<kWQ51, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
     }
 }
 
@@ -698,7 +816,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
         float* Cm = C + (size_t)m0 * N;
         hipError_t e;
         if (direct_eligible(wtype, AMODE, mr, nb, W, Am))
-            e = direct_dispatch(wtype, afmt, mr, rpw, W, (const uint8_t*)Am, Cm, N, nb, s);
+            e = direct_dispatch(wtype, afmt, QUANT, mr, rpw, W, Am, Cm, N, nb, s);
         else if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
@@ -724,7 +842,9 @@ bool gemv_fused_profitable(int wtype, int M, int N, int K) {
     const int rpw = pick_rpw(N, kAFQ);
     const int nb = K / 32, KT = (nb + 7) & ~7;
     // one K tile only: with several, each tile's quantisation would wait for the previous tile
-    if (gemv_lds_bytes(wtype, M, KT, kAFQ, rpw) > kGemvLdsBudget) return false;
+    // (the register-direct form stages only the activation rows, for 4-byte aligned weights)
+    const bool direct = !is_kquant(wtype) && (nb & 1) == 0 && (size_t)M * nb * kQ81Bytes <= kGemvLdsBudget;
+    if (!direct && gemv_lds_bytes(wtype, M, KT, kAFQ, rpw) > kGemvLdsBudget) return false;
     const long long wgs = (N + rpw - 1) / rpw;
     return (long long)M * wgs * nb <= KSQ_GEMV_FUSED_MAX_WORK;
 }

@@ -468,24 +468,27 @@ def test_long_row_decode(dev, oracle, wtype, M, N, K):
 @pytest.mark.parametrize("wtype", [0, 1, 4, 5, 6])
 @pytest.mark.parametrize("M", [1, 2])
 def test_direct_decode_kernel(dev, oracle, wtype, M):
-    """The register-direct decode kernel (pre-quantised activations, 1-2 rows, block pairs
-    loaded straight into VGPRs): 1, 2 and 4 rows per workgroup, a ragged last workgroup, and
-    the cases it must leave to the LDS kernel (odd block count; weights only 2-byte aligned);
-    weights 4 bytes into their buffer still take it.  Bars: TOL against the oracle."""
+    """The register-direct decode kernels (1-2 activation rows, block pairs loaded straight into
+    VGPRs; pre-quantised activations, or fp32 ones quantised per workgroup): 1, 2, 4 and 8 rows
+    per workgroup, a ragged last workgroup, and the cases they must leave to the LDS kernel (odd
+    block count; weights only 2-byte aligned); weights 4 bytes into their buffer still take
+    them.  Bars: TOL against the oracle for both entries."""
     import torch
     from ksq import ops, synth
     g = np.random.default_rng(2600 + 10 * wtype + M)
     for N, K, off in ((50, 256, 0), (600, 512, 0), (1101, 2048, 0), (257, 4096, 4), (300, 224, 0),
-                      (130, 1024, 2)):
+                      (130, 1024, 2), (2051, 1024, 0), (1000, 14336, 0)):
         w = synth.weights(wtype, g, N, K).reshape(-1)
         x = synth.activations(g, M, K)
         q = oracle.quantize_q8_1(x)
         buf = torch.zeros(w.size + 16, dtype=torch.uint8, device=dev)
         buf[off:off + w.size] = _t(w, dev)
         y = ops.gemm(wtype, 1, buf[off:off + w.size], _t(q, dev), M, N, K)
+        y32 = ops.gemm(wtype, 0, buf[off:off + w.size], _t(x, dev), M, N, K)
         torch.cuda.synchronize()
         ref = oracle.gemm_f64(wtype, q, w, M, N, K)
         assert _rel_err(y.cpu().numpy(), ref) <= TOL, (N, K, off)
+        assert _rel_err(y32.cpu().numpy(), ref) <= TOL, (N, K, off)
 
 
 @pytest.mark.parametrize("wtype,M,N,K", [(0, 1, 7168, 512), (1, 2, 9728, 2560), (4, 3, 4096, 4096),
