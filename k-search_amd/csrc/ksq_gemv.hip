@@ -22,8 +22,9 @@
 //    fp32 epilogue is the reference formula.
 //  * The 64 lane partials are combined with xor shuffles; lane 0 stores.
 //  * Rows longer than the LDS tile are walked in K tiles.
-//  * 1-2 quantised activation rows on 32-element block types take gemv_direct_kernel instead:
-//    lanes load 4-byte-aligned block pairs straight into VGPRs (no LDS round trip).
+//  * 1-2 quantised activation rows (Q6_K: 1) take the register-direct kernels instead: lanes
+//    load 4-byte-aligned block pairs (K-quants: unit pairs) straight into VGPRs, no LDS round
+//    trip; fp32 rows of 32-element block types are quantised per workgroup beside them.
 #include "ksq_device.h"
 #include "ksq_internal.h"
 
@@ -425,8 +426,9 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
 // straight into VGPRs: no LDS round trip, no barrier, no wait for other lanes.  Measured on
 // MI355X against gemv_row_kernel (weights streamed from HBM, us): Q4_0 M = 1 N = K = 4096
 // 4.78 -> 4.14, N = 14336 K = 4096 11.2 -> 8.7, N = 512 K = 7168 3.11 -> 2.57; Q8_0
-// N = K = 4096 6.1 -> 5.4; Q5_1 N = 4096 K = 14336 14.3 -> 11.0.  Issuing two pairs' loads
-// ahead was mixed (-5% to +3%); long rows that stage activations by DMA keep gemv_row_kernel.
+// N = K = 4096 6.1 -> 5.4; Q5_1 N = 4096 K = 14336 14.3 -> 11.0; Q4_K N = 14336 K = 4096
+// 11.9 -> 8.8; Q6_K 15.8 -> 13.8.  Issuing two pairs' loads ahead was mixed (-5% to +3%);
+// long rows that stage activations by DMA keep gemv_row_kernel.
 
 // NW dwords from p (4-byte aligned) by 16-, 8- and 4-byte loads.
 template <int NW>
@@ -518,6 +520,146 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restr
             for (int m = 0; m < MR; m++) {
                 acc[m] += reg_block_dot<WT, AS, 0>(w, a[m]);
                 acc[m] += reg_block_dot<WT, AS, BB>(w, a[m] + 9);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = wave_sum(acc[m]);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                for (int q = 1; q < WPR; q++) acc[m] += red[wave + q][m];
+        }
+    }
+    if (part == 0 && lane == 0 && row < N) {
+#pragma unroll
+        for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row] = acc[m];
+    }
+}
+
+// K-quant form: a lane task is a pair of 32-element units that share their quant bytes.
+//   Q4_K (144-byte super-blocks, 16-byte aligned in rows of K/256 of them): units 2g, 2g+1
+//        = the low / high nibbles of qs[32g .. 32g+31]; the lane loads the 16-byte head
+//        (d, dmin, 12 scale bytes) and those 32 quant bytes.
+//   Q6_K (210-byte super-blocks, 2-byte aligned): units j, j+2 (j = 4n + h, h < 2) = the low /
+//        high nibbles of ql[64n + 32h ..] with bits 2g.. of qh[32n ..]; the lane loads both
+//        32-byte spans, the 16 scale bytes and d, re-aligning odd super-blocks with alignbyte.
+// Integer dots and fp32 unit formulas are those of gemv_row_kernel.
+// A span of NW little-endian words at p (2-byte aligned), loaded as NW + 1 aligned dwords and
+// re-aligned later (raw_span / realign), so that all loads of a lane task issue before the first
+// v_alignbyte waits on one (left to itself the scheduler starts on the first spans and issues
+// the rest one memory latency later).
+//   fwd:  from p rounded down to 4 bytes; the caller guarantees 4 readable bytes after the span.
+//   back: from 4 (p 4-byte aligned) or 2 bytes before p, ending at p + 4 NW - 1 or p + 4 NW + 1;
+//         the caller guarantees 4 readable bytes before p and, for p = 2 mod 4, 2 after the span.
+template <int NW, bool BACK>
+__device__ __forceinline__ void raw_span(const uint8_t* __restrict__ p, uint32_t* raw) {
+    const int sh = (int)((uintptr_t)p & 3u);
+    load_dwords<NW + 1>((const uint32_t*)(BACK ? p - 4 + sh : p - sh), raw);
+}
+template <int NW, bool BACK>
+__device__ __forceinline__ void realign(const uint8_t* p, const uint32_t* raw, uint32_t* w) {
+    const int sh = (int)((uintptr_t)p & 3u);
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+        w[i] = BACK ? (sh ? __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], 2) : raw[i + 1])
+                    : __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
+}
+
+template <int WT, int MR, int RPW>
+__global__ __launch_bounds__(256) void gemv_direct_kq_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                             float* __restrict__ C, int N, int nb, int ldc) {
+    static_assert(is_kquant(WT) && (MR == 1 || MR == 2), "K-quant types, 1-2 activation rows");
+    constexpr int WPR = 4 / RPW;
+    constexpr int SB = Fmt<WT>::span;
+    __shared__ float red[4][MR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int part = wave % WPR;
+    const int row = blockIdx.x * RPW + wave / WPR;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; m++) acc[m] = 0.0f;
+    if (row < N) {
+        const uint8_t* wrow = W + (size_t)row * (nb / 8) * SB;
+        const int ntask = (nb / 8) * 4;
+        for (int t = part * 64 + lane; t < ntask; t += 64 * WPR) {
+            const int sbi = t >> 2, sub = t & 3;
+            const uint8_t* sb = wrow + (size_t)sbi * SB;
+            if constexpr (WT == kWQ4K) {
+                uint32_t hd[4], q[8], a[MR][18];
+                load_dwords<4>((const uint32_t*)sb, hd);
+                load_dwords<8>((const uint32_t*)(sb + 16 + 32 * sub), q);
+#pragma unroll
+                for (int m = 0; m < MR; m++)
+                    load_dwords<18>((const uint32_t*)(A + ((size_t)m * nb + 8 * sbi + 2 * sub) * kQ81Bytes), a[m]);
+                int sc0, mn0, sc1, mn1;
+                q4_K_scale_min(2 * sub, hd + 1, sc0, mn0);
+                q4_K_scale_min(2 * sub + 1, hd + 1, sc1, mn1);
+                const float d = f16_to_f32(hd[0] & 0xFFFFu), dmin = f16_to_f32(hd[0] >> 16);
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    int s0 = 0, s1 = 0;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        s0 = dot4((int)(q[i] & 0x0F0F0F0Fu), (int)a[m][1 + i], s0);
+                        s1 = dot4((int)((q[i] >> 4) & 0x0F0F0F0Fu), (int)a[m][10 + i], s1);
+                    }
+                    acc[m] += d * (f16_to_f32(a[m][0] & 0xFFFFu) * (float)(sc0 * s0)) -
+                              dmin * (f16_to_f32(a[m][0] >> 16) * (float)mn0);
+                    acc[m] += d * (f16_to_f32(a[m][9] & 0xFFFFu) * (float)(sc1 * s1)) -
+                              dmin * (f16_to_f32(a[m][9] >> 16) * (float)mn1);
+                }
+            } else {
+                const int n = sub >> 1, h = sub & 1;
+                const int j0 = 4 * n + h, j1 = j0 + 2;
+                const uint8_t* pl = sb + 64 * n + 32 * h;  // ql span, ends <= byte 127 (+4 read) of 210
+                const uint8_t* ph = sb + 128 + 32 * n;     // qh span, ends <= byte 191 (+4 read)
+                const uint8_t* ps = sb + 192;              // scales: reads 188 or 190 .. 207 or 209
+                uint32_t rl[9], rh[9], rs[5], a[MR][2][9];
+                raw_span<8, false>(pl, rl);
+                raw_span<8, false>(ph, rh);
+                raw_span<4, true>(ps, rs);
+                const uint32_t dbits = read_u16(sb + 208);
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    load_dwords<9>((const uint32_t*)(A + ((size_t)m * nb + 8 * sbi + j0) * kQ81Bytes), a[m][0]);
+                    load_dwords<9>((const uint32_t*)(A + ((size_t)m * nb + 8 * sbi + j1) * kQ81Bytes), a[m][1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                uint32_t ql[8], qh[8], sc[4];
+                realign<8, false>(pl, rl, ql);
+                realign<8, false>(ph, rh, qh);
+                realign<4, true>(ps, rs, sc);
+                const float d = f16_to_f32(dbits);
+                // scales 2j, 2j + 1 of unit j = 4n + h (+ 2): bytes 8n + 2h (+ 4) of the 16, i.e.
+                // the low or high half of word 2n (2n + 1); no register array indexed at run time
+                const uint32_t sw0 = n ? sc[2] : sc[0], sw1 = n ? sc[3] : sc[1];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const int g = 2 * e + h;
+                    const int lsft = e ? 4 : 0;
+                    const uint32_t sw = (e ? sw1 : sw0) >> (16 * h);
+                    const int c0 = (int)(int8_t)(sw & 0xFFu), c1 = (int)(int8_t)((sw >> 8) & 0xFFu);
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        const uint32_t* av = a[m][e];
+                        int s0 = 0, s1 = 0, z0 = 0, z1 = 0;
+#pragma unroll
+                        for (int i = 0; i < 8; i++) {
+                            const uint32_t v = ((ql[i] >> lsft) & 0x0F0F0F0Fu) | (((qh[i] >> (2 * g)) << 4) & 0x30303030u);
+                            if (i < 4) { s0 = dot4((int)v, (int)av[1 + i], s0); z0 = dot4(0x01010101, (int)av[1 + i], z0); }
+                            else       { s1 = dot4((int)v, (int)av[1 + i], s1); z1 = dot4(0x01010101, (int)av[1 + i], z1); }
+                        }
+                        const int is0 = s0 - 32 * z0, is1 = s1 - 32 * z1;
+                        acc[m] += d * (f16_to_f32(av[0] & 0xFFFFu) * (float)(c0 * is0 + c1 * is1));
+                    }
+                }
             }
         }
     }
@@ -760,14 +902,39 @@ static hipError_t direct_launch(bool quant, int mr, int rpw, const uint8_t* W, c
 #ifndef KSQ_GEMV_DIRECT_FQ
 #define KSQ_GEMV_DIRECT_FQ 1
 #endif
+#ifndef KSQ_GEMV_DIRECT_KQ
+#define KSQ_GEMV_DIRECT_KQ 1
+#endif
 static bool direct_eligible(int wtype, int amode, int mr, int nb, const void* W, const void* A) {
-    if (is_kquant(wtype) || mr > 2 || (nb & 1) || ((uintptr_t)W & 3) || ((uintptr_t)A & 3)) return false;
+    // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
+    // vs 17.0 us), 1 row 13-18% faster; Q4_K 10-20% faster with 1 or 2
+    if (is_kquant(wtype))
+        return KSQ_GEMV_DIRECT_KQ && amode == kAL2 && mr <= (wtype == kWQ4K ? 2 : 1) && (nb & 7) == 0 &&
+               ((uintptr_t)A & 3) == 0 && ((uintptr_t)W & (wtype == kWQ4K ? 3 : 1)) == 0;
+    if (mr > 2 || (nb & 1) || ((uintptr_t)W & 3) || ((uintptr_t)A & 3)) return false;
     if (amode == kAFQ) return KSQ_GEMV_DIRECT_FQ && (size_t)mr * nb * kQ81Bytes <= kGemvLdsBudget;
     return amode == kAL2;
 }
 
 static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int rpw, const uint8_t* W, const void* A,
                                   float* C, int N, int nb, hipStream_t s) {
+    if (wtype == kWQ4K || wtype == kWQ6K) {
+        const uint8_t* Aq = (const uint8_t*)A;
+        const dim3 blk(256);
+#define KSQ_KQ_LAUNCH(WT)                                                                                          \
+    if (mr == 1) {                                                                                                 \
+        if (rpw == 4) hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 1, 4>), dim3((N + 3) / 4), blk, 0, s, W, Aq, C, N, nb, N); \
+        else if (rpw == 2) hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 1, 2>), dim3((N + 1) / 2), blk, 0, s, W, Aq, C, N, nb, N); \
+        else hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 1, 1>), dim3(N), blk, 0, s, W, Aq, C, N, nb, N);          \
+    } else {                                                                                                       \
+        if (rpw == 4) hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 2, 4>), dim3((N + 3) / 4), blk, 0, s, W, Aq, C, N, nb, N); \
+        else if (rpw == 2) hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 2, 2>), dim3((N + 1) / 2), blk, 0, s, W, Aq, C, N, nb, N); \
+        else hipLaunchKernelGGL((gemv_direct_kq_kernel<WT, 2, 1>), dim3(N), blk, 0, s, W, Aq, C, N, nb, N);          \
+    }
+        if (wtype == kWQ4K) { KSQ_KQ_LAUNCH(kWQ4K) } else { KSQ_KQ_LAUNCH(kWQ6K) }
+#undef KSQ_KQ_LAUNCH
+        return hipGetLastError();
+    }
     switch (wtype) {
         case kWQ40: return direct_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
         case kWQ80:

@@ -491,6 +491,31 @@ def test_direct_decode_kernel(dev, oracle, wtype, M):
         assert _rel_err(y32.cpu().numpy(), ref) <= TOL, (N, K, off)
 
 
+@pytest.mark.parametrize("wtype", [2, 3])
+@pytest.mark.parametrize("M", [1, 2])
+def test_direct_decode_kquant(dev, oracle, wtype, M):
+    """The register-direct decode kernel on Q4_K / Q6_K (lane tasks = unit pairs sharing their
+    quant bytes; Q6_K super-blocks are 210 bytes, so odd ones are 2-byte aligned and re-aligned
+    in registers): 1, 2 and 4 rows per workgroup, odd super-block counts per row, weights 4 bytes
+    into their buffer, pre-quantised and fp32 entries.  Bars: TOL against the oracle."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(2700 + 10 * wtype + M)
+    for N, K, off in ((50, 256, 0), (601, 768, 0), (1101, 2048, 0), (257, 4096, 4), (131, 1280, 4),
+                      (1000, 14336, 0)):
+        w = synth.weights(wtype, g, N, K).reshape(-1)
+        x = synth.activations(g, M, K)
+        q = oracle.quantize_q8_1(x)
+        buf = torch.zeros(w.size + 16, dtype=torch.uint8, device=dev)
+        buf[off:off + w.size] = _t(w, dev)
+        y = ops.gemm(wtype, 1, buf[off:off + w.size], _t(q, dev), M, N, K)
+        y32 = ops.gemm(wtype, 0, buf[off:off + w.size], _t(x, dev), M, N, K)
+        torch.cuda.synchronize()
+        ref = oracle.gemm_f64(wtype, q, w, M, N, K)
+        assert _rel_err(y.cpu().numpy(), ref) <= TOL, (N, K, off)
+        assert _rel_err(y32.cpu().numpy(), ref) <= TOL, (N, K, off)
+
+
 @pytest.mark.parametrize("wtype,M,N,K", [(0, 1, 7168, 512), (1, 2, 9728, 2560), (4, 3, 4096, 4096),
                                          (6, 4, 2560, 2560), (0, 8, 18944, 3584)])
 def test_prequantized_small_m_routing(dev, oracle, wtype, M, N, K):
