@@ -492,54 +492,69 @@ __device__ __forceinline__ float reg_block_dot(const uint32_t* raw, const uint32
     else return dw * da * (float)s + f16_to_f32(half_at<OFF + 2>(raw)) * f16_to_f32(a[0] >> 16);
 }
 
-// C[m][row] for m < MR (1 or 2); RPW rows per 256-thread workgroup, 4 / RPW waves per row
-// (their partial sums meet in LDS).  A: block_q8_1 (or block_q8s when AS) [MR][nb], nb even.
+// C[m][row] for m < MR (1 or 2); RPW rows per 256-thread workgroup: 8 = two rows per wave (each
+// activation pair a lane loads serves both), 4 = one, 2 or 1 = 4 / RPW waves per row (their
+// partial sums meet in LDS).  A: block_q8_1 (or block_q8s when AS) [MR][nb], nb even.
 template <int WT, int MR, bool AS, int RPW>
 __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
                                                           float* __restrict__ C, int N, int nb, int ldc) {
     static_assert(!is_kquant(WT) && (MR == 1 || MR == 2), "32-element block types, 1-2 activation rows");
-    constexpr int WPR = 4 / RPW;
+    constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
+    constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
     constexpr int BB = block_bytes(WT), PW = BB / 2;  // dwords per block pair
     __shared__ float red[4][MR];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int part = wave % WPR;
-    const int row = blockIdx.x * RPW + wave / WPR;
-    float acc[MR];
+    const int row0 = blockIdx.x * RPW + (wave / WPR) * VR;
+    float acc[VR][MR];
 #pragma unroll
-    for (int m = 0; m < MR; m++) acc[m] = 0.0f;
-    if (row < N) {
-        const uint32_t* wrow = (const uint32_t*)(W + (size_t)row * nb * BB);
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = 0.0f;
+    if (row0 < N) {
         const int np = nb >> 1;
         for (int p = part * 64 + lane; p < np; p += 64 * WPR) {
-            uint32_t w[PW], a[MR][18];
-            load_dwords<PW>(wrow + (size_t)p * PW, w);
+            uint32_t w[VR][PW], a[MR][18];
+#pragma unroll
+            for (int v = 0; v < VR; v++)
+                if (row0 + v < N) load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
 #pragma unroll
             for (int m = 0; m < MR; m++)
                 load_dwords<18>((const uint32_t*)(A + ((size_t)m * nb + 2 * p) * kQ81Bytes), a[m]);
 #pragma unroll
-            for (int m = 0; m < MR; m++) {
-                acc[m] += reg_block_dot<WT, AS, 0>(w, a[m]);
-                acc[m] += reg_block_dot<WT, AS, BB>(w, a[m] + 9);
-            }
+            for (int v = 0; v < VR; v++)
+                if (row0 + v < N) {
+#pragma unroll
+                    for (int m = 0; m < MR; m++) {
+                        acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a[m]);
+                        acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a[m] + 9);
+                    }
+                }
         }
     }
 #pragma unroll
-    for (int m = 0; m < MR; m++) acc[m] = wave_sum(acc[m]);
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = wave_sum(acc[v][m]);
     if constexpr (WPR > 1) {
         if (lane == 0) {
 #pragma unroll
-            for (int m = 0; m < MR; m++) red[wave][m] = acc[m];
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[0][m];
         }
         __syncthreads();
         if (part == 0) {
 #pragma unroll
             for (int m = 0; m < MR; m++)
-                for (int q = 1; q < WPR; q++) acc[m] += red[wave + q][m];
+                for (int q = 1; q < WPR; q++) acc[0][m] += red[wave + q][m];
         }
     }
-    if (part == 0 && lane == 0 && row < N) {
+    if (part == 0 && lane == 0) {
 #pragma unroll
-        for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row] = acc[m];
+        for (int v = 0; v < VR; v++)
+            if (row0 + v < N) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+            }
     }
 }
 
@@ -859,11 +874,20 @@ static hipError_t row_launch_mr(int mr, int rpw, const uint8_t* W, const void* A
     }
 }
 
+// Two rows per wave once that still leaves 1024 workgroups, or 256 on rows of 384+ blocks
+// (measured, us: Q4_0 M = 1 N = 14336 K = 4096 8.7 -> 8.0, N = 4096 K = 14336 10.0 -> 8.3;
+// fewer workgroups lost: Q4_0 N = K = 2560 2.91 -> 3.16, Q5_0 N = K = 4096 4.41 -> 4.69).
+static int direct_rpw(int rpw, int N, int nb) {
+    const int wgs8 = (N + 7) / 8;
+    return (rpw == 4 && (wgs8 >= 1024 || (nb >= 384 && wgs8 >= kGemvMinWGs))) ? 8 : rpw;
+}
+
 template <int WT, bool AS, int MR>
 static hipError_t direct_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
                                     hipStream_t s) {
     const dim3 blk(256);
-    switch (rpw) {
+    switch (direct_rpw(rpw, N, nb)) {
+        case 8: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 8>), dim3((N + 7) / 8), blk, 0, s, W, A, C, N, nb, ldc); break;
         case 4: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, 0, s, W, A, C, N, nb, ldc); break;
         case 2: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, 0, s, W, A, C, N, nb, ldc); break;
         default: hipLaunchKernelGGL((gemv_direct_kernel<WT, MR, AS, 1>), dim3(N), blk, 0, s, W, A, C, N, nb, ldc); break;

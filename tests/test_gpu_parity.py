@@ -470,14 +470,14 @@ def test_long_row_decode(dev, oracle, wtype, M, N, K):
 def test_direct_decode_kernel(dev, oracle, wtype, M):
     """The register-direct decode kernels (1-2 activation rows, block pairs loaded straight into
     VGPRs; pre-quantised activations, or fp32 ones quantised per workgroup): 1, 2, 4 and 8 rows
-    per workgroup, a ragged last workgroup, and the cases they must leave to the LDS kernel (odd
+    per workgroup (8 = two rows per wave), a ragged last workgroup, and the cases they must leave to the LDS kernel (odd
     block count; weights only 2-byte aligned); weights 4 bytes into their buffer still take
     them.  Bars: TOL against the oracle for both entries."""
     import torch
     from ksq import ops, synth
     g = np.random.default_rng(2600 + 10 * wtype + M)
     for N, K, off in ((50, 256, 0), (600, 512, 0), (1101, 2048, 0), (257, 4096, 4), (300, 224, 0),
-                      (130, 1024, 2), (2051, 1024, 0), (1000, 14336, 0)):
+                      (130, 1024, 2), (2051, 1024, 0), (1000, 14336, 0), (2049, 12288, 0)):
         w = synth.weights(wtype, g, N, K).reshape(-1)
         x = synth.activations(g, M, K)
         q = oracle.quantize_q8_1(x)
