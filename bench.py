@@ -36,8 +36,8 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 # HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB per
 # dispatch, mean of 6) over `bench.py --only gemm|gemv`, scaled by the factors a plain
 # 256 MiB copy gives the same counters (reads x2.0, writes x1.0); summaries in profiles/.
-TRAFFIC_MMQ_Q4_0_M2048 = int((41725.5 * 2.0 + 32910.2 * 1.0) * 1024)
-TRAFFIC_GEMV_Q4_0_M1 = int((4652.2 * 2.0 + 32.0 * 1.0) * 1024)
+TRAFFIC_MMQ_Q4_0_M2048 = int((41715.8 * 2.0 + 32941.8 * 1.0) * 1024)
+TRAFFIC_GEMV_Q4_0_M1 = int((4642.2 * 2.0 + 32.0 * 1.0) * 1024)
 
 
 def log(msg: str) -> None:

@@ -299,10 +299,15 @@ bool skinny_supported(int wtype, int afmt, int M, int N, int K, const void* W, c
 // on rows up to 8192 elements only for N >= 7168 (Q4_0 N = 12288, K = 5120: 15.2 vs 17.3 at
 // M = 4; N = 5120, K = 5120: 11.0 vs 9.6 the other way), at M = 1 only on very short rows
 // (N = 7168, K = 512: 2.7 vs 3.7); below N = 2048 (N = 512, K = 7168: 5.8 vs 3.4 at M = 2) and on
-// long rows (N = 5120, K = 12288: 19.8 vs 11.1 at M = 2) the decode kernel wins.
+// long rows (N = 5120, K = 12288: 19.8 vs 11.1 at M = 2) the decode kernel wins.  At M = 2 the
+// register-direct decode kernel wins everywhere but on very short rows (N = 7168, K = 512: 2.7
+// vs 4.8) and for Q8_0 on 3584..8192-square shapes (N = K = 7168: 16.6 vs 18.0); elsewhere it is
+// 5-32% faster (Q4_0 N = 14336, K = 4096: 9.8 vs 13.0; N = K = 4096: 4.8 vs 5.2).
 bool skinny_preferred(int wtype, int M, int N, int K) {
-    (void)wtype;
     if (M == 1) return K <= 1024 && N >= 4096;
+    if (M == 2)
+        return (K <= 1024 && N >= 4096) ||
+               (wtype == kWQ80 && N >= 3584 && N <= 8192 && K >= 3584 && K <= 8192);
     if (N < 2048) return false;
     if (K <= 4096) return true;
     if (K <= 8192) return N >= 7168;

@@ -424,7 +424,8 @@ def test_skinny_q8s_native(dev, oracle, M):
                                          (0, 8, 4096, 4096), (4, 3, 2560, 2560), (0, 3, 4096, 4096),
                                          (0, 2, 7168, 512), (1, 4, 9728, 2560), (4, 8, 18944, 3584),
                                          (0, 5, 3584, 18944), (1, 8, 7168, 7168), (5, 4, 12288, 5120),
-                                         (2, 8, 4096, 4096), (3, 7, 12288, 5120), (2, 5, 7168, 7168)])
+                                         (2, 8, 4096, 4096), (3, 7, 12288, 5120), (2, 5, 7168, 7168),
+                                         (1, 2, 4096, 4096), (0, 2, 14336, 4096)])
 def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
     """M = 2..8 by default: large matrices take the MFMA GEMM (the measured crossovers), short
     rows on wide matrices the 4x4x4-MFMA small-batch kernel, the rest the decode kernel; each way
