@@ -125,6 +125,24 @@ KSQ_API void ksq_gemm_q5_1_q8_1(const uint8_t* weight, const uint8_t* activation
  * x 16-byte aligned, y 4-byte aligned.  stream: hipStream_t or NULL. */
 KSQ_API int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream);
 
+/* The reference's other Q8_1 quantisers, [M][K] -> block_q8_1 [M][K/32], each bit for bit
+ * (x 16-byte and y 4-byte aligned; KSQ_ERR_TYPE for an unknown variant):
+ *   KSQ_Q81_REF        quantize_row_q8_1_ref, the same as ksq_quantize_q8_1
+ *   KSQ_Q81_CUDA       the reference's device kernel quantize_q8_1_kernel
+ *                      (include/quantize.h:301-336): half-to-even rounding
+ *   KSQ_Q81_NUMPY      the test harness' quantize_to_q8_1
+ *                      (llm_kernel_test/reference/quantize.py:165-214): true division,
+ *                      d = 1 for an all-zero block, NumPy's pairwise float32 sum; finite x
+ *   KSQ_Q81_FUSED_F16  the fused FP16-activation kernels' quantize_fp16_to_q8_1_smem
+ *                      (kernels/gemm/gemm_fused.cuh:76-145): x is fp16 (uint16 bits), tree
+ *                      max/sum, q from 1/half(d), clamp [-127, 127]
+ * x is fp32 for the first three. */
+#define KSQ_Q81_REF 0
+#define KSQ_Q81_CUDA 1
+#define KSQ_Q81_NUMPY 2
+#define KSQ_Q81_FUSED_F16 3
+KSQ_API int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int K, void* stream);
+
 /* fp32 [M][K] -> block_q8s [M][K/32] by the native W8A8C8 operator's per-block rules
  * (variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93, bit for bit).  Same alignment
  * rules as ksq_quantize_q8_1. */

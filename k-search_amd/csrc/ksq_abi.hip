@@ -230,6 +230,19 @@ int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* stream) {
     return ok();
 }
 
+int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int K, void* stream) {
+    if (variant < KSQ_Q81_REF || variant > KSQ_Q81_FUSED_F16)
+        return set_error(KSQ_ERR_TYPE, "unknown Q8_1 quantiser variant %d", variant);
+    if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
+    if (M == 0 || K == 0) return ok();
+    if (!x || !y) return set_error(KSQ_ERR_NULL, "x or y is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 3u))
+        return set_error(KSQ_ERR_ALIGN, "x must be 16-byte and y 4-byte aligned");
+    hipError_t e = ksq::launch_quantize_variant(variant, x, y, M, K, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "quantize launch");
+    return ok();
+}
+
 int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
     if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
     if (M == 0 || K == 0) return ok();

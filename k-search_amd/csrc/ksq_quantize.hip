@@ -173,6 +173,144 @@ hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K,
     return launch_quantize(kAQ81, x, y, rows, K, s);
 }
 
+// ---- the reference's other Q8_1 quantisers (ksq_quantize_q8_1_variant) -----------------
+// One lane per 32-value block, as the reference's own device quantiser runs; block_q8_1 out.
+//   1 quantize_q8_1_kernel (include/quantize.h:301-336): fmaxf/sequential-sum, id = 1/d,
+//     round half to even (__float2int_rn: NaN -> 0), clamp [-128, 127]
+//   2 quantize_to_q8_1 (llm_kernel_test/reference/quantize.py:165-214, NumPy): d = amax/127
+//     or 1 when amax is 0, q = round_half_even(x / d) by true division, s = NumPy's pairwise
+//     float32 sum (eight strided accumulators, tree-combined)
+//   3 quantize_fp16_to_q8_1_smem (kernels/gemm/gemm_fused.cuh:76-145): fp16 input, max and
+//     sum by the shared-memory tree (16, 8, 4, 2 apart, then 0 with 1), id = 1 / half(d),
+//     q = roundf (half away from zero), saturated to int8, then clamp [-127, 127]
+
+// (int) of an already-rounded float as the device converts it (NaN -> 0), clamped to int8.
+__device__ __forceinline__ int sat_i8(float r) {
+    return (r != r) ? 0 : (int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+}
+
+template <int VAR>
+__device__ __forceinline__ void quantize_block_variant(const float* v, uint32_t* out) {
+#pragma clang fp contract(off)
+    float d, sum;
+    if constexpr (VAR == 1) {
+        float amax = 0.0f;
+        sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+            sum += v[j];
+        }
+        d = amax / 127.0f;
+    } else if constexpr (VAR == 2) {
+        float amax = 0.0f;
+        bool nan = false;
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            const float a = __builtin_fabsf(v[j]);
+            nan |= (a != a);
+            amax = a > amax ? a : amax;
+        }
+        d = (!nan && amax > 0.0f) ? amax / 127.0f : 1.0f;
+        float r[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) r[j] = v[j];
+#pragma unroll
+        for (int i = 8; i < 32; i += 8)
+#pragma unroll
+            for (int j = 0; j < 8; j++) r[j] += v[i + j];
+        sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+    } else {
+        float m[32], t[32];
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+            m[j] = __builtin_fabsf(v[j]);
+            t[j] = v[j];
+        }
+#pragma unroll
+        for (int w = 16; w >= 2; w >>= 1)
+#pragma unroll
+            for (int j = 0; j < w; j++) {
+                m[j] = __builtin_fmaxf(m[j], m[j + w]);
+                t[j] += t[j + w];
+            }
+        d = __builtin_fmaxf(m[0], m[1]) / 127.0f;
+        sum = t[0] + t[1];
+    }
+    const uint32_t dh = f32_to_f16(d);
+    out[0] = dh | (f32_to_f16(sum) << 16);
+    float id = 0.0f;
+    if constexpr (VAR == 1) id = (d > 0.0f) ? 1.0f / d : 0.0f;
+    if constexpr (VAR == 3) {
+        const float dr = f16_to_f32(dh);
+        id = (dr != 0.0f) ? 1.0f / dr : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float x = v[4 * i + k];
+            int q;
+            if constexpr (VAR == 1) q = sat_i8(__builtin_rintf(x * id));
+            else if constexpr (VAR == 2) q = sat_i8(__builtin_rintf(x / d));
+            else {
+                q = sat_i8(roundf(x * id));
+                q = q < -127 ? -127 : q;
+            }
+            w |= (uint32_t)(q & 0xFF) << (8 * k);
+        }
+        out[1 + i] = w;
+    }
+}
+
+template <int VAR>
+__global__ __launch_bounds__(256) void quantize_q8_1_variant_kernel(const void* __restrict__ x, uint8_t* __restrict__ y,
+                                                                    int64_t nblocks) {
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    float v[32];
+    if constexpr (VAR == 3) {
+        const u32x4* src = (const u32x4*)((const uint16_t*)x + b * 32);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 w = src[i];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                v[8 * i + 2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                v[8 * i + 2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    } else {
+        const f32x4* src = (const f32x4*)((const float*)x + b * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f32x4 q = src[i];
+            v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+        }
+    }
+    uint32_t out[9];
+    quantize_block_variant<VAR>(v, out);
+    uint32_t* dst = (uint32_t*)(y + b * kQ81Bytes);
+#pragma unroll
+    for (int i = 0; i < 9; i++) dst[i] = out[i];
+}
+
+hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
+    if (variant == 0) return launch_quantize_q8_1((const float*)x, y, rows, K, s);
+    const int64_t nblocks = rows * (int64_t)(K / 32);
+    if (nblocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)((nblocks + 255) / 256)), blk(256);
+    switch (variant) {
+        case 1: hipLaunchKernelGGL(quantize_q8_1_variant_kernel<1>, grid, blk, 0, s, x, y, nblocks); break;
+        case 2: hipLaunchKernelGGL(quantize_q8_1_variant_kernel<2>, grid, blk, 0, s, x, y, nblocks); break;
+        case 3: hipLaunchKernelGGL(quantize_q8_1_variant_kernel<3>, grid, blk, 0, s, x, y, nblocks); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;

@@ -44,6 +44,7 @@ SIGNATURES = {
     "gemm_w8a8c8_q8_0_q8_1": ([_P, _P, _P, _I, _I, _I], None),
     "ksq_quantize_q8_1": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8s": ([_P, _P, _I, _I, _P], _I),
+    "ksq_quantize_q8_1_variant": ([_I, _P, _P, _I, _I, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),

@@ -83,6 +83,25 @@ def quantize_q8_1(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Ten
     return out
 
 
+Q81_REF, Q81_CUDA, Q81_NUMPY, Q81_FUSED_F16 = 0, 1, 2, 3
+
+
+def quantize_q8_1_variant(x: torch.Tensor, variant: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[..., K] -> uint8 [..., K/32, 36] block_q8_1 by one of the reference's quantisers:
+    Q81_REF quantize_row_q8_1_ref, Q81_CUDA its device kernel (half-even), Q81_NUMPY the
+    harness' quantize_to_q8_1, Q81_FUSED_F16 the fused FP16 kernels' quantiser (x float16)."""
+    want = torch.float16 if variant == Q81_FUSED_F16 else torch.float32
+    if x.dtype != want or not x.is_cuda:
+        raise RuntimeError(f"quantize_q8_1_variant({variant}) expects a CUDA {want} tensor")
+    x = x.contiguous()
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if out is None:
+        out = torch.empty((*x.shape[:-1], K // 32, 36), dtype=torch.uint8, device=x.device)
+    check(lib().ksq_quantize_q8_1_variant(variant, _ptr(x), _ptr(out), rows, K, _stream()))
+    return out
+
+
 def quantize_q8s(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 [..., K] -> uint8 [..., K/32, 36] block_q8s (the native W8A8C8 operator's rules)."""
     if x.dtype != torch.float32 or not x.is_cuda:

@@ -30,6 +30,13 @@
  *                        known-answer blocks for the nibble and qh bit order
  *   native W8A8C8        closed-form quantiser checks (ties, tiny blocks -> d = 1,
  *                        true division vs reciprocal), per-block composition
+ *   Q8_1 variants        device kernel: numpy rint/cumsum restatement, ties,
+ *                        zero block, inf; NumPy harness: NumPy itself running
+ *                        the harness expressions, sum-order-sensitive blocks;
+ *                        fused FP16: exact-sum blocks, ties, 1/half(d) vs 1/d.
+ *                        Parity unpinned: the fused quantiser's tree sum order
+ *                        (visible only at fp16 ties of s) and its int8
+ *                        conversion where |v*id| >= 127.5 (subnormal half(d)).
  */
 #include <math.h>
 #include <stdint.h>
@@ -535,6 +542,109 @@ static void quantize_block_q8s(const float* xs, uint8_t* blk) {
 
 KSQ_API void ksq_ref_quantize_row_q8s(const float* x, uint8_t* y, int64_t k) {
     for (int64_t i = 0; i < k / 32; i++) quantize_block_q8s(x + i * 32, y + i * 36);
+}
+
+/* ------------------------------------------------------------------------ */
+/* The reference's other Q8_1 quantisers, all writing block_q8_1.            */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_q8_1_kernel (include/quantize.h:301-336), the reference's device quantiser:
+ * amax = fmaxf(amax, fabsf(v)) from 0, sequential fp32 sum, d = amax / 127, ds = (half(d),
+ * half(sum)), id = d > 0 ? 1/d : 0, q = clamp(__float2int_rn(x * id), -128, 127):
+ * round half to even, NaN -> 0 (the device conversion). */
+static void q81_block_cuda(const float* xs, uint8_t* blk) {
+    float amax = 0.0f, sum = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        amax = fmaxf(amax, fabsf(xs[j]));
+        sum += xs[j];
+    }
+    const float d = amax / 127.0f;
+    wr_f16(blk + 0, d);
+    wr_f16(blk + 2, sum);
+    const float id = (d > 0) ? 1.0f / d : 0.0f;
+    for (int j = 0; j < 32; j++) {
+        int32_t q = cvt_i32_device(rintf(xs[j] * id));   /* rintf: the default nearest-even mode */
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        blk[4 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* NumPy's float32 sum of 32 contiguous values (pairwise_sum of numpy's umath loops, the
+ * path np.sum takes along a contiguous axis): eight accumulators r[j] = a[j] + a[j+8] +
+ * a[j+16] + a[j+24] in that order, combined as ((r0+r1)+(r2+r3)) + ((r4+r5)+(r6+r7)). */
+static float np_sum32_f32(const float* a) {
+    float r[8];
+    for (int j = 0; j < 8; j++) r[j] = a[j];
+    for (int i = 8; i < 32; i += 8)
+        for (int j = 0; j < 8; j++) r[j] += a[i + j];
+    return ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+}
+
+/* quantize_to_q8_1 (llm_kernel_test/reference/quantize.py:165-214), the harness quantiser,
+ * for finite input: amax = max|x|, d = amax > 0 ? amax / 127 : 1 (float32), q = clip(
+ * round_half_even(x / d), -128, 127) (true division), s = np.sum (above), ds = (half(d),
+ * half(s)). */
+static void q81_block_numpy(const float* xs, uint8_t* blk) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        const float a = fabsf(xs[j]);
+        amax = (a > amax || a != a) ? a : amax;   /* np.max propagates NaN */
+        if (amax != amax) break;
+    }
+    const float d = (amax > 0.0f) ? amax / 127.0f : 1.0f;
+    wr_f16(blk + 0, d);
+    wr_f16(blk + 2, np_sum32_f32(xs));
+    for (int j = 0; j < 32; j++) {
+        int32_t q = cvt_i32_device(rintf(xs[j] / d));
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        blk[4 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* quantize_fp16_to_q8_1_smem (kernels/gemm/gemm_fused.cuh:76-145), the fused FP16-activation
+ * kernels' quantiser: fp16 input; max and sum as the shared-memory tree (pairs 16, 8, 4, 2
+ * apart, then element 0 with element 1); d = max / 127; ds = (half(d), half(sum));
+ * id = 1 / half(d) (0 when half(d) is 0); q = clamp((int)roundf(v * id), -127, 127).  The
+ * float -> int8 conversion is taken as saturating (PTX float-to-integer cvt clamps); it only
+ * matters where |v * id| reaches 127.5, i.e. when half(d) is subnormal. */
+static void q81_block_fused_f16(const uint16_t* hs, uint8_t* blk) {
+    float m[32], s[32], v[32];
+    for (int t = 0; t < 32; t++) {
+        v[t] = ksq_ref_f16_to_f32(hs[t]);
+        m[t] = fabsf(v[t]);
+        s[t] = v[t];
+    }
+    for (int w = 16; w >= 2; w >>= 1)
+        for (int t = 0; t < w; t++) {
+            m[t] = fmaxf(m[t], m[t + w]);
+            s[t] += s[t + w];
+        }
+    const float mx = fmaxf(m[0], m[1]), sum = s[0] + s[1];
+    const float d = mx / 127.0f;
+    wr_f16(blk + 0, d);
+    wr_f16(blk + 2, sum);
+    const float dh = rd_f16(blk);
+    const float id = (dh != 0.0f) ? 1.0f / dh : 0.0f;
+    for (int t = 0; t < 32; t++) {
+        int32_t q = cvt_i32_device(roundf(v[t] * id));
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);     /* the int8_t conversion */
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);     /* max(-127, min(127, q)) */
+        blk[4 + t] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* variant 0: quantize_row_q8_1_ref, 1: quantize_q8_1_kernel, 2: the NumPy harness,
+ * 3: the fused FP16 quantiser (x holds fp16 bits). */
+KSQ_API void ksq_ref_quantize_row_q8_1_variant(int variant, const void* x, uint8_t* y, int64_t k) {
+    if (variant == 0) {
+        ksq_ref_quantize_row_q8_1((const float*)x, y, k);
+        return;
+    }
+    for (int64_t i = 0; i < k / 32; i++) {
+        if (variant == 1) q81_block_cuda((const float*)x + i * 32, y + i * 36);
+        else if (variant == 2) q81_block_numpy((const float*)x + i * 32, y + i * 36);
+        else q81_block_fused_f16((const uint16_t*)x + i * 32, y + i * 36);
+    }
 }
 
 /* The whole operator, kernel.cu:46-117: per output, blocks in order, each activation

@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
             f = getattr(L, "ksq_ref_" + name)
             f.argtypes = [P, P]
             f.restype = ctypes.c_int32
+        L.ksq_ref_quantize_row_q8_1_variant.argtypes = [i32, P, P, i64]
+        L.ksq_ref_quantize_row_q8_1_variant.restype = None
         L.ksq_ref_dequantize_row_legacy.argtypes = [i32, P, P, i64]
         L.ksq_ref_sumi_legacy_q8_1.argtypes = [i32, P, P]
         L.ksq_ref_sumi_legacy_q8_1.restype = ctypes.c_int32
@@ -105,6 +107,20 @@ def quantize_q8_1(x: np.ndarray) -> np.ndarray:
     M, K = x.shape
     y = np.empty((M, K // 32, 36), dtype=np.uint8)
     lib().ksq_ref_quantize_row_q8_1(_p(x), _p(y), M * K)
+    return y
+
+
+def quantize_q8_1_variant(x: np.ndarray, variant: int) -> np.ndarray:
+    """[M, K] -> block_q8_1 bytes [M, K/32, 36] by one of the reference's Q8_1 quantisers:
+    0 quantize_row_q8_1_ref, 1 its device kernel (half-even), 2 the NumPy harness'
+    quantize_to_q8_1, 3 the fused FP16-activation kernels' quantiser (x fp16)."""
+    if variant == 3:
+        x = np.ascontiguousarray(x, dtype=np.float16)
+    else:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, 36), dtype=np.uint8)
+    lib().ksq_ref_quantize_row_q8_1_variant(variant, _p(x), _p(y), M * K)
     return y
 
 

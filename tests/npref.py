@@ -187,3 +187,39 @@ def quantize_q8s(x: np.ndarray) -> np.ndarray:
     out[..., 0:4] = d[..., None].view(np.uint8)
     out[..., 4:] = q.view(np.uint8)
     return out
+
+
+def quantize_q8_1_numpy_harness(x: np.ndarray) -> np.ndarray:
+    """The test harness' quantize_to_q8_1 as NumPy runs it (np.max, np.where, true division,
+    np.round half-even, np.sum's pairwise float32 order, np.float16 packing), for finite x."""
+    M, K = x.shape
+    a = x.reshape(M, K // 32, 32).astype(np.float32)
+    mx = np.max(np.abs(a), axis=2)
+    d = np.where(mx > 0, mx / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    q = np.round(a / d[:, :, None]).clip(-128, 127).astype(np.int8)
+    s = np.sum(a, axis=2)
+    out = np.zeros((M, K // 32, 36), dtype=np.uint8)
+    out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(M, K // 32, 2)
+    with np.errstate(over="ignore"):
+        out[:, :, 2:4] = s.astype(np.float16).view(np.uint8).reshape(M, K // 32, 2)
+    out[:, :, 4:] = q.view(np.uint8)
+    return out
+
+
+def quantize_q8_1_device_rint(x: np.ndarray) -> np.ndarray:
+    """The reference's device quantiser (fmaxf max, sequential sum by cumsum, id = 1/d,
+    np.rint half-even, clamp), for finite x."""
+    M, K = x.shape
+    a = x.reshape(M, K // 32, 32).astype(np.float32)
+    amax = np.max(np.abs(a), axis=2)
+    s = np.cumsum(a, axis=2, dtype=np.float32)[:, :, -1]
+    d = (amax / np.float32(127.0)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d > 0, np.float32(1.0) / d, np.float32(0.0)).astype(np.float32)
+    q = np.rint(a * idv[:, :, None]).clip(-128, 127).astype(np.int8)
+    out = np.zeros((M, K // 32, 36), dtype=np.uint8)
+    out[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(M, K // 32, 2)
+    with np.errstate(over="ignore"):
+        out[:, :, 2:4] = s.astype(np.float16).view(np.uint8).reshape(M, K // 32, 2)
+    out[:, :, 4:] = q.view(np.uint8)
+    return out

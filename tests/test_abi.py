@@ -76,6 +76,15 @@ def test_empty_calls_are_noops():
     assert L.ksq_gemm(0, 0, None, None, None, 0, 5, 64, None, 0, None) == 0
     assert L.ksq_gemm(0, 0, None, None, None, 5, 0, 64, None, 0, None) == 0
     assert L.ksq_quantize_q8_1(None, None, 0, 64, None) == 0
+    assert L.ksq_quantize_q8_1_variant(2, None, None, 0, 64, None) == 0
+
+
+def test_quantize_variant_rejects_unknown_variant():
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_quantize_q8_1_variant(4, None, None, 1, 64, None) == 4      # KSQ_ERR_TYPE
+    assert L.ksq_quantize_q8_1_variant(-1, None, None, 1, 64, None) == 4
+    assert L.ksq_quantize_q8_1_variant(1, None, None, 1, 48, None) == 2      # KSQ_ERR_SHAPE
 
 
 def test_workspace_size():

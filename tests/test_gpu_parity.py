@@ -72,6 +72,36 @@ def test_quantize_q8_1_bit_exact(dev, oracle):
         assert np.array_equal(q.cpu().numpy(), oracle.quantize_q8_1(x)), (M, K)
 
 
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+def test_quantize_q8_1_variants_bit_exact(dev, oracle, variant):
+    """ksq_quantize_q8_1_variant: the reference's device quantiser (1), the NumPy harness
+    quantiser (2) and the fused FP16 kernels' quantiser (3) against their oracle statements, bit
+    for bit, over magnitudes 2^-20 .. 2^11, zero blocks, rounding ties, large sums; fp16 input
+    with blocks whose d is subnormal in fp16 (variant 3); infinite inputs (1, 3)."""
+    import torch
+    from ksq import ops
+    g = np.random.default_rng(150 + variant)
+    for M, K in ((1, 4096), (5, 1024), (300, 96)):
+        x = g.standard_normal((M, K), dtype=np.float32) * np.exp2(g.integers(-20, 12, (M, 1))).astype(np.float32)
+        if M == 5:
+            x[0, :32] = 0.0
+            x[1, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5, 3.49999976]
+            x[1, 8:32] = 0.0
+            x[2, 32:64] *= 3e4 if variant != 3 else 1.0
+            x[3, 64:96] = x[3, 64:96] * np.float32(2.0 ** -18)     # fp16: d below 2^-14
+            if variant in (1, 3):
+                x[4, 96] = np.inf
+        if variant == 3:
+            xh = x.astype(np.float16)
+            q = ops.quantize_q8_1_variant(_t(xh, dev), 3)
+            want = oracle.quantize_q8_1_variant(xh, 3)
+        else:
+            q = ops.quantize_q8_1_variant(_t(x, dev), variant)
+            want = oracle.quantize_q8_1_variant(x, variant)
+        torch.cuda.synchronize()
+        assert np.array_equal(q.cpu().numpy(), want), (variant, M, K)
+
+
 def test_golden_fixture_on_gpu(dev):
     """The committed fixtures reproduce on the GPU with no CPU oracle in the loop."""
     import torch

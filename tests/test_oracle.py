@@ -69,6 +69,90 @@ def test_quantize_q8_1_known_answers(oracle):
     assert np.all(z == 0)
 
 
+def test_q8_1_variant_device_kernel(oracle):
+    """quantize_q8_1_kernel (quantize.h:301-336): against a numpy restatement with np.rint and
+    a cumsum sequential sum, plus the ties that separate it from quantize_row_q8_1_ref."""
+    g = np.random.default_rng(40)
+    x = g.standard_normal((16, 1024), dtype=np.float32) * np.exp2(g.integers(-20, 12, (16, 1))).astype(np.float32)
+    x[3, :32] = 0.0
+    x[7, 64:96] *= 3e4
+    assert np.array_equal(oracle.quantize_q8_1_variant(x, 1), npref.quantize_q8_1_device_rint(x))
+    blk = np.zeros((1, 32), dtype=np.float32)
+    blk[0, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5, 3.49999976]
+    qs = oracle.quantize_q8_1_variant(blk, 1)[0, 0, 4:].view(np.int8)
+    assert list(qs[:8]) == [127, 2, -2, 0, 0, 2, -126, 3]          # half to even
+    assert list(oracle.quantize_q8_1_variant(blk, 0)[0, 0, 4:12].view(np.int8)) == [127, 3, -3, 1, -1, 2, -127, 3]
+    assert np.all(oracle.quantize_q8_1_variant(np.zeros((1, 32), np.float32), 1) == 0)
+    # an infinite input: amax = d = inf, id = 0, inf * 0 = NaN converts to 0 on the device
+    inf = np.zeros((1, 32), dtype=np.float32)
+    inf[0, 0], inf[0, 1] = np.inf, 3.0
+    q = oracle.quantize_q8_1_variant(inf, 1)[0, 0]
+    assert np.all(q[4:] == 0) and q[0:2].view(np.float16)[0] == np.inf
+
+
+def test_q8_1_variant_numpy_harness(oracle):
+    """quantize_to_q8_1 (llm_kernel_test/reference/quantize.py:165-214): bit for bit against
+    NumPy running the harness' own expressions (NumPy fixes the pairwise sum order, the
+    float32 true division and the half-even round), over magnitudes from 2^-20 to 2^11."""
+    g = np.random.default_rng(41)
+    x = g.standard_normal((64, 1024), dtype=np.float32) * np.exp2(g.integers(-20, 12, (64, 1))).astype(np.float32)
+    x[3, :32] = 0.0                                    # d = 1 for the all-zero block
+    x[9, 32:64] *= 3e4
+    assert np.array_equal(oracle.quantize_q8_1_variant(x, 2), npref.quantize_q8_1_numpy_harness(x))
+    z = oracle.quantize_q8_1_variant(np.zeros((1, 32), np.float32), 2)[0, 0]
+    assert z[0:2].view(np.float16)[0] == np.float16(1.0) and np.all(z[2:] == 0)
+    blk = np.zeros((1, 32), dtype=np.float32)
+    blk[0, :6] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5]
+    assert list(oracle.quantize_q8_1_variant(blk, 2)[0, 0, 4:10].view(np.int8)) == [127, 2, -2, 0, 0, 2]
+    # blocks whose fp16 s differs between NumPy's pairwise order and a left-to-right sum:
+    # the oracle follows NumPy on each
+    g2 = np.random.default_rng(7)
+    hits = []
+    while len(hits) < 3:
+        b = (g2.standard_normal(32) * np.exp2(g2.integers(-6, 10, 32))).astype(np.float32)
+        if np.sum(b).astype(np.float16) != np.cumsum(b, dtype=np.float32)[-1].astype(np.float16):
+            hits.append(b)
+    for b in hits:
+        got = oracle.quantize_q8_1_variant(b[None, :], 2)[0, 0, 2:4].view(np.float16)[0]
+        assert got == np.sum(b).astype(np.float16)
+
+
+def test_q8_1_variant_fused_f16(oracle):
+    """quantize_fp16_to_q8_1_smem (gemm_fused.cuh:76-145): fp16 input, q from 1/half(d),
+    roundf, clamp +-127.  Checked on blocks whose sums are exact in any order against a numpy
+    statement, on ties, and on a value where 1/half(d) and 1/d round differently.  The tree
+    order of the sum itself only shows where the fp16 rounding of s meets a tie: unpinned."""
+    g = np.random.default_rng(42)
+    # multiples of 2^-8 below 2^7: every partial sum of 32 is exact in fp32
+    xi = g.integers(-2 ** 15, 2 ** 15, (32, 256)).astype(np.float32) * np.float32(2.0 ** -8)
+    x = xi.astype(np.float16)
+    got = oracle.quantize_q8_1_variant(x, 3)
+    a = x.astype(np.float32).reshape(32, 8, 32)
+    d = (np.abs(a).max(axis=2) / np.float32(127.0)).astype(np.float32)
+    dh = d.astype(np.float16)
+    idv = (np.float32(1.0) / dh.astype(np.float32)).astype(np.float32)
+    y = (a * idv[:, :, None]).astype(np.float64)
+    q = (np.sign(y) * np.floor(np.abs(y) + 0.5)).clip(-127, 127).astype(np.int8)
+    assert np.array_equal(got[:, :, 0:2].view(np.float16)[:, :, 0], dh)
+    assert np.array_equal(got[:, :, 2:4].view(np.float16)[:, :, 0], a.sum(axis=2, dtype=np.float64).astype(np.float16))
+    assert np.array_equal(got[:, :, 4:].view(np.int8), q)
+    blk = np.zeros((1, 32), dtype=np.float16)
+    blk[0, :6] = [127.0, 2.5, -2.5, 0.5, -0.5, -127.0]
+    assert list(oracle.quantize_q8_1_variant(blk, 3)[0, 0, 4:10].view(np.int8)) == [127, 3, -3, 1, -1, -127]
+    # 1/half(d) against 1/d: amax = 100 -> d = 0.787401..., half(d) = 0.78759766
+    d32 = np.float32(100.0) / np.float32(127.0)
+    i_h = np.float32(1.0) / np.float32(np.float16(d32))
+    i_d = np.float32(1.0) / d32
+    cand = np.arange(-100.0, 100.0, 2.0 ** -4).astype(np.float16).astype(np.float32)
+    rh = np.floor(np.abs(cand * i_h) + 0.5)
+    rd = np.floor(np.abs(cand * i_d) + 0.5)
+    v = cand[np.flatnonzero(rh != rd)[0]]
+    blk = np.zeros((1, 32), dtype=np.float16)
+    blk[0, 0], blk[0, 1] = 100.0, v
+    q1 = int(oracle.quantize_q8_1_variant(blk, 3)[0, 0, 5].view(np.int8))
+    assert abs(q1) == int(np.floor(np.abs(v * i_h) + 0.5)) != int(np.floor(np.abs(v * i_d) + 0.5))
+
+
 def test_quantize_q8_1_amax_maps_to_127(oracle):
     g = np.random.default_rng(3)
     x = g.standard_normal((64, 256), dtype=np.float32)
