@@ -143,6 +143,15 @@ KSQ_API int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* st
 #define KSQ_Q81_FUSED_F16 3
 KSQ_API int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int K, void* stream);
 
+/* The reference's fused FP16-activation GEMM gemm_q4_0_fp16_fused (kernels/gemm/gemm_fused.cuh:
+ * 311-338) in its orientation: Q4_0 weight [M][K/32] (M weight rows), fp16 activations [N][K]
+ * (uint16 bits, 16-byte aligned), output fp32 [M][N] (weight-row major).  Activations are
+ * quantised by its quantize_fp16_to_q8_1_smem rules (KSQ_Q81_FUSED_F16, bit-exact), block
+ * dots bit-exact; the result is computed in ksq_gemm's [N][M] orientation in the library's
+ * workspace pool and transposed. */
+KSQ_API int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output,
+                                     int M, int N, int K, void* stream);
+
 /* fp32 [M][K] -> block_q8s [M][K/32] by the native W8A8C8 operator's per-block rules
  * (variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93, bit for bit).  Same alignment
  * rules as ksq_quantize_q8_1. */
@@ -153,7 +162,8 @@ KSQ_API int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* str
 KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
 
 /* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype (the block_q8s forms pair
- * with Q8_0 weights only, KSQ_ERR_TYPE otherwise).  workspace may be
+ * with Q8_0 weights only, KSQ_ERR_TYPE otherwise; KSQ_A_F16 takes fp16 activations, 16-byte
+ * aligned, quantised by the fused FP16 kernels' rules as KSQ_Q81_FUSED_F16).  workspace may be
  * NULL (then a per-device pool owned by the library is used, which makes the call
  * allocate on first use and when sizes grow).  Returns a ksq_status. */
 KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,

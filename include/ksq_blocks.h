@@ -146,6 +146,7 @@ enum ksq_atype {
     KSQ_A_Q8_1 = 1,  /* pre-quantised block_q8_1 [M][K/32] */
     KSQ_A_F32_Q8S = 2, /* fp32 [M][K], quantised to block_q8s inside the call (native W8A8C8 rules) */
     KSQ_A_Q8S = 3,   /* pre-quantised block_q8s [M][K/32] */
+    KSQ_A_F16 = 4,   /* fp16 [M][K], quantised to Q8_1 inside the call by the fused FP16 kernels' rules */
 };
 
 #endif /* KSQ_BLOCKS_H */

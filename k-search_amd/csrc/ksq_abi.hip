@@ -79,12 +79,14 @@ int pool_get(size_t bytes, void** out) {
 int block_elems(int wtype) { return (wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) ? 256 : 32; }
 
 bool atype_f32(int atype) { return atype == KSQ_A_F32 || atype == KSQ_A_F32_Q8S; }
+// activations that arrive unquantised (fp32 or fp16) and are quantised into the workspace
+bool atype_raw(int atype) { return atype_f32(atype) || atype == KSQ_A_F16; }
 int atype_fmt(int atype) { return (atype == KSQ_A_F32_Q8S || atype == KSQ_A_Q8S) ? ksq::kAQ8S : ksq::kAQ81; }
 
 int check_common(int wtype, int atype, const void* weight, const void* activation, const void* output, int M,
                  int N, int K) {
     if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q5_1) return set_error(KSQ_ERR_TYPE, "unknown weight type %d", wtype);
-    if (atype < KSQ_A_F32 || atype > KSQ_A_Q8S) return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
+    if (atype < KSQ_A_F32 || atype > KSQ_A_F16) return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
     if (atype_fmt(atype) == ksq::kAQ8S && wtype != KSQ_W_Q8_0)
         return set_error(KSQ_ERR_TYPE, "block_q8s activations pair with Q8_0 weights only (weight type %d)", wtype);
     if (M < 0 || N < 0 || K < 0) return set_error(KSQ_ERR_SHAPE, "negative shape M=%d N=%d K=%d", M, N, K);
@@ -98,8 +100,8 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
     if (w & 1u) return set_error(KSQ_ERR_ALIGN, "weight must be 2-byte aligned");
     if ((wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) && (w & 3u))
         return set_error(KSQ_ERR_ALIGN, "K-quant weight must be 4-byte aligned");
-    if (atype_f32(atype) && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "fp32 activation must be 16-byte aligned");
-    if (!atype_f32(atype) && (a & 3u)) return set_error(KSQ_ERR_ALIGN, "quantised activation must be 4-byte aligned");
+    if (atype_raw(atype) && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "fp32 / fp16 activation must be 16-byte aligned");
+    if (!atype_raw(atype) && (a & 3u)) return set_error(KSQ_ERR_ALIGN, "quantised activation must be 4-byte aligned");
     if (o & 3u) return set_error(KSQ_ERR_ALIGN, "output must be 4-byte aligned");
     return KSQ_OK;
 }
@@ -147,7 +149,7 @@ GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq, bool mmqh) {
         w.q = w.qds + align256((size_t)M * (size_t)(K / 32) * 4u);
         splits = ksq::mmqh_splits(M, N, K);
     } else {
-        w.q = atype_f32(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
+        w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
         splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
     }
     w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
@@ -243,6 +245,29 @@ int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int
     return ok();
 }
 
+int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output, int M, int N,
+                             int K, void* stream) {
+    // the reference's orientation: M weight rows, N activation rows, output [M][N]; computed as
+    // ksq_gemm's [N][M] into the workspace, then transposed
+    int st = check_common(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, output, N, M, K);
+    if (st != KSQ_OK) return st;
+    if (M == 0 || N == 0) return ok();
+    hipStream_t s = (hipStream_t)stream;
+    if (K == 0) {
+        hipError_t e = ksq::launch_fill_zero(output, (int64_t)M * N, s);
+        return e == hipSuccess ? ok() : hip_error(e, "fill launch");
+    }
+    const size_t gws = align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K));
+    void* p = nullptr;
+    st = pool_get(gws + (size_t)M * (size_t)N * sizeof(float), &p);
+    if (st != KSQ_OK) return st;
+    float* tmp = (float*)((uint8_t*)p + gws);
+    st = ksq_gemm(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, tmp, N, M, K, gws ? p : nullptr, gws, stream);
+    if (st != KSQ_OK) return st;
+    hipError_t e = ksq::launch_transpose_f32(tmp, output, N, M, s);
+    return e == hipSuccess ? ok() : hip_error(e, "transpose launch");
+}
+
 int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
     if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
     if (M == 0 || K == 0) return ok();
@@ -285,9 +310,9 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     // fp32 activations are quantised to the start of the (16-byte aligned) workspace, which is
     // what the MFMA path then reads
-    const bool f32 = atype_f32(atype);
-    const bool mmqh = afmt == ksq::kAQ81 && use_mmqh(wtype, M, N, K, weight);
-    const bool mmq = !mmqh && use_mmq(wtype, M, N, K, weight, f32 || aligned16(activation));
+    const bool f32 = atype_f32(atype), f16 = atype == KSQ_A_F16;
+    const bool mmqh = afmt == ksq::kAQ81 && !f16 && use_mmqh(wtype, M, N, K, weight);
+    const bool mmq = !mmqh && use_mmq(wtype, M, N, K, weight, f32 || f16 || aligned16(activation));
     const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq, mmqh);
     uint8_t* ws = (uint8_t*)workspace;
     if (L.total) {
@@ -312,8 +337,10 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
         e = ksq::launch_mmqh((const uint8_t*)weight, qh, ds, output, M, N, K, partials, s);
         return e == hipSuccess ? ok() : hip_error(e, "f16 mfma launch");
     }
-    if (f32) {
-        hipError_t e = ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
+    if (f32 || f16) {
+        // fp16 input takes the fused FP16 kernels' quantiser (kernels/gemm/gemm_fused.cuh:76-145)
+        hipError_t e = f16 ? ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, activation, ws, M, K, s)
+                           : ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
         Aq = ws;
     }

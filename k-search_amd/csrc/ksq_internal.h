@@ -19,6 +19,8 @@ hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, i
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 // variant 0-3 of ksq_quantize_q8_1_variant (x fp32, or fp16 bits for variant 3)
 hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
+// out [cols][rows] = in [rows][cols], fp32
+hipError_t launch_transpose_f32(const float* in, float* out, int rows, int cols, hipStream_t s);
 // The q8h activation layout of the f16-MFMA GEMM: the block_q8_1 quants of [rows][K] as fp16 q/8
 // (qh, [rows][K], 16-byte aligned) and the block ds words (ds, [rows][K/32]); from fp32 (the same
 // quants and ds as block_q8_1, bit for bit) or converted from block_q8_1 blocks.

@@ -311,6 +311,33 @@ hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64
     return hipGetLastError();
 }
 
+// out[c][r] = in[r][c] for in [rows][cols]: 32 x 32 tiles through LDS (33-float pitch, so
+// the column reads are conflict free), 256 threads = 32 columns x 8 row groups.
+__global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                                            int rows, int cols) {
+    __shared__ float tile[32][33];
+    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+    for (int i = 0; i < 32; i += 8) {
+        const int r = r0 + ty + i, c = c0 + tx;
+        if (r < rows && c < cols) tile[ty + i][tx] = in[(size_t)r * cols + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 32; i += 8) {
+        const int c = c0 + ty + i, r = r0 + tx;
+        if (r < rows && c < cols) out[(size_t)c * rows + r] = tile[tx][ty + i];
+    }
+}
+
+hipError_t launch_transpose_f32(const float* in, float* out, int rows, int cols, hipStream_t s) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+    hipLaunchKernelGGL(transpose_f32_kernel, grid, dim3(256), 0, s, in, out, rows, cols);
+    return hipGetLastError();
+}
+
 __global__ void fill_zero_kernel(float* __restrict__ p, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;

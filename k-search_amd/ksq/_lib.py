@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(PKG_ROOT, "libksq.so")
 
 # enum ksq_wtype / ksq_atype / ksq_status (include/ksq_blocks.h, include/ksq.h)
 W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
-A_F32, A_Q8_1, A_F32_Q8S, A_Q8S = 0, 1, 2, 3
+A_F32, A_Q8_1, A_F32_Q8S, A_Q8S, A_F16 = 0, 1, 2, 3, 4
 STATUS = {0: "KSQ_OK", 1: "KSQ_ERR_NULL", 2: "KSQ_ERR_SHAPE", 3: "KSQ_ERR_ALIGN",
           4: "KSQ_ERR_TYPE", 5: "KSQ_ERR_WORKSPACE", 6: "KSQ_ERR_HIP"}
 
@@ -45,6 +45,7 @@ SIGNATURES = {
     "ksq_quantize_q8_1": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8s": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8_1_variant": ([_I, _P, _P, _I, _I, _P], _I),
+    "ksq_gemm_q4_0_fp16_fused": ([_P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),

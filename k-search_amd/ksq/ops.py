@@ -54,6 +54,19 @@ def gemm(wtype: int, atype: int, weight: torch.Tensor, activation: torch.Tensor,
     return out
 
 
+def gemm_q4_0_fp16_fused(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """The reference's gemm_q4_0_fp16_fused orientation: Q4_0 weight [M, K/32] (M weight rows),
+    fp16 activation [N, K], output fp32 [M, N]."""
+    if activation.dtype != torch.float16 or not activation.is_cuda or not weight.is_cuda:
+        raise RuntimeError("gemm_q4_0_fp16_fused expects CUDA uint8 weights and float16 activations")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=weight.device)
+    check(lib().ksq_gemm_q4_0_fp16_fused(_ptr(weight), _ptr(activation.contiguous()), _ptr(out), M, N, K,
+                                         _stream()))
+    return out
+
+
 def forward(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
             entry: str = "gemm_w4a32c8_q4_0_fp32_int8") -> torch.Tensor:
     """The harness wrapper: forward(weight, activation, M, N, K) -> fp32 [M, N]."""

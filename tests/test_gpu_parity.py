@@ -102,6 +102,30 @@ def test_quantize_q8_1_variants_bit_exact(dev, oracle, variant):
         assert np.array_equal(q.cpu().numpy(), want), (variant, M, K)
 
 
+@pytest.mark.parametrize("wtype", [0, 1, 2, 4])
+def test_fp16_activation_entries(dev, oracle, wtype):
+    """fp16 activations (KSQ_A_F16): quantised by the fused FP16 kernels' rules, then every
+    route (decode, small-batch, MFMA); and, for Q4_0, the reference's gemm_q4_0_fp16_fused
+    orientation (M weight rows, output [M][N]).  Bar: TOL against the oracle on the same
+    quantised blocks."""
+    import torch
+    from ksq import ops, synth
+    from ksq._lib import A_F16
+    g = np.random.default_rng(170 + wtype)
+    for M, N, K in ((1, 300, 512), (3, 1024, 2048), (8, 4096, 1024), (64, 520, 768), (300, 256, 4096)):
+        w = synth.weights(wtype, g, N, K)
+        xh = synth.activations(g, M, K).astype(np.float16)
+        ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1_variant(xh, 3), w, M, N, K)
+        wt = _t(w, dev)
+        y = ops.gemm(wtype, A_F16, wt, _t(xh, dev), M, N, K)
+        torch.cuda.synchronize()
+        assert _rel_err(y.cpu().numpy(), ref) <= TOL, (M, N, K)
+        if wtype == 0:
+            yt = ops.gemm_q4_0_fp16_fused(wt, _t(xh, dev), N, M, K)
+            torch.cuda.synchronize()
+            assert np.array_equal(yt.cpu().numpy(), y.cpu().numpy().T), (M, N, K)
+
+
 def test_golden_fixture_on_gpu(dev):
     """The committed fixtures reproduce on the GPU with no CPU oracle in the loop."""
     import torch
