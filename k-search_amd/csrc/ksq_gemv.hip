@@ -581,6 +581,106 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restr
     }
 }
 
+// 3-8 activation rows (quantised input, 32-element block types): the same register-direct
+// weight loads, with the K tile's activation rows staged in LDS once per workgroup by LDS DMA
+// while the first weight pair of every lane is in flight.  A lane reads each activation pair once and
+// applies it to its VR weight rows.
+// LDS bytes per staged activation row of ktp block pairs: 72 B a pair, plus the DMA's
+// alignment shift and read-ahead slack
+__host__ __device__ constexpr int direct_mr_apitch(int ktp) { return (ktp * 72 + 16 + 15) & ~15; }
+
+template <int WT, int MR, bool AS, int RPW>
+__global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                             float* __restrict__ C, int N, int nb, int ktp, int ldc) {
+    static_assert(!is_kquant(WT) && MR >= 1 && MR <= 8, "32-element block types, 1-8 activation rows");
+    constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
+    constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
+    constexpr int BB = block_bytes(WT), PW = BB / 2;
+    extern __shared__ __attribute__((aligned(16))) uint32_t sact[];   // [MR][apitch bytes]
+    const int apitch = direct_mr_apitch(ktp);
+    __shared__ float red[4][MR];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int part = wave % WPR;
+    const int row0 = blockIdx.x * RPW + (wave / WPR) * VR;
+    const int np = nb >> 1;
+    float acc[VR][MR];
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = 0.0f;
+    for (int t0 = 0; t0 < np; t0 += ktp) {
+        const int tp = (np - t0) < ktp ? (np - t0) : ktp;
+        int p = t0 + part * 64 + lane;
+        uint32_t w[VR][PW];
+        if (p < t0 + tp) {
+#pragma unroll
+            for (int v = 0; v < VR; v++)
+                if (row0 + v < N)
+                    load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+        }
+        // stage the tile: row m's tp pairs (tp * 72 contiguous bytes from pair t0) are copied by
+        // wave m % 4 with LDS DMA; its first byte lands at ashift[m] (the source's offset mod 16)
+        int ashift[MR];
+#pragma unroll
+        for (int m = 0; m < MR; m++) {
+            const uint8_t* g = A + ((size_t)m * nb + 2 * (size_t)t0) * kQ81Bytes;
+            ashift[m] = (int)((uintptr_t)g & 15);
+            if ((m & 3) == wave) wave_copy_to_lds(g, (uint8_t*)sact + (size_t)m * apitch + ashift[m], tp * 72, lane);
+        }
+        wait_vmem();
+        __syncthreads();
+        if (row0 < N) {
+            for (bool first = true; p < t0 + tp; p += 64 * WPR, first = false) {
+                if (!first) {
+#pragma unroll
+                    for (int v = 0; v < VR; v++)
+                        if (row0 + v < N)
+                            load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+                }
+#pragma unroll
+                for (int m = 0; m < MR; m++) {
+                    const uint32_t* src = (const uint32_t*)((const uint8_t*)sact + (size_t)m * apitch + ashift[m] +
+                                                            (size_t)(p - t0) * 72);
+                    uint32_t a[18];
+#pragma unroll
+                    for (int i = 0; i < 18; i++) a[i] = src[i];
+#pragma unroll
+                    for (int v = 0; v < VR; v++)
+                        if (row0 + v < N) {
+                            acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a);
+                            acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a + 9);
+                        }
+                }
+            }
+        }
+        if (t0 + ktp < np) __syncthreads();   // the next tile overwrites the LDS
+    }
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = wave_sum(acc[v][m]);
+    if constexpr (WPR > 1) {
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++) red[wave][m] = acc[0][m];
+        }
+        __syncthreads();
+        if (part == 0) {
+#pragma unroll
+            for (int m = 0; m < MR; m++)
+                for (int q = 1; q < WPR; q++) acc[0][m] += red[wave + q][m];
+        }
+    }
+    if (part == 0 && lane == 0) {
+#pragma unroll
+        for (int v = 0; v < VR; v++)
+            if (row0 + v < N) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+            }
+    }
+}
+
 // K-quant form: a lane task is a pair of 32-element units that share their quant bytes.
 //   Q4_K (144-byte super-blocks, 16-byte aligned in rows of K/256 of them): units 2g, 2g+1
 //        = the low / high nibbles of qs[32g .. 32g+31]; the lane loads the 16-byte head
@@ -943,6 +1043,51 @@ static hipError_t direct_launch(bool quant, int mr, int rpw, const uint8_t* W, c
                    : direct_launch_rpw<WT, AS, 2>(rpw, W, (const uint8_t*)A, C, N, nb, ldc, s);
 }
 
+// Pairs per K tile of gemv_direct_mr_kernel: the whole row while MR rows of it fit the LDS
+// budget, else the largest multiple of 64 pairs that does.
+static int direct_mr_ktp(int mr, int nb) {
+    const int np = nb >> 1;
+    if ((size_t)mr * direct_mr_apitch(np) <= kGemvLdsBudget) return np;
+    int ktp = 64;
+    while ((size_t)mr * direct_mr_apitch(ktp + 64) <= kGemvLdsBudget) ktp += 64;
+    return ktp;
+}
+
+template <int WT, bool AS, int MR>
+static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
+                                       hipStream_t s) {
+    const int ktp = direct_mr_ktp(MR, nb);
+    const size_t lds = (size_t)MR * direct_mr_apitch(ktp);
+    const dim3 blk(256);
+    // two rows per wave on long rows for up to 5 activation rows (past that the doubled
+    // accumulators cost occupancy): Q4_0 N = 4096, K = 14336, M = 3 14.8 -> 11.7 us, M = 8
+    // 24.4 -> 28.2 the other way
+    if (rpw == 4 && MR <= 5 && nb >= 384 && (N + 7) / 8 >= kGemvMinWGs) rpw = 8;
+    switch (rpw) {
+        case 8:
+            if constexpr (MR <= 5)
+                hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 8>), dim3((N + 7) / 8), blk, lds, s, W, A, C, N, nb, ktp, ldc);
+            break;
+        case 4: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        default: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 1>), dim3(N), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+    }
+    return hipGetLastError();
+}
+
+template <int WT, bool AS>
+static hipError_t direct_mr_launch(int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
+                                   hipStream_t s) {
+    switch (mr) {
+        case 3: return direct_mr_launch_rpw<WT, AS, 3>(rpw, W, A, C, N, nb, ldc, s);
+        case 4: return direct_mr_launch_rpw<WT, AS, 4>(rpw, W, A, C, N, nb, ldc, s);
+        case 5: return direct_mr_launch_rpw<WT, AS, 5>(rpw, W, A, C, N, nb, ldc, s);
+        case 6: return direct_mr_launch_rpw<WT, AS, 6>(rpw, W, A, C, N, nb, ldc, s);
+        case 7: return direct_mr_launch_rpw<WT, AS, 7>(rpw, W, A, C, N, nb, ldc, s);
+        default: return direct_mr_launch_rpw<WT, AS, 8>(rpw, W, A, C, N, nb, ldc, s);
+    }
+}
+
 // The register-direct kernels take 1-2 activation rows (quantised ones read from L2, or fp32
 // ones quantised per workgroup) for 32-element block types when every block pair is 4-byte
 // aligned; the fp32 form also needs the quantised rows to fit the LDS budget.
@@ -952,7 +1097,16 @@ static hipError_t direct_launch(bool quant, int mr, int rpw, const uint8_t* W, c
 #ifndef KSQ_GEMV_DIRECT_KQ
 #define KSQ_GEMV_DIRECT_KQ 1
 #endif
-static bool direct_eligible(int wtype, int amode, int mr, int nb, const void* W, const void* A) {
+#ifndef KSQ_GEMV_DIRECT_MR
+#define KSQ_GEMV_DIRECT_MR 1
+#endif
+// 3-8 rows: the register-direct form measured 9% faster over 108 decode shapes (M = 3..8, Q4_0 /
+// Q8_0 / Q4_1), but for grids of 256-511 four-row workgroups (N = 1536, K = 5120: 5.6 vs 5.1 us
+// at M = 4), where gemv_row_kernel stays.
+static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw, const void* W, const void* A) {
+    if (amode == kADMA && mr >= 3)
+        return KSQ_GEMV_DIRECT_MR && !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 &&
+               ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 && !(rpw == 4 && (N + 3) / 4 < 512);
     // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
     // vs 17.0 us), 1 row 13-18% faster; Q4_K 10-20% faster with 1 or 2
     if (is_kquant(wtype))
@@ -981,6 +1135,18 @@ static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int r
         if (wtype == kWQ4K) { KSQ_KQ_LAUNCH(kWQ4K) } else { KSQ_KQ_LAUNCH(kWQ6K) }
 #undef KSQ_KQ_LAUNCH
         return hipGetLastError();
+    }
+    if (mr >= 3) {
+        const uint8_t* Aq = (const uint8_t*)A;
+        switch (wtype) {
+            case kWQ40: return direct_mr_launch<kWQ40, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+            case kWQ80:
+                return afmt == kAQ8S ? direct_mr_launch<kWQ80, true>(mr, rpw, W, Aq, C, N, nb, N, s)
+                                     : direct_mr_launch<kWQ80, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+            case kWQ41: return direct_mr_launch<kWQ41, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+            case kWQ50: return direct_mr_launch<kWQ50, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+            default: return direct_mr_launch<kWQ51, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+        }
     }
     switch (wtype) {
         case kWQ40: return direct_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
@@ -1029,7 +1195,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
                                : (const void*)((const float*)A + (size_t)m0 * K);
         float* Cm = C + (size_t)m0 * N;
         hipError_t e;
-        if (direct_eligible(wtype, AMODE, mr, nb, W, Am))
+        if (direct_eligible(wtype, AMODE, mr, nb, N, rpw, W, Am))
             e = direct_dispatch(wtype, afmt, QUANT, mr, rpw, W, Am, Cm, N, nb, s);
         else if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
         else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);

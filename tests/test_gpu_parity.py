@@ -546,6 +546,25 @@ def test_direct_decode_kernel(dev, oracle, wtype, M):
         assert _rel_err(y32.cpu().numpy(), ref) <= TOL, (N, K, off)
 
 
+@pytest.mark.parametrize("wtype", [0, 1, 4, 5, 6])
+@pytest.mark.parametrize("M", [3, 5, 8, 11])
+def test_direct_decode_multirow(dev, oracle, wtype, M):
+    """The register-direct decode kernel for 3-8 activation rows (LDS-DMA-staged activations,
+    decode kernel forced): one and two rows per wave, 1-4 waves per row, K tiles (8 rows of
+    224 blocks), a ragged last workgroup, 11 rows as chunks of 8 + 3, and the cases left to
+    gemv_row_kernel (odd block count; 256-511 four-row workgroups).  Bar: TOL against the
+    oracle."""
+    from ksq import synth
+    g = np.random.default_rng(2800 + 10 * wtype + M)
+    for N, K in ((300, 512), (2051, 1024), (2049, 12288), (1030, 7168), (4100, 224), (1536, 1024)):
+        w = synth.weights(wtype, g, N, K)
+        x = synth.activations(g, M, K)
+        q = oracle.quantize_q8_1(x)
+        y = _gpu_gemm(dev, wtype, w, q, M, N, K, atype=1, path=1)
+        ref = oracle.gemm_f64(wtype, q, w, M, N, K)
+        assert _rel_err(y, ref) <= TOL, (N, K)
+
+
 @pytest.mark.parametrize("wtype", [2, 3])
 @pytest.mark.parametrize("M", [1, 2])
 def test_direct_decode_kquant(dev, oracle, wtype, M):
