@@ -617,9 +617,14 @@ bool mmq_preferred(int wtype, int M, int N, int K) {
     if (wtype == kWQ4K) return (M >= 7 && nk >= 1.2e7) || (M >= 5 && nk >= 5.0e7);
     if (wtype == kWQ6K) return M >= 7 && K <= 7168 && nk >= 1.5e7;
     if (!nib && wtype != kWQ80) return false;
+    // with the register-direct decode kernels (3-8 rows) the crossovers moved: nibble types at
+    // M = 5, 6 stay on the decode kernel to N * K = 1e8 (N = 3584, K = 18944, M = 5: 18.3 vs 21.7
+    // MFMA); Q8_0 at M = 7, 8 takes the MFMA GEMM only for 2e7 <= N * K < 3e7 (N = K = 5120:
+    // 15.7 vs 17.2 small-batch; N = K = 7168: 26.5 vs 23.1 small-batch, N = 14336, K = 4096:
+    // 28.4 vs 25.2 decode)
     bool pref;
-    if (M >= 7) pref = nk >= 2.0e7;
-    else if (M >= 5) pref = nib && nk >= 6.0e7;
+    if (M >= 7) pref = nk >= 2.0e7 && (nib || nk < 3.0e7);
+    else if (M >= 5) pref = nib && nk >= 1.0e8;
     else pref = false;
     if (pref && K <= 3584 && skinny_preferred(wtype, M, N, K)) return false;
     return pref;

@@ -308,6 +308,10 @@ bool skinny_preferred(int wtype, int M, int N, int K) {
     if (M == 2)
         return (K <= 1024 && N >= 4096) ||
                (wtype == kWQ80 && N >= 3584 && N <= 8192 && K >= 3584 && K <= 8192);
+    // 3-5 rows against the register-direct decode kernel: rows of up to 3584 elements below
+    // N = 14336 (0.6% above the per-shape best over 81 shapes; Q4_0 N = 14336, K = 4096, M = 4:
+    // 13.0 decode vs 15.8; N = 3584, K = 3584: 4.8 vs 6.1 the other way)
+    if (M <= 5) return N >= 2048 && N < 14336 && K <= 3584;
     if (N < 2048) return false;
     if (K <= 4096) return true;
     if (K <= 8192) return N >= 7168;
