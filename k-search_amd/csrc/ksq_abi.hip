@@ -302,7 +302,7 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     const uint8_t* Aq = (const uint8_t*)activation;
     const int afmt = atype_fmt(atype);
-    if (atype_f32(atype) && ksq::gemv_fused_profitable(wtype, M, N, K) && !use_mmq(wtype, M, N, K, weight, true) &&
+    if (atype_f32(atype) && ksq::gemv_fused_profitable(wtype, M, N, K, weight) && !use_mmq(wtype, M, N, K, weight, true) &&
         g_path != 3) {
         hipError_t e = ksq::launch_gemv_f32(wtype, afmt, (const uint8_t*)weight, (const float*)activation, output, M,
                                             N, K, s);

@@ -589,8 +589,10 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restr
 // alignment shift and read-ahead slack
 __host__ __device__ constexpr int direct_mr_apitch(int ktp) { return (ktp * 72 + 16 + 15) & ~15; }
 
-template <int WT, int MR, bool AS, int RPW>
-__global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+// FQ: the activations arrive as fp32 [MR][32 nb] and the workgroup quantises the (single) K
+// tile into the same LDS layout instead (the device quantiser, bit-identical blocks).
+template <int WT, int MR, bool AS, int RPW, bool FQ>
+__global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
                                                              float* __restrict__ C, int N, int nb, int ktp, int ldc) {
     static_assert(!is_kquant(WT) && MR >= 1 && MR <= 8, "32-element block types, 1-8 activation rows");
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
@@ -621,13 +623,37 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
         // stage the tile: row m's tp pairs (tp * 72 contiguous bytes from pair t0) are copied by
         // wave m % 4 with LDS DMA; its first byte lands at ashift[m] (the source's offset mod 16)
         int ashift[MR];
+        if constexpr (FQ) {
+            const float* X = (const float*)Ain;
+            const int K = nb * 32;
+            for (int e = threadIdx.x; e < MR * 2 * tp; e += 256) {
+                const int m = e / (2 * tp), u = e - m * 2 * tp;   // block u of row m's tile
+                const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)(2 * t0 + u) * 32);
+                float x[32];
 #pragma unroll
-        for (int m = 0; m < MR; m++) {
-            const uint8_t* g = A + ((size_t)m * nb + 2 * (size_t)t0) * kQ81Bytes;
-            ashift[m] = (int)((uintptr_t)g & 15);
-            if ((m & 3) == wave) wave_copy_to_lds(g, (uint8_t*)sact + (size_t)m * apitch + ashift[m], tp * 72, lane);
+                for (int i = 0; i < 8; i++) {
+                    const f32x4 q = src[i];
+                    x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+                }
+                uint32_t blk[9];
+                if constexpr (AS) quantize_block_q8s(x, blk);
+                else quantize_block_q8_1(x, blk);
+                uint32_t* dst = (uint32_t*)((uint8_t*)sact + (size_t)m * apitch + (size_t)u * kQ81Bytes);
+#pragma unroll
+                for (int i = 0; i < 9; i++) dst[i] = blk[i];
+            }
+#pragma unroll
+            for (int m = 0; m < MR; m++) ashift[m] = 0;
+        } else {
+            const uint8_t* A = (const uint8_t*)Ain;
+#pragma unroll
+            for (int m = 0; m < MR; m++) {
+                const uint8_t* g = A + ((size_t)m * nb + 2 * (size_t)t0) * kQ81Bytes;
+                ashift[m] = (int)((uintptr_t)g & 15);
+                if ((m & 3) == wave) wave_copy_to_lds(g, (uint8_t*)sact + (size_t)m * apitch + ashift[m], tp * 72, lane);
+            }
+            wait_vmem();
         }
-        wait_vmem();
         __syncthreads();
         if (row0 < N) {
             for (bool first = true; p < t0 + tp; p += 64 * WPR, first = false) {
@@ -1053,10 +1079,11 @@ static int direct_mr_ktp(int mr, int nb) {
     return ktp;
 }
 
-template <int WT, bool AS, int MR>
-static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
+template <int WT, bool AS, int MR, bool FQ>
+static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int ldc,
                                        hipStream_t s) {
     const int ktp = direct_mr_ktp(MR, nb);
+    if (FQ && ktp != (nb >> 1)) return hipErrorNotSupported;   // fused quantisation: one K tile
     const size_t lds = (size_t)MR * direct_mr_apitch(ktp);
     const dim3 blk(256);
     // two rows per wave on long rows for up to 5 activation rows (past that the doubled
@@ -1066,26 +1093,30 @@ static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const uint8_t*
     switch (rpw) {
         case 8:
             if constexpr (MR <= 5)
-                hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 8>), dim3((N + 7) / 8), blk, lds, s, W, A, C, N, nb, ktp, ldc);
+                hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 8, FQ>), dim3((N + 7) / 8), blk, lds, s, W, A, C, N, nb, ktp, ldc);
             break;
-        case 4: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
-        case 2: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
-        default: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 1>), dim3(N), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        case 4: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 4, FQ>), dim3((N + 3) / 4), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 2, FQ>), dim3((N + 1) / 2), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        default: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 1, FQ>), dim3(N), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
     }
     return hipGetLastError();
 }
 
 template <int WT, bool AS>
-static hipError_t direct_mr_launch(int mr, int rpw, const uint8_t* W, const uint8_t* A, float* C, int N, int nb, int ldc,
-                                   hipStream_t s) {
+static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb,
+                                   int ldc, hipStream_t s) {
+#define KSQ_MR_CASE(MRV) \
+    return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s) \
+                 : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, s);
     switch (mr) {
-        case 3: return direct_mr_launch_rpw<WT, AS, 3>(rpw, W, A, C, N, nb, ldc, s);
-        case 4: return direct_mr_launch_rpw<WT, AS, 4>(rpw, W, A, C, N, nb, ldc, s);
-        case 5: return direct_mr_launch_rpw<WT, AS, 5>(rpw, W, A, C, N, nb, ldc, s);
-        case 6: return direct_mr_launch_rpw<WT, AS, 6>(rpw, W, A, C, N, nb, ldc, s);
-        case 7: return direct_mr_launch_rpw<WT, AS, 7>(rpw, W, A, C, N, nb, ldc, s);
-        default: return direct_mr_launch_rpw<WT, AS, 8>(rpw, W, A, C, N, nb, ldc, s);
+        case 3: KSQ_MR_CASE(3)
+        case 4: KSQ_MR_CASE(4)
+        case 5: KSQ_MR_CASE(5)
+        case 6: KSQ_MR_CASE(6)
+        case 7: KSQ_MR_CASE(7)
+        default: KSQ_MR_CASE(8)
     }
+#undef KSQ_MR_CASE
 }
 
 // The register-direct kernels take 1-2 activation rows (quantised ones read from L2, or fp32
@@ -1107,6 +1138,8 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
     if (amode == kADMA && mr >= 3)
         return KSQ_GEMV_DIRECT_MR && !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 &&
                ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 && !(rpw == 4 && (N + 3) / 4 < 512);
+    if (amode == kAFQ && mr >= 3)   // gemv_fused_profitable admitted it: one K tile, no grid exclusion
+        return !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && direct_mr_ktp(mr, nb) == (nb >> 1);
     // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
     // vs 17.0 us), 1 row 13-18% faster; Q4_K 10-20% faster with 1 or 2
     if (is_kquant(wtype))
@@ -1137,15 +1170,14 @@ static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int r
         return hipGetLastError();
     }
     if (mr >= 3) {
-        const uint8_t* Aq = (const uint8_t*)A;
         switch (wtype) {
-            case kWQ40: return direct_mr_launch<kWQ40, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+            case kWQ40: return direct_mr_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
             case kWQ80:
-                return afmt == kAQ8S ? direct_mr_launch<kWQ80, true>(mr, rpw, W, Aq, C, N, nb, N, s)
-                                     : direct_mr_launch<kWQ80, false>(mr, rpw, W, Aq, C, N, nb, N, s);
-            case kWQ41: return direct_mr_launch<kWQ41, false>(mr, rpw, W, Aq, C, N, nb, N, s);
-            case kWQ50: return direct_mr_launch<kWQ50, false>(mr, rpw, W, Aq, C, N, nb, N, s);
-            default: return direct_mr_launch<kWQ51, false>(mr, rpw, W, Aq, C, N, nb, N, s);
+                return afmt == kAQ8S ? direct_mr_launch<kWQ80, true>(quant, mr, rpw, W, A, C, N, nb, N, s)
+                                     : direct_mr_launch<kWQ80, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+            case kWQ41: return direct_mr_launch<kWQ41, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+            case kWQ50: return direct_mr_launch<kWQ50, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+            default: return direct_mr_launch<kWQ51, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
         }
     }
     switch (wtype) {
@@ -1182,13 +1214,13 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
     if (afmt == kAQ8S && wtype != kWQ80) return hipErrorNotSupported;
     const int nb = K / 32;
     if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
-    const int chunk = QUANT ? 8 : kMaxFusedRows;
+    const int chunk = (QUANT || M > kMaxFusedRows) ? 8 : kMaxFusedRows;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
         const int dma_min = mr == 1 ? kGemvDmaMinBlocks1 : kGemvDmaMinBlocks2;
         const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows && nb < dma_min ? kAL2 : kADMA);
         // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
-        const int rpw = pick_rpw(N, AMODE);
+        const int rpw = pick_rpw(N, (AMODE == kAFQ && mr > kMaxFusedRows) ? kADMA : AMODE);
         int KT = (nb + 7) & ~7;
         while (KT > 64 && gemv_lds_bytes(wtype, mr, KT, AMODE, rpw) > kGemvLdsBudget) KT = ((KT / 2) + 63) & ~63;
         const void* Am = QUANT ? (const void*)((const uint8_t*)A + (size_t)m0 * nb * kQ81Bytes)
@@ -1217,8 +1249,25 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 #define KSQ_GEMV_FUSED_MAX_WORK 420000ll
 #endif
 
-bool gemv_fused_profitable(int wtype, int M, int N, int K) {
-    if (M < 1 || M > kMaxFusedRows) return false;
+bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W) {
+    if (M < 1 || M > 8) return false;
+#ifndef KSQ_GEMV_FUSED_MR
+#define KSQ_GEMV_FUSED_MR 1
+#endif
+    if (M > kMaxFusedRows) {
+        if (!KSQ_GEMV_FUSED_MR) return false;
+        // 3-8 rows: gemv_direct_mr_kernel quantising its single K tile, where the quantised path
+        // would take the decode kernel too (not the small-batch kernel), while the repeated work
+        // stays under 2e5 block quantisations (measured: Q4_0 N = 512, K = 7168, M = 3 7.0 -> 6.4
+        // us at 1.7e5; N = K = 4096, M = 3 9.3 -> 10.3 the other way at 3.9e5)
+        const int nb = K / 32;
+        if (is_kquant(wtype) || (nb & 1) || ((uintptr_t)W & 3) || direct_mr_ktp(M, nb) != (nb >> 1)) return false;
+        if (skinny_preferred(wtype, M, N, K)) return false;
+        int rpw = pick_rpw(N, kADMA);
+        if (rpw == 4 && M <= 5 && nb >= 384 && (N + 7) / 8 >= kGemvMinWGs) rpw = 8;
+        const long long wgs = (N + rpw - 1) / rpw;
+        return (long long)M * wgs * nb <= 200000ll;
+    }
     const int rpw = pick_rpw(N, kAFQ);
     const int nb = K / 32, KT = (nb + 7) & ~7;
     // one K tile only: with several, each tile's quantisation would wait for the previous tile

@@ -39,7 +39,7 @@ hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X
                            hipStream_t s);
 // Whether launch_gemv_f32 beats quantise + launch_gemv for this shape (M <= 2 and a bounded
 // amount of repeated quantisation).
-bool gemv_fused_profitable(int wtype, int M, int N, int K);
+bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W);
 
 // Small-batch GEMM (1 <= M <= 8) on the 4x4x4 int8 MFMA for the 32-element block types
 // (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1; block_q8s activations with Q8_0).  W and A 4-byte aligned.

@@ -556,13 +556,17 @@ def test_direct_decode_multirow(dev, oracle, wtype, M):
     oracle."""
     from ksq import synth
     g = np.random.default_rng(2800 + 10 * wtype + M)
-    for N, K in ((300, 512), (2051, 1024), (2049, 12288), (1030, 7168), (4100, 224), (1536, 1024)):
+    for N, K in ((300, 512), (2051, 1024), (2049, 12288), (1030, 7168), (4100, 224), (1536, 1024), (512, 7168)):
         w = synth.weights(wtype, g, N, K)
         x = synth.activations(g, M, K)
         q = oracle.quantize_q8_1(x)
         y = _gpu_gemm(dev, wtype, w, q, M, N, K, atype=1, path=1)
         ref = oracle.gemm_f64(wtype, q, w, M, N, K)
         assert _rel_err(y, ref) <= TOL, (N, K)
+        if M <= 8:
+            # the fp32 entry: small grids quantise inside the same kernel (one K tile)
+            y32 = _gpu_gemm(dev, wtype, w, x, M, N, K, atype=0, path=0)
+            assert _rel_err(y32, ref) <= TOL, (N, K, "fp32")
 
 
 @pytest.mark.parametrize("wtype", [2, 3])
