@@ -81,7 +81,7 @@ def test_quantize_q8_1_variants_bit_exact(dev, oracle, variant):
     import torch
     from ksq import ops
     g = np.random.default_rng(150 + variant)
-    for M, K in ((1, 4096), (5, 1024), (300, 96)):
+    for M, K in ((1, 4096), (5, 1024), (300, 96), (2048, 4096)):
         x = g.standard_normal((M, K), dtype=np.float32) * np.exp2(g.integers(-20, 12, (M, 1))).astype(np.float32)
         if M == 5:
             x[0, :32] = 0.0
