@@ -1122,6 +1122,8 @@ static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W
 // The register-direct kernels take 1-2 activation rows (quantised ones read from L2, or fp32
 // ones quantised per workgroup) for 32-element block types when every block pair is 4-byte
 // aligned; the fp32 form also needs the quantised rows to fit the LDS budget.
+// Build-time switches (-DKSQ_GEMV_DIRECT_FQ=0 etc.) that route the register-direct cases back to
+// gemv_row_kernel, for A/B measurement; both sides compute the same block formulas.
 #ifndef KSQ_GEMV_DIRECT_FQ
 #define KSQ_GEMV_DIRECT_FQ 1
 #endif
