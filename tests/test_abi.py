@@ -60,6 +60,8 @@ FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced by the 
     ((0, 0, FAKE, FAKE + 4, FAKE, 1, 1, 32), 3),      # fp32 activation not 16-byte aligned
     ((0, 1, FAKE, FAKE + 2, FAKE, 1, 1, 32), 3),      # Q8_1 activation not 4-byte aligned
     ((0, 0, FAKE, FAKE, FAKE + 2, 1, 1, 32), 3),      # output not 4-byte aligned
+    ((0, 5, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # activation type past KSQ_A_F16
+    ((0, 4, FAKE, FAKE + 8, FAKE, 1, 1, 32), 3),      # fp16 activation not 16-byte aligned
 ])
 def test_gemm_rejects_bad_arguments(args, status):
     from ksq import _lib
@@ -77,6 +79,16 @@ def test_empty_calls_are_noops():
     assert L.ksq_gemm(0, 0, None, None, None, 5, 0, 64, None, 0, None) == 0
     assert L.ksq_quantize_q8_1(None, None, 0, 64, None) == 0
     assert L.ksq_quantize_q8_1_variant(2, None, None, 0, 64, None) == 0
+
+
+def test_fp16_fused_entry_rejects_bad_arguments():
+    """ksq_gemm_q4_0_fp16_fused validates like ksq_gemm, in its own (M weight rows) orientation."""
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE + 8, FAKE, 4, 2, 64, None) == 3   # activation alignment
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 4, 2, 48, None) == 2       # K % 32
+    assert L.ksq_gemm_q4_0_fp16_fused(None, FAKE, FAKE, 4, 2, 64, None) == 1       # null weight
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 0, 2, 64, None) == 0       # empty: no-op
 
 
 def test_quantize_variant_rejects_unknown_variant():
