@@ -589,15 +589,57 @@ __global__ __launch_bounds__(256) void gemv_direct_kernel(const uint8_t* __restr
 // alignment shift and read-ahead slack
 __host__ __device__ constexpr int direct_mr_apitch(int ktp) { return (ktp * 72 + 16 + 15) & ~15; }
 
+// Weight words of block pair p of a row for the 3-8-row kernel: the pair's bytes for 32-element
+// types; for Q4_K the 16-byte head of super-block p / 4 and the 32 quant bytes of its unit pair
+// p % 4 (units 2(p % 4), +1: the low / high nibbles), whose activation blocks are again pair p.
+template <int WT>
+struct MrW { static constexpr int NW = (WT == kWQ4K) ? 12 : block_bytes(WT) / 2; };
+
+template <int WT>
+__device__ __forceinline__ void mr_load_w(const uint8_t* __restrict__ W, int row, int nb, int p, uint32_t* w) {
+    if constexpr (WT == kWQ4K) {
+        const uint8_t* sb = W + ((size_t)row * (nb / 8) + (size_t)(p >> 2)) * kQ4KBytes;
+        load_dwords<4>((const uint32_t*)sb, w);
+        load_dwords<8>((const uint32_t*)(sb + 16 + 32 * (p & 3)), w + 4);
+    } else {
+        constexpr int BB = block_bytes(WT), PW = BB / 2;
+        load_dwords<PW>((const uint32_t*)(W + (size_t)row * nb * BB) + (size_t)p * PW, w);
+    }
+}
+
+// acc += the pair's two unit dots against activation blocks a[0..8], a[9..17]
+template <int WT, bool AS>
+__device__ __forceinline__ void mr_pair_acc(float& acc, const uint32_t* w, const uint32_t* a, int p) {
+    if constexpr (WT == kWQ4K) {
+        const int sub = p & 3;
+        int sc0, mn0, sc1, mn1;
+        q4_K_scale_min(2 * sub, w + 1, sc0, mn0);
+        q4_K_scale_min(2 * sub + 1, w + 1, sc1, mn1);
+        const float d = f16_to_f32(w[0] & 0xFFFFu), dmin = f16_to_f32(w[0] >> 16);
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            s0 = dot4((int)(w[4 + i] & 0x0F0F0F0Fu), (int)a[1 + i], s0);
+            s1 = dot4((int)((w[4 + i] >> 4) & 0x0F0F0F0Fu), (int)a[10 + i], s1);
+        }
+        acc += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc0 * s0)) - dmin * (f16_to_f32(a[0] >> 16) * (float)mn0);
+        acc += d * (f16_to_f32(a[9] & 0xFFFFu) * (float)(sc1 * s1)) - dmin * (f16_to_f32(a[9] >> 16) * (float)mn1);
+    } else {
+        acc += reg_block_dot<WT, AS, 0>(w, a);
+        acc += reg_block_dot<WT, AS, block_bytes(WT)>(w, a + 9);
+    }
+}
+
 // FQ: the activations arrive as fp32 [MR][32 nb] and the workgroup quantises the (single) K
 // tile into the same LDS layout instead (the device quantiser, bit-identical blocks).
 template <int WT, int MR, bool AS, int RPW, bool FQ>
 __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
                                                              float* __restrict__ C, int N, int nb, int ktp, int ldc) {
-    static_assert(!is_kquant(WT) && MR >= 1 && MR <= 8, "32-element block types, 1-8 activation rows");
+    static_assert((!is_kquant(WT) || WT == kWQ4K) && MR >= 1 && MR <= 8 && !(FQ && is_kquant(WT)),
+                  "32-element block types or Q4_K, 1-8 activation rows");
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
     constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
-    constexpr int BB = block_bytes(WT), PW = BB / 2;
+    constexpr int PW = MrW<WT>::NW;
     extern __shared__ __attribute__((aligned(16))) uint32_t sact[];   // [MR][apitch bytes]
     const int apitch = direct_mr_apitch(ktp);
     __shared__ float red[4][MR];
@@ -617,8 +659,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
         if (p < t0 + tp) {
 #pragma unroll
             for (int v = 0; v < VR; v++)
-                if (row0 + v < N)
-                    load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+                if (row0 + v < N) mr_load_w<WT>(W, row0 + v, nb, p, w[v]);
         }
         // stage the tile: row m's tp pairs (tp * 72 contiguous bytes from pair t0) are copied by
         // wave m % 4 with LDS DMA; its first byte lands at ashift[m] (the source's offset mod 16)
@@ -660,8 +701,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
                 if (!first) {
 #pragma unroll
                     for (int v = 0; v < VR; v++)
-                        if (row0 + v < N)
-                            load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+                        if (row0 + v < N) mr_load_w<WT>(W, row0 + v, nb, p, w[v]);
                 }
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
@@ -672,10 +712,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
                     for (int i = 0; i < 18; i++) a[i] = src[i];
 #pragma unroll
                     for (int v = 0; v < VR; v++)
-                        if (row0 + v < N) {
-                            acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a);
-                            acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a + 9);
-                        }
+                        if (row0 + v < N) mr_pair_acc<WT, AS>(acc[v][m], w[v], a, p);
                 }
             }
         }
@@ -1105,9 +1142,11 @@ static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const void* A,
 template <int WT, bool AS>
 static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb,
                                    int ldc, hipStream_t s) {
-#define KSQ_MR_CASE(MRV) \
-    return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s) \
-                 : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, s);
+#define KSQ_MR_CASE(MRV)                                                                  \
+    if constexpr (is_kquant(WT)) return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s) \
+                                              : hipErrorNotSupported;                                             \
+    else return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s)                   \
+                      : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, s);
     switch (mr) {
         case 3: KSQ_MR_CASE(3)
         case 4: KSQ_MR_CASE(4)
@@ -1137,9 +1176,14 @@ static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W
 // Q8_0 / Q4_1), but for grids of 256-511 four-row workgroups (N = 1536, K = 5120: 5.6 vs 5.1 us
 // at M = 4), where gemv_row_kernel stays.
 static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw, const void* W, const void* A) {
+    // Q4_K: 3-5 rows on long rows or narrow matrices (Q4_K N = 3584, K = 18944, M = 4: 25.7 ->
+    // 20.6 us; N = 512, K = 7168, M = 3: 3.9 -> 3.4); at N = K = 4096 it is 6-10% slower, and at 8
+    // rows (the per-unit scale decode repeated per activation row) up to 2x
+    if (amode == kADMA && mr >= 3 && wtype == kWQ4K && !(mr <= 5 && (nb >= 224 || N <= 2560))) return false;
     if (amode == kADMA && mr >= 3)
-        return KSQ_GEMV_DIRECT_MR && !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 &&
-               ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 && !(rpw == 4 && (N + 3) / 4 < 512);
+        return KSQ_GEMV_DIRECT_MR && (!is_kquant(wtype) || (KSQ_GEMV_DIRECT_KQ && wtype == kWQ4K && (nb & 7) == 0)) &&
+               (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 &&
+               !(rpw == 4 && (N + 3) / 4 < 512);
     if (amode == kAFQ && mr >= 3)   // gemv_fused_profitable admitted it: one K tile, no grid exclusion
         return !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && direct_mr_ktp(mr, nb) == (nb >> 1);
     // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
@@ -1154,6 +1198,7 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
 
 static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int rpw, const uint8_t* W, const void* A,
                                   float* C, int N, int nb, hipStream_t s) {
+    if (mr >= 3 && wtype == kWQ4K) return direct_mr_launch<kWQ4K, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
     if (wtype == kWQ4K || wtype == kWQ6K) {
         const uint8_t* Aq = (const uint8_t*)A;
         const dim3 blk(256);

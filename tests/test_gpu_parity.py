@@ -569,6 +569,23 @@ def test_direct_decode_multirow(dev, oracle, wtype, M):
             assert _rel_err(y32, ref) <= TOL, (N, K, "fp32")
 
 
+@pytest.mark.parametrize("M", [3, 5])
+def test_direct_decode_multirow_q4_k(dev, oracle, M):
+    """The 3-8-row register-direct decode kernel on Q4_K (lane task = the unit pair sharing one
+    32-byte quant span, activation pairs staged by LDS DMA): 1-2 rows per wave, 1-4 waves per
+    row, K tiles, a ragged last workgroup, and a grid of 256-511 four-row workgroups (left to
+    gemv_row_kernel).  Bar: TOL against the oracle."""
+    from ksq import synth
+    g = np.random.default_rng(2900 + M)
+    for N, K in ((300, 512), (2051, 1024), (2049, 12288), (1030, 7168), (1536, 1024), (4100, 7168)):
+        w = synth.weights(2, g, N, K)
+        x = synth.activations(g, M, K)
+        q = oracle.quantize_q8_1(x)
+        y = _gpu_gemm(dev, 2, w, q, M, N, K, atype=1, path=1)
+        ref = oracle.gemm_f64(2, q, w, M, N, K)
+        assert _rel_err(y, ref) <= TOL, (N, K)
+
+
 @pytest.mark.parametrize("wtype", [2, 3])
 @pytest.mark.parametrize("M", [1, 2])
 def test_direct_decode_kquant(dev, oracle, wtype, M):
