@@ -607,23 +607,35 @@ __device__ __forceinline__ void mr_load_w(const uint8_t* __restrict__ W, int row
     }
 }
 
+// Per-pair weight context decoded once for all activation rows (Q4_K: d, dmin and the two
+// units' 6-bit scales and mins; nothing for the 32-element types).
+template <int WT>
+struct MrCtx {
+    float d = 0.0f, dmin = 0.0f;
+    int sc0 = 0, mn0 = 0, sc1 = 0, mn1 = 0;
+    __device__ __forceinline__ void prep(const uint32_t* w, int p) {
+        if constexpr (WT == kWQ4K) {
+            const int sub = p & 3;
+            q4_K_scale_min(2 * sub, w + 1, sc0, mn0);
+            q4_K_scale_min(2 * sub + 1, w + 1, sc1, mn1);
+            d = f16_to_f32(w[0] & 0xFFFFu);
+            dmin = f16_to_f32(w[0] >> 16);
+        }
+    }
+};
+
 // acc += the pair's two unit dots against activation blocks a[0..8], a[9..17]
 template <int WT, bool AS>
-__device__ __forceinline__ void mr_pair_acc(float& acc, const uint32_t* w, const uint32_t* a, int p) {
+__device__ __forceinline__ void mr_pair_acc(float& acc, const MrCtx<WT>& c, const uint32_t* w, const uint32_t* a) {
     if constexpr (WT == kWQ4K) {
-        const int sub = p & 3;
-        int sc0, mn0, sc1, mn1;
-        q4_K_scale_min(2 * sub, w + 1, sc0, mn0);
-        q4_K_scale_min(2 * sub + 1, w + 1, sc1, mn1);
-        const float d = f16_to_f32(w[0] & 0xFFFFu), dmin = f16_to_f32(w[0] >> 16);
         int s0 = 0, s1 = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             s0 = dot4((int)(w[4 + i] & 0x0F0F0F0Fu), (int)a[1 + i], s0);
             s1 = dot4((int)((w[4 + i] >> 4) & 0x0F0F0F0Fu), (int)a[10 + i], s1);
         }
-        acc += d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(sc0 * s0)) - dmin * (f16_to_f32(a[0] >> 16) * (float)mn0);
-        acc += d * (f16_to_f32(a[9] & 0xFFFFu) * (float)(sc1 * s1)) - dmin * (f16_to_f32(a[9] >> 16) * (float)mn1);
+        acc += c.d * (f16_to_f32(a[0] & 0xFFFFu) * (float)(c.sc0 * s0)) - c.dmin * (f16_to_f32(a[0] >> 16) * (float)c.mn0);
+        acc += c.d * (f16_to_f32(a[9] & 0xFFFFu) * (float)(c.sc1 * s1)) - c.dmin * (f16_to_f32(a[9] >> 16) * (float)c.mn1);
     } else {
         acc += reg_block_dot<WT, AS, 0>(w, a);
         acc += reg_block_dot<WT, AS, block_bytes(WT)>(w, a + 9);
@@ -703,6 +715,9 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
                     for (int v = 0; v < VR; v++)
                         if (row0 + v < N) mr_load_w<WT>(W, row0 + v, nb, p, w[v]);
                 }
+                MrCtx<WT> ctx[VR];
+#pragma unroll
+                for (int v = 0; v < VR; v++) ctx[v].prep(w[v], p);
 #pragma unroll
                 for (int m = 0; m < MR; m++) {
                     const uint32_t* src = (const uint32_t*)((const uint8_t*)sact + (size_t)m * apitch + ashift[m] +
@@ -712,7 +727,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
                     for (int i = 0; i < 18; i++) a[i] = src[i];
 #pragma unroll
                     for (int v = 0; v < VR; v++)
-                        if (row0 + v < N) mr_pair_acc<WT, AS>(acc[v][m], w[v], a, p);
+                        if (row0 + v < N) mr_pair_acc<WT, AS>(acc[v][m], ctx[v], w[v], a);
                 }
             }
         }
@@ -1176,10 +1191,8 @@ static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W
 // Q8_0 / Q4_1), but for grids of 256-511 four-row workgroups (N = 1536, K = 5120: 5.6 vs 5.1 us
 // at M = 4), where gemv_row_kernel stays.
 static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw, const void* W, const void* A) {
-    // Q4_K: 3-5 rows on long rows or narrow matrices (Q4_K N = 3584, K = 18944, M = 4: 25.7 ->
-    // 20.6 us; N = 512, K = 7168, M = 3: 3.9 -> 3.4); at N = K = 4096 it is 6-10% slower, and at 8
-    // rows (the per-unit scale decode repeated per activation row) up to 2x
-    if (amode == kADMA && mr >= 3 && wtype == kWQ4K && !(mr <= 5 && (nb >= 224 || N <= 2560))) return false;
+    // Q4_K included: measured 5-33% faster over 36 shapes at M = 3..8 (N = 3584, K = 18944, M = 4:
+    // 25.9 -> 17.3 us), once the scale decode is done once per pair rather than per activation row
     if (amode == kADMA && mr >= 3)
         return KSQ_GEMV_DIRECT_MR && (!is_kquant(wtype) || (KSQ_GEMV_DIRECT_KQ && wtype == kWQ4K && (nb & 7) == 0)) &&
                (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 &&

@@ -569,7 +569,7 @@ def test_direct_decode_multirow(dev, oracle, wtype, M):
             assert _rel_err(y32, ref) <= TOL, (N, K, "fp32")
 
 
-@pytest.mark.parametrize("M", [3, 5])
+@pytest.mark.parametrize("M", [3, 5, 8])
 def test_direct_decode_multirow_q4_k(dev, oracle, M):
     """The 3-8-row register-direct decode kernel on Q4_K (lane task = the unit pair sharing one
     32-byte quant span, activation pairs staged by LDS DMA): 1-2 rows per wave, 1-4 waves per
