@@ -607,14 +607,18 @@ static int pick_config(int wtype, int M, int N, int K) {
 // kernel also applies it keeps rows of up to 3584 elements (Q8_0 N = 18944, K = 3584, M = 8:
 // 26.4 vs 36.5).
 // K-quants (decode kernel vs MFMA GEMM only): Q4_K from M = 7 once N * K >= 1.2e7 (N = K = 4096,
-// M = 8: 1.08x) and at M = 5, 6 from 5e7 (N = 7168, K = 7168, M = 5: 1.20x); Q6_K from M = 7 on
+// M = 8: 1.08x), at M = 5, 6 as below; Q6_K from M = 7 on
 // rows of up to 7168 elements once N * K >= 1.5e7 (N = 12288, K = 5120, M = 8: 1.30x; with
 // K = 14336 the decode kernel stays 1.15x faster).
 bool mmq_preferred(int wtype, int M, int N, int K) {
     if (M > 8) return true;
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
     const double nk = (double)N * (double)K;
-    if (wtype == kWQ4K) return (M >= 7 && nk >= 1.2e7) || (M >= 5 && nk >= 5.0e7);
+    // Q4_K at M = 5, 6 against the register-direct decode kernel: the MFMA GEMM on rows of up to
+    // 5120 elements once N * K >= 2e7 (N = 12288, K = 5120: 20.9 vs 23.4 us) and on very short
+    // rows (N = 7168, K = 512: 6.6 vs 8.2); longer rows stay on the decode kernel (N = 4096,
+    // K = 14336: 16.6 vs 19.6)
+    if (wtype == kWQ4K) return (M >= 7 && nk >= 1.2e7) || (M >= 5 && ((nk >= 2.0e7 && K <= 5120) || K <= 1024));
     if (wtype == kWQ6K) return M >= 7 && K <= 7168 && nk >= 1.5e7;
     if (!nib && wtype != kWQ80) return false;
     // with the register-direct decode kernels (3-8 rows) the crossovers moved: nibble types at
