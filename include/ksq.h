@@ -147,10 +147,12 @@ KSQ_API int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, in
  * 311-338) in its orientation: Q4_0 weight [M][K/32] (M weight rows), fp16 activations [N][K]
  * (uint16 bits, 16-byte aligned), output fp32 [M][N] (weight-row major).  Activations are
  * quantised by its quantize_fp16_to_q8_1_smem rules (KSQ_Q81_FUSED_F16, bit-exact), block
- * dots bit-exact; the result is computed in ksq_gemm's [N][M] orientation in the library's
- * workspace pool and transposed. */
+ * dots bit-exact.  workspace: ksq_gemm_q4_0_fp16_fused_workspace_size(M, N, K) bytes of device
+ * memory, 256-byte aligned, or NULL for the library's per-device pool (which may allocate). */
+KSQ_API size_t ksq_gemm_q4_0_fp16_fused_workspace_size(int M, int N, int K);
 KSQ_API int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output,
-                                     int M, int N, int K, void* stream);
+                                     int M, int N, int K, void* workspace, size_t workspace_bytes,
+                                     void* stream);
 
 /* fp32 [M][K] -> block_q8s [M][K/32] by the native W8A8C8 operator's per-block rules
  * (variants/deepseek_v3/w8a8c8_q8_0_q8_1/kernel.cu:66-93, bit for bit).  Same alignment
@@ -180,16 +182,6 @@ KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* a
 KSQ_API int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,
                               int M, int N, int K, void* stream);
 
-/* Debug: fp32 [M][K] -> the q8h activation layout of the f16-MFMA GEMM: qh [M][K] fp16 holding
- * q/8 and ds [M][K/32] the block_q8_1 ds words, with the quants and ds of ksq_quantize_q8_1.
- * x and qh 16-byte aligned, ds 4-byte aligned. */
-KSQ_API int ksq_debug_quantize_q8h(const float* x, void* qh, uint32_t* ds, int M, int K, void* stream);
-
-/* Debug: the same per-block integer dots from the f16-MFMA prefill GEMM of Q4_0 weights
- * (the activations converted to its fp16 q/8 layout first).  K % 64 == 0. */
-KSQ_API int ksq_debug_block_sumi_f16mfma(const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N,
-                                         int K, void* stream);
-
 /* ---- expert-grouped MoE (no reference counterpart for GGML types) ----------
  * output[t][n] = sum over the top_k experts e chosen for token t of
  *                w[t][e] * (Q8_1(activation[t]) . weight[e][n]),
@@ -217,16 +209,38 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
                                         const float* router_logits, float* output,
                                         int T, int N, int K, int E, int top_k);
 
-/* Path selection for testing and benchmarking: 0 = automatic (default),
- * 1 = always the v_dot4 decode kernels, 2 = always the int8 MFMA GEMM where it applies,
- * 3 = the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies,
- * 4 = the f16-MFMA GEMM for Q4_0 where it applies. */
+/* Path selection for testing and benchmarking, for calls made from the calling host thread
+ * (other threads keep their own setting): 0 = automatic (default), 1 = always the v_dot4 decode
+ * kernels, 2 = always the int8 MFMA GEMM where it applies, 3 = the 4x4x4-MFMA small-batch
+ * kernel for M <= 8 where it applies. */
 KSQ_API int ksq_set_path(int path);
 
-/* MFMA tile configuration for tuning: 0 = chosen from (M, N) (default); 1 = 128x128 tile,
- * K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with K step 4; 5 = 32x128; 6 = 128x128 with
- * K step 4 and the next step's loads prefetched into registers. */
+/* MFMA tile configuration for tuning, for calls made from the calling host thread: 0 = chosen
+ * from (M, N) (default); 1 = 128x128 tile, K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with
+ * K step 4; 5 = 32x128; 6 = 128x128 with K step 4 and the next step's loads prefetched into
+ * registers. */
 KSQ_API int ksq_set_mmq_config(int config);
+
+/* Debug: the kernel families the last ksq_gemm / drop-in / MoE / fused-FP16 call made on the
+ * calling host thread launched, as a bit set of: */
+#define KSQ_ENG_QUANTIZE (1u << 0)        /* separate activation quantise launch */
+#define KSQ_ENG_GEMV_ROW (1u << 1)        /* gemv_row_kernel (LDS-staged v_dot4 decode) */
+#define KSQ_ENG_GEMV_ROW_FQ (1u << 2)     /* gemv_row_kernel quantising fp32 rows per workgroup */
+#define KSQ_ENG_GEMV_DIRECT (1u << 3)     /* gemv_direct_kernel (1-2 rows, register-direct) */
+#define KSQ_ENG_GEMV_DIRECT_FQ (1u << 4)  /* gemv_direct_fq_kernel (fp32 rows quantised per workgroup) */
+#define KSQ_ENG_GEMV_MR (1u << 5)         /* gemv_direct_mr_kernel (3-8 rows) */
+#define KSQ_ENG_GEMV_MR_FQ (1u << 6)      /* gemv_direct_mr_kernel quantising fp32 rows */
+#define KSQ_ENG_GEMV_KQ (1u << 7)         /* gemv_direct_kq_kernel (Q4_K / Q6_K, 1-2 rows) */
+#define KSQ_ENG_SKINNY (1u << 8)          /* skinny_kernel (4x4x4 int8 MFMA, M <= 8) */
+#define KSQ_ENG_MMQ_CFG(c) (1u << (8 + (c))) /* mmq_kernel with tile configuration c = 1..6 */
+#define KSQ_ENG_SPLITK (1u << 15)         /* the MFMA GEMM split along K, plus its reduction */
+#define KSQ_ENG_MOE_ROUTE (1u << 16)      /* MoE routing kernel */
+#define KSQ_ENG_MOE_GROUP (1u << 17)      /* MoE grouping / tile schedule kernel */
+#define KSQ_ENG_MOE_TILE64 (1u << 18)     /* grouped mmq_kernel, 64-row tiles */
+#define KSQ_ENG_MOE_TILE128 (1u << 19)    /* grouped mmq_kernel, 128-row tiles */
+#define KSQ_ENG_MOE_COMBINE (1u << 20)    /* top_k > 2 slot-ordered combine */
+#define KSQ_ENG_TRANSPOSE (1u << 21)      /* output transpose (fused FP16 orientation) */
+KSQ_API uint32_t ksq_debug_last_engines(void);
 
 #ifdef __cplusplus
 }

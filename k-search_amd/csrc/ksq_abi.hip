@@ -22,7 +22,8 @@ namespace {
 
 thread_local int g_status = KSQ_OK;
 thread_local char g_message[256] = "ok";
-int g_path = 0;
+thread_local int g_path = 0;              // ksq_set_path: a per-thread routing override
+thread_local uint32_t g_engines = 0;      // kernel families of the thread's last call
 
 int set_error(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int set_error(int status, const char* fmt, ...) {
@@ -45,15 +46,18 @@ int hip_error(hipError_t e, const char* where) {
 }
 
 // Per-device scratch: the quantised copy of fp32 activations, split-K partial sums and the
-// MoE routing tables when the caller passes no workspace.
+// MoE routing tables when the caller passes no workspace.  A pool that must grow takes a new,
+// larger buffer and keeps the outgrown one until ksq_release(): a graph captured earlier may
+// still read and write it.  Growing is refused while the stream captures a graph.
 struct Pool {
     void* ptr = nullptr;
     size_t size = 0;
+    std::vector<void*> retired;
 };
 std::mutex g_pool_mu;
 std::vector<Pool> g_pools;
 
-int pool_get(size_t bytes, void** out) {
+int pool_get(size_t bytes, hipStream_t s, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_error(e, "hipGetDevice");
@@ -61,15 +65,20 @@ int pool_get(size_t bytes, void** out) {
     if ((int)g_pools.size() <= dev) g_pools.resize(dev + 1);
     Pool& p = g_pools[dev];
     if (p.size < bytes) {
-        if (p.ptr) {
-            e = hipFree(p.ptr);  // synchronises the device: no launch still reads the old buffer
-            p.ptr = nullptr;
-            p.size = 0;
-            if (e != hipSuccess) return hip_error(e, "hipFree(workspace)");
-        }
-        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
-        e = hipMalloc(&p.ptr, want);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return set_error(KSQ_ERR_WORKSPACE,
+                             "the workspace pool would have to grow to %zu bytes during graph capture; "
+                             "pass a workspace",
+                             bytes);
+        size_t want = 2 * p.size;
+        if (want < bytes) want = bytes;
+        if (want < (1u << 20)) want = 1u << 20;
+        void* np = nullptr;
+        e = hipMalloc(&np, want);
         if (e != hipSuccess) return hip_error(e, "hipMalloc(workspace)");
+        if (p.ptr) p.retired.push_back(p.ptr);
+        p.ptr = np;
         p.size = want;
     }
     *out = p.ptr;
@@ -125,33 +134,18 @@ bool use_skinny(int wtype, int afmt, int M, int N, int K, const void* W, const v
 }
 
 
-// The f16-MFMA GEMM (Q4_0) on path 4 only: measured slower than the int8 MFMA GEMM at every
-// shape tried (M = 2048, N = K = 4096: 138 vs 113 us), so the automatic path does not take it.
-bool use_mmqh(int wtype, int M, int N, int K, const void* W) {
-    return g_path == 4 && ksq::mmqh_supported(wtype, M, N, K, W);
-}
-
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Workspace of one ksq_gemm call: [quantised activations][split-K partial sums], each part
-// 256-byte aligned.  `mmq` is whether the int8 MFMA path runs (alignment permitting), `mmqh`
-// whether the f16-MFMA path does: its activations are the q8h layout [qh: M*K fp16][ds: M*K/32
-// words], for quantised input too (converted from block_q8_1).
+// 256-byte aligned.  `mmq` is whether the int8 MFMA path runs (alignment permitting).
 struct GemmWs {
-    size_t q, qds, p, total;
+    size_t q, p, total;
 };
 
-GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq, bool mmqh) {
+GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
     GemmWs w{};
-    int splits = 1;
-    if (mmqh) {
-        w.qds = align256((size_t)M * (size_t)K * 2u);
-        w.q = w.qds + align256((size_t)M * (size_t)(K / 32) * 4u);
-        splits = ksq::mmqh_splits(M, N, K);
-    } else {
-        w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
-        splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
-    }
+    w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
+    const int splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
     w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
     w.total = w.q + w.p;
     return w;
@@ -175,6 +169,10 @@ int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* 
 }
 
 }  // namespace
+
+namespace ksq {
+void note_engine(uint32_t bits) { g_engines |= bits; }
+}  // namespace ksq
 
 extern "C" {
 
@@ -201,17 +199,20 @@ void ksq_release(void) {
     int cur = 0;
     (void)hipGetDevice(&cur);
     for (size_t d = 0; d < g_pools.size(); d++) {
-        if (g_pools[d].ptr) {
+        if (g_pools[d].ptr || !g_pools[d].retired.empty()) {
             (void)hipSetDevice((int)d);
-            (void)hipFree(g_pools[d].ptr);
+            if (g_pools[d].ptr) (void)hipFree(g_pools[d].ptr);
+            for (void* r : g_pools[d].retired) (void)hipFree(r);
         }
         g_pools[d] = Pool{};
     }
     (void)hipSetDevice(cur);
 }
 
+uint32_t ksq_debug_last_engines(void) { return g_engines; }
+
 int ksq_set_path(int path) {
-    if (path < 0 || path > 4) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
+    if (path < 0 || path > 3) return set_error(KSQ_ERR_TYPE, "unknown path %d", path);
     g_path = path;
     return ok();
 }
@@ -245,10 +246,17 @@ int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int
     return ok();
 }
 
+size_t ksq_gemm_q4_0_fp16_fused_workspace_size(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    return align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K)) +
+           align256((size_t)M * (size_t)N * sizeof(float));
+}
+
 int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output, int M, int N,
-                             int K, void* stream) {
+                             int K, void* workspace, size_t workspace_bytes, void* stream) {
     // the reference's orientation: M weight rows, N activation rows, output [M][N]; computed as
     // ksq_gemm's [N][M] into the workspace, then transposed
+    g_engines = 0;
     int st = check_common(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, output, N, M, K);
     if (st != KSQ_OK) return st;
     if (M == 0 || N == 0) return ok();
@@ -258,13 +266,20 @@ int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activat
         return e == hipSuccess ? ok() : hip_error(e, "fill launch");
     }
     const size_t gws = align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K));
-    void* p = nullptr;
-    st = pool_get(gws + (size_t)M * (size_t)N * sizeof(float), &p);
-    if (st != KSQ_OK) return st;
+    const size_t need = ksq_gemm_q4_0_fp16_fused_workspace_size(M, N, K);
+    void* p = workspace;
+    if (p) {
+        if (workspace_bytes < need) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+        if ((uintptr_t)p & 255u) return set_error(KSQ_ERR_ALIGN, "workspace must be 256-byte aligned");
+    } else {
+        st = pool_get(need, s, &p);
+        if (st != KSQ_OK) return st;
+    }
     float* tmp = (float*)((uint8_t*)p + gws);
     st = ksq_gemm(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, tmp, N, M, K, gws ? p : nullptr, gws, stream);
     if (st != KSQ_OK) return st;
     hipError_t e = ksq::launch_transpose_f32(tmp, output, N, M, s);
+    g_engines |= KSQ_ENG_TRANSPOSE;
     return e == hipSuccess ? ok() : hip_error(e, "transpose launch");
 }
 
@@ -283,15 +298,12 @@ size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     const bool mmq_possible =
         (g_path != 1) && (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K)) && (K % 256) == 0;
-    const size_t a = gemm_ws(wtype, atype, M, N, K, mmq_possible, false).total;
-    const size_t b = (wtype == KSQ_W_Q4_0 && g_path == 4 && (K % 64) == 0)
-                         ? gemm_ws(wtype, atype, M, N, K, false, true).total
-                         : 0;
-    return a > b ? a : b;
+    return gemm_ws(wtype, atype, M, N, K, mmq_possible).total;
 }
 
 int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output, int M, int N,
              int K, void* workspace, size_t workspace_bytes, void* stream) {
+    g_engines = 0;
     int st = check_common(wtype, atype, weight, activation, output, M, N, K);
     if (st != KSQ_OK) return st;
     if (M == 0 || N == 0) return ok();
@@ -308,12 +320,11 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
                                             N, K, s);
         return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
     }
-    // fp32 activations are quantised to the start of the (16-byte aligned) workspace, which is
-    // what the MFMA path then reads
+    // fp32 / fp16 activations are quantised to the start of the (16-byte aligned) workspace,
+    // which is what the GEMM then reads
     const bool f32 = atype_f32(atype), f16 = atype == KSQ_A_F16;
-    const bool mmqh = afmt == ksq::kAQ81 && !f16 && use_mmqh(wtype, M, N, K, weight);
-    const bool mmq = !mmqh && use_mmq(wtype, M, N, K, weight, f32 || f16 || aligned16(activation));
-    const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq, mmqh);
+    const bool mmq = use_mmq(wtype, M, N, K, weight, f32 || f16 || aligned16(activation));
+    const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq);
     uint8_t* ws = (uint8_t*)workspace;
     if (L.total) {
         if (ws) {
@@ -322,26 +333,18 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
             if ((uintptr_t)ws & 15u) return set_error(KSQ_ERR_ALIGN, "workspace must be 16-byte aligned");
         } else {
             void* p = nullptr;
-            st = pool_get(L.total, &p);
+            st = pool_get(L.total, s, &p);
             if (st != KSQ_OK) return st;
             ws = (uint8_t*)p;
         }
     }
     float* partials = L.p ? (float*)(ws + L.q) : nullptr;
-    if (mmqh) {
-        _Float16* qh = (_Float16*)ws;
-        uint32_t* ds = (uint32_t*)(ws + L.qds);
-        hipError_t e = f32 ? ksq::launch_quantize_q8h((const float*)activation, qh, ds, M, K, s)
-                           : ksq::launch_q8_1_to_q8h(Aq, qh, ds, M, K, s);
-        if (e != hipSuccess) return hip_error(e, f32 ? "quantize launch" : "q8h conversion launch");
-        e = ksq::launch_mmqh((const uint8_t*)weight, qh, ds, output, M, N, K, partials, s);
-        return e == hipSuccess ? ok() : hip_error(e, "f16 mfma launch");
-    }
     if (f32 || f16) {
         // fp16 input takes the fused FP16 kernels' quantiser (kernels/gemm/gemm_fused.cuh:76-145)
         hipError_t e = f16 ? ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, activation, ws, M, K, s)
                            : ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
+        g_engines |= KSQ_ENG_QUANTIZE;
         Aq = ws;
     }
     st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, partials, s);
@@ -366,34 +369,6 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
         return set_error(KSQ_ERR_SHAPE, "MFMA path needs K %% 256 == 0 and 16-byte aligned operands");
     hipError_t e = ksq::launch_mmq_block_sumi(wtype, (const uint8_t*)weight, act_q8_1, out, M, N, K, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_error(e, "mfma block_sumi launch");
-}
-
-int ksq_debug_quantize_q8h(const float* x, void* qh, uint32_t* ds, int M, int K, void* stream) {
-    if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
-    if (M == 0 || K == 0) return ok();
-    if (!x || !qh || !ds) return set_error(KSQ_ERR_NULL, "x, qh or ds is NULL");
-    if (((uintptr_t)x & 15u) || ((uintptr_t)qh & 15u) || ((uintptr_t)ds & 3u))
-        return set_error(KSQ_ERR_ALIGN, "x and qh must be 16-byte and ds 4-byte aligned");
-    hipError_t e = ksq::launch_quantize_q8h(x, (_Float16*)qh, ds, M, K, (hipStream_t)stream);
-    return e == hipSuccess ? ok() : hip_error(e, "quantize launch");
-}
-
-int ksq_debug_block_sumi_f16mfma(const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N, int K,
-                                 void* stream) {
-    int st = check_common(KSQ_W_Q4_0, KSQ_A_Q8_1, weight, act_q8_1, out, M, N, K);
-    if (st != KSQ_OK) return st;
-    if (M == 0 || N == 0 || K == 0) return ok();
-    if (!ksq::mmqh_supported(KSQ_W_Q4_0, M, N, K, weight)) return set_error(KSQ_ERR_SHAPE, "f16 MFMA path needs K %% 64 == 0");
-    void* p = nullptr;
-    const size_t qb = align256((size_t)M * K * 2);
-    st = pool_get(qb + align256((size_t)M * (K / 32) * 4), &p);
-    if (st != KSQ_OK) return st;
-    _Float16* qh = (_Float16*)p;
-    uint32_t* ds = (uint32_t*)((uint8_t*)p + qb);
-    hipError_t e = ksq::launch_q8_1_to_q8h(act_q8_1, qh, ds, M, K, (hipStream_t)stream);
-    if (e == hipSuccess)
-        e = ksq::launch_mmqh_block_sumi((const uint8_t*)weight, qh, ds, out, M, N, K, (hipStream_t)stream);
-    return e == hipSuccess ? ok() : hip_error(e, "f16 mfma block_sumi launch");
 }
 
 // ---- expert-grouped MoE --------------------------------------------------------
@@ -426,6 +401,7 @@ MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
 int moe_run(int wtype, const void* weights, const float* activation, const float* logits, const int32_t* ids_in,
             const float* wts_in, float* output, int T, int N, int K, int E, int top_k, int renorm, int32_t* ids_out,
             float* wts_out, void* workspace, size_t ws_bytes, hipStream_t s) {
+    g_engines = 0;
     if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q5_1 || wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K)
         return set_error(KSQ_ERR_TYPE, "MoE GEMM supports the 32-element block types (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1)");
     if (T < 0 || N < 0 || K < 0 || E < 1 || E > 256 || top_k < 1 || top_k > E)
@@ -443,7 +419,7 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
         if (ws_bytes < L.total) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, L.total);
         if ((uintptr_t)ws & 255u) return set_error(KSQ_ERR_ALIGN, "MoE workspace must be 256-byte aligned");
     } else {
-        int st = pool_get(L.total, &ws);
+        int st = pool_get(L.total, s, &ws);
         if (st != KSQ_OK) return st;
     }
     uint8_t* base = (uint8_t*)ws;
@@ -455,6 +431,7 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     if (logits) {
         e = ksq::launch_moe_route(logits, T, E, top_k, renorm, ids, wts, s);
         if (e != hipSuccess) return hip_error(e, "route launch");
+        g_engines |= KSQ_ENG_MOE_ROUTE;
     } else {
         ids = (int32_t*)ids_in;
         wts = (float*)wts_in;
@@ -466,6 +443,7 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     int32_t* trow0 = (int32_t*)(base + L.trow0);
     e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
     if (e != hipSuccess) return hip_error(e, "group launch");
+    g_engines |= KSQ_ENG_QUANTIZE | KSQ_ENG_MOE_GROUP;
     float* scratch = top_k > 2 ? (float*)(base + L.scratch) : nullptr;
     if (!scratch) {
         e = ksq::launch_fill_zero(output, (int64_t)T * N, s);
@@ -475,8 +453,9 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, tile_rows, a, s);
     if (e != hipSuccess) return hip_error(e, "grouped gemm launch");
     if (scratch) {
-        e = ksq::launch_moe_combine(scratch, output, T, N, top_k, s);
+        e = ksq::launch_moe_combine(scratch, ids, output, T, N, top_k, E, s);
         if (e != hipSuccess) return hip_error(e, "combine launch");
+        g_engines |= KSQ_ENG_MOE_COMBINE;
     }
     return ok();
 }

@@ -1287,11 +1287,17 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
                                : (const void*)((const float*)A + (size_t)m0 * K);
         float* Cm = C + (size_t)m0 * N;
         hipError_t e;
-        if (direct_eligible(wtype, AMODE, mr, nb, N, rpw, W, Am))
+        if (direct_eligible(wtype, AMODE, mr, nb, N, rpw, W, Am)) {
+            note_engine(is_kquant(wtype) && mr <= 2 ? KSQ_ENG_GEMV_KQ
+                        : mr >= 3 ? (QUANT ? KSQ_ENG_GEMV_MR : KSQ_ENG_GEMV_MR_FQ)
+                                  : (QUANT ? KSQ_ENG_GEMV_DIRECT : KSQ_ENG_GEMV_DIRECT_FQ));
             e = direct_dispatch(wtype, afmt, QUANT, mr, rpw, W, Am, Cm, N, nb, s);
-        else if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
-        else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
-        else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        } else {
+            note_engine(AMODE == kAFQ ? KSQ_ENG_GEMV_ROW_FQ : KSQ_ENG_GEMV_ROW);
+            if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+            else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+            else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

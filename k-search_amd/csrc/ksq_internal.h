@@ -8,7 +8,14 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/ksq.h"
+
 namespace ksq {
+
+// Kernel families a call launched, recorded per host thread (ksq_debug_last_engines; the bit
+// values are the KSQ_ENG_* constants of include/ksq.h).  The launchers add their bit; the ABI
+// layer clears the record when a call starts.
+void note_engine(uint32_t bits);
 
 // Quantised-activation formats: block_q8_1 (fp16 d and s) or block_q8s (fp32 d, the native
 // W8A8C8 operator's block; used with Q8_0 weights only).
@@ -21,12 +28,6 @@ hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K,
 hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 // out [cols][rows] = in [rows][cols], fp32
 hipError_t launch_transpose_f32(const float* in, float* out, int rows, int cols, hipStream_t s);
-// The q8h activation layout of the f16-MFMA GEMM: the block_q8_1 quants of [rows][K] as fp16 q/8
-// (qh, [rows][K], 16-byte aligned) and the block ds words (ds, [rows][K/32]); from fp32 (the same
-// quants and ds as block_q8_1, bit for bit) or converted from block_q8_1 blocks.
-hipError_t launch_quantize_q8h(const float* x, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s);
-hipError_t launch_q8_1_to_q8h(const uint8_t* a, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s);
-
 // Decode GEMV/GEMM on v_dot4 (mul_mat_vec_q family), any M.
 // wtype: 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q4_1, 5 Q5_0, 6 Q5_1.
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
@@ -64,18 +65,8 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
 // In-order sum of `splits` partial [M][N] results (P) into C.
 hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits, hipStream_t s);
 
-// Prefill GEMM for Q4_0 weights on the f16 MFMA (exact integer block dots, one FMA per output
-// and block) over q8h activations; K % 64 == 0.  Splits along K for small grids like launch_mmq
-// (mmqh_splits; partials of splits * M * N floats).
-bool mmqh_supported(int wtype, int M, int N, int K, const void* W);
-int mmqh_splits(int M, int N, int K);
-hipError_t launch_mmqh(const uint8_t* W, const _Float16* QH, const uint32_t* DS, float* C, int M, int N, int K,
-                       float* partials, hipStream_t s);
-// Its integer block dots (sumi) as [M][N][K/32] (debug entry for the bit-exact check).
-hipError_t launch_mmqh_block_sumi(const uint8_t* W, const _Float16* QH, const uint32_t* DS, int32_t* out, int M,
-                                  int N, int K, hipStream_t s);
-
-// Force one of the MFMA tile configurations (1..6) or automatic choice (0); -1 if out of range.
+// Force one of the MFMA tile configurations (1..6) or automatic choice (0) for the calling host
+// thread; -1 if out of range.
 int mmq_set_config(int c);
 
 // Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /
@@ -103,8 +94,10 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int re
 hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
                             int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
                             hipStream_t s);
-// out[t][n] = sum_s scratch[t*top_k + s][n] in slot order (top_k > 2 combine).
-hipError_t launch_moe_combine(const float* scratch, float* out, int T, int N, int top_k, hipStream_t s);
+// out[t][n] = sum_s scratch[t*top_k + s][n] in slot order over the slots whose id is in [0, E)
+// (top_k > 2 combine).
+hipError_t launch_moe_combine(const float* scratch, const int32_t* ids, float* out, int T, int N, int top_k, int E,
+                              hipStream_t s);
 
 // Per-block integer dots [M][N][nblk] from the same device block-dot code the
 // decode kernels use (debug entry for the bit-exact check).

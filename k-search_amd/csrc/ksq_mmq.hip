@@ -539,7 +539,7 @@ using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, mor
 using TileT = Tile<32, 128, 8, 1, 1, 3>;    // skinny: M <= 32, the four waves side by side along N
 using TileP = Tile<128, 128, 4, 2, 2, 2, true>;  // 128 x 128, K step 4, next step's loads prefetched
 
-static int g_mmq_config = 0;  // 0 = automatic
+static thread_local int g_mmq_config = 0;  // 0 = automatic; set per host thread
 
 int mmq_set_config(int c) {
     if (c < 0 || c > 6) return -1;
@@ -618,7 +618,8 @@ bool mmq_preferred(int wtype, int M, int N, int K) {
     // 5120 elements once N * K >= 2e7 (N = 12288, K = 5120: 20.9 vs 23.4 us) and on very short
     // rows (N = 7168, K = 512: 6.6 vs 8.2); longer rows stay on the decode kernel (N = 4096,
     // K = 14336: 16.6 vs 19.6)
-    if (wtype == kWQ4K) return (M >= 7 && nk >= 1.2e7) || (M >= 5 && ((nk >= 2.0e7 && K <= 5120) || K <= 1024));
+    if (wtype == kWQ4K)
+        return (M >= 7 && nk >= 1.2e7) || (M >= 5 && M <= 6 && ((nk >= 2.0e7 && K <= 5120) || K <= 1024));
     if (wtype == kWQ6K) return M >= 7 && K <= 7168 && nk >= 1.5e7;
     if (!nib && wtype != kWQ80) return false;
     // with the register-direct decode kernels (3-8 rows) the crossovers moved: nibble types at
@@ -785,6 +786,7 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
                       float* partials, hipStream_t s) {
     const int cfg = pick_config(wtype, M, N, K);
     const int splits = split_cfg(cfg, wtype, M, N, K);
+    note_engine(KSQ_ENG_MMQ_CFG(cfg) | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
     if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s);
     if (!partials) return hipErrorInvalidValue;
     hipError_t e = launch_cfg<false>(cfg, wtype, afmt, W, A, partials, nullptr, M, N, K, splits, s);
@@ -815,6 +817,7 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     const int nb = K / 32;
     if (is_kquant(wtype)) return hipErrorNotSupported;
     mt.expert_stride = (size_t)N * nb * block_bytes(wtype);
+    note_engine(tile_rows == TileL::BM ? KSQ_ENG_MOE_TILE128 : KSQ_ENG_MOE_TILE64);
     if (tile_rows == TileL::BM) {
         const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileL::BN - 1) / TileL::BN));
         return launch_t<TileL, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);

@@ -126,21 +126,27 @@ hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int til
     return hipGetLastError();
 }
 
-__global__ void moe_combine_kernel(const float* __restrict__ scratch, float* __restrict__ out, int T, int N,
-                                   int top_k) {
+// Slots whose expert id is outside [0, E) were not grouped, so their scratch rows were never
+// written: they contribute nothing (as they do for top_k <= 2, where nothing is added for them).
+__global__ void moe_combine_kernel(const float* __restrict__ scratch, const int32_t* __restrict__ ids,
+                                   float* __restrict__ out, int T, int N, int top_k, int E) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)T * N) return;
     const int64_t t = i / N, n = i - t * N;
     float acc = 0.0f;
-    for (int s = 0; s < top_k; s++) acc += scratch[((size_t)t * top_k + s) * N + n];
+    for (int s = 0; s < top_k; s++) {
+        const int e = ids[(size_t)t * top_k + s];
+        if (e >= 0 && e < E) acc += scratch[((size_t)t * top_k + s) * N + n];
+    }
     out[i] = acc;
 }
 
-hipError_t launch_moe_combine(const float* scratch, float* out, int T, int N, int top_k, hipStream_t s) {
+hipError_t launch_moe_combine(const float* scratch, const int32_t* ids, float* out, int T, int N, int top_k, int E,
+                              hipStream_t s) {
     const int64_t n = (int64_t)T * N;
     if (n == 0) return hipSuccess;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, scratch, out, T, N,
-                       top_k);
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, scratch, ids, out, T,
+                       N, top_k, E);
     return hipGetLastError();
 }
 

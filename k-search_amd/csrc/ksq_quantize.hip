@@ -28,26 +28,13 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// Four packed int8 quants -> four fp16 values q/8 (two dwords), exactly: v_perm_b32 puts the
-// biased bytes u = q + 128 under 0x58 high bytes, fp16 128 + u/8, and the packed subtract of
-// 144 leaves q/8 (7 significant bits).
-__device__ __forceinline__ void q4_to_h8ths(uint32_t x, uint32_t& lo, uint32_t& hi) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const uint32_t u = x ^ 0x80808080u;
-    const h2 k = h2{(_Float16)144.0f, (_Float16)144.0f};
-    lo = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x58585858u, u, 0x04010400u)) - k);
-    hi = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x58585858u, u, 0x04030402u)) - k);
-}
-
 // Output formats: kQF81 block_q8_1 (quantize_row_q8_1_ref), kQF8S block_q8s (the native W8A8C8
-// operator's rules), both 36-byte blocks of 9 dwords; kQF8H the q8h layout of the f16-MFMA GEMM:
-// the block_q8_1 quants as fp16 q/8 in y ([rows][K], 64 B per block) and its ds word in ds.
-constexpr int kQF81 = 0, kQF8S = 1, kQF8H = 2;
+// operator's rules), both 36-byte blocks of 9 dwords.
+constexpr int kQF81 = 0, kQF8S = 1;
 
 template <int FMT>
 __global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float* __restrict__ x,
-                                                                     uint8_t* __restrict__ y,
-                                                                     uint32_t* __restrict__ ds, int64_t nblocks) {
+                                                                     uint8_t* __restrict__ y, int64_t nblocks) {
     __shared__ float stage_all[kQWaves][64 * kQPitch];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     float* stage = stage_all[w];
@@ -85,58 +72,19 @@ __global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float
         else quantize_block_q8_1(v, q);
     }
     wave_lds_sync();
+    // 64 x 9 dwords, odd pitch: conflict free
     uint32_t* ostage = (uint32_t*)stage;
-    if constexpr (FMT == kQF8H) {
-        // 64 x 16 dwords of fp16 quants (pitch 17: conflict free), then 4 KB of coalesced stores
-        if (lane < nblk) {
-            ds[blk0 + lane] = q[0];
+    if (lane < nblk) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                uint32_t lo, hi;
-                q4_to_h8ths(q[1 + j], lo, hi);
-                ostage[lane * 17 + 2 * j] = lo;
-                ostage[lane * 17 + 2 * j + 1] = hi;
-            }
-        }
-        wave_lds_sync();
-        uint32_t* dst = (uint32_t*)(y + blk0 * 64);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const int idx = lane + 64 * j;   // dword idx of the wave's 64 x 16
-            if (idx < nblk * 16) dst[idx] = ostage[(idx >> 4) * 17 + (idx & 15)];
-        }
-    } else {
-        // 64 x 9 dwords, odd pitch: conflict free
-        if (lane < nblk) {
-#pragma unroll
-            for (int j = 0; j < 9; j++) ostage[lane * 9 + j] = q[j];
-        }
-        wave_lds_sync();
-        uint32_t* dst = (uint32_t*)(y + blk0 * 36);
-#pragma unroll
-        for (int j = 0; j < 9; j++) {
-            const int idx = lane + 64 * j;
-            if (idx < nblk * 9) dst[idx] = ostage[idx];
-        }
+        for (int j = 0; j < 9; j++) ostage[lane * 9 + j] = q[j];
     }
-}
-
-// block_q8_1 -> q8h: one thread per block.
-__global__ __launch_bounds__(256) void q8_1_to_q8h_kernel(const uint8_t* __restrict__ a, uint8_t* __restrict__ qh,
-                                                         uint32_t* __restrict__ ds, int64_t nblocks) {
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (g >= nblocks) return;
-    const uint32_t* p = (const uint32_t*)(a + g * kQ81Bytes);
-    uint32_t v[9];
+    wave_lds_sync();
+    uint32_t* dst = (uint32_t*)(y + blk0 * 36);
 #pragma unroll
-    for (int i = 0; i < 9; i++) v[i] = p[i];
-    ds[g] = v[0];
-    uint32_t o[16];
-#pragma unroll
-    for (int j = 0; j < 8; j++) q4_to_h8ths(v[1 + j], o[2 * j], o[2 * j + 1]);
-    u32x4* d = (u32x4*)(qh + g * 64);
-#pragma unroll
-    for (int c = 0; c < 4; c++) d[c] = u32x4{o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
+    for (int j = 0; j < 9; j++) {
+        const int idx = lane + 64 * j;
+        if (idx < nblk * 9) dst[idx] = ostage[idx];
+    }
 }
 
 hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
@@ -145,27 +93,10 @@ hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, i
     const int64_t grid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
     if (afmt == kAQ8S)
         hipLaunchKernelGGL(quantize_q8_1_kernel<kQF8S>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y,
-                           nullptr, nblocks);
+                           nblocks);
     else
         hipLaunchKernelGGL(quantize_q8_1_kernel<kQF81>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y,
-                           nullptr, nblocks);
-    return hipGetLastError();
-}
-
-hipError_t launch_quantize_q8h(const float* x, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s) {
-    const int64_t nblocks = rows * (int64_t)(K / 32);
-    if (nblocks == 0) return hipSuccess;
-    const int64_t grid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
-    hipLaunchKernelGGL(quantize_q8_1_kernel<kQF8H>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, (uint8_t*)qh,
-                       ds, nblocks);
-    return hipGetLastError();
-}
-
-hipError_t launch_q8_1_to_q8h(const uint8_t* a, _Float16* qh, uint32_t* ds, int64_t rows, int K, hipStream_t s) {
-    const int64_t nblocks = rows * (int64_t)(K / 32);
-    if (nblocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(q8_1_to_q8h_kernel, dim3((unsigned)((nblocks + 255) / 256)), dim3(256), 0, s, a, (uint8_t*)qh,
-                       ds, nblocks);
+                           nblocks);
     return hipGetLastError();
 }
 

@@ -333,6 +333,7 @@ hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A
     const long long wave_target = M <= 4 ? 4096 : 1024;
     int nwv = 4;
     while (nwv < max_nwv && (long long)wgs * nwv < wave_target && steps >= 2 * nwv) nwv *= 2;
+    note_engine(KSQ_ENG_SKINNY);
     switch (wtype) {
         case kWQ40: return skinny_launch_mp<kWQ40, false>(nwv, W, A, C, M, N, nb, s);
         case kWQ80:

@@ -16,6 +16,12 @@ LIB_PATH = os.path.join(PKG_ROOT, "libksq.so")
 # enum ksq_wtype / ksq_atype / ksq_status (include/ksq_blocks.h, include/ksq.h)
 W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
 A_F32, A_Q8_1, A_F32_Q8S, A_Q8S, A_F16 = 0, 1, 2, 3, 4
+# KSQ_ENG_* bits of ksq_debug_last_engines (include/ksq.h)
+ENG = {"quantize": 1 << 0, "gemv_row": 1 << 1, "gemv_row_fq": 1 << 2, "gemv_direct": 1 << 3,
+       "gemv_direct_fq": 1 << 4, "gemv_mr": 1 << 5, "gemv_mr_fq": 1 << 6, "gemv_kq": 1 << 7, "skinny": 1 << 8,
+       **{f"mmq{c}": 1 << (8 + c) for c in range(1, 7)}, "splitk": 1 << 15, "moe_route": 1 << 16,
+       "moe_group": 1 << 17, "moe_tile64": 1 << 18, "moe_tile128": 1 << 19, "moe_combine": 1 << 20,
+       "transpose": 1 << 21}
 STATUS = {0: "KSQ_OK", 1: "KSQ_ERR_NULL", 2: "KSQ_ERR_SHAPE", 3: "KSQ_ERR_ALIGN",
           4: "KSQ_ERR_TYPE", 5: "KSQ_ERR_WORKSPACE", 6: "KSQ_ERR_HIP"}
 
@@ -45,15 +51,15 @@ SIGNATURES = {
     "ksq_quantize_q8_1": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8s": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8_1_variant": ([_I, _P, _P, _I, _I, _P], _I),
-    "ksq_gemm_q4_0_fp16_fused": ([_P, _P, _P, _I, _I, _I, _P], _I),
+    "ksq_gemm_q4_0_fp16_fused_workspace_size": ([_I, _I, _I], _SZ),
+    "ksq_gemm_q4_0_fp16_fused": ([_P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi_mfma": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
-    "ksq_debug_block_sumi_f16mfma": ([_P, _P, _P, _I, _I, _I, _P], _I),
-    "ksq_debug_quantize_q8h": ([_P, _P, _P, _I, _I, _P], _I),
     "ksq_set_path": ([_I], _I),
     "ksq_set_mmq_config": ([_I], _I),
+    "ksq_debug_last_engines": ([], ctypes.c_uint32),
     "ksq_moe_workspace_size": ([_I, _I, _I, _I, _I, _I], _SZ),
     "ksq_moe_gemm": ([_I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _SZ, _P], _I),
     "ksq_moe_gemm_routed": ([_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P, _SZ, _P], _I),

@@ -55,16 +55,21 @@ def gemm(wtype: int, atype: int, weight: torch.Tensor, activation: torch.Tensor,
 
 
 def gemm_q4_0_fp16_fused(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
-                         out: torch.Tensor | None = None) -> torch.Tensor:
+                         out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """The reference's gemm_q4_0_fp16_fused orientation: Q4_0 weight [M, K/32] (M weight rows),
     fp16 activation [N, K], output fp32 [M, N]."""
     if activation.dtype != torch.float16 or not activation.is_cuda or not weight.is_cuda:
         raise RuntimeError("gemm_q4_0_fp16_fused expects CUDA uint8 weights and float16 activations")
     if out is None:
         out = torch.empty((M, N), dtype=torch.float32, device=weight.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     check(lib().ksq_gemm_q4_0_fp16_fused(_ptr(weight), _ptr(activation.contiguous()), _ptr(out), M, N, K,
-                                         _stream()))
+                                         _ptr(workspace), ws_bytes, _stream()))
     return out
+
+
+def gemm_q4_0_fp16_fused_workspace_size(M: int, N: int, K: int) -> int:
+    return lib().ksq_gemm_q4_0_fp16_fused_workspace_size(M, N, K)
 
 
 def forward(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
@@ -128,31 +133,21 @@ def quantize_q8s(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tens
     return out
 
 
-def quantize_q8h(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """fp32 [M, K] -> the f16-MFMA GEMM's activation layout: (qh fp16 [M, K] = q/8, ds int32
-    [M, K/32] = the block_q8_1 ds words) with the quants of quantize_q8_1 (debug)."""
-    x = x.contiguous()
-    M, K = x.shape
-    qh = torch.empty((M, K), dtype=torch.float16, device=x.device)
-    ds = torch.empty((M, K // 32), dtype=torch.int32, device=x.device)
-    check(lib().ksq_debug_quantize_q8h(_ptr(x), _ptr(qh), _ptr(ds), M, K, _stream()))
-    return qh, ds
-
-
 def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int, N: int, K: int,
-               mfma: bool | str = False) -> torch.Tensor:
+               mfma: bool = False) -> torch.Tensor:
     """Per-block integer dots [M, N, nblk] from the device block-dot code (debug): the v_dot4
-    decode kernels, the int8 MFMA GEMM (mfma=True) or the f16-MFMA GEMM of Q4_0 (mfma="f16")."""
+    decode helpers, or the int8 MFMA GEMM's tiles (mfma=True)."""
     nblk = K // 16 if wtype == W_Q6_K else K // 32
     out = torch.empty((M, N, nblk), dtype=torch.int32, device=weight.device)
-    if mfma == "f16":
-        if wtype != W_Q4_0:
-            raise ValueError("the f16-MFMA GEMM takes Q4_0 weights")
-        check(lib().ksq_debug_block_sumi_f16mfma(_ptr(weight), _ptr(act_q8_1), _ptr(out), M, N, K, _stream()))
-        return out
     fn = lib().ksq_debug_block_sumi_mfma if mfma else lib().ksq_debug_block_sumi
     check(fn(wtype, _ptr(weight), _ptr(act_q8_1), _ptr(out), M, N, K, _stream()))
     return out
+
+
+def last_engines() -> set[str]:
+    """Kernel families the calling thread's last libksq call launched (ksq_debug_last_engines)."""
+    bits = lib().ksq_debug_last_engines()
+    return {k for k, v in _lib.ENG.items() if bits & v}
 
 
 def moe_gemm(wtype: int, weights: torch.Tensor, activation: torch.Tensor, router_logits: torch.Tensor,
@@ -189,9 +184,9 @@ def moe_workspace_size(wtype: int, T: int, N: int, K: int, E: int, top_k: int) -
 
 
 def set_path(path: int) -> None:
-    """0 automatic, 1 v_dot4 decode kernels only, 2 int8 MFMA GEMM where it applies,
-    3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it applies, 4 the f16-MFMA GEMM for
-    Q4_0 where it applies."""
+    """Routing override for calls from this thread: 0 automatic, 1 v_dot4 decode kernels only,
+    2 int8 MFMA GEMM where it applies, 3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it
+    applies."""
     check(lib().ksq_set_path(path))
 
 
@@ -203,5 +198,5 @@ def release() -> None:
     lib().ksq_release()
 
 
-__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "quantize_q8h", "block_sumi", "set_path",
+__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "block_sumi", "last_engines", "set_path",
            "workspace_size", "moe_gemm", "moe_gemm_routed", "moe_workspace_size", "release", "_lib"]

@@ -229,7 +229,8 @@ class DefinitionRunner:
             res["compilation"] = {"success": False, "errors": [str(e)], "warnings": [], "diagnostics": []}
             return self._save(res, attempt_dir)
         cfgs = test_configs(spec, self.all_configs)
-        threshold = (spec.get("accuracy") or {}).get("threshold") or 0.05
+        threshold = (spec.get("accuracy") or {}).get("threshold")
+        threshold = 0.05 if threshold is None else threshold   # unified_test_runner.py:410
         N, K = cfgs[0]["N"], cfgs[0]["K"]
         g = torch.Generator(device=self.dev)
         g.manual_seed(self.seed + zlib.crc32(name.encode()))
@@ -275,23 +276,38 @@ class DefinitionRunner:
                 "finite": finite, "exact": exact}
 
     def _exact(self, w, x, y, wtype, atype, M, N, K, g) -> dict:
-        """Sampled rows x columns: quantised activations, block dots and fp32 outputs."""
+        """Sampled rows x columns of the definition's own call: quantised activations bit-exact,
+        fp32 within 1e-3 of the fp64 block formula.  Then the same entry on unit-scale inputs
+        (refcheck "unit-scale exactness"): its outputs must equal the exact integer sums of the
+        block dots, which checks the integer block dots of the engine that produced them."""
         rows = sorted({0, M - 1, *torch.randint(0, M, (2,), generator=g, device=self.dev).tolist()})
         cols = sorted(set(torch.randint(0, N, (64,), generator=g, device=self.dev).tolist()) | {0, N - 1})
         xr = x[rows].contiguous()
         q8s = atype == _lib.A_F32_Q8S
         a_dev = (ops.quantize_q8s if q8s else ops.quantize_q8_1)(xr)
-        wc = w[cols].contiguous()
-        s_dev = ops.block_sumi(wtype, wc, a_dev, len(rows), len(cols), K)
         torch.cuda.synchronize()
-        x_np, w_np = xr.cpu().numpy(), wc.cpu().numpy()
+        x_np, w_np = xr.cpu().numpy(), w[cols].contiguous().cpu().numpy()
         a_ref = (refcheck.quantize_q8s if q8s else refcheck.quantize_q8_1)(x_np)
         q_ok = bool(np.array_equal(a_dev.cpu().numpy(), a_ref))
-        s_ok = bool(np.array_equal(s_dev.cpu().numpy(), refcheck.block_sumi(wtype, a_ref, w_np)))
         ref64 = refcheck.gemm_q8s_f64(a_ref, w_np) if q8s else refcheck.gemm_f64(wtype, a_ref, w_np)
         err = refcheck.max_rel_err(y[rows][:, cols].cpu().numpy(), ref64)
+        s_ok, engines = self._unit_scale(wtype, atype, M, N, K, cols)
         return {"passed": q_ok and s_ok and err <= 1e-3, "quantize_bit_exact": q_ok, "block_dots_bit_exact": s_ok,
-                "max_rel_err_vs_fp64": err, "rows": rows, "columns_sampled": len(cols)}
+                "max_rel_err_vs_fp64": err, "rows": rows, "columns_sampled": len(cols), "engines": engines}
+
+    def _unit_scale(self, wtype, atype, M, N, K, cols):
+        rng = np.random.default_rng(self.seed + 17 * M + N)
+        wu = refcheck.unit_weights(wtype, rng, N, K)
+        xu = refcheck.unit_activations(rng, M, K, qmax=refcheck.unit_qmax(wtype, K),
+                                       onehot=refcheck.onehot_pattern(M, K // 32))
+        q8s = atype == _lib.A_F32_Q8S
+        yu = ops.gemm(wtype, atype, torch.from_numpy(wu).to(self.dev), torch.from_numpy(xu).to(self.dev), M, N, K)
+        engines = sorted(ops.last_engines())
+        au = (refcheck.quantize_q8s if q8s else refcheck.quantize_q8_1)(xu)
+        ref, bound = refcheck.exact_gemm(wtype, au, wu[cols], q8s=q8s)
+        ok = bool(bound.max() < 2.0 ** 24 and np.array_equal(yu[:, cols].cpu().numpy(), ref.astype(np.float32)))
+        del wu, yu
+        return ok, engines
 
     def _performance(self, w, x, entry, M, N, K, wtype) -> dict:
         fn = lambda: ops.forward(w, x, M, N, K, entry=entry)  # noqa: E731

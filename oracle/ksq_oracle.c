@@ -21,8 +21,10 @@
  *   sumi (Q4_0, Q8_0)    brute-force integer dot, known-answer blocks
  *   gemm (fp32 order)    fp64 block formula (gemm_ref.py:100-153 form) and a
  *                        dequantise-then-matmul numpy path
- *   Q4_K / Q6_K          independent encoder (layout written from the public
- *                        GGML description) -> oracle decoder round trip,
+ *   Q4_K / Q6_K          byte-literal super-blocks packed by hand from the public
+ *                        GGML field description against hand-computed values
+ *                        (all 16 six-bit slots distinct, distinct quarters and
+ *                        qh bit pairs), an independent encoder round trip,
  *                        integer-sum path vs dequantise-then-fp64-dot path
  *   MoE                  routing invariants, composition with the dense oracle
  *   Q4_1 / Q5_0 / Q5_1   numpy restatement of the harness formula
@@ -33,10 +35,12 @@
  *   Q8_1 variants        device kernel: numpy rint/cumsum restatement, ties,
  *                        zero block, inf; NumPy harness: NumPy itself running
  *                        the harness expressions, sum-order-sensitive blocks;
- *                        fused FP16: exact-sum blocks, ties, 1/half(d) vs 1/d.
- *                        Parity unpinned: the fused quantiser's tree sum order
- *                        (visible only at fp16 ties of s) and its int8
- *                        conversion where |v*id| >= 127.5 (subnormal half(d)).
+ *                        fused FP16: exact-sum blocks, ties, 1/half(d) vs 1/d,
+ *                        constructed blocks whose fp16 s differs between its
+ *                        shared-memory tree and a left-to-right sum.
+ *                        Parity unpinned: the fused quantiser's int8 conversion
+ *                        where |v*id| >= 127.5 (reachable only when half(d) is
+ *                        subnormal), taken as saturating.
  */
 #include <math.h>
 #include <stdint.h>

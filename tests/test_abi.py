@@ -85,10 +85,10 @@ def test_fp16_fused_entry_rejects_bad_arguments():
     """ksq_gemm_q4_0_fp16_fused validates like ksq_gemm, in its own (M weight rows) orientation."""
     from ksq import _lib
     L = _lib.lib()
-    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE + 8, FAKE, 4, 2, 64, None) == 3   # activation alignment
-    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 4, 2, 48, None) == 2       # K % 32
-    assert L.ksq_gemm_q4_0_fp16_fused(None, FAKE, FAKE, 4, 2, 64, None) == 1       # null weight
-    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 0, 2, 64, None) == 0       # empty: no-op
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE + 8, FAKE, 4, 2, 64, None, 0, None) == 3   # activation alignment
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 4, 2, 48, None, 0, None) == 2       # K % 32
+    assert L.ksq_gemm_q4_0_fp16_fused(None, FAKE, FAKE, 4, 2, 64, None, 0, None) == 1       # null weight
+    assert L.ksq_gemm_q4_0_fp16_fused(FAKE, FAKE, FAKE, 0, 2, 64, None, 0, None) == 0       # empty: no-op
 
 
 def test_quantize_variant_rejects_unknown_variant():
@@ -100,20 +100,16 @@ def test_quantize_variant_rejects_unknown_variant():
 
 
 def test_workspace_size():
-    """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K); on
-    path 4 (the f16-MFMA GEMM of Q4_0) the q8h activations (fp16 quants + ds words) for both."""
+    """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K)."""
     from ksq import _lib
     L = _lib.lib()
     assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == 2048 * 128 * 36
     assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == 0
     assert L.ksq_gemm_workspace_size(1, 0, 2048, 4096, 4096) == 2048 * 128 * 36
-    q8h = 2048 * 4096 * 2 + 2048 * 128 * 4
-    assert L.ksq_set_path(4) == 0
-    try:
-        assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == q8h
-        assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == q8h
-    finally:
-        L.ksq_set_path(0)
+    # the fused FP16 orientation: the quantised copy of its N x K activations plus an M x N
+    # transposition buffer, each 256-byte aligned
+    assert L.ksq_gemm_q4_0_fp16_fused_workspace_size(4096, 8, 4096) == 8 * 128 * 36 + 4096 * 8 * 4
+    assert L.ksq_gemm_q4_0_fp16_fused_workspace_size(4096, 3, 4096) == 13824 + 49152
 
 
 def test_void_entry_records_error():
@@ -138,6 +134,6 @@ def test_set_path_validation():
     L = _lib.lib()
     assert L.ksq_set_path(5) == 4
     assert L.ksq_set_path(-1) == 4
+    assert L.ksq_set_path(4) == 4
     assert L.ksq_set_path(3) == 0
-    assert L.ksq_set_path(4) == 0
     assert L.ksq_set_path(0) == 0

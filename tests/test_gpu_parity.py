@@ -385,63 +385,6 @@ def test_mfma_tile_configs(dev, oracle, cfg, wtype):
     assert _rel_err(y, ref) <= TOL
 
 
-# ------------------------------------------------------------------ f16-MFMA GEMM (Q4_0)
-def test_quantize_q8h_bit_exact(dev, oracle):
-    """The q8h activation layout holds exactly the block_q8_1 quants (as fp16 q/8) and ds words."""
-    import torch
-    from ksq import ops
-    g = np.random.default_rng(2600)
-    for M, K in ((1, 64), (3, 1024), (257, 96), (130, 4096)):
-        x = g.standard_normal((M, K), dtype=np.float32)
-        if M == 3:
-            x[1, :8] = [127.0, 2.5, -2.5, 0.5, -0.5, 1.5, -126.5, 3.49999976]
-            x[2, 32:64] *= 3e4
-            x[0, 64] = np.inf
-        qh, ds = ops.quantize_q8h(_t(x, dev))
-        torch.cuda.synchronize()
-        ref = oracle.quantize_q8_1(x).reshape(M, K // 32, 36)
-        q = (qh.cpu().numpy().astype(np.float64) * 8).reshape(M, K // 32, 32)
-        assert np.array_equal(q, ref[:, :, 4:].view(np.int8).astype(np.float64)), (M, K)
-        assert np.array_equal(ds.cpu().numpy().view(np.uint32), ref[:, :, :4].copy().view(np.uint32)[:, :, 0]), (M, K)
-
-
-def test_block_sumi_f16mfma_bit_exact(dev, oracle):
-    """The f16-MFMA tiles return the reference's integer block dots exactly (as sumi / 8)."""
-    from ksq import ops, synth
-    g = np.random.default_rng(2700)
-    for M, N, K in ((160, 96, 512), (33, 130, 64)):
-        w = synth.weights(0, g, N, K)
-        a = oracle.quantize_q8_1(synth.activations(g, M, K))
-        a[0, 0, 4:] = np.uint8(0x80)     # all -128 quants against the weights' nibbles
-        got = ops.block_sumi(0, _t(w, dev), _t(a, dev), M, N, K, mfma="f16").cpu().numpy()
-        assert np.array_equal(got, oracle.block_sumi(0, a, w, M, N, K)), (M, N, K)
-
-
-@pytest.mark.parametrize("M,N,K,atype", [(200, 136, 512, 0), (130, 200, 768, 1), (64, 4096, 4096, 0),
-                                         (300, 520, 1088, 0), (1, 256, 128, 1)])
-def test_f16mfma_gemm(dev, oracle, M, N, K, atype):
-    """Path 4 (the f16-MFMA GEMM of Q4_0) on ragged shapes, split-K grids and both activation
-    inputs (fp32 quantised to q8h, block_q8_1 converted to q8h); repeats bit for bit."""
-    import torch
-    from ksq import ops, synth
-    g = np.random.default_rng(2800 + M)
-    w = synth.weights(0, g, N, K)
-    x = synth.activations(g, M, K)
-    a = oracle.quantize_q8_1(x)
-    inp = _t(x, dev) if atype == 0 else _t(a, dev)
-    ops.set_path(4)
-    try:
-        y1 = ops.gemm(0, atype, _t(w, dev), inp, M, N, K)
-        y2 = ops.gemm(0, atype, _t(w, dev), inp, M, N, K)
-        torch.cuda.synchronize()
-    finally:
-        ops.set_path(0)
-    assert torch.equal(y1, y2)
-    rows = np.arange(M) if M <= 16 else np.sort(g.choice(M, 16, replace=False))
-    ref = oracle.gemm_f64(0, a[rows], w, len(rows), N, K)
-    assert _rel_err(y1.cpu().numpy()[rows], ref) <= TOL, (M, N, K)
-
-
 SKINNY_WTYPES = [0, 1, 4, 5, 6]          # the 32-element block types of the 4x4x4-MFMA kernel
 
 
@@ -474,17 +417,30 @@ def test_skinny_q8s_native(dev, oracle, M):
     assert _rel_err(y, ref) <= TOL
 
 
-@pytest.mark.parametrize("wtype,M,N,K", [(0, 6, 11008, 4096), (4, 5, 18944, 3584), (1, 7, 14336, 4096),
-                                         (0, 8, 4096, 4096), (4, 3, 2560, 2560), (0, 3, 4096, 4096),
-                                         (0, 2, 7168, 512), (1, 4, 9728, 2560), (4, 8, 18944, 3584),
-                                         (0, 5, 3584, 18944), (1, 8, 7168, 7168), (5, 4, 12288, 5120),
-                                         (2, 8, 4096, 4096), (3, 7, 12288, 5120), (2, 5, 7168, 7168),
-                                         (1, 2, 4096, 4096), (0, 2, 14336, 4096)])
-def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
+ENGINE_FAMILIES = {"decode": {"gemv_row", "gemv_row_fq", "gemv_direct", "gemv_direct_fq", "gemv_mr", "gemv_mr_fq",
+                               "gemv_kq"},
+                   "skinny": {"skinny"}, "mmq": {f"mmq{c}" for c in range(1, 7)}}
+
+
+def _family(engines):
+    fams = {f for f, names in ENGINE_FAMILIES.items() if engines & names}
+    assert len(fams) == 1, engines
+    return fams.pop()
+
+
+@pytest.mark.parametrize("wtype,M,N,K,expect", [
+    (0, 6, 11008, 4096, "skinny"), (4, 5, 18944, 3584, "decode"), (1, 7, 14336, 4096, "skinny"),
+    (0, 8, 4096, 4096, "skinny"), (4, 3, 2560, 2560, "skinny"), (0, 3, 4096, 4096, "decode"),
+    (0, 2, 7168, 512, "decode"), (1, 4, 9728, 2560, "skinny"), (4, 8, 18944, 3584, "skinny"),
+    (0, 5, 3584, 18944, "decode"), (1, 8, 7168, 7168, "skinny"), (5, 4, 12288, 5120, "decode"),
+    (2, 8, 4096, 4096, "mmq"), (3, 7, 12288, 5120, "mmq"), (2, 5, 7168, 7168, "decode"),
+    (1, 2, 4096, 4096, "decode"), (0, 2, 14336, 4096, "decode"), (2, 5, 12288, 5120, "mmq"),
+    (2, 6, 7168, 512, "mmq"), (2, 8, 4096, 1024, "decode")])
+def test_small_m_default_routing(dev, oracle, wtype, M, N, K, expect):
     """M = 2..8 by default: large matrices take the MFMA GEMM (the measured crossovers), short
-    rows on wide matrices the 4x4x4-MFMA small-batch kernel, the rest the decode kernel; each way
-    the fp32 entry matches the oracle, with the library pool and with a caller workspace of
-    exactly ksq_gemm_workspace_size bytes."""
+    rows on wide matrices the 4x4x4-MFMA small-batch kernel, the rest the decode kernel (the
+    engine family each shape takes is asserted); each way the fp32 entry matches the oracle,
+    with the library pool and with a caller workspace of exactly ksq_gemm_workspace_size bytes."""
     import torch
     from ksq import ops, synth
     g = np.random.default_rng(2300 + M)
@@ -492,6 +448,7 @@ def test_small_m_default_routing(dev, oracle, wtype, M, N, K):
     x = synth.activations(g, M, K)
     wt, xt = _t(w, dev), _t(x, dev)
     y1 = ops.gemm(wtype, 0, wt, xt, M, N, K)
+    assert _family(ops.last_engines()) == expect
     ws = torch.empty(max(ops.workspace_size(wtype, 0, M, N, K), 1), dtype=torch.uint8, device=dev)
     y2 = ops.gemm(wtype, 0, wt, xt, M, N, K, workspace=ws)
     torch.cuda.synchronize()

@@ -121,7 +121,7 @@ def test_q8_1_variant_fused_f16(oracle):
     """quantize_fp16_to_q8_1_smem (gemm_fused.cuh:76-145): fp16 input, q from 1/half(d),
     roundf, clamp +-127.  Checked on blocks whose sums are exact in any order against a numpy
     statement, on ties, and on a value where 1/half(d) and 1/d round differently.  The tree
-    order of the sum itself only shows where the fp16 rounding of s meets a tie: unpinned."""
+    order of the sum: test_q8_1_variant_fused_f16_tree_sum."""
     g = np.random.default_rng(42)
     # multiples of 2^-8 below 2^7: every partial sum of 32 is exact in fp32
     xi = g.integers(-2 ** 15, 2 ** 15, (32, 256)).astype(np.float32) * np.float32(2.0 ** -8)
@@ -538,3 +538,122 @@ def test_gemm_w8a8c8_composition(oracle):
     # a Q8_1 (fp16 scale) activation path is a different operator: it differs at the fp16 level
     q81 = oracle.gemm(1, oracle.quantize_q8_1(x), w, M, N, K)
     assert np.abs(q81 - want).max() > 1e-7 * np.abs(want).max()
+
+
+# ---- byte-literal K-quant super-blocks (written from the public GGML field description) ----
+# Q4_K: {fp16 d, fp16 dmin, u8 scales[12], u8 qs[128]}; value of element 64g + 32h + l
+# = d * sc_j * q - dmin * m_j, j = 2g + h, q = low (h = 0) or high (h = 1) nibble of qs[32g + l];
+# 6-bit (sc_j, m_j): j < 4 in the low 6 bits of scales[j] / scales[j + 4]; j >= 4 low 4 bits in
+# scales[j + 4] (sc low nibble, m high nibble), top 2 bits in the top 2 bits of scales[j - 4] (sc)
+# and scales[j] (m).  Chosen fields: d = 1, dmin = 0.5,
+#   sc = 1, 2, 3, 4, 37, 46, 55, 63      m = 5, 6, 7, 8, 17, 29, 42, 60
+# packed by hand:
+#   scales[0..3]  = 1|2<<6, 2|2<<6, 3|3<<6, 4|3<<6         = 0x81 0x82 0xC3 0xC4
+#   scales[4..7]  = 5|1<<6, 6|1<<6, 7|2<<6, 8|3<<6         = 0x45 0x46 0x87 0xC8
+#   scales[8..11] = 5|1<<4, 14|13<<4, 7|10<<4, 15|12<<4     = 0x15 0xDE 0xA7 0xCF
+# qs: group g bytes 0x15, 0x26, 0x37, 0x48 (low nibble 5 + g, high 1 + g) except byte l = 31 of
+# every group, 0x9A (low 10, high 9).
+Q4_K_LITERAL = bytes([0x00, 0x3C, 0x00, 0x38,
+                      0x81, 0x82, 0xC3, 0xC4, 0x45, 0x46, 0x87, 0xC8, 0x15, 0xDE, 0xA7, 0xCF]
+                     + [0x15] * 31 + [0x9A] + [0x26] * 31 + [0x9A] + [0x37] * 31 + [0x9A] + [0x48] * 31 + [0x9A])
+# hand-computed values per sub-block j for l < 31 and l = 31:
+#   j0 1*5-2.5=2.5  1*10-2.5=7.5 | j1 2*1-3=-1    2*9-3=15     | j2 3*6-3.5=14.5  3*10-3.5=26.5
+#   j3 4*2-4=4      4*9-4=32     | j4 37*7-8.5=250.5 37*10-8.5=361.5 | j5 46*3-14.5=123.5 46*9-14.5=399.5
+#   j6 55*8-21=419  55*10-21=529 | j7 63*4-30=222 63*9-30=537
+Q4_K_VALUES = [(2.5, 7.5), (-1.0, 15.0), (14.5, 26.5), (4.0, 32.0), (250.5, 361.5), (123.5, 399.5),
+               (419.0, 529.0), (222.0, 537.0)]
+# Q6_K: {u8 ql[128], u8 qh[64], i8 scales[16], fp16 d}; element 128n + 32Q + l of half n, quarter Q:
+# q = 4 bits of ql (Q0: low of ql[64n+l], Q1: low of ql[64n+32+l], Q2: high of ql[64n+l], Q3:
+# high of ql[64n+32+l]) | bits 2Q, 2Q+1 of qh[32n+l] as bits 4-5; value d * sc[8n + 2Q + l/16] * (q - 32).
+# Chosen: d = 0.25; ql half 0 = 0x21 x32, 0x43 x32; half 1 = 0x65 x32, 0x87 x32 except ql[5] = 0x2F;
+# qh half 0 = 0xE4 (Q0..Q3 high bits 0, 1, 2, 3), half 1 = 0x1B (3, 2, 1, 0);
+# scales = -128 127 -3 5 -7 11 -13 17 19 -23 29 -31 37 -41 43 -47.
+# So q - 32: half 0 Q0..Q3 = 1-32, 19-32, 34-32, 52-32 = -31 -13 2 20; half 1 = 53-32, 39-32, 22-32,
+# 8-32 = 21 7 -10 -24; element 5 (ql 0x2F): 15-32 = -17.
+Q6_K_LITERAL = bytes([0x2F if i == 5 else 0x21 for i in range(32)] + [0x43] * 32 + [0x65] * 32 + [0x87] * 32
+                     + [0xE4] * 32 + [0x1B] * 32
+                     + [0x80, 0x7F, 0xFD, 0x05, 0xF9, 0x0B, 0xF3, 0x11, 0x13, 0xE9, 0x1D, 0xE1, 0x25, 0xD7, 0x2B, 0xD1]
+                     + [0x00, 0x34])
+# hand-computed values for the 16 sixteen-element sub-blocks (0.25 * sc * (q - 32)); element 5: 0.25*-128*-17
+Q6_K_VALUES = [992.0, -984.25, 9.75, -16.25, -3.5, 5.5, -65.0, 85.0,
+               99.75, -120.75, 50.75, -54.25, -92.5, 102.5, -258.0, 282.0]
+
+
+def test_q4_K_byte_literal(oracle):
+    """The oracle's Q4_K decoder on a hand-packed super-block: distinct scales and mins in all 16
+    six-bit slots (high bits of j >= 4 included) and distinct quants per group and half, so a
+    swapped scale/min high-bit source, a swapped nibble/sub-block pairing or a wrong group order
+    each changes some value."""
+    assert len(Q4_K_LITERAL) == 144
+    blk = np.frombuffer(Q4_K_LITERAL, dtype=np.uint8)
+    sc = [1, 2, 3, 4, 37, 46, 55, 63]
+    mn = [5, 6, 7, 8, 17, 29, 42, 60]
+    for j in range(8):
+        assert oracle.q4_K_scale_min(j, blk[4:16]) == (sc[j], mn[j])
+    got = oracle.dequantize(2, blk[None, None, :], 1, 256)[0]
+    want = np.empty(256)
+    for j, (v, v31) in enumerate(Q4_K_VALUES):
+        want[32 * j:32 * j + 32] = v
+        want[32 * j + 31] = v31
+    assert np.array_equal(got.astype(np.float64), want)
+    # integer block dot of sub-block 4 against an all-ones Q8_1 block (d = 1, s = 32): 31*7 + 10
+    a = np.zeros((1, 8, 36), np.uint8)
+    a[..., 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    a[..., 2:4] = np.array([32.0], np.float16).view(np.uint8)
+    a[..., 4:] = 1
+    assert oracle.block_sumi(2, a, blk[None, None, :], 1, 1, 256)[0, 0].tolist() == \
+        [31 * 5 + 10, 31 * 1 + 9, 31 * 6 + 10, 31 * 2 + 9, 31 * 7 + 10, 31 * 3 + 9, 31 * 8 + 10, 31 * 4 + 9]
+
+
+def test_q6_K_byte_literal(oracle):
+    """The oracle's Q6_K decoder on a hand-packed super-block: distinct ql nibbles and qh bit pairs
+    per quarter and half, sixteen distinct int8 scales (-128 and 127 included), so a swapped quarter
+    order, qh bit pair, scale index or half changes some value."""
+    assert len(Q6_K_LITERAL) == 210
+    blk = np.frombuffer(Q6_K_LITERAL, dtype=np.uint8)
+    got = oracle.dequantize(3, blk[None, None, :], 1, 256)[0].astype(np.float64)
+    want = np.repeat(np.array(Q6_K_VALUES), 16)
+    want[5] = 0.25 * -128 * -17
+    assert np.array_equal(got, want)
+    a = np.zeros((1, 8, 36), np.uint8)
+    a[..., 0:2] = np.array([1.0], np.float16).view(np.uint8)
+    a[..., 4:] = 1
+    s = oracle.block_sumi(3, a, blk[None, None, :], 1, 1, 256)[0, 0]
+    # sixteen-element sums of (q - 32): half 0 -31, -13, 2, 20 per quarter; element 5 is -17
+    assert s.tolist()[:8] == [15 * -31 + -17, 16 * -31, 16 * -13, 16 * -13, 16 * 2, 16 * 2, 16 * 20, 16 * 20]
+    assert s.tolist()[8:] == [16 * 21, 16 * 21, 16 * 7, 16 * 7, 16 * -10, 16 * -10, 16 * -24, 16 * -24]
+
+
+def test_q8_1_variant_fused_f16_tree_sum(oracle):
+    """The fused FP16 quantiser's s is the shared-memory tree of gemm_fused.cuh:93-121 (x[i] + x[i+16],
+    then + 8, + 4, + 2 apart, then s0 + s1, all fp32): on blocks whose fp16 s differs between that
+    tree and a left-to-right fp32 sum, the oracle follows the tree (restated here by halving)."""
+    g = np.random.default_rng(43)
+
+    def tree(b):
+        v = b.astype(np.float32)
+        while v.size > 1:
+            h = v.size // 2
+            v = (v[:h] + v[h:]).astype(np.float32)
+        return v[0]
+
+    hits = 0
+    for _ in range(20000):
+        # one 2048 and a +-1 or 3 (an fp16 rounding tie of s near 2049) among fp16-subnormal-scale
+        # values that a left-to-right fp32 sum absorbs one by one but the tree adds up first
+        bf = np.zeros(32, np.float32)
+        bf[g.integers(0, 32)] = 2048.0
+        bf[g.integers(0, 32)] += np.float32(g.choice([1.0, 3.0, -1.0]))
+        small = g.integers(1, 4, size=32) * np.float32(2.0 ** -14) * g.choice([-1, 1], size=32)
+        bf = np.where((bf == 0) & (g.random(32) < 0.8), small, bf).astype(np.float32)
+        b = bf.astype(np.float16)
+        bf = b.astype(np.float32)
+        t, seq = np.float32(tree(bf)).astype(np.float16), np.cumsum(bf, dtype=np.float32)[-1].astype(np.float16)
+        if t == seq:
+            continue
+        got = oracle.quantize_q8_1_variant(b[None, :], 3)[0, 0, 2:4].view(np.float16)[0]
+        assert got == t, (got, t, seq)
+        hits += 1
+        if hits == 5:
+            break
+    assert hits == 5
