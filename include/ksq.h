@@ -171,6 +171,17 @@ KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K
 KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,
              int M, int N, int K, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): ksq_gemm whose scratch
+ * (the quantised copy of fp32 / fp16 activations, split-K partial sums) is a static device array
+ * of KSQ_NOALLOC_SCRATCH_BYTES on each GPU, held until the process ends.  Makes no hipMalloc /
+ * hipFree.  A call whose ksq_gemm_workspace_size() exceeds KSQ_NOALLOC_SCRATCH_BYTES returns
+ * KSQ_ERR_WORKSPACE without launching.  All calls on one GPU share that GPU's array: calls that
+ * overlap on one GPU (concurrent streams) race; calls in one stream are ordered. */
+#define KSQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+KSQ_API int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const void* activation, float* output,
+                             int M, int N, int K, void* stream);
+
 /* Debug: per-block integer dot products out[M][N][nblk] (nblk = K/32, or K/16 for
  * Q6_K) computed by the device block-dot code of the decode kernels. */
 KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,

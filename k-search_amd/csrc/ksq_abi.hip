@@ -85,6 +85,30 @@ int pool_get(size_t bytes, hipStream_t s, void** out) {
     return KSQ_OK;
 }
 
+// ksq_gemm_noalloc's scratch: a file-scope device array (one copy per GPU, allocated with the
+// code object and held until the process ends).  Host code never passes `scratch` itself to a
+// kernel: that name is a host-side stand-in.  The device address of each GPU's copy comes from
+// hipGetSymbolAddress, once per device, with that device current.
+__device__ __attribute__((aligned(256))) uint8_t scratch[KSQ_NOALLOC_SCRATCH_BYTES];
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_ptr;
+
+int scratch_get(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_error(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize(dev + 1, nullptr);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return KSQ_OK;
+}
+
 int block_elems(int wtype) { return (wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) ? 256 : 32; }
 
 bool atype_f32(int atype) { return atype == KSQ_A_F32 || atype == KSQ_A_F32_Q8S; }
@@ -349,6 +373,27 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     st = run_matmul(wtype, afmt, (const uint8_t*)weight, Aq, output, M, N, K, partials, s);
     return st == KSQ_OK ? ok() : st;
+}
+
+int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const void* activation, float* output, int M, int N,
+                     int K, void* stream) {
+    g_engines = 0;
+    int st = check_common(wtype, atype, weight, activation, output, M, N, K);
+    if (st != KSQ_OK) return st;
+    if (M == 0 || N == 0) return ok();
+    // the workspace ksq_gemm would ask for (an upper bound of what this call uses)
+    const size_t need = ksq_gemm_workspace_size(wtype, atype, M, N, K);
+    if (need > (size_t)KSQ_NOALLOC_SCRATCH_BYTES)
+        return set_error(KSQ_ERR_WORKSPACE,
+                         "ksq_gemm_noalloc: this call needs %zu bytes of scratch, more than the %u-byte static "
+                         "scratch; use ksq_gemm with a workspace",
+                         need, (unsigned)KSQ_NOALLOC_SCRATCH_BYTES);
+    void* p = nullptr;
+    st = scratch_get(&p);
+    if (st != KSQ_OK) return st;
+    // every byte of the scratch a call reads is written first by the same call (quantised
+    // activations, split-K partials), so nothing needs clearing
+    return ksq_gemm(wtype, atype, weight, activation, output, M, N, K, p, (size_t)KSQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N,

@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(PKG_ROOT, "libksq.so")
 # enum ksq_wtype / ksq_atype / ksq_status (include/ksq_blocks.h, include/ksq.h)
 W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
 A_F32, A_Q8_1, A_F32_Q8S, A_Q8S, A_F16 = 0, 1, 2, 3, 4
+NOALLOC_SCRATCH_BYTES = 32 << 20   # KSQ_NOALLOC_SCRATCH_BYTES
 # KSQ_ENG_* bits of ksq_debug_last_engines (include/ksq.h)
 ENG = {"quantize": 1 << 0, "gemv_row": 1 << 1, "gemv_row_fq": 1 << 2, "gemv_direct": 1 << 3,
        "gemv_direct_fq": 1 << 4, "gemv_mr": 1 << 5, "gemv_mr_fq": 1 << 6, "gemv_kq": 1 << 7, "skinny": 1 << 8,
@@ -55,6 +56,7 @@ SIGNATURES = {
     "ksq_gemm_q4_0_fp16_fused": ([_P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
+    "ksq_gemm_noalloc": ([_I, _I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi_mfma": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_set_path": ([_I], _I),
