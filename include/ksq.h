@@ -229,7 +229,7 @@ KSQ_API int ksq_set_path(int path);
 /* MFMA tile configuration for tuning, for calls made from the calling host thread: 0 = chosen
  * from (M, N) (default); 1 = 128x128 tile, K step 8; 2 = 128x64; 3 = 64x64; 4 = 128x128 with
  * K step 4; 5 = 32x128; 6 = 128x128 with K step 4 and the next step's loads prefetched into
- * registers. */
+ * registers; 7 = 64x128. */
 KSQ_API int ksq_set_mmq_config(int config);
 
 /* Debug: the kernel families the last ksq_gemm / drop-in / MoE / fused-FP16 call made on the
@@ -243,14 +243,14 @@ KSQ_API int ksq_set_mmq_config(int config);
 #define KSQ_ENG_GEMV_MR_FQ (1u << 6)      /* gemv_direct_mr_kernel quantising fp32 rows */
 #define KSQ_ENG_GEMV_KQ (1u << 7)         /* gemv_direct_kq_kernel (Q4_K / Q6_K, 1-2 rows) */
 #define KSQ_ENG_SKINNY (1u << 8)          /* skinny_kernel (4x4x4 int8 MFMA, M <= 8) */
-#define KSQ_ENG_MMQ_CFG(c) (1u << (8 + (c))) /* mmq_kernel with tile configuration c = 1..6 */
-#define KSQ_ENG_SPLITK (1u << 15)         /* the MFMA GEMM split along K, plus its reduction */
-#define KSQ_ENG_MOE_ROUTE (1u << 16)      /* MoE routing kernel */
-#define KSQ_ENG_MOE_GROUP (1u << 17)      /* MoE grouping / tile schedule kernel */
-#define KSQ_ENG_MOE_TILE64 (1u << 18)     /* grouped mmq_kernel, 64-row tiles */
-#define KSQ_ENG_MOE_TILE128 (1u << 19)    /* grouped mmq_kernel, 128-row tiles */
-#define KSQ_ENG_MOE_COMBINE (1u << 20)    /* top_k > 2 slot-ordered combine */
-#define KSQ_ENG_TRANSPOSE (1u << 21)      /* output transpose (fused FP16 orientation) */
+#define KSQ_ENG_MMQ_CFG(c) (1u << (8 + (c))) /* mmq_kernel with tile configuration c = 1..7 */
+#define KSQ_ENG_SPLITK (1u << 16)         /* the MFMA GEMM split along K, plus its reduction */
+#define KSQ_ENG_MOE_ROUTE (1u << 17)      /* MoE routing */
+#define KSQ_ENG_MOE_GROUP (1u << 18)      /* MoE grouping / tile schedule */
+#define KSQ_ENG_MOE_TILE64 (1u << 19)     /* grouped mmq_kernel, 64-row tiles */
+#define KSQ_ENG_MOE_TILE128 (1u << 20)    /* grouped mmq_kernel, 128-row tiles */
+#define KSQ_ENG_MOE_COMBINE (1u << 21)    /* slot-ordered combine of per-entry rows */
+#define KSQ_ENG_TRANSPOSE (1u << 22)      /* output transpose (fused FP16 orientation) */
 KSQ_API uint32_t ksq_debug_last_engines(void);
 
 #ifdef __cplusplus

@@ -419,6 +419,13 @@ int ksq_debug_block_sumi_mfma(int wtype, const void* weight, const uint8_t* act_
 // ---- expert-grouped MoE --------------------------------------------------------
 namespace {
 
+#ifndef KSQ_MOE_SCRATCH_MIN_TOPK
+#define KSQ_MOE_SCRATCH_MIN_TOPK 3
+#endif
+// Whether the grouped GEMM writes per-entry rows to scratch (combined afterwards in slot order)
+// instead of adding into the output with atomics.
+bool moe_uses_scratch(int top_k) { return top_k >= KSQ_MOE_SCRATCH_MIN_TOPK; }
+
 struct MoeLayout {
     size_t aq, ids, wts, rows, eend, ntiles, texp, trow0, scratch, total;
     int max_tiles;
@@ -438,7 +445,7 @@ MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
     L.ntiles = off; off = align256(off + 4);
     L.texp = off; off = align256(off + (size_t)L.max_tiles * 4);
     L.trow0 = off; off = align256(off + (size_t)L.max_tiles * 4);
-    L.scratch = off; off = align256(off + (top_k > 2 ? ent * (size_t)N * 4 : 0));
+    L.scratch = off; off = align256(off + (moe_uses_scratch(top_k) ? ent * (size_t)N * 4 : 0));
     L.total = off;
     return L;
 }
@@ -471,29 +478,36 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     uint8_t* aq = base + L.aq;
     int32_t* ids = ids_out ? ids_out : (int32_t*)(base + L.ids);
     float* wts = wts_out ? wts_out : (float*)(base + L.wts);
-    hipError_t e = ksq::launch_quantize_q8_1(activation, aq, T, K, s);
+    // top_k <= 2 accumulates straight into the output, which the quantiser's launch zeroes
+    // beside its own work when the output allows 16-byte stores; top_k > 2 writes per-entry
+    // rows to scratch and combines them
+    float* scratch = moe_uses_scratch(top_k) ? (float*)(base + L.scratch) : nullptr;
+    const int64_t nout = (int64_t)T * N;
+    const bool zero_fused = !scratch && ((uintptr_t)output & 15u) == 0 && (nout & 3) == 0;
+    hipError_t e = zero_fused ? ksq::launch_quantize_q8_1_zero(activation, aq, T, K, output, nout, s)
+                              : ksq::launch_quantize_q8_1(activation, aq, T, K, s);
     if (e != hipSuccess) return hip_error(e, "quantize launch");
-    if (logits) {
-        e = ksq::launch_moe_route(logits, T, E, top_k, renorm, ids, wts, s);
-        if (e != hipSuccess) return hip_error(e, "route launch");
-        g_engines |= KSQ_ENG_MOE_ROUTE;
-    } else {
-        ids = (int32_t*)ids_in;
-        wts = (float*)wts_in;
+    if (!scratch && !zero_fused) {
+        e = ksq::launch_fill_zero(output, nout, s);
+        if (e != hipSuccess) return hip_error(e, "fill launch");
     }
     int32_t* rows = (int32_t*)(base + L.rows);
     int32_t* eend = (int32_t*)(base + L.eend);
     int32_t* ntiles = (int32_t*)(base + L.ntiles);
     int32_t* texp = (int32_t*)(base + L.texp);
     int32_t* trow0 = (int32_t*)(base + L.trow0);
-    e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
-    if (e != hipSuccess) return hip_error(e, "group launch");
-    g_engines |= KSQ_ENG_QUANTIZE | KSQ_ENG_MOE_GROUP;
-    float* scratch = top_k > 2 ? (float*)(base + L.scratch) : nullptr;
-    if (!scratch) {
-        e = ksq::launch_fill_zero(output, (int64_t)T * N, s);
-        if (e != hipSuccess) return hip_error(e, "fill launch");
+    if (logits) {
+        e = ksq::launch_moe_route_group(logits, T, E, top_k, renorm, ids, wts, tile_rows, rows, eend, ntiles, texp,
+                                        trow0, s);
+        if (e != hipSuccess) return hip_error(e, "route launch");
+        g_engines |= KSQ_ENG_MOE_ROUTE;
+    } else {
+        ids = (int32_t*)ids_in;
+        wts = (float*)wts_in;
+        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
+        if (e != hipSuccess) return hip_error(e, "group launch");
     }
+    g_engines |= KSQ_ENG_QUANTIZE | KSQ_ENG_MOE_GROUP;
     ksq::MoeTilesArgs a{ntiles, texp, trow0, eend, rows, wts, scratch, top_k};
     e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, tile_rows, a, s);
     if (e != hipSuccess) return hip_error(e, "grouped gemm launch");

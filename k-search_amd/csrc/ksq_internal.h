@@ -24,6 +24,10 @@ constexpr int kAQ81 = 0, kAQ8S = 1;
 // fp32 [rows][K] -> [rows][K/32] 36-byte blocks of format afmt; x 16-byte aligned, y 4-byte aligned.
 hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
+// The same quantisation plus zeroing nzero floats at `zero` (16-byte aligned, nzero % 4 == 0) in
+// the same launch.
+hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, int K, float* zero, int64_t nzero,
+                                     hipStream_t s);
 // variant 0-3 of ksq_quantize_q8_1_variant (x fp32, or fp16 bits for variant 3)
 hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 // out [cols][rows] = in [rows][cols], fp32
@@ -89,6 +93,10 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
 // MoE routing: softmax over E logits per token, top_k by logit (ties -> lower expert).
 hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
                             hipStream_t s);
+// Routing and grouping in one launch (one workgroup): launch_moe_route then launch_moe_group.
+hipError_t launch_moe_route_group(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
+                                  int tile_rows, int32_t* rows, int32_t* expert_end, int32_t* num_tiles,
+                                  int32_t* tile_expert, int32_t* tile_row0, hipStream_t s);
 // Stable grouping of the T*top_k (token, slot) entries by expert, plus the tile schedule
 // for tiles of `tile_rows` rows.  max_tiles = T*top_k/tile_rows + E bounds num_tiles.
 hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,

@@ -133,11 +133,16 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     __shared__ __attribute__((aligned(16))) uint16_t sDwH[BN][8];  // side-term weight factor, fp16 bits
     __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == kWQ4K ? BN : 1][8];  // Q4_K: its low part
     __shared__ int32_t sRows[MOE ? BM : 1];                        // MoE: entry index of each tile row
+    __shared__ int32_t sTok[MOE ? BM : 1];                         // MoE: its token (activation row)
+    __shared__ float sWt[MOE ? BM : 1];                            // MoE: its routing weight * out_scale
 
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
+    // MoE grid: x = column tile, y = entry of the tile schedule, so the row tiles that share a
+    // column of an expert's weights are dispatched N / BN workgroups apart, i.e. to the same XCD
+    // (and its L2) when N / BN is a multiple of 8
     const int m0 = (MOE ? 0 : (int)blockIdx.y) * BM;
-    const int n0 = (MOE ? (int)blockIdx.y : (int)blockIdx.x) * BN;
+    const int n0 = (int)blockIdx.x * BN;
     const int l32 = lane & 31, hi = lane >> 5;
     constexpr float da_scale = 1.0f / S::out_scale;
     static_assert(!is_kquant(WT) || KB == 8, "K-quants stage one 256-element super-block per K step");
@@ -149,13 +154,20 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         if (t < BN) *(uint4*)&sDwH[t][0] = uint4{0, 0, 0, 0};
     }
     if constexpr (MOE) {
-        const int tile = blockIdx.x;
+        const int tile = blockIdx.y;
         if (tile >= moe.num_tiles[0]) return;           // surplus workgroups of the worst-case grid
         const int e = moe.tile_expert[tile];
         const int r0 = moe.tile_row0[tile];
         M = min(BM, moe.expert_end[e] - r0);             // valid rows of this tile
         W += (size_t)e * moe.expert_stride;
-        if (t < BM) sRows[t] = moe.rows[r0 + min(t, M - 1)];
+        if (t < BM) {
+            // per-row routing data read once here, so neither the staging nor the epilogue waits
+            // on a global load or divides per element
+            const int ent = moe.rows[r0 + min(t, M - 1)];
+            sRows[t] = ent;
+            sTok[t] = ent / moe.top_k;
+            sWt[t] = moe.weights[ent] * S::out_scale;
+        }
     }
     __syncthreads();
 
@@ -170,6 +182,8 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) bias[r] = DUMP ? 0 : (int)kMagic;
 
+    const bool wave_has_rows = M - m0 - wm * 32 * TM > 0;   // wave-uniform
+
     // split-K: workgroup z of gridDim.z covers K steps [z*steps/Z, (z+1)*steps/Z) and writes its
     // partial sums to C + z*M*N (the caller adds the partials)
     const int nsteps = nb / KB, Z = (int)gridDim.z, z = (int)blockIdx.z;
@@ -178,7 +192,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     // ---- staging of 32-element blocks, split into the global loads and the LDS writes
     // activation chunk g (4 Q8_1 blocks = 144 B = 9 x 16 B) of staged row sr
     auto load_act = [&](int sr, int g, int kb0, uint32_t* v) {
-        const int am = MOE ? (sRows[sr] / moe.top_k) : min(m0 + sr, M - 1);
+        const int am = MOE ? sTok[sr] : min(m0 + sr, M - 1);
         const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * kQ81Bytes;
 #pragma unroll
         for (int i = 0; i < 9; i++) {
@@ -390,8 +404,8 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         f32x4 edw[4];
         auto epilogue = [&](int b, int u, int i, int j, const i32x16& res) {
             const int lm = wm * 32 * TM + i * 32 + l32;          // local activation row
-            const int nbase = wn * 32 * TN + j * 32 + 4 * hi;    // local weight row of r = 0
             if constexpr (DUMP) {
+                const int nbase = wn * 32 * TN + j * 32 + 4 * hi;    // local weight row of r = 0
                 const int gm = m0 + lm;
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
@@ -400,6 +414,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                         dump[((size_t)gm * N + gn) * nb * S::SUB + (kb0 + b) * S::SUB + (u - b * S::SUB)] = res[r];
                 }
             } else {
+                const int nbase = wn * 32 * TN + j * 32 + 4 * hi;    // local weight row of r = 0
                 if (i == 0) {
 #pragma unroll
                     for (int q = 0; q < 4; q++) edw[q] = *(const f32x4*)&sDw[u][nbase + 8 * q];
@@ -441,15 +456,19 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             }
             return __builtin_amdgcn_mfma_i32_32x32x32_i8(bb, af[i], bias, 0, 0, 0);
         };
-        i32x16 cur = mfma_step(0);
+        // A wave whose rows all lie past the tile's last row (ragged MoE tiles, the last row
+        // tile of a ragged M) skips its MFMAs and epilogues; staging and barriers stay shared.
+        if (wave_has_rows) {
+            i32x16 cur = mfma_step(0);
 #pragma unroll
-        for (int q = 0; q < NQ; q++) {
-            const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
-            const int j = (q / TM) % TN, i = q % TM;
-            i32x16 nxt = bias;
-            if (q + 1 < NQ) nxt = mfma_step(q + 1);
-            epilogue(b, b * SUBN + h, i, j, cur);
-            cur = nxt;
+            for (int q = 0; q < NQ; q++) {
+                const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
+                const int j = (q / TM) % TN, i = q % TM;
+                i32x16 nxt = bias;
+                if (q + 1 < NQ) nxt = mfma_step(q + 1);
+                epilogue(b, b * SUBN + h, i, j, cur);
+                cur = nxt;
+            }
         }
 
         if constexpr (S::side && !DUMP) {
@@ -481,7 +500,6 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         constexpr int kTP = 33;   // padded row pitch (floats) of the [32 m][32 n] transpose
         static_assert(4 * 32 * kTP * 4 <= BM * T::APitch, "transpose scratch fits the activation tile");
         float* tp = (float*)sA + wave * 32 * kTP;
-        constexpr float out_scale = S::out_scale;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -495,10 +513,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 for (int p = 0; p < 16; p++) {
                     const int lm = wm * 32 * TM + i * 32 + 2 * p + hi;   // local activation row
                     if (lm < M && gn < N) {
-                        const int ent = sRows[lm];
-                        const float v = out_scale * tp[(2 * p + hi) * kTP + l32] * moe.weights[ent];
-                        if (moe.scratch) moe.scratch[(size_t)ent * N + gn] = v;
-                        else unsafeAtomicAdd(C + (size_t)(ent / moe.top_k) * N + gn, v);
+                        const float v = tp[(2 * p + hi) * kTP + l32] * sWt[lm];
+                        if (moe.scratch) moe.scratch[(size_t)sRows[lm] * N + gn] = v;
+                        else unsafeAtomicAdd(C + (size_t)sTok[lm] * N + gn, v);
                     }
                 }
                 __builtin_amdgcn_wave_barrier();
@@ -538,11 +555,12 @@ using TileS = Tile<64, 64, 8, 1, 1, 3>;     // 32 x 32 per wave, 4x the workgrou
 using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, more resident workgroups
 using TileT = Tile<32, 128, 8, 1, 1, 3>;    // skinny: M <= 32, the four waves side by side along N
 using TileP = Tile<128, 128, 4, 2, 2, 2, true>;  // 128 x 128, K step 4, next step's loads prefetched
+using TileW = Tile<64, 128, 8, 1, 2, 3>;    // 64 x 128: 32 x 64 per wave, 64-row granularity
 
 static thread_local int g_mmq_config = 0;  // 0 = automatic; set per host thread
 
 int mmq_set_config(int c) {
-    if (c < 0 || c > 6) return -1;
+    if (c < 0 || c > 7) return -1;
     g_mmq_config = c;
     return 0;
 }
@@ -741,6 +759,7 @@ static int split_cfg(int cfg, int wtype, int M, int N, int K) {
         case 3: return split_for<TileS>(wtype, M, N, K);
         case 5: return split_for<TileT>(wtype, M, N, K);
         case 6: return split_for<TileP>(wtype, M, N, K);
+        case 7: return split_for<TileW>(wtype, M, N, K);
         default: return split_for<TileK4>(wtype, M, N, K);
     }
 }
@@ -760,6 +779,7 @@ static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, con
         case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
         case 5: return launch_t<TileT, DUMP, false>(wtype, afmt, grid(32, 128), W, A, C, dump, M, N, nb, mt, s);
         case 6: return launch_t<TileP, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 7: return launch_t<TileW, DUMP, false>(wtype, afmt, grid(64, 128), W, A, C, dump, M, N, nb, mt, s);
         default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
     }
 }
@@ -798,9 +818,12 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
 // the experts average 384+ rows, then for the nibble types 128 x 128 (measured on MI355X, Q4_0,
 // N = 4096, K = 14336, 2048 tokens top-2 of 8 experts: 989 vs 1184 us; 512 tokens: 486 vs 396 us
 // the other way).
+#ifndef KSQ_MOE_TILE128_MIN_ROWS
+#define KSQ_MOE_TILE128_MIN_ROWS 100000
+#endif
 int mmq_moe_tile_rows(int wtype, int T, int E, int top_k) {
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
-    return (nib && (long long)T * top_k >= 384ll * E) ? 128 : 64;
+    return (nib && (long long)T * top_k >= (long long)KSQ_MOE_TILE128_MIN_ROWS * E) ? 128 : 64;
 }
 
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
@@ -819,11 +842,18 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     mt.expert_stride = (size_t)N * nb * block_bytes(wtype);
     note_engine(tile_rows == TileL::BM ? KSQ_ENG_MOE_TILE128 : KSQ_ENG_MOE_TILE64);
     if (tile_rows == TileL::BM) {
-        const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileL::BN - 1) / TileL::BN));
+        const dim3 grid((unsigned)((N + TileL::BN - 1) / TileL::BN), (unsigned)max_tiles);
         return launch_t<TileL, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
     }
-    if (tile_rows != TileS::BM) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)max_tiles, (unsigned)((N + TileS::BN - 1) / TileS::BN));
+    if (tile_rows != 64) return hipErrorInvalidValue;
+#ifndef KSQ_MOE_TILEW
+#define KSQ_MOE_TILEW 1
+#endif
+    if (KSQ_MOE_TILEW) {
+        const dim3 grid((unsigned)((N + TileW::BN - 1) / TileW::BN), (unsigned)max_tiles);
+        return launch_t<TileW, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
+    }
+    const dim3 grid((unsigned)((N + TileS::BN - 1) / TileS::BN), (unsigned)max_tiles);
     return launch_t<TileS, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
 }
 

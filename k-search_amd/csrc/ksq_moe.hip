@@ -17,10 +17,9 @@
 
 namespace ksq {
 
-__global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
-                                 int32_t* __restrict__ ids, float* __restrict__ w) {
-    const int t = blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= T) return;
+// Softmax over token t's E logits, then the top_k experts by logit (ties -> lower index).
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int top_k, int renorm,
+                                            int32_t* __restrict__ ids, float* __restrict__ w) {
     const float* l = logits + (size_t)t * E;
     float mx = l[0];
     for (int e = 1; e < E; e++) mx = (l[e] > mx) ? l[e] : mx;
@@ -45,6 +44,12 @@ __global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E,
         for (int s = 0; s < top_k; s++) w[(size_t)t * top_k + s] /= wsum;
 }
 
+__global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
+                                 int32_t* __restrict__ ids, float* __restrict__ w) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < T) route_token(logits, t, E, top_k, renorm, ids, w);
+}
+
 hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
                             hipStream_t s) {
     if (T <= 0) return hipSuccess;
@@ -59,12 +64,10 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int re
 constexpr int kGroupThreads = 1024;
 constexpr int kGroupWaves = kGroupThreads / 64;
 
-__global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
-                                                                  int tile_rows, int32_t* __restrict__ rows,
-                                                                  int32_t* __restrict__ expert_end,
-                                                                  int32_t* __restrict__ num_tiles,
-                                                                  int32_t* __restrict__ tile_expert,
-                                                                  int32_t* __restrict__ tile_row0) {
+__device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, int total, int E, int tile_rows,
+                                              int32_t* __restrict__ rows, int32_t* __restrict__ expert_end,
+                                              int32_t* __restrict__ num_tiles, int32_t* __restrict__ tile_expert,
+                                              int32_t* __restrict__ tile_row0) {
     __shared__ int32_t count[256];
     __shared__ int32_t cursor[256];
     __shared__ int32_t wcnt[kGroupWaves][256];
@@ -118,11 +121,39 @@ __global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t*
     }
 }
 
+__global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
+                                                                  int tile_rows, int32_t* __restrict__ rows,
+                                                                  int32_t* __restrict__ expert_end,
+                                                                  int32_t* __restrict__ num_tiles,
+                                                                  int32_t* __restrict__ tile_expert,
+                                                                  int32_t* __restrict__ tile_row0) {
+    group_entries(ids, total, E, tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
+}
+
+// Routing and grouping in one workgroup: the threads route the tokens (each its share), the
+// barrier makes the ids visible to the whole workgroup, then the same grouping as above.
+__global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(
+    const float* __restrict__ logits, int T, int E, int top_k, int renorm, int32_t* __restrict__ ids,
+    float* __restrict__ w, int tile_rows, int32_t* __restrict__ rows, int32_t* __restrict__ expert_end,
+    int32_t* __restrict__ num_tiles, int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_row0) {
+    for (int t = threadIdx.x; t < T; t += kGroupThreads) route_token(logits, t, E, top_k, renorm, ids, w);
+    __syncthreads();
+    group_entries(ids, T * top_k, E, tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
+}
+
 hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
                             int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
                             hipStream_t s) {
     hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, ids, T * top_k, E, tile_rows, rows,
                        expert_end, num_tiles, tile_expert, tile_row0);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_route_group(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
+                                  int tile_rows, int32_t* rows, int32_t* expert_end, int32_t* num_tiles,
+                                  int32_t* tile_expert, int32_t* tile_row0, hipStream_t s) {
+    hipLaunchKernelGGL(moe_route_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, logits, T, E, top_k, renorm, ids, w,
+                       tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
     return hipGetLastError();
 }
 

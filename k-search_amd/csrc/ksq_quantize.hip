@@ -32,13 +32,13 @@ __device__ __forceinline__ void wave_lds_sync() {
 // operator's rules), both 36-byte blocks of 9 dwords.
 constexpr int kQF81 = 0, kQF8S = 1;
 
+// The 64 blocks of wave w of workgroup `wg`.
 template <int FMT>
-__global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float* __restrict__ x,
-                                                                     uint8_t* __restrict__ y, int64_t nblocks) {
-    __shared__ float stage_all[kQWaves][64 * kQPitch];
+__device__ __forceinline__ void quantize_wave(const float* __restrict__ x, uint8_t* __restrict__ y, int64_t nblocks,
+                                              int64_t wg, float* stage_all) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    float* stage = stage_all[w];
-    const int64_t blk0 = ((int64_t)blockIdx.x * kQWaves + w) * 64;
+    float* stage = stage_all + w * 64 * kQPitch;
+    const int64_t blk0 = (wg * kQWaves + w) * 64;
     if (blk0 >= nblocks) return;
     const int nblk = (int)((nblocks - blk0) < 64 ? (nblocks - blk0) : 64);
 
@@ -87,6 +87,36 @@ __global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float
     }
 }
 
+template <int FMT>
+__global__ __launch_bounds__(64 * kQWaves) void quantize_q8_1_kernel(const float* __restrict__ x,
+                                                                     uint8_t* __restrict__ y, int64_t nblocks) {
+    __shared__ float stage_all[kQWaves * 64 * kQPitch];
+    quantize_wave<FMT>(x, y, nblocks, blockIdx.x, stage_all);
+}
+
+// The quantiser's workgroups plus zero-filling ones: workgroups from qgrid on clear 32 KiB each
+// of `zero` (n4 16-byte groups), so an output that is accumulated into later needs no launch
+// of its own.
+constexpr int kZeroBytesPerWG = 32768;
+
+__global__ __launch_bounds__(64 * kQWaves) void quantize_zero_kernel(const float* __restrict__ x,
+                                                                     uint8_t* __restrict__ y, int64_t nblocks,
+                                                                     int64_t qgrid, float* __restrict__ zero,
+                                                                     int64_t n4) {
+    __shared__ float stage_all[kQWaves * 64 * kQPitch];
+    if ((int64_t)blockIdx.x < qgrid) {
+        quantize_wave<kQF81>(x, y, nblocks, blockIdx.x, stage_all);
+        return;
+    }
+    const int64_t base = ((int64_t)blockIdx.x - qgrid) * (kZeroBytesPerWG / 16);
+    f32x4* z = (f32x4*)zero;
+#pragma unroll
+    for (int i = 0; i < kZeroBytesPerWG / 16 / (64 * kQWaves); i++) {
+        const int64_t k = base + i * (64 * kQWaves) + threadIdx.x;
+        if (k < n4) z[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
     const int64_t nblocks = rows * (int64_t)(K / 32);
     if (nblocks == 0) return hipSuccess;
@@ -102,6 +132,18 @@ hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, i
 
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
     return launch_quantize(kAQ81, x, y, rows, K, s);
+}
+
+hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, int K, float* zero, int64_t nzero,
+                                     hipStream_t s) {
+    const int64_t nblocks = rows * (int64_t)(K / 32);
+    const int64_t qgrid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
+    const int64_t n4 = nzero / 4;
+    const int64_t zgrid = (n4 * 16 + kZeroBytesPerWG - 1) / kZeroBytesPerWG;
+    if (qgrid + zgrid == 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_zero_kernel, dim3((unsigned)(qgrid + zgrid)), dim3(64 * kQWaves), 0, s, x, y, nblocks,
+                       qgrid, zero, n4);
+    return hipGetLastError();
 }
 
 // ---- the reference's other Q8_1 quantisers (ksq_quantize_q8_1_variant) -----------------

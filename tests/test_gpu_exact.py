@@ -210,7 +210,7 @@ def _engine_cases():
                       {"quantize", "gemv_row" if wt == 3 else "gemv_mr"} if kq else {"gemv_mr_fq"}, 0))
         # MFMA GEMM, every tile configuration (K-quants take the automatic tile for 4 and 6)
         # (the K-step-4 tiles split this 4-workgroup grid in two along K)
-        for cfg in range(1, 7):
+        for cfg in range(1, 8):
             eng = {f"mmq{cfg}", "splitk"} if cfg in (4, 6) else {f"mmq{cfg}"}
             cases.append((f"mmq_cfg{cfg}_w{wt}", wt, 150, 136, 512, 1, 2, cfg, {"mmq3"} if kq and cfg in (4, 6) else eng,
                           0))
@@ -287,11 +287,13 @@ def test_engine_table_covers_every_engine():
 
 # ------------------------------------------------------------------ MoE engines
 @pytest.mark.parametrize("wtype", LEGACY)
-@pytest.mark.parametrize("T,E,top_k,tile", [(96, 4, 2, 64), (96, 4, 3, 64), (800, 4, 2, 128)])
-def test_exact_moe_engines(dev, wtype, T, E, top_k, tile):
+@pytest.mark.parametrize("T,E,top_k,tile,skew", [(96, 4, 2, 64, False), (96, 4, 3, 64, False),
+                                                 (800, 4, 2, 64, False), (300, 4, 2, 64, True)])
+def test_exact_moe_engines(dev, wtype, T, E, top_k, tile, skew):
     """Grouped GEMM in 64- and 128-row tiles, and the top_k > 2 combine, per block type; with
     top_k = 3 one slot of one token carries an out-of-range expert id, which contributes
-    nothing."""
+    nothing.  Skewed routing (expert shares 0.55 / 0.3 / 0.1 / 0.05) leaves 128-row tiles whose
+    waves hold 0, 1 or 2 of their 32-row sub-tiles."""
     import torch
     from ksq import ops, refcheck
     from oracle import oracle
@@ -301,7 +303,8 @@ def test_exact_moe_engines(dev, wtype, T, E, top_k, tile):
     g = np.random.default_rng(4500 + 10 * wtype + top_k)
     w = np.stack([refcheck.unit_weights(wtype, g, N, K) for _ in range(E)])
     x = refcheck.unit_activations(g, T, K, qmax=QMAX_F32[wtype], onehot=refcheck.onehot_pattern(T, K // 32))
-    ids = np.stack([g.choice(E, size=top_k, replace=False) for _ in range(T)]).astype(np.int32)
+    p = np.array([0.55, 0.3, 0.1, 0.05]) if skew else None
+    ids = np.stack([g.choice(E, size=top_k, replace=False, p=p) for _ in range(T)]).astype(np.int32)
     if top_k == 3:
         ids[7, 1] = E
     wts = (2.0 ** -g.integers(0, 3, size=(T, top_k))).astype(np.float32)

@@ -367,7 +367,7 @@ def test_moe_config4_sampled(dev, oracle):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
 @pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_mfma_tile_configs(dev, oracle, cfg, wtype):
     """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile)."""
@@ -419,7 +419,7 @@ def test_skinny_q8s_native(dev, oracle, M):
 
 ENGINE_FAMILIES = {"decode": {"gemv_row", "gemv_row_fq", "gemv_direct", "gemv_direct_fq", "gemv_mr", "gemv_mr_fq",
                                "gemv_kq"},
-                   "skinny": {"skinny"}, "mmq": {f"mmq{c}" for c in range(1, 7)}}
+                   "skinny": {"skinny"}, "mmq": {f"mmq{c}" for c in range(1, 8)}}
 
 
 def _family(engines):
