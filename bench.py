@@ -9,11 +9,15 @@ on fp32 activations [2048, 4096] -> fp32 [2048, 4096], i.e. quantize_q8_1 plus
 the int8-MFMA GEMM.  Inputs are seeded synthetic tensors resident in HBM before
 timing; weights and activations rotate over several copies so successive steps
 do not re-read one buffer from the 256 MB MALL.  Launch sequences are captured
-in HIP graphs and replayed, so host-side launch cost (ctypes) is not timed.  The W
-untimed warm-up steps (default 256: two eager, the rest replays of the captured
-step graph) bring the GPU clocks to their steady state before the K timed steps.
+in HIP graphs and replayed, so host-side launch cost (ctypes) is not timed.
+
+Order: the other BASELINE configs and the GEMV are timed first (which also brings the GPU
+clocks to their steady state), then the W untimed warm-up steps (the first two eager, the
+rest replays of the captured step graph), then the K timed steps, then per-step samples
+for the median and p10 / p90, then the CPU baselines.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+    python bench.py --only NAME --steps K --warmup W     (profiling: one kernel sequence, eager)
 
 Prints ONE JSON line on stdout (progress goes to stderr).
 """
@@ -21,11 +25,12 @@ from __future__ import annotations
 
 import argparse
 import json
-
-import numpy as np
 import os
+import platform
 import sys
 import time
+
+import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path[:0] = [ROOT, os.path.join(ROOT, "k-search_amd")]
@@ -33,11 +38,23 @@ sys.path[:0] = [ROOT, os.path.join(ROOT, "k-search_amd")]
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 
-# HBM bytes per launch from two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, KiB per
-# dispatch, mean of 6) over `bench.py --only gemm|gemv`, scaled by the factors a plain
-# 256 MiB copy gives the same counters (reads x2.0, writes x1.0); summaries in profiles/.
-TRAFFIC_MMQ_Q4_0_M2048 = int((41715.8 * 2.0 + 32941.8 * 1.0) * 1024)
-TRAFFIC_GEMV_Q4_0_M1 = int((4642.2 * 2.0 + 32.0 * 1.0) * 1024)
+# HBM bytes per launch of the dominant kernels, from two rocprofv3 --pmc passes (FETCH_SIZE,
+# WRITE_SIZE, KiB per dispatch) over `bench.py --only ...`, scaled by the factors a plain 256 MiB
+# copy gives the same counters (reads x2.0, writes x1.0; profiles/copy_calibration.md).  Each
+# figure names the committed summary it comes from.
+TRAFFIC = {
+    "gemm": (int((41688.8 * 2.0 + 33052.6) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
+    "gemv": (int((4641.9 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
+    "q8_0_M1": (int((8737.5 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q8_0_M8": (int((8894.7 * 2.0 + 128.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q8_0_M32": (int(((9337.1 + 2068.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q4_K_M128": (int((18492.5 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "q6_K_M128": (int((26582.8 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "moe_q4_0_T512_E8_top2": (int(((166837.1 + 4137.5 + 19.0) * 2.0 + 57344.0 + 30976.0 + 12.2) * 1024),
+                              "profiles/moe_q4_0_t512_e8_top2.md"),
+}
+
+ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe")
 
 
 def log(msg: str) -> None:
@@ -56,7 +73,8 @@ def capture(fn, n: int):
 
 
 def time_graph(g, replays: int) -> float:
-    """Milliseconds for `replays` replays of graph g (HIP events, torch's current stream)."""
+    """Milliseconds for `replays` replays of graph g (HIP events on torch's current stream, which
+    the graph's kernels run on)."""
     import torch
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -68,98 +86,285 @@ def time_graph(g, replays: int) -> float:
     return s.elapsed_time(e)
 
 
-def cpu_baseline(M: int, N: int, K: int, budget_s: float = 10.0) -> dict:
-    """The reference CPU path (quantize_row_q8_1_ref + gemm_w4a8_reference's loop and
-    accumulation order, restated in oracle/ksq_oracle.c) on the box's host cores, over
-    a bounded sample of the workload's activation rows."""
-    from ksq import synth
-    from oracle import oracle
-    threads = max(1, min(16, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()))
-    g = synth.rng(1)
-    w = synth.weights(0, g, N, K)
-    # calibrate on a few rows, then size the sample to ~budget_s
-    probe = max(threads, 8)
-    x = synth.activations(g, probe, K)
-    t0 = time.perf_counter()
-    oracle.gemm(0, oracle.quantize_q8_1(x), w, probe, N, K, nthreads=threads)
-    per_row = (time.perf_counter() - t0) / probe
-    rows = int(max(probe, min(M, budget_s / max(per_row, 1e-9))))
-    x = synth.activations(g, rows, K)
-    t0 = time.perf_counter()
-    a = oracle.quantize_q8_1(x)
-    oracle.gemm(0, a, w, rows, N, K, nthreads=threads)
-    dt = time.perf_counter() - t0
-    return {"value": round(2.0 * rows * N * K / dt / 1e12, 6), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {M} activation rows x N=K={K}: quantize_row_q8_1_ref + gemm_w4a8_reference "
-                      f"loop order (oracle/ksq_oracle.c, gcc -O2, OpenMP over outputs), {dt:.2f} s"}
+def replay_samples(g, n: int) -> list[float]:
+    """Milliseconds of each of n separate replays of g (an event pair around each)."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    torch.cuda.synchronize()
+    for s, e in ev:
+        s.record()
+        g.replay()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in ev]
 
 
-def graph_ms(fn, n: int, reps: int) -> float:
-    """Average ms per fn(i) call over `reps` replays of a graph of n calls.  One eager call
-    first, so the library's workspace pool is sized before capture (no hipMalloc inside)."""
+def dist(samples_ms, per: int = 1) -> dict:
+    a = np.asarray(samples_ms, dtype=np.float64) / per
+    return {"median_ms": round(float(np.median(a)), 6), "p10_ms": round(float(np.percentile(a, 10)), 6),
+            "p90_ms": round(float(np.percentile(a, 90)), 6), "samples": int(a.size)}
+
+
+def graph_stats(fn, n: int, reps: int) -> tuple[float, dict]:
+    """(average ms per fn(i) call over `reps` replays of a graph of n calls, per-call distribution
+    over the replays).  One eager call first, so the library's workspace pool is sized before
+    capture."""
     import torch
     fn(0)
     torch.cuda.synchronize()
     g = capture(fn, n)
     g.replay()
-    return time_graph(g, reps) / (reps * n)
+    ms = time_graph(g, reps) / (reps * n)
+    d = dist(replay_samples(g, max(8, reps)), per=n)
+    del g
+    return ms, d
 
 
-def hbm_entry(bytes_, ms, ops=None):
+def hbm_entry(bytes_, ms, d, ops=None, name=None):
     gbs = bytes_ / (ms * 1e-3) / 1e9
-    d = {"avg_ms": round(ms, 6), "algorithmic_bytes": int(bytes_), "GB/s": round(gbs, 1),
+    e = {"avg_ms": round(ms, 6), **d, "algorithmic_bytes": int(bytes_), "GB/s": round(gbs, 1),
          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    if name in TRAFFIC:
+        e["roofline"]["traffic"], e["roofline"]["traffic_source"] = TRAFFIC[name]
     if ops is not None:
-        d["TOPS"] = round(ops / (ms * 1e-3) / 1e12, 3)
-    return d
+        e["TOPS"] = round(ops / (ms * 1e-3) / 1e12, 3)
+    return e
 
 
-def other_configs(g, dev, reps: int) -> dict:
-    """BASELINE configs 1, 3 and 4, each on rotating weight copies (> 256 MB MALL in total)."""
-    import torch
-    import ksq
-    from ksq import ops, synth
-    out = {}
-    # config 1: Q8_0 x Q8_1, M in {1, 8, 32}, N = K = 4096
-    N, K = 4096, 4096
-    w = synth.weights(ksq.W_Q8_0, g, N, K)
-    copies = 32
-    Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
-    for M in (1, 8, 32):
-        aq = ops.quantize_q8_1(torch.from_numpy(synth.activations(g, M, K)).to(dev))
-        o = torch.empty((M, N), dtype=torch.float32, device=dev)
-        ms = graph_ms(lambda i: ops.gemm(ksq.W_Q8_0, ksq.A_Q8_1, Wc[i % copies], aq, M, N, K, out=o), copies, reps)
-        out[f"q8_0_M{M}"] = hbm_entry(N * (K // 32) * 34 + M * (K // 32) * 36 + M * N * 4, ms, 2.0 * M * N * K)
-    del Wc
-    # config 3: K-quants at M = 128, N = 14336, K = 4096
-    M, N, K = 128, 14336, 4096
-    aq = ops.quantize_q8_1(torch.from_numpy(synth.activations(g, M, K)).to(dev))
-    o = torch.empty((M, N), dtype=torch.float32, device=dev)
-    for wt, name, sb in ((ksq.W_Q4_K, "q4_K", 144), (ksq.W_Q6_K, "q6_K", 210)):
+# ---------------------------------------------------------------- workloads (GPU)
+class Workloads:
+    """Seeded inputs of every BASELINE config on the device, and one call of each."""
+
+    def __init__(self, dev):
+        import torch
+
+        import ksq
+        from ksq import ops, synth
+        self.torch, self.ksq, self.ops, self.synth, self.dev = torch, ksq, ops, synth, dev
+        self.g = synth.rng(2024)
+
+    def t(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a)).to(self.dev)
+
+    def config2(self, copies: int = 8):
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        M, N, K = 2048, 4096, 4096
+        w_np = synth.weights(ksq.W_Q4_0, g, N, K)
+        x_np = synth.activations(g, M, K)
+        W = [self.t(w_np) for _ in range(copies)]
+        X = [self.t(x_np) for _ in range(copies)]
+        out = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        ws = self.torch.empty(ops.workspace_size(0, 0, M, N, K), dtype=self.torch.uint8, device=self.dev)
+        AQ = [ops.quantize_q8_1(X[i]) for i in range(copies)]
+        self.torch.cuda.synchronize()
+
+        def step(i):
+            ops.gemm(ksq.W_Q4_0, ksq.A_F32, W[i % copies], X[i % copies], M, N, K, out=out, workspace=ws)
+
+        def gemm_only(i):
+            ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, W[i % copies], AQ[i % copies], M, N, K, out=out)
+
+        return (M, N, K), step, gemm_only
+
+    def gemv(self, copies: int = 64):
+        """Config 0: 64 weight copies (604 MB, > 2x the MALL)."""
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        M, N, K = 1, 4096, 4096
+        wv = synth.weights(ksq.W_Q4_0, g, N, K)
+        W = [self.t(wv) for _ in range(copies)]
+        x = self.t(synth.activations(g, M, K))
+        aq = ops.quantize_q8_1(x)
+        out = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        ws = self.torch.empty(max(1, ops.workspace_size(0, 0, M, N, K)), dtype=self.torch.uint8, device=self.dev)
+
+        def q81(i):
+            ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, W[i % copies], aq, M, N, K, out=out)
+
+        def f32(i):
+            ops.gemm(ksq.W_Q4_0, ksq.A_F32, W[i % copies], x, M, N, K, out=out, workspace=ws)
+
+        return (M, N, K), q81, f32, copies
+
+    def read(self, copies: int = 64):
+        """A plain streaming read of 9,437,184 bytes (the config-0 weight matrix's size) by the
+        library's calibration read kernel, rotating over 64 copies (604 MB)."""
+        B = [self.torch.ones(9437184, dtype=self.torch.uint8, device=self.dev) for _ in range(copies)]
+        r = self.ops.stream_read(B[0])
+
+        def rd(i):
+            self.ops.stream_read(B[i % copies], out=r)
+
+        return rd, copies
+
+    def q8_0(self, M: int, copies: int = 32):
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        N, K = 4096, 4096
+        w = synth.weights(ksq.W_Q8_0, g, N, K)
+        W = [self.t(w) for _ in range(copies)]
+        aq = ops.quantize_q8_1(self.t(synth.activations(g, M, K)))
+        o = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        return (M, N, K), (lambda i: ops.gemm(ksq.W_Q8_0, ksq.A_Q8_1, W[i % copies], aq, M, N, K, out=o)), copies
+
+    def kquant(self, wt: int, copies: int = 8):
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        M, N, K = 128, 14336, 4096
         w = synth.weights(wt, g, N, K)
-        copies = 8
-        Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
-        ms = graph_ms(lambda i: ops.gemm(wt, ksq.A_Q8_1, Wc[i % copies], aq, M, N, K, out=o), copies, reps)
-        out[f"{name}_M128"] = hbm_entry(N * (K // 256) * sb + M * (K // 32) * 36 + M * N * 4, ms, 2.0 * M * N * K)
-        del Wc
-    # config 4: MoE, 512 tokens, 8 experts of 4096 -> 14336 Q4_0, top-2 (whole call: quantize,
-    # route, group, zero-fill, grouped GEMM)
-    T, E, N, K, k = 512, 8, 14336, 4096, 2
-    w = np.stack([synth.weights(ksq.W_Q4_0, g, N, K) for _ in range(E)])
-    copies = 2
-    Wc = [torch.from_numpy(w).to(dev) for _ in range(copies)]
-    x = torch.from_numpy(synth.activations(g, T, K)).to(dev)
-    lg = torch.from_numpy(synth.router_logits(g, T, E)).to(dev)
-    o = torch.empty((T, N), dtype=torch.float32, device=dev)
-    ws = torch.empty(ops.moe_workspace_size(0, T, N, K, E, k), dtype=torch.uint8, device=dev)
-    ms = graph_ms(lambda i: ops.moe_gemm(ksq.W_Q4_0, Wc[i % copies], x, lg, T, N, K, E, k, out=o, workspace=ws),
-                  copies, reps)
+        W = [self.t(w) for _ in range(copies)]
+        aq = ops.quantize_q8_1(self.t(synth.activations(g, M, K)))
+        o = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        return (M, N, K), (lambda i: ops.gemm(wt, ksq.A_Q8_1, W[i % copies], aq, M, N, K, out=o)), copies
+
+    def moe(self, copies: int = 2):
+        """Config 4: 512 tokens, 8 experts of 4096 -> 14336 Q4_0, top-2 (the whole call: quantise,
+        route, group, grouped GEMM, weighted scatter-add)."""
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        T, E, N, K, k = 512, 8, 14336, 4096, 2
+        w = np.stack([synth.weights(ksq.W_Q4_0, g, N, K) for _ in range(E)])
+        W = [self.t(w) for _ in range(copies)]
+        x = self.t(synth.activations(g, T, K))
+        lg = self.t(synth.router_logits(g, T, E))
+        o = self.torch.empty((T, N), dtype=self.torch.float32, device=self.dev)
+        ws = self.torch.empty(ops.moe_workspace_size(0, T, N, K, E, k), dtype=self.torch.uint8, device=self.dev)
+        fn = lambda i: ops.moe_gemm(ksq.W_Q4_0, W[i % copies], x, lg, T, N, K, E, k, out=o, workspace=ws)  # noqa: E731
+        return (T, E, N, K, k), fn, copies
+
+
+def other_configs(wl: Workloads, reps: int = 4) -> dict:
+    """BASELINE configs 1, 3 and 4, each on rotating weight copies (> 256 MB MALL in total)."""
+    out = {}
+    for M in (1, 8, 32):
+        (M, N, K), fn, copies = wl.q8_0(M)
+        ms, d = graph_stats(fn, copies, reps)
+        out[f"q8_0_M{M}"] = hbm_entry(N * (K // 32) * 34 + M * (K // 32) * 36 + M * N * 4, ms, d, 2.0 * M * N * K,
+                                      f"q8_0_M{M}")
+        del fn
+    for wt, name, sb in ((wl.ksq.W_Q4_K, "q4_K", 144), (wl.ksq.W_Q6_K, "q6_K", 210)):
+        (M, N, K), fn, copies = wl.kquant(wt)
+        ms, d = graph_stats(fn, copies, reps)
+        out[f"{name}_M128"] = hbm_entry(N * (K // 256) * sb + M * (K // 32) * 36 + M * N * 4, ms, d, 2.0 * M * N * K,
+                                        f"{name}_M128")
+        del fn
+    (T, E, N, K, k), fn, copies = wl.moe()
+    ms, d = graph_stats(fn, copies, reps)
     moe_bytes = E * N * (K // 32) * 18 + T * K * 4 + T * E * 4 + T * N * 4
-    out["moe_q4_0_T512_E8_top2"] = hbm_entry(moe_bytes, ms, 2.0 * T * k * N * K)
-    del Wc
-    torch.cuda.empty_cache()
+    out["moe_q4_0_T512_E8_top2"] = hbm_entry(moe_bytes, ms, d, 2.0 * T * k * N * K, "moe_q4_0_T512_E8_top2")
+    del fn
+    wl.torch.cuda.empty_cache()
     return out
+
+
+# ---------------------------------------------------------------- CPU baselines
+def cpu_info() -> dict:
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"cpu_model": model, "nproc": os.cpu_count(), "affinity_cpus": aff}
+
+
+def _timed(fn) -> float:
+    t0 = time.perf_counter()
+    fn()
+    return time.perf_counter() - t0
+
+
+def cpu_baselines(budget_s: float = 1.2) -> dict:
+    """The reference CPU path restated in oracle/ksq_oracle.c (quantize_row_q8_1_ref plus the
+    gemm_w4a8_reference / gemm_w8a8_reference loop and accumulation order, the same loops over
+    K-quant blocks, and for MoE the same dense loops on each expert's gathered rows), timed on
+    the host cores of this box, single-threaded and with OpenMP over outputs on every core of the
+    box's CPU share (at most 16 threads: the share of one GPU on these boxes).  Each measurement
+    runs a bounded sample of the workload's activation rows (stated), sized to about budget_s."""
+    from ksq import synth
+    from oracle import oracle
+    info = cpu_info()
+    allc = max(1, min(16, info["affinity_cpus"] or 1))
+    g = synth.rng(1)
+    res = {"cpu": info, "threads_all": allc, "configs": {}}
+
+    def run(name, M, N, K, wtype, w, ops_per_row):
+        x = synth.activations(g, 8, K)
+        a = oracle.quantize_q8_1(x)
+        per_row = _timed(lambda: oracle.gemm(wtype, a, w, 8, N, K, nthreads=1)) / 8
+        entry = {"M": M, "N": N, "K": K}
+        for mode, nt in (("single_thread", 1), ("all_cores", allc)):
+            rows = int(max(1, min(M, budget_s / max(per_row / nt, 1e-9))))
+            xs = synth.activations(g, rows, K)
+            dt = _timed(lambda: oracle.gemm(wtype, oracle.quantize_q8_1(xs), w, rows, N, K, nthreads=nt))
+            entry[mode] = {"TOPS": round(ops_per_row * rows / dt / 1e12, 6), "threads": nt,
+                           "ms_per_row": round(dt / rows * 1e3, 4), "rows_timed": rows,
+                           "ms_full_call_est": round(dt / rows * M * 1e3, 3)}
+        res["configs"][name] = entry
+
+    w = synth.weights(0, g, 4096, 4096)
+    run("c0_q4_0_M1", 1, 4096, 4096, 0, w, 2.0 * 4096 * 4096)
+    run("c2_q4_0_M2048", 2048, 4096, 4096, 0, w, 2.0 * 4096 * 4096)
+    w = synth.weights(1, g, 4096, 4096)
+    for M in (1, 8, 32):
+        run(f"c1_q8_0_M{M}", M, 4096, 4096, 1, w, 2.0 * 4096 * 4096)
+    for wt, name in ((2, "c3_q4_K_M128"), (3, "c3_q6_K_M128")):
+        run(name, 128, 14336, 4096, wt, synth.weights(wt, g, 14336, 4096), 2.0 * 14336 * 4096)
+    # MoE: route, gather each expert's rows, the dense reference loop per expert
+    T, E, N, K, k = 512, 8, 14336, 4096, 2
+    we = [synth.weights(0, g, N, K) for _ in range(E)]
+    lg = synth.router_logits(g, T, E)
+    ids, _ = oracle.moe_route(lg, k)
+    entry = {"T": T, "E": E, "N": N, "K": K, "top_k": k}
+    for mode, nt in (("single_thread", 1), ("all_cores", allc)):
+        t_rows = 8 if nt == 1 else 64
+        xs = synth.activations(g, t_rows, K)
+        sub = ids[:t_rows]
+
+        def moe_call():
+            a = oracle.quantize_q8_1(xs)
+            for e in range(E):
+                rows = np.nonzero((sub == e).any(axis=1))[0]
+                if len(rows):
+                    oracle.gemm(0, a[rows], we[e], len(rows), N, K, nthreads=nt)
+        dt = _timed(moe_call)
+        entries = int((sub >= 0).sum())
+        entry[mode] = {"TOPS": round(2.0 * entries * N * K / dt / 1e12, 6), "threads": nt, "tokens_timed": t_rows,
+                       "ms_full_call_est": round(dt / t_rows * T * 1e3, 3)}
+    res["configs"]["c4_moe_T512_E8_top2"] = entry
+    return res
+
+
+# ---------------------------------------------------------------- profiling mode
+def only(args, dev) -> int:
+    """Launch just one kernel sequence --warmup + --steps times, eagerly (for rocprofv3)."""
+    import torch
+    wl = Workloads(dev)
+    if args.only == "copy":
+        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain copy of 256 MiB
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        fn = lambda i: dst.copy_(src)  # noqa: E731
+    elif args.only == "read":
+        fn, _ = wl.read()
+    elif args.only in ("gemm", "step"):
+        _, step, gemm_only = wl.config2()
+        fn = gemm_only if args.only == "gemm" else step
+    elif args.only in ("gemv", "gemv_f32"):
+        _, q81, f32, _ = wl.gemv()
+        fn = q81 if args.only == "gemv" else f32
+    elif args.only.startswith("q8_0_m"):
+        _, fn, _ = wl.q8_0(int(args.only[6:]))
+    elif args.only in ("q4_k", "q6_k"):
+        _, fn, _ = wl.kquant(wl.ksq.W_Q4_K if args.only == "q4_k" else wl.ksq.W_Q6_K)
+    else:
+        _, fn, _ = wl.moe()
+    for i in range(args.warmup + args.steps):
+        fn(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"only": args.only, "launches": args.warmup + args.steps}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -168,10 +373,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=64)
     ap.add_argument("--warmup", type=int, default=256,
                     help="untimed steps before the timed ones (the first two eager, the rest as replays of "
-                         "the captured step graph): brings the GPU clocks to their steady state")
+                         "the captured step graph)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemv", "step", "copy"],
-                    help="profiling mode: launch just that kernel sequence --steps times, eagerly, and exit")
+    ap.add_argument("--only", choices=ONLY, help="profiling mode: launch just that kernel sequence, eagerly, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build runs the quantized matmul path on a single "
@@ -179,47 +383,34 @@ def main() -> int:
         return 2
 
     import torch
-
-    import ksq
-    from ksq import ops, synth
-
     dev = torch.device("cuda:0")
-    if args.only == "copy":
-        # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain copy of 256 MiB
-        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(args.warmup + args.steps):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"only": "copy", "bytes": src.numel() * 4, "launches": args.warmup + args.steps}))
-        return 0
-    M, N, K = 2048, 4096, 4096
-    copies = 8
-    g = synth.rng(2024)
-    log(f"bench: inputs M={M} N={N} K={K}, {copies} rotating copies")
-    w_np = synth.weights(ksq.W_Q4_0, g, N, K)
-    x_np = synth.activations(g, M, K)
-    W = [torch.from_numpy(w_np).to(dev) for _ in range(copies)]
-    X = [torch.from_numpy(x_np).to(dev) for _ in range(copies)]
-    out = torch.empty((M, N), dtype=torch.float32, device=dev)
-    ws = torch.empty(ops.workspace_size(0, 0, M, N, K), dtype=torch.uint8, device=dev)
-    AQ = [ops.quantize_q8_1(X[i]) for i in range(copies)]
-    torch.cuda.synchronize()
+    if args.only:
+        return only(args, dev)
 
-    def step(i):
-        ops.gemm(ksq.W_Q4_0, ksq.A_F32, W[i % copies], X[i % copies], M, N, K, out=out, workspace=ws)
+    wl = Workloads(dev)
+    # ---- the other BASELINE configs first (this also brings the clocks to their steady state)
+    log("bench: BASELINE configs 1, 3, 4")
+    configs = other_configs(wl)
 
-    def gemm_only(i):
-        ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, W[i % copies], AQ[i % copies], M, N, K, out=out)
+    # ---- decode GEMV, config 0 shape, and the one-shot read of the same number of bytes
+    log("bench: config 0 GEMV")
+    (Mv, Nv, Kv), gemv_q81, gemv_f32, gcopies = wl.gemv()
+    reps = 8
+    gemv_ms, gemv_d = graph_stats(gemv_q81, gcopies, reps)
+    gemv_f32_ms, gemv_f32_d = graph_stats(gemv_f32, gcopies, reps)
+    del gemv_q81, gemv_f32
+    rd, rcopies = wl.read()
+    read_ms, read_d = graph_stats(rd, rcopies, reps)
+    del rd
+    torch.cuda.empty_cache()
+    gemv_bytes = Nv * (Kv // 32) * 18 + Mv * (Kv // 32) * 36 + Mv * Nv * 4
+    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
+    f32_bytes = Nv * (Kv // 32) * 18 + Mv * Kv * 4 + Mv * Nv * 4
+    read_gbs = 9437184 / (read_ms * 1e-3) / 1e9
 
-    if args.only in ("gemm", "step"):
-        fn = gemm_only if args.only == "gemm" else step
-        for i in range(args.warmup + args.steps):
-            fn(i)
-        torch.cuda.synchronize()
-        print(json.dumps({"only": args.only, "launches": args.warmup + args.steps}), flush=True)
-        return 0
-
+    # ---- headline: config 2 steps
+    (M, N, K), step, gemm_only = wl.config2()
+    log(f"bench: config 2 inputs M={M} N={N} K={K}, 8 rotating copies")
     n_eager = min(args.warmup, 2)            # sizes the library's workspace pool before capture
     for i in range(n_eager):
         step(i)
@@ -234,46 +425,19 @@ def main() -> int:
     wall = (time.perf_counter() - t0) / args.steps * 1e3
     ops_per_step = 2.0 * M * N * K
     tops = ops_per_step / (ms * 1e-3) / 1e12
-
+    del g_step
+    # per-step distribution: separate replays of a one-step graph
+    g1 = capture(step, 1)
+    step_d = dist(replay_samples(g1, 48))
+    del g1
     g_gemm = capture(gemm_only, args.steps)
     g_gemm.replay()
     gemm_ms = time_graph(g_gemm, 1) / args.steps
     gemm_tops = ops_per_step / (gemm_ms * 1e-3) / 1e12
-    del g_step, g_gemm
-
-    # ---- decode GEMV, config 0 shape: 64 weight copies (604 MB, > 2x the MALL)
-    Mv, Nv, Kv = 1, 4096, 4096
-    gcopies = 64
-    wv_np = synth.weights(ksq.W_Q4_0, g, Nv, Kv)
-    WV = [torch.from_numpy(wv_np).to(dev) for _ in range(gcopies)]
-    xv = torch.from_numpy(synth.activations(g, Mv, Kv)).to(dev)
-    aqv = ops.quantize_q8_1(xv)
-    outv = torch.empty((Mv, Nv), dtype=torch.float32, device=dev)
-    wsv = torch.empty(ops.workspace_size(0, 0, Mv, Nv, Kv), dtype=torch.uint8, device=dev)
-
-    def gemv(i):
-        ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, WV[i % gcopies], aqv, Mv, Nv, Kv, out=outv)
-
-    def gemv_f32(i):
-        ops.gemm(ksq.W_Q4_0, ksq.A_F32, WV[i % gcopies], xv, Mv, Nv, Kv, out=outv, workspace=wsv)
-
-    if args.only == "gemv":
-        for i in range(args.warmup + args.steps):
-            gemv(i)
-        torch.cuda.synchronize()
-        print(json.dumps({"only": "gemv", "launches": args.warmup + args.steps}), flush=True)
-        return 0
-
-    reps = 8
-    g_v = capture(gemv, gcopies)
-    g_v.replay()
-    gemv_ms = time_graph(g_v, reps) / (reps * gcopies)
-    g_vf = capture(gemv_f32, gcopies)
-    g_vf.replay()
-    gemv_f32_ms = time_graph(g_vf, reps) / (reps * gcopies)
-    gemv_bytes = Nv * (Kv // 32) * 18 + Mv * (Kv // 32) * 36 + Mv * Nv * 4
-    gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
-    f32_bytes = Nv * (Kv // 32) * 18 + Mv * Kv * 4 + Mv * Nv * 4
+    del g_gemm
+    g1 = capture(gemm_only, 1)
+    gemm_d = dist(replay_samples(g1, 48))
+    del g1
 
     result = {
         "metric": "Q4_0×Q8_1 GEMM TOPS at M=2048; GEMV HBM GB/s at M=1 (N=K=4096)",
@@ -290,31 +454,39 @@ def main() -> int:
         "data": "synthetic, seeded (Q4_0 nibbles U[0,15], d=|N(0,0.02)|; activations N(0,1))",
         "config": {"workload": "q4_0_q8_1_prefill_gemm (BASELINE config 2)", "M": M, "N": N, "K": K,
                    "entry": "gemm_w4a32c8_q4_0_fp32_int8: quantize_q8_1 + int8-MFMA GEMM",
-                   "rotating_copies": copies, "host_wall_ms_per_step": round(wall, 5)},
+                   "rotating_copies": 8, "host_wall_ms_per_step": round(wall, 5),
+                   "step_distribution": step_d},
         "roofline": {"bound": "mfma", "kernel": "mmq_kernel<0> (Q4_0 x Q8_1, v_mfma_i32_32x32x32_i8)",
                      "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC_MMQ_Q4_0_M2048,
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC["gemm"][0],
+                     "traffic_source": TRAFFIC["gemm"][1],
                      "traffic_unit": "bytes per launch (algorithmic: %d)" % (
                          N * (K // 32) * 18 + M * (K // 32) * 36 + M * N * 4),
-                     "avg_kernel_ms": round(gemm_ms, 5),
+                     "avg_kernel_ms": round(gemm_ms, 5), "kernel_distribution": gemm_d,
                      "note": "int8 ops = 2*M*N*K per launch over the HIP-event time of graph-replayed launches"},
         "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(gemv_gbs, 1), "unit": "GB/s",
-                    "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6),
+                    "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6), **gemv_d,
                     "algorithmic_bytes": gemv_bytes,
                     "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
                                  "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-                                 "traffic": TRAFFIC_GEMV_Q4_0_M1},
-                    "fp32_entry_ms": round(gemv_f32_ms, 6),
+                                 "traffic": TRAFFIC["gemv"][0], "traffic_source": TRAFFIC["gemv"][1]},
+                    "fp32_entry_ms": round(gemv_f32_ms, 6), "fp32_entry_distribution": gemv_f32_d,
                     "fp32_entry_gbs": round(f32_bytes / (gemv_f32_ms * 1e-3) / 1e9, 1),
+                    "one_shot_read_9437184B": {"ms": round(read_ms, 6), **read_d, "GB/s": round(read_gbs, 1),
+                                               "how": "ksq_debug_stream_read of 9,437,184 bytes, 64 rotating copies"},
+                    "frac_of_one_shot_read": round(read_ms / gemv_ms, 4),
                     "weight_copies": gcopies},
+        "configs": configs,
     }
-    del WV, g_v, g_vf
-    torch.cuda.empty_cache()
-    log("bench: other BASELINE configs")
-    result["configs"] = other_configs(g, dev, reps=4)
     if not args.no_cpu_baseline:
-        log("bench: cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(M, N, K)
+        log("bench: cpu baselines")
+        cb = cpu_baselines()
+        c2 = cb["configs"]["c2_q4_0_M2048"]
+        result["cpu_baseline"] = {
+            "value": c2["all_cores"]["TOPS"], "unit": "TOPS", "cores": cb["threads_all"], "kind": "port",
+            "sample": f"{c2['all_cores']['rows_timed']} of 2048 activation rows x N=K=4096: quantize_row_q8_1_ref + "
+                      f"gemm_w4a8_reference loop order (oracle/ksq_oracle.c, gcc -O2, OpenMP over outputs)",
+            "single_thread_TOPS": c2["single_thread"]["TOPS"], **cb}
     print(json.dumps(result), flush=True)
     return 0
 

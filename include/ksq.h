@@ -182,6 +182,13 @@ KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activ
 KSQ_API int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const void* activation, float* output,
                              int M, int N, int K, void* stream);
 
+/* Debug / calibration: a plain streaming read of `bytes` device bytes at p (16-byte aligned,
+ * bytes % 16 == 0) with the decode kernels' 16-byte loads, 32 KiB per workgroup; writes one XOR
+ * word per workgroup to out (ksq_debug_stream_read_outputs(bytes) words).  The read-only speed of
+ * a given byte count, the ceiling a bandwidth-bound kernel of that size is measured against. */
+KSQ_API size_t ksq_debug_stream_read_outputs(size_t bytes);
+KSQ_API int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream);
+
 /* Debug: per-block integer dot products out[M][N][nblk] (nblk = K/32, or K/16 for
  * Q6_K) computed by the device block-dot code of the decode kernels. */
 KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,

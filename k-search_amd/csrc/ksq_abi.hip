@@ -396,6 +396,17 @@ int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const void* activ
     return ksq_gemm(wtype, atype, weight, activation, output, M, N, K, p, (size_t)KSQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
+size_t ksq_debug_stream_read_outputs(size_t bytes) { return ksq::stream_read_outputs(bytes); }
+
+int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream) {
+    if (bytes == 0) return ok();
+    if (!p || !out) return set_error(KSQ_ERR_NULL, "p or out is NULL");
+    if (((uintptr_t)p & 15u) || (bytes & 15u) || ((uintptr_t)out & 3u))
+        return set_error(KSQ_ERR_ALIGN, "p must be 16-byte aligned, bytes a multiple of 16, out 4-byte aligned");
+    hipError_t e = ksq::launch_stream_read(p, bytes, out, (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_error(e, "stream read launch");
+}
+
 int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N,
                          int K, void* stream) {
     int st = check_common(wtype, KSQ_A_Q8_1, weight, act_q8_1, out, M, N, K);

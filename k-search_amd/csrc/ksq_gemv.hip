@@ -1393,6 +1393,40 @@ __global__ void block_sumi_kernel(int wtype, const uint8_t* __restrict__ W, cons
     out[idx] = r;
 }
 
+// Calibration: a plain streaming read of `bytes` (16-byte aligned, a multiple of 16) with the
+// decode kernels' load width, 32 KiB per workgroup, each workgroup XOR-folding what it read into
+// one word of out (so the loads cannot be elided).
+constexpr int kReadBytesPerWG = 32768;
+
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                          uint32_t* __restrict__ out) {
+    const int64_t base = (int64_t)blockIdx.x * (kReadBytesPerWG / 16);
+    u32x4 v[kReadBytesPerWG / 16 / 256];
+#pragma unroll
+    for (int i = 0; i < kReadBytesPerWG / 16 / 256; i++) {
+        const int64_t k = base + i * 256 + threadIdx.x;
+        v[i] = k < n16 ? p[k] : u32x4{0, 0, 0, 0};
+    }
+    uint32_t x = 0;
+#pragma unroll
+    for (int i = 0; i < kReadBytesPerWG / 16 / 256; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
+    __shared__ uint32_t red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+size_t stream_read_outputs(size_t bytes) { return (bytes + kReadBytesPerWG - 1) / kReadBytesPerWG; }
+
+hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s) {
+    const int64_t n16 = (int64_t)(bytes / 16);
+    const size_t grid = stream_read_outputs(bytes);
+    if (grid == 0) return hipSuccess;
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4*)p, n16, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N,
                              int K, hipStream_t s) {
     const int nblk = (wtype == 3) ? K / 16 : K / 32;

@@ -112,6 +112,11 @@ hipError_t launch_moe_combine(const float* scratch, const int32_t* ids, float* o
 hipError_t launch_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N,
                              int K, hipStream_t s);
 
+// Calibration read of `bytes` bytes at p (16-byte aligned, bytes % 16 == 0); writes
+// stream_read_outputs(bytes) words to out.
+size_t stream_read_outputs(size_t bytes);
+hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s);
+
 // Fill `n` floats with zero (a kernel, so it can be captured in a graph).
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
 

@@ -144,6 +144,15 @@ def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int,
     return out
 
 
+def stream_read(buf: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Calibration read of every byte of buf (ksq_debug_stream_read); returns the XOR words."""
+    nbytes = buf.numel() * buf.element_size()
+    if out is None:
+        out = torch.empty(max(1, lib().ksq_debug_stream_read_outputs(nbytes)), dtype=torch.int32, device=buf.device)
+    check(lib().ksq_debug_stream_read(_ptr(buf), nbytes, _ptr(out), _stream()))
+    return out
+
+
 def last_engines() -> set[str]:
     """Kernel families the calling thread's last libksq call launched (ksq_debug_last_engines)."""
     bits = lib().ksq_debug_last_engines()

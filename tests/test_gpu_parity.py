@@ -775,3 +775,18 @@ def test_mfma_split_k(dev, oracle, wtype, M, N, K):
     rows = np.arange(M) if M <= 16 else np.sort(g.choice(M, 12, replace=False))
     ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1(x[rows]), w, len(rows), N, K)
     assert _rel_err(y1.cpu().numpy()[rows], ref) <= TOL
+
+
+def test_stream_read_calibration(dev):
+    """ksq_debug_stream_read reads every byte: its per-workgroup XOR words match numpy's over the
+    same 32 KiB chunks (ragged last chunk included)."""
+    import torch
+    from ksq import ops
+    g = np.random.default_rng(2900)
+    for nbytes in (16, 32768, 9437184, 100000 - 100000 % 16):
+        a = g.integers(0, 256, nbytes, dtype=np.uint8)
+        got = ops.stream_read(_t(a, dev))
+        torch.cuda.synchronize()
+        words = np.pad(a, (0, (-nbytes) % 32768)).view(np.uint32).reshape(-1, 8192)
+        want = np.bitwise_xor.reduce(words, axis=1)
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want), nbytes
