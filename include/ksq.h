@@ -159,13 +159,37 @@ KSQ_API int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16
  * rules as ksq_quantize_q8_1. */
 KSQ_API int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream);
 
+/* fp32 [M][K] -> block_q8f [M][K/32] (fp32 d and s), bit for bit with one of two reference
+ * quantisers (same alignment rules as ksq_quantize_q8_1; KSQ_ERR_TYPE for an unknown rule):
+ *   KSQ_Q8F_RNE     the deepseek_v2 W4A32C8 operator (core/operators/quant_gemm/variants/
+ *                   deepseek_v2/w4a32c8_q4_0_fp32_int8/reference.py:50-73, float32 scalar
+ *                   arithmetic as NumPy >= 2 evaluates it): d = amax / 127 (1 for an
+ *                   all-zero block), q = round-half-even(x / d) by true division, clamped to
+ *                   [-128, 127], s = sequential fp32 sum
+ *   KSQ_Q8F_LROUND  the generated lm_head kernel (best_kernels_GLM-5/quant_gemm/
+ *                   w4a32c8_q4_0_fp32_int8_llama3_8b_lm_head_n128256_k4096/kernel.cu:85-107):
+ *                   d = amax / 127 when amax > 1e-10 (else 1), q = lroundf(x * (127 /
+ *                   max(amax, 1e-10))) (half away from zero), s = sequential fp32 sum */
+#define KSQ_Q8F_RNE 0
+#define KSQ_Q8F_LROUND 1
+KSQ_API int ksq_quantize_q8f(int rule, const float* x, uint8_t* y, int M, int K, void* stream);
+
+/* The deepseek_v2 W4A32C8 operator (core/operators/quant_gemm/variants/deepseek_v2/
+ * w4a32c8_q4_0_fp32_int8: spec.json entry "forward", reference.py:5-94): Q4_0 weights, fp32
+ * activations quantised per block by its rules (KSQ_Q8F_RNE: fp32 d_a and s_a), contribution
+ * d_w*(d_a*sumi - 8*s_a) in fp32 (reference.py:86).  K % 256 == 0. */
+KSQ_API void gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2(const uint8_t* weight, const float* activation, float* output,
+                                                     int M, int N, int K);
+
 /* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the quantised copy of
  * fp32 activations, 0 for pre-quantised activations. */
 KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
 
 /* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype (the block_q8s forms pair
  * with Q8_0 weights only, KSQ_ERR_TYPE otherwise; KSQ_A_F16 takes fp16 activations, 16-byte
- * aligned, quantised by the fused FP16 kernels' rules as KSQ_Q81_FUSED_F16).  workspace may be
+ * aligned, quantised by the fused FP16 kernels' rules as KSQ_Q81_FUSED_F16; the block_q8f forms
+ * pair with Q4_0, Q5_0 and Q8_0 weights, need K % 256 == 0 and run on the int8 MFMA GEMM at
+ * every M, block contribution d_w*(d_a*sumi - c*s_a) with c = 8 / 16 / 0 in fp32).  workspace may be
  * NULL (then a per-device pool owned by the library is used, which makes the call
  * allocate on first use and when sizes grow).  Returns a ksq_status. */
 KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,

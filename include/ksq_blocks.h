@@ -19,6 +19,12 @@
  * that kernel keeps the per-block scale in fp32 and never stores a sum, so its
  * quantised activations are {float d; int8 qs[32]}, 36 B with qs at the same
  * offset as block_q8_1.
+ * block_q8f is the activation block of the generated kernels that keep the Q8_1 scale and sum
+ * in fp32: the deepseek_v2 W4A32C8 operator's reference
+ * (core/operators/quant_gemm/variants/deepseek_v2/w4a32c8_q4_0_fp32_int8/reference.py:50-73)
+ * and the lm_head kernel's quantiser (best_kernels_GLM-5/quant_gemm/
+ * w4a32c8_q4_0_fp32_int8_llama3_8b_lm_head_n128256_k4096/kernel.cu:85-107) compute d_a and
+ * s_a as fp32 and never round them to fp16; {float d; float s; int8 qs[32]}, 40 B.
  * The K-quant super-blocks are absent from the reference; they follow the
  * public GGML layout (ggml-common.h, QK_K = 256):
  *   block_q4_K  {half d; half dmin; u8 scales[12]; u8 qs[128]}      144 B
@@ -84,6 +90,12 @@ typedef struct {
 } ksq_block_q8s;
 
 typedef struct {
+    float d;                    /* fp32 scale */
+    float s;                    /* fp32 sequential sum of the 32 source floats */
+    int8_t qs[KSQ_QK8_1];
+} ksq_block_q8f;
+
+typedef struct {
     uint16_t d;                          /* super-block scale for the 6-bit sub-block scales */
     uint16_t dmin;                       /* super-block scale for the 6-bit sub-block mins */
     uint8_t scales[KSQ_K_SCALE_SIZE];    /* 8 scales + 8 mins, 6 bits each */
@@ -121,6 +133,9 @@ KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_1, qh) == 4, "block_q5_1.qh at offset 4"
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q5_1, qs) == 8, "block_q5_1.qs at offset 8");
 KSQ_STATIC_ASSERT(sizeof(ksq_block_q8s) == 36, "block_q8s must be 36 bytes");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q8s, qs) == 4, "block_q8s.qs at offset 4, as in block_q8_1");
+KSQ_STATIC_ASSERT(sizeof(ksq_block_q8f) == 40, "block_q8f must be 40 bytes");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q8f, s) == 4, "block_q8f.s at offset 4");
+KSQ_STATIC_ASSERT(offsetof(ksq_block_q8f, qs) == 8, "block_q8f.qs at offset 8");
 KSQ_STATIC_ASSERT(sizeof(ksq_block_q4_K) == 144, "block_q4_K must be 144 bytes");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_K, scales) == 4, "block_q4_K.scales at offset 4");
 KSQ_STATIC_ASSERT(offsetof(ksq_block_q4_K, qs) == 16, "block_q4_K.qs at offset 16");
@@ -147,6 +162,9 @@ enum ksq_atype {
     KSQ_A_F32_Q8S = 2, /* fp32 [M][K], quantised to block_q8s inside the call (native W8A8C8 rules) */
     KSQ_A_Q8S = 3,   /* pre-quantised block_q8s [M][K/32] */
     KSQ_A_F16 = 4,   /* fp16 [M][K], quantised to Q8_1 inside the call by the fused FP16 kernels' rules */
+    KSQ_A_Q8F = 5,   /* pre-quantised block_q8f [M][K/32] (Q4_0, Q5_0, Q8_0 weights; K % 256 == 0) */
+    KSQ_A_F32_Q8F_RNE = 6,    /* fp32 [M][K] -> block_q8f inside the call, rule KSQ_Q8F_RNE */
+    KSQ_A_F32_Q8F_LROUND = 7, /* fp32 [M][K] -> block_q8f inside the call, rule KSQ_Q8F_LROUND */
 };
 
 #endif /* KSQ_BLOCKS_H */

@@ -111,19 +111,33 @@ int scratch_get(void** out) {
 
 int block_elems(int wtype) { return (wtype == KSQ_W_Q4_K || wtype == KSQ_W_Q6_K) ? 256 : 32; }
 
-bool atype_f32(int atype) { return atype == KSQ_A_F32 || atype == KSQ_A_F32_Q8S; }
+bool atype_q8f(int atype) {
+    return atype == KSQ_A_Q8F || atype == KSQ_A_F32_Q8F_RNE || atype == KSQ_A_F32_Q8F_LROUND;
+}
+bool atype_f32(int atype) {
+    return atype == KSQ_A_F32 || atype == KSQ_A_F32_Q8S || atype == KSQ_A_F32_Q8F_RNE || atype == KSQ_A_F32_Q8F_LROUND;
+}
 // activations that arrive unquantised (fp32 or fp16) and are quantised into the workspace
 bool atype_raw(int atype) { return atype_f32(atype) || atype == KSQ_A_F16; }
-int atype_fmt(int atype) { return (atype == KSQ_A_F32_Q8S || atype == KSQ_A_Q8S) ? ksq::kAQ8S : ksq::kAQ81; }
+int atype_fmt(int atype) {
+    if (atype == KSQ_A_F32_Q8S || atype == KSQ_A_Q8S) return ksq::kAQ8S;
+    return atype_q8f(atype) ? ksq::kAQ8F : ksq::kAQ81;
+}
+// bytes of one quantised activation block
+size_t atype_block_bytes(int atype) { return atype_q8f(atype) ? 40u : 36u; }
 
 int check_common(int wtype, int atype, const void* weight, const void* activation, const void* output, int M,
                  int N, int K) {
     if (wtype < KSQ_W_Q4_0 || wtype > KSQ_W_Q5_1) return set_error(KSQ_ERR_TYPE, "unknown weight type %d", wtype);
-    if (atype < KSQ_A_F32 || atype > KSQ_A_F16) return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
+    if (atype < KSQ_A_F32 || atype > KSQ_A_F32_Q8F_LROUND)
+        return set_error(KSQ_ERR_TYPE, "unknown activation type %d", atype);
     if (atype_fmt(atype) == ksq::kAQ8S && wtype != KSQ_W_Q8_0)
         return set_error(KSQ_ERR_TYPE, "block_q8s activations pair with Q8_0 weights only (weight type %d)", wtype);
+    if (atype_q8f(atype) && wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q5_0 && wtype != KSQ_W_Q8_0)
+        return set_error(KSQ_ERR_TYPE, "block_q8f activations pair with Q4_0, Q5_0 and Q8_0 weights (weight type %d)",
+                         wtype);
     if (M < 0 || N < 0 || K < 0) return set_error(KSQ_ERR_SHAPE, "negative shape M=%d N=%d K=%d", M, N, K);
-    const int be = block_elems(wtype);
+    const int be = atype_q8f(atype) ? 256 : block_elems(wtype);
     if (K % be != 0) return set_error(KSQ_ERR_SHAPE, "K=%d is not a multiple of %d", K, be);
     if (M == 0 || N == 0) return KSQ_OK;
     if (!output) return set_error(KSQ_ERR_NULL, "output is NULL");
@@ -135,6 +149,8 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
         return set_error(KSQ_ERR_ALIGN, "K-quant weight must be 4-byte aligned");
     if (atype_raw(atype) && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "fp32 / fp16 activation must be 16-byte aligned");
     if (!atype_raw(atype) && (a & 3u)) return set_error(KSQ_ERR_ALIGN, "quantised activation must be 4-byte aligned");
+    if (atype == KSQ_A_Q8F && (a & 15u)) return set_error(KSQ_ERR_ALIGN, "block_q8f activation must be 16-byte aligned");
+    if (atype_q8f(atype) && (w & 15u)) return set_error(KSQ_ERR_ALIGN, "weight must be 16-byte aligned with block_q8f");
     if (o & 3u) return set_error(KSQ_ERR_ALIGN, "output must be 4-byte aligned");
     return KSQ_OK;
 }
@@ -168,7 +184,7 @@ struct GemmWs {
 
 GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
     GemmWs w{};
-    w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * 36u) : 0;
+    w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * atype_block_bytes(atype)) : 0;
     const int splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
     w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
     w.total = w.q + w.p;
@@ -178,7 +194,8 @@ GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
 int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* C, int M, int N, int K,
                float* partials, hipStream_t s) {
     hipError_t e;
-    const bool mmq = use_mmq(wtype, M, N, K, W, aligned16(Aq));
+    // block_q8f runs on the MFMA GEMM only (check_common has checked its shape and alignment)
+    const bool mmq = afmt == ksq::kAQ8F || use_mmq(wtype, M, N, K, W, aligned16(Aq));
     if (mmq) {
         e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, partials, s);
         if (e != hipSuccess) return hip_error(e, "mmq launch");
@@ -318,10 +335,23 @@ int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
     return ok();
 }
 
+int ksq_quantize_q8f(int rule, const float* x, uint8_t* y, int M, int K, void* stream) {
+    if (rule != KSQ_Q8F_RNE && rule != KSQ_Q8F_LROUND)
+        return set_error(KSQ_ERR_TYPE, "unknown block_q8f quantiser rule %d", rule);
+    if (M < 0 || K < 0 || K % 32) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d", M, K);
+    if (M == 0 || K == 0) return ok();
+    if (!x || !y) return set_error(KSQ_ERR_NULL, "x or y is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 3u))
+        return set_error(KSQ_ERR_ALIGN, "x must be 16-byte and y 4-byte aligned");
+    hipError_t e = ksq::launch_quantize_q8f(rule, x, y, M, K, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "quantize launch");
+    return ok();
+}
+
 size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const bool mmq_possible =
-        (g_path != 1) && (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K)) && (K % 256) == 0;
+    const bool mmq_possible = atype_q8f(atype) ||
+        ((g_path != 1) && (g_path == 2 || ksq::mmq_preferred(wtype, M, N, K)) && (K % 256) == 0);
     return gemm_ws(wtype, atype, M, N, K, mmq_possible).total;
 }
 
@@ -338,8 +368,8 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     const uint8_t* Aq = (const uint8_t*)activation;
     const int afmt = atype_fmt(atype);
-    if (atype_f32(atype) && ksq::gemv_fused_profitable(wtype, M, N, K, weight) && !use_mmq(wtype, M, N, K, weight, true) &&
-        g_path != 3) {
+    if (atype_f32(atype) && !atype_q8f(atype) && ksq::gemv_fused_profitable(wtype, M, N, K, weight) &&
+        !use_mmq(wtype, M, N, K, weight, true) && g_path != 3) {
         hipError_t e = ksq::launch_gemv_f32(wtype, afmt, (const uint8_t*)weight, (const float*)activation, output, M,
                                             N, K, s);
         return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
@@ -347,7 +377,7 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     // fp32 / fp16 activations are quantised to the start of the (16-byte aligned) workspace,
     // which is what the GEMM then reads
     const bool f32 = atype_f32(atype), f16 = atype == KSQ_A_F16;
-    const bool mmq = use_mmq(wtype, M, N, K, weight, f32 || f16 || aligned16(activation));
+    const bool mmq = atype_q8f(atype) || use_mmq(wtype, M, N, K, weight, f32 || f16 || aligned16(activation));
     const GemmWs L = gemm_ws(wtype, atype, M, N, K, mmq);
     uint8_t* ws = (uint8_t*)workspace;
     if (L.total) {
@@ -365,8 +395,12 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     float* partials = L.p ? (float*)(ws + L.q) : nullptr;
     if (f32 || f16) {
         // fp16 input takes the fused FP16 kernels' quantiser (kernels/gemm/gemm_fused.cuh:76-145)
-        hipError_t e = f16 ? ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, activation, ws, M, K, s)
-                           : ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
+        hipError_t e;
+        if (f16) e = ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, activation, ws, M, K, s);
+        else if (atype_q8f(atype))
+            e = ksq::launch_quantize_q8f(atype == KSQ_A_F32_Q8F_RNE ? KSQ_Q8F_RNE : KSQ_Q8F_LROUND,
+                                         (const float*)activation, ws, M, K, s);
+        else e = ksq::launch_quantize(afmt, (const float*)activation, ws, M, K, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
         g_engines |= KSQ_ENG_QUANTIZE;
         Aq = ws;
@@ -577,5 +611,6 @@ KSQ_DROPIN(ksq_gemm_q4_1_q8_1, KSQ_W_Q4_1, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(ksq_gemm_q5_0_q8_1, KSQ_W_Q5_0, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(ksq_gemm_q5_1_q8_1, KSQ_W_Q5_1, KSQ_A_Q8_1, uint8_t)
 KSQ_DROPIN(gemm_w8a8c8_q8_0_q8_1, KSQ_W_Q8_0, KSQ_A_F32_Q8S, float)
+KSQ_DROPIN(gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2, KSQ_W_Q4_0, KSQ_A_F32_Q8F_RNE, float)
 
 }  // extern "C"

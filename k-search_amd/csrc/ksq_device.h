@@ -159,6 +159,47 @@ __device__ __forceinline__ void quantize_block_q8s(const float* v, uint32_t* out
     }
 }
 
+// Quantise 32 floats to one block_q8f (fp32 d and s).  out[0] = d bits, out[1] = s bits,
+// out[2..9] = quants.  s is the sequential fp32 sum in both rules.
+//   RNE (deepseek_v2/w4a32c8_q4_0_fp32_int8/reference.py:50-73, float32 scalar arithmetic
+//       as NumPy >= 2 evaluates it): d = amax / 127, 1 when amax is 0; q = round-half-even of
+//       the fp32 quotient x / d, clamped to [-128, 127]
+//   LROUND (best_kernels_GLM-5/.../lm_head_n128256_k4096/kernel.cu:85-107): d = amax / 127
+//       when amax > 1e-10, else 1; q = lroundf(x * (127 / fmaxf(amax, 1e-10))), half away from
+//       zero; |x * scale| <= 127 * (1 + 2^-23) for finite x, so q fits int8 without a clamp
+constexpr int kQ8FRne = 0, kQ8FLround = 1;
+template <int RULE>
+__device__ __forceinline__ void quantize_block_q8f(const float* v, uint32_t* out) {
+#pragma clang fp contract(off)
+    float amax = 0.0f, sum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+        sum += v[j];
+    }
+    float d, scale = 0.0f;
+    if constexpr (RULE == kQ8FRne) {
+        d = amax > 0.0f ? amax / 127.0f : 1.0f;
+    } else {
+        d = amax > 1e-10f ? amax / 127.0f : 1.0f;
+        scale = 127.0f / __builtin_fmaxf(amax, 1e-10f);
+    }
+    out[0] = __builtin_bit_cast(uint32_t, d);
+    out[1] = __builtin_bit_cast(uint32_t, sum);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float x = v[4 * j + t];
+            const float r = (RULE == kQ8FRne) ? __builtin_rintf(x / d) : roundf(x * scale);
+            const int q = (r != r) ? 0 : (int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+            packed |= ((uint32_t)q & 0xFFu) << (8 * t);
+        }
+        out[2 + j] = packed;
+    }
+}
+
 // Bits 0..3 of x moved to bit 4 of the four bytes of a word: the fifth bit of four
 // consecutive Q5_0 / Q5_1 quants.  The product places bit k of x at bit 8k (its shifted
 // copies x, x<<7, x<<14, x<<21 do not overlap, so nothing carries).

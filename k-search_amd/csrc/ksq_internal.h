@@ -17,13 +17,16 @@ namespace ksq {
 // layer clears the record when a call starts.
 void note_engine(uint32_t bits);
 
-// Quantised-activation formats: block_q8_1 (fp16 d and s) or block_q8s (fp32 d, the native
-// W8A8C8 operator's block; used with Q8_0 weights only).
-constexpr int kAQ81 = 0, kAQ8S = 1;
+// Quantised-activation formats: block_q8_1 (fp16 d and s), block_q8s (fp32 d, the native
+// W8A8C8 operator's block; used with Q8_0 weights only) or block_q8f (fp32 d and s, 40 bytes;
+// int8 MFMA GEMM only, with Q4_0, Q5_0 and Q8_0 weights).
+constexpr int kAQ81 = 0, kAQ8S = 1, kAQ8F = 2;
 
 // fp32 [rows][K] -> [rows][K/32] 36-byte blocks of format afmt; x 16-byte aligned, y 4-byte aligned.
 hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 hipError_t launch_quantize_q8_1(const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
+// fp32 [rows][K] -> block_q8f [rows][K/32] by rule KSQ_Q8F_RNE / KSQ_Q8F_LROUND (0 / 1).
+hipError_t launch_quantize_q8f(int rule, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 // The same quantisation plus zeroing nzero floats at `zero` (16-byte aligned, nzero % 4 == 0) in
 // the same launch.
 hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, int K, float* zero, int64_t nzero,

@@ -113,23 +113,31 @@ __device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
     for (int i = 0; i < NW; i++) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], sh);
 }
 
-// AS: the activations are block_q8s (fp32 scale, no sum; Q8_0 weights only).
+// AF: activation block format: kAQ81 block_q8_1 (fp16 d, s), kAQ8S block_q8s (fp32 d, no sum;
+// Q8_0 weights only), kAQ8F block_q8f (fp32 d and s, 40 bytes; Q4_0, Q5_0, Q8_0 weights), whose
+// s_a term is subtracted in the epilogue instead of running on the f16 MFMA.
 // T::PIPE (tiles of 128 x 128 with K steps of 4 blocks; 32-element block types, no MoE): the
 // global loads of K step k+1 are issued into registers before step k computes (threads 0..127
 // hold an activation chunk, 128..255 a weight chunk), so their latency hides behind the MFMAs.
-template <class T, int WT, bool DUMP, bool MOE, bool AS>
+template <class T, int WT, bool DUMP, bool MOE, int AF>
 __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
                                                           int32_t* __restrict__ dump, int M, int N, int nb,
                                                           MoeTiles moe) {
     using S = WShape<WT, T::KB>;
     constexpr int BM = T::BM, BN = T::BN, KB = T::KB, TM = T::TM, TN = T::TN;
+    constexpr bool AS = AF == kAQ8S, AFS = AF == kAQ8F;
+    constexpr int ABW = AFS ? 10 : 9;                  // dwords per activation block
+    constexpr int AQ = AFS ? 2 : 1;                    // dword offset of the quants in a block
+    // the s_a term: f16 MFMA for block_q8_1, an epilogue subtraction for block_q8f
+    constexpr bool SIDE_MFMA = S::side && AF == kAQ81, SIDE_SUB = S::side && AFS;
     __shared__ __attribute__((aligned(16))) uint8_t sA[BM * T::APitch];
     __shared__ __attribute__((aligned(16))) uint8_t sW[BN * S::WPitch];
     __shared__ __attribute__((aligned(16))) float sDa[KB][BM];     // d_a' (d_a/8 for Q4_0)
     __shared__ __attribute__((aligned(16))) float sNc[KB][BM];     // -12582912 * d_a'
     __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
     __shared__ __attribute__((aligned(16))) uint16_t sSaH[BM][8];  // -s_a, fp16 bits (side term)
+    __shared__ __attribute__((aligned(16))) float sNs[SIDE_SUB ? KB : 1][SIDE_SUB ? BM : 1];  // -s_a, fp32
     __shared__ __attribute__((aligned(16))) uint16_t sDwH[BN][8];  // side-term weight factor, fp16 bits
     __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == kWQ4K ? BN : 1][8];  // Q4_K: its low part
     __shared__ int32_t sRows[MOE ? BM : 1];                        // MoE: entry index of each tile row
@@ -147,6 +155,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     constexpr float da_scale = 1.0f / S::out_scale;
     static_assert(!is_kquant(WT) || KB == 8, "K-quants stage one 256-element super-block per K step");
     static_assert(!AS || WT == kWQ80, "block_q8s activations pair with Q8_0 weights only");
+    static_assert(!AFS || WT == kWQ40 || WT == kWQ50 || WT == kWQ80,
+                  "block_q8f activations pair with Q4_0, Q5_0 and Q8_0 weights");
+    static_assert(!(AFS && MOE), "the grouped GEMM reads block_q8_1 activations");
 
     if constexpr (KB == 4) {
         // the f16 side-term MFMA contracts 8 block slots; slots 4..7 stay zero
@@ -190,12 +201,13 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     const int kb_lo = (int)((long long)nsteps * z / Z) * KB, kb_hi = (int)((long long)nsteps * (z + 1) / Z) * KB;
     if constexpr (!MOE) C += (size_t)z * (size_t)M * (size_t)N;
     // ---- staging of 32-element blocks, split into the global loads and the LDS writes
-    // activation chunk g (4 Q8_1 blocks = 144 B = 9 x 16 B) of staged row sr
+    // activation chunk g (4 blocks = 144 B = 9 x 16 B, or 160 B = 10 x 16 B for block_q8f) of
+    // staged row sr
     auto load_act = [&](int sr, int g, int kb0, uint32_t* v) {
         const int am = MOE ? sTok[sr] : min(m0 + sr, M - 1);
-        const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * kQ81Bytes;
+        const uint8_t* p = A + ((size_t)am * nb + kb0 + 4 * g) * (4 * ABW);
 #pragma unroll
-        for (int i = 0; i < 9; i++) {
+        for (int i = 0; i < ABW; i++) {
             const u32x4 x = *(const u32x4*)(p + 16 * i);
             v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
         }
@@ -204,16 +216,21 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int kb = 4 * g + j;
+            const uint32_t* bv = v + ABW * j;
             u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
-            dst[0] = u32x4{v[9 * j + 1], v[9 * j + 2], v[9 * j + 3], v[9 * j + 4]};
-            dst[1] = u32x4{v[9 * j + 5], v[9 * j + 6], v[9 * j + 7], v[9 * j + 8]};
-            // block_q8s: the fp32 scale with its two lowest mantissa bits cleared (22 significant
-            // bits), so that 12582912 * d_a' stays exact (relative change < 2^-21)
-            const float da = AS ? __builtin_bit_cast(float, v[9 * j] & ~3u)
-                                : f16_to_f32(v[9 * j] & 0xFFFFu) * da_scale;
+            dst[0] = u32x4{bv[AQ], bv[AQ + 1], bv[AQ + 2], bv[AQ + 3]};
+            dst[1] = u32x4{bv[AQ + 4], bv[AQ + 5], bv[AQ + 6], bv[AQ + 7]};
+            // fp32 scales (block_q8s, block_q8f) with their two lowest mantissa bits cleared (22
+            // significant bits), so that 12582912 * d_a' stays exact (relative change < 2^-21);
+            // da_scale is a power of two
+            const float da = (AS || AFS) ? __builtin_bit_cast(float, bv[0] & ~3u) * da_scale
+                                         : f16_to_f32(bv[0] & 0xFFFFu) * da_scale;
             sDa[kb][sr] = da;
             sNc[kb][sr] = -kMagicF * da;
-            sSaH[sr][kb] = (uint16_t)((v[9 * j] >> 16) ^ 0x8000u);
+            // block_q8f: the term -c*s_a in the main term's units (c = out_scale: 8 for Q4_0,
+            // 16 for Q5_0), i.e. -s_a
+            if constexpr (SIDE_SUB) sNs[kb][sr] = -__builtin_bit_cast(float, bv[1]);
+            if constexpr (SIDE_MFMA) sSaH[sr][kb] = (uint16_t)((bv[0] >> 16) ^ 0x8000u);
         }
     };
     // weight chunk g (4 blocks: 72 / 136 / 80 / 88 / 96 B, 8-byte aligned) of staged row sr
@@ -272,7 +289,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     static_assert(!PIPE || (KB == 4 && BM == 128 && BN == 128),
                   "the pipelined staging covers 128 x 128 tiles with 4-block K steps");
     // PIPE: one chunk per thread and K step; threads 0..127 activation row t, 128..255 weight row t-128
-    uint32_t pre[PIPE ? 36 : 1];
+    uint32_t pre[PIPE ? 4 * ABW : 1];
     const bool pre_act = t < 128;
     auto pre_load = [&](int kb0) {
         if constexpr (PIPE) {
@@ -294,7 +311,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         // ---- stage activations
         for (int c = t; c < BM * (KB / 4); c += 256) {
             const int sr = c / (KB / 4), g = c % (KB / 4);
-            uint32_t v[36];
+            uint32_t v[4 * ABW];
             load_act(sr, g, kb0, v);
             store_act(sr, g, v);
         }
@@ -420,6 +437,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                     for (int q = 0; q < 4; q++) edw[q] = *(const f32x4*)&sDw[u][nbase + 8 * q];
                 }
                 const float da = sDa[b][lm], nc = sNc[b][lm];
+                const float ns = SIDE_SUB ? sNs[b][lm] : 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
 #pragma unroll
@@ -428,7 +446,9 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                         // reads element 0 with this compiler
                         const int e = res[4 * q + p];
                         const float f = __builtin_bit_cast(float, e);
-                        acc[i][j][4 * q + p] = fmaf(edw[q][p], fmaf(f, da, nc), acc[i][j][4 * q + p]);
+                        float x = fmaf(f, da, nc);              // sumi * d_a'
+                        if constexpr (SIDE_SUB) x = x + ns;     // (d_a*sumi - c*s_a) / c, one rounding
+                        acc[i][j][4 * q + p] = fmaf(edw[q][p], x, acc[i][j][4 * q + p]);
                     }
                 }
             }
@@ -471,7 +491,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             }
         }
 
-        if constexpr (S::side && !DUMP) {
+        if constexpr (SIDE_MFMA && !DUMP) {
             // side term: acc[n][m] += sum_k f[n][k] * (-s_a[m][k]) over the staged blocks, f = d_w
             // (Q4_0, Q5_0), -m (Q4_1, Q5_1) or dmin*m/8 as an fp16 hi + lo pair (Q4_K); f16 MFMA
             // over 8 block slots, exact products
@@ -722,13 +742,13 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, float* __restr
     }
 }
 
-template <class T, int WT, bool DUMP, bool MOE, bool AS = false>
+template <class T, int WT, bool DUMP, bool MOE, int AF = kAQ81>
 static hipError_t launch_k(dim3 grid, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump, int M, int N,
                            int nb, const MoeTiles& mt, hipStream_t s) {
     if constexpr (is_kquant(WT) && (T::KB != 8 || MOE)) {
         return hipErrorNotSupported;
     } else {
-        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AS>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
+        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AF>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
         return hipGetLastError();
     }
 }
@@ -736,9 +756,23 @@ static hipError_t launch_k(dim3 grid, const uint8_t* W, const uint8_t* A, float*
 template <class T, bool DUMP, bool MOE>
 static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, const uint8_t* A, float* C,
                            int32_t* dump, int M, int N, int nb, const MoeTiles& mt, hipStream_t s) {
-    if (afmt == kAQ8S) {
-        if (wtype != kWQ80) return hipErrorNotSupported;
-        return launch_k<T, kWQ80, DUMP, MOE, true>(grid, W, A, C, dump, M, N, nb, mt, s);
+    if (afmt != kAQ81) {
+        // the fp32-scale activation blocks: plain GEMM only (no block-dot dump, no MoE)
+        if constexpr (DUMP || MOE) {
+            return hipErrorNotSupported;
+        } else {
+            if (afmt == kAQ8S) {
+                if (wtype != kWQ80) return hipErrorNotSupported;
+                return launch_k<T, kWQ80, false, false, kAQ8S>(grid, W, A, C, dump, M, N, nb, mt, s);
+            }
+            if (afmt != kAQ8F) return hipErrorNotSupported;
+            switch (wtype) {
+                case kWQ40: return launch_k<T, kWQ40, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
+                case kWQ50: return launch_k<T, kWQ50, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
+                case kWQ80: return launch_k<T, kWQ80, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
+                default: return hipErrorNotSupported;
+            }
+        }
     }
     switch (wtype) {
         case kWQ40: return launch_k<T, kWQ40, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);

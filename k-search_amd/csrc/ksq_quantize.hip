@@ -1,4 +1,4 @@
-// ksq_quantize.hip - fp32 activations -> block_q8_1 (or block_q8s) on gfx950.
+// ksq_quantize.hip - fp32 activations -> block_q8_1 (or block_q8s, block_q8f) on gfx950.
 //
 // Same arithmetic as quantize_row_q8_1_ref (kernelevalplus-main/include/quantize.h:165-193);
 // the reference's own device kernel (quantize.h:302-337) rounds half-even with
@@ -29,8 +29,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // Output formats: kQF81 block_q8_1 (quantize_row_q8_1_ref), kQF8S block_q8s (the native W8A8C8
-// operator's rules), both 36-byte blocks of 9 dwords.
-constexpr int kQF81 = 0, kQF8S = 1;
+// operator's rules), both 36-byte blocks of 9 dwords; kQF8FRne / kQF8FLround block_q8f (fp32 d
+// and s, 40-byte blocks of 10 dwords) by the two rules of quantize_block_q8f.
+constexpr int kQF81 = 0, kQF8S = 1, kQF8FRne = 2, kQF8FLround = 3;
+template <int FMT>
+constexpr int out_words() { return FMT >= kQF8FRne ? 10 : 9; }
 
 // The 64 blocks of wave w of workgroup `wg`.
 template <int FMT>
@@ -63,27 +66,30 @@ __device__ __forceinline__ void quantize_wave(const float* __restrict__ x, uint8
     }
     wave_lds_sync();
 
-    uint32_t q[9];
+    constexpr int OW = out_words<FMT>();
+    uint32_t q[OW];
     if (lane < nblk) {
         float v[32];
 #pragma unroll
         for (int j = 0; j < 32; j++) v[j] = stage[lane * kQPitch + j];
         if constexpr (FMT == kQF8S) quantize_block_q8s(v, q);
+        else if constexpr (FMT == kQF8FRne) quantize_block_q8f<kQ8FRne>(v, q);
+        else if constexpr (FMT == kQF8FLround) quantize_block_q8f<kQ8FLround>(v, q);
         else quantize_block_q8_1(v, q);
     }
     wave_lds_sync();
-    // 64 x 9 dwords, odd pitch: conflict free
+    // 64 x OW dwords (9: odd pitch, conflict free; 10: two-way conflicts)
     uint32_t* ostage = (uint32_t*)stage;
     if (lane < nblk) {
 #pragma unroll
-        for (int j = 0; j < 9; j++) ostage[lane * 9 + j] = q[j];
+        for (int j = 0; j < OW; j++) ostage[lane * OW + j] = q[j];
     }
     wave_lds_sync();
-    uint32_t* dst = (uint32_t*)(y + blk0 * 36);
+    uint32_t* dst = (uint32_t*)(y + blk0 * (4 * OW));
 #pragma unroll
-    for (int j = 0; j < 9; j++) {
+    for (int j = 0; j < OW; j++) {
         const int idx = lane + 64 * j;
-        if (idx < nblk * 9) dst[idx] = ostage[idx];
+        if (idx < nblk * OW) dst[idx] = ostage[idx];
     }
 }
 
@@ -127,6 +133,21 @@ hipError_t launch_quantize(int afmt, const float* x, uint8_t* y, int64_t rows, i
     else
         hipLaunchKernelGGL(quantize_q8_1_kernel<kQF81>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y,
                            nblocks);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_q8f(int rule, const float* x, uint8_t* y, int64_t rows, int K, hipStream_t s) {
+    const int64_t nblocks = rows * (int64_t)(K / 32);
+    if (nblocks == 0) return hipSuccess;
+    const int64_t grid = (nblocks + kQBlocksPerWG - 1) / kQBlocksPerWG;
+    if (rule == kQ8FRne)
+        hipLaunchKernelGGL(quantize_q8_1_kernel<kQF8FRne>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y,
+                           nblocks);
+    else if (rule == kQ8FLround)
+        hipLaunchKernelGGL(quantize_q8_1_kernel<kQF8FLround>, dim3((unsigned)grid), dim3(64 * kQWaves), 0, s, x, y,
+                           nblocks);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -11,8 +11,8 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from ._lib import (A_F32, A_F32_Q8S, A_Q8_1, W_Q4_0, W_Q4_1, W_Q4_K, W_Q5_0, W_Q5_1, W_Q6_K, W_Q8_0, check,
-                   lib)
+from ._lib import (A_F32, A_F32_Q8F_RNE, A_F32_Q8S, A_Q8_1, Q8F_LROUND, Q8F_RNE, W_Q4_0, W_Q4_1, W_Q4_K,
+                   W_Q5_0, W_Q5_1, W_Q6_K, W_Q8_0, check, lib)
 
 # Definition-style entry points of include/ksq.h -> (weight type, activation type)
 ENTRY_POINTS = {
@@ -32,6 +32,8 @@ ENTRY_POINTS = {
     "ksq_gemm_q5_1_q8_1": (W_Q5_1, A_Q8_1),
     # the native deepseek_v3 W8A8C8 operator (spec.json entry point "gemm_w8a8c8_q8_0_q8_1")
     "gemm_w8a8c8_q8_0_q8_1": (W_Q8_0, A_F32_Q8S),
+    # the deepseek_v2 W4A32C8 operator (spec.json entry point "forward"): fp32 d_a and s_a
+    "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2": (W_Q4_0, A_F32_Q8F_RNE),
 }
 
 
@@ -82,7 +84,7 @@ def forward(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: i
     wtype, atype = ENTRY_POINTS[entry]
     if weight.dtype != torch.uint8:
         raise RuntimeError(f"expected scalar type Byte for weight but found {weight.dtype}")
-    want = torch.float32 if atype in (A_F32, A_F32_Q8S) else torch.uint8
+    want = torch.float32 if atype in (A_F32, A_F32_Q8S, A_F32_Q8F_RNE) else torch.uint8
     if activation.dtype != want:
         raise RuntimeError(f"expected scalar type {want} for activation but found {activation.dtype}")
     return gemm(wtype, atype, weight, activation, int(M), int(N), int(K))
@@ -130,6 +132,20 @@ def quantize_q8s(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tens
     if out is None:
         out = torch.empty((*x.shape[:-1], K // 32, 36), dtype=torch.uint8, device=x.device)
     check(lib().ksq_quantize_q8s(_ptr(x), _ptr(out), rows, K, _stream()))
+    return out
+
+
+def quantize_q8f(x: torch.Tensor, rule: int = Q8F_RNE, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [..., K] -> uint8 [..., K/32, 40] block_q8f (fp32 d and s): rule Q8F_RNE the deepseek_v2
+    operator's quantiser, Q8F_LROUND the lm_head kernel's."""
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise RuntimeError("quantize_q8f expects a CUDA float32 tensor")
+    x = x.contiguous()
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if out is None:
+        out = torch.empty((*x.shape[:-1], K // 32, 40), dtype=torch.uint8, device=x.device)
+    check(lib().ksq_quantize_q8f(rule, _ptr(x), _ptr(out), rows, K, _stream()))
     return out
 
 
@@ -207,5 +223,5 @@ def release() -> None:
     lib().ksq_release()
 
 
-__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "block_sumi", "last_engines", "set_path",
+__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "quantize_q8f", "block_sumi", "last_engines", "set_path",
            "workspace_size", "moe_gemm", "moe_gemm_routed", "moe_workspace_size", "release", "_lib"]

@@ -210,8 +210,13 @@ def weight_terms(wtype: int, w: np.ndarray):
 
 
 def act_terms(a: np.ndarray, q8s: bool = False):
-    """block_q8_1 (or block_q8s) activations [M, K/32, 36] -> (A [M, K] = d_a * q_a, s_a [M, K/32])."""
-    M, nb, _ = a.shape
+    """block_q8_1 (or block_q8s) activations [M, K/32, 36], or block_q8f [M, K/32, 40] (fp32 d and s),
+    -> (A [M, K] = d_a * q_a, s_a [M, K/32])."""
+    M, nb, nbytes = a.shape
+    if nbytes == 40:
+        f = np.ascontiguousarray(a[..., 0:8]).view(np.float32).astype(np.float64)
+        q = np.ascontiguousarray(a[..., 8:40]).view(np.int8).astype(np.int64)
+        return (f[..., 0:1] * q).reshape(M, -1), f[..., 1]
     d = (np.ascontiguousarray(a[..., 0:4]).view(np.float32)[..., 0].astype(np.float64) if q8s
          else _f16(a[..., 0:2]))
     s = np.zeros((M, nb)) if q8s else _f16(a[..., 2:4])

@@ -702,6 +702,130 @@ KSQ_API void ksq_ref_gemm_q8_0_q8s_f64(const uint8_t* A, const uint8_t* W, doubl
 }
 
 /* ------------------------------------------------------------------------ */
+/* block_q8f {float d; float s; int8 qs[32]}: the quantisers that keep the   */
+/* activation scale and sum in fp32.                                         */
+/* ------------------------------------------------------------------------ */
+
+/* core/operators/quant_gemm/variants/deepseek_v2/w4a32c8_q4_0_fp32_int8/reference.py:50-73,
+ * evaluated as NumPy >= 2 does (NEP 50: a Python float or int meeting a numpy.float32 scalar
+ * keeps float32): a_max = max(a_max, abs(a)) from 0.0; d_a = a_max / 127.0 in float32, 1.0
+ * when a_max is 0; a_sum = left-to-right float32 sum from 0.0; q = int(round(a / d_a)),
+ * Python's round of the float32 quotient (half to even), clamped to [-128, 127]. */
+static void q8f_block_rne(const float* xs, uint8_t* blk) {
+    float amax = 0.0f, sum = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        const float a = fabsf(xs[j]);
+        if (a > amax) amax = a;          /* Python max(a_max, abs(a)) keeps a_max unless a > a_max */
+        sum += xs[j];
+    }
+    const float d = (amax > 0.0f) ? amax / 127.0f : 1.0f;
+    memcpy(blk, &d, 4);
+    memcpy(blk + 4, &sum, 4);
+    for (int j = 0; j < 32; j++) {
+        int32_t q = cvt_i32_device(rintf(xs[j] / d));   /* rintf: the default nearest-even mode */
+        q = q < -128 ? -128 : (q > 127 ? 127 : q);
+        blk[8 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+/* best_kernels_GLM-5/quant_gemm/w4a32c8_q4_0_fp32_int8_llama3_8b_lm_head_n128256_k4096/
+ * kernel.cu:68-107 (compute_block): a_max = fmaxf(a_max, fabsf(a)) and a_sum += a in element
+ * order; d_a = a_max > 1e-10f ? a_max / 127.0f : 1.0f; scale = 127.0f / fmaxf(a_max, 1e-10f);
+ * q = (int8)(uint8)lroundf(a * scale), half away from zero. */
+static void q8f_block_lround(const float* xs, uint8_t* blk) {
+    float amax = 0.0f, sum = 0.0f;
+    for (int j = 0; j < 32; j++) {
+        amax = fmaxf(amax, fabsf(xs[j]));
+        sum += xs[j];
+    }
+    const float d = (amax > 1e-10f) ? amax / 127.0f : 1.0f;
+    const float scale = 127.0f / fmaxf(amax, 1e-10f);
+    memcpy(blk, &d, 4);
+    memcpy(blk + 4, &sum, 4);
+    for (int j = 0; j < 32; j++) blk[8 + j] = (uint8_t)lroundf(xs[j] * scale);
+}
+
+/* rule 0: the deepseek_v2 operator (KSQ_Q8F_RNE), 1: the lm_head kernel (KSQ_Q8F_LROUND). */
+KSQ_API void ksq_ref_quantize_row_q8f(int rule, const float* x, uint8_t* y, int64_t k) {
+    for (int64_t i = 0; i < k / 32; i++) {
+        if (rule == 0) q8f_block_rne(x + i * 32, y + i * 40);
+        else q8f_block_lround(x + i * 32, y + i * 40);
+    }
+}
+
+/* The GEMM over block_q8f activations, fp32 in block order as reference.py:32-89 runs it
+ * under NEP 50 (acc, d_w from struct '<e' and every product stay float32):
+ *   Q4_0  acc += d_w * (d_a * sumi - 8.0 * s_a)     (reference.py:86; kernel.cu:106)
+ *   Q5_0  acc += d_w * (d_a * sumi - 16.0 * s_a)    (gemm_quant_formats.cuh:207's form)
+ *   Q8_0  acc += d_w * (d_a * sumi)                 (s unused)
+ * sumi over the stored (unsigned for Q4_0 / Q5_0) quants, as the block_q8_1 dots. */
+KSQ_API void ksq_ref_gemm_q8f(int wtype, const uint8_t* A, const uint8_t* W, float* C, int M, int N, int K,
+                              int nthreads) {
+    const int nb = K / 32;
+    const int wbytes = wtype == KSQ_W_Q4_0 ? 18 : wtype == KSQ_W_Q8_0 ? 34 : legacy_bytes(wtype);
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float acc = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 40;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * wbytes;
+                float d_a, s_a;
+                memcpy(&d_a, ab, 4);
+                memcpy(&s_a, ab + 4, 4);
+                const float d_w = rd_f16(wb);
+                /* the sumi helpers read the quants at ablk + 4: pass the block 4 bytes on */
+                if (wtype == KSQ_W_Q4_0) {
+                    const float sumi = (float)ksq_ref_sumi_q4_0_q8_1(wb, ab + 4);
+                    acc += d_w * (d_a * sumi - 8.0f * s_a);
+                } else if (wtype == KSQ_W_Q5_0) {
+                    const float sumi = (float)ksq_ref_sumi_legacy_q8_1(wtype, wb, ab + 4);
+                    acc += d_w * (d_a * sumi - 16.0f * s_a);
+                } else {
+                    const float sumi = (float)ksq_ref_sumi_q8_0_q8_1(wb, ab + 4);
+                    acc += d_w * (d_a * sumi);
+                }
+            }
+            C[(int64_t)i * N + j] = acc;
+        }
+    }
+}
+
+/* The same block terms accumulated in fp64 (tolerance reference). */
+KSQ_API void ksq_ref_gemm_q8f_f64(int wtype, const uint8_t* A, const uint8_t* W, double* C, int M, int N, int K,
+                                  int nthreads) {
+    const int nb = K / 32;
+    const int wbytes = wtype == KSQ_W_Q4_0 ? 18 : wtype == KSQ_W_Q8_0 ? 34 : legacy_bytes(wtype);
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            double acc = 0.0;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* ab = A + ((int64_t)i * nb + b) * 40;
+                const uint8_t* wb = W + ((int64_t)j * nb + b) * wbytes;
+                float d_a, s_a;
+                memcpy(&d_a, ab, 4);
+                memcpy(&s_a, ab + 4, 4);
+                const double d_w = rd_f16(wb);
+                if (wtype == KSQ_W_Q4_0)
+                    acc += d_w * ((double)d_a * ksq_ref_sumi_q4_0_q8_1(wb, ab + 4) - 8.0 * s_a);
+                else if (wtype == KSQ_W_Q5_0)
+                    acc += d_w * ((double)d_a * ksq_ref_sumi_legacy_q8_1(wtype, wb, ab + 4) - 16.0 * s_a);
+                else
+                    acc += d_w * (double)d_a * ksq_ref_sumi_q8_0_q8_1(wb, ab + 4);
+            }
+            C[(int64_t)i * N + j] = acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* K-quants (absent from the reference).  Layout and arithmetic restate the  */
 /* public GGML k-quant algorithm (llama.cpp ggml-quants.c dequantize_row_q4_K */
 /* / dequantize_row_q6_K and ggml-cuda vecdotq.cuh vec_dot_q4_K_q8_1_impl_mmq */

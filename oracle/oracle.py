@@ -7,7 +7,9 @@ never imports this module.
 All buffers are numpy arrays; quantised tensors are flat uint8 byte arrays in
 the reference layouts (block_q4_0 18 B, block_q8_0 34 B, block_q8_1 36 B,
 block_q4_1 20 B, block_q5_0 22 B, block_q5_1 24 B, block_q4_K 144 B, block_q6_K
-210 B) or the native W8A8C8 operator's activation block (block_q8s 36 B).
+210 B), the native W8A8C8 operator's activation block (block_q8s 36 B) or the
+fp32-scale activation block of the deepseek_v2 operator and the lm_head kernel
+(block_q8f 40 B: fp32 d, fp32 s, 32 int8).
 """
 from __future__ import annotations
 
@@ -66,6 +68,9 @@ def lib() -> ctypes.CDLL:
         L.ksq_ref_gemm_legacy.argtypes = [i32, P, P, P, i32, i32, i32, i32]
         L.ksq_ref_gemm_w8a8c8.argtypes = [P, P, P, i32, i32, i32, i32]
         L.ksq_ref_gemm_q8_0_q8s_f64.argtypes = [P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_quantize_row_q8f.argtypes = [i32, P, P, i64]
+        L.ksq_ref_gemm_q8f.argtypes = [i32, P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_q8f_f64.argtypes = [i32, P, P, P, i32, i32, i32, i32]
         L.ksq_ref_q4_K_scale_min.argtypes = [i32, P, P, P]
         L.ksq_ref_sumi_q4_K_q8_1.argtypes = [P, i32, P]
         L.ksq_ref_sumi_q4_K_q8_1.restype = ctypes.c_int32
@@ -199,6 +204,31 @@ def gemm_q8s_f64(a_q8s: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthre
     w = np.ascontiguousarray(w, dtype=np.uint8)
     C = np.empty((M, N), dtype=np.float64)
     lib().ksq_ref_gemm_q8_0_q8s_f64(_p(a), _p(w), _p(C), M, N, K, nthreads or max_threads())
+    return C
+
+
+Q8F_RNE, Q8F_LROUND = 0, 1
+
+
+def quantize_q8f(x: np.ndarray, rule: int) -> np.ndarray:
+    """fp32 [M, K] -> block_q8f bytes [M, K/32, 40]: rule 0 the deepseek_v2 operator's
+    quantiser (round half to even of x / d), 1 the lm_head kernel's (lroundf(x * 127/amax))."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, 40), dtype=np.uint8)
+    lib().ksq_ref_quantize_row_q8f(rule, _p(x), _p(y), M * K)
+    return y
+
+
+def gemm_q8f(wtype: int, a_q8f: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 0,
+             f64: bool = False) -> np.ndarray:
+    """Q4_0 / Q5_0 / Q8_0 weights x block_q8f activations: the deepseek_v2 operator's fp32 block
+    order (or fp64 accumulation of the same block terms with f64=True)."""
+    a = np.ascontiguousarray(a_q8f, dtype=np.uint8)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float64 if f64 else np.float32)
+    fn = lib().ksq_ref_gemm_q8f_f64 if f64 else lib().ksq_ref_gemm_q8f
+    fn(wtype, _p(a), _p(w), _p(C), M, N, K, nthreads or max_threads())
     return C
 
 

@@ -49,7 +49,7 @@ FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced by the 
 
 @pytest.mark.parametrize("args,status", [
     ((9, 0, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # unknown weight type
-    ((0, 7, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # unknown activation type
+    ((0, 8, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # unknown activation type
     ((0, 0, FAKE, FAKE, FAKE, -1, 1, 32), 2),         # negative M
     ((0, 0, FAKE, FAKE, FAKE, 1, 1, 48), 2),          # K % 32
     ((2, 0, FAKE, FAKE, FAKE, 1, 1, 288), 2),         # K-quant needs K % 256
@@ -60,8 +60,14 @@ FAKE = 1 << 20  # a 16-byte aligned non-null address; never dereferenced by the 
     ((0, 0, FAKE, FAKE + 4, FAKE, 1, 1, 32), 3),      # fp32 activation not 16-byte aligned
     ((0, 1, FAKE, FAKE + 2, FAKE, 1, 1, 32), 3),      # Q8_1 activation not 4-byte aligned
     ((0, 0, FAKE, FAKE, FAKE + 2, 1, 1, 32), 3),      # output not 4-byte aligned
-    ((0, 5, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # activation type past KSQ_A_F16
+    ((0, 9, FAKE, FAKE, FAKE, 1, 1, 32), 4),          # activation type past KSQ_A_F32_Q8F_LROUND
     ((0, 4, FAKE, FAKE + 8, FAKE, 1, 1, 32), 3),      # fp16 activation not 16-byte aligned
+    ((4, 5, FAKE, FAKE, FAKE, 1, 1, 256), 4),         # block_q8f with Q4_1 weights
+    ((3, 6, FAKE, FAKE, FAKE, 1, 1, 256), 4),         # block_q8f with Q6_K weights
+    ((0, 5, FAKE, FAKE, FAKE, 1, 1, 32), 2),          # block_q8f needs K % 256
+    ((0, 7, FAKE, FAKE, FAKE, 1, 1, 224), 2),
+    ((0, 5, FAKE, FAKE + 4, FAKE, 1, 1, 256), 3),     # block_q8f activation not 16-byte aligned
+    ((1, 6, FAKE + 2, FAKE, FAKE, 1, 1, 256), 3),     # weight not 16-byte aligned with block_q8f
 ])
 def test_gemm_rejects_bad_arguments(args, status):
     from ksq import _lib
@@ -99,6 +105,15 @@ def test_quantize_variant_rejects_unknown_variant():
     assert L.ksq_quantize_q8_1_variant(1, None, None, 1, 48, None) == 2      # KSQ_ERR_SHAPE
 
 
+def test_quantize_q8f_rejects_bad_arguments():
+    from ksq import _lib
+    L = _lib.lib()
+    assert L.ksq_quantize_q8f(2, FAKE, FAKE, 1, 64, None) == 4       # unknown rule
+    assert L.ksq_quantize_q8f(0, FAKE, FAKE, 1, 48, None) == 2       # K % 32
+    assert L.ksq_quantize_q8f(1, FAKE + 4, FAKE, 1, 64, None) == 3   # x alignment
+    assert L.ksq_quantize_q8f(1, None, None, 0, 64, None) == 0       # empty: no-op
+
+
 def test_workspace_size():
     """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K)."""
     from ksq import _lib
@@ -106,6 +121,9 @@ def test_workspace_size():
     assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == 2048 * 128 * 36
     assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == 0
     assert L.ksq_gemm_workspace_size(1, 0, 2048, 4096, 4096) == 2048 * 128 * 36
+    # block_q8f (fp32 d and s): 40-byte blocks
+    assert L.ksq_gemm_workspace_size(0, 6, 2048, 4096, 4096) == 2048 * 128 * 40
+    assert L.ksq_gemm_workspace_size(0, 5, 2048, 4096, 4096) == 0
     # the fused FP16 orientation: the quantised copy of its N x K activations plus an M x N
     # transposition buffer, each 256-byte aligned
     assert L.ksq_gemm_q4_0_fp16_fused_workspace_size(4096, 8, 4096) == 8 * 128 * 36 + 4096 * 8 * 4

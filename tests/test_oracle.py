@@ -657,3 +657,148 @@ def test_q8_1_variant_fused_f16_tree_sum(oracle):
         if hits == 5:
             break
     assert hits == 5
+
+
+# ---- block_q8f: fp32 d_a and s_a (deepseek_v2 operator reference.py:50-73; lm_head kernel.cu:85-107)
+
+def _q8f_fields(blk):
+    blk = np.ascontiguousarray(blk)
+    return blk[0:4].view(np.float32)[0], blk[4:8].view(np.float32)[0], blk[8:40].view(np.int8)
+
+
+def test_quantize_q8f_known_answers(oracle):
+    """Hand-computed blocks: with amax = 127 both rules have d = 1 and differ only in how ties
+    round (reference.py's round(): half to even; lroundf: half away from zero)."""
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, :8] = [127.0, 2.5, -2.5, 3.5, 0.5, -0.5, -126.5, 1.25]
+    d, s, q = _q8f_fields(oracle.quantize_q8f(blk, 0)[0, 0])
+    assert d == 1.0 and s == 5.25
+    assert list(q[:8]) == [127, 2, -2, 4, 0, 0, -126, 1] and not q[8:].any()
+    d, s, q = _q8f_fields(oracle.quantize_q8f(blk, 1)[0, 0])
+    assert d == 1.0 and s == 5.25
+    assert list(q[:8]) == [127, 3, -3, 4, 1, -1, -127, 1] and not q[8:].any()
+    # all-zero block: d = 1 (reference.py: `if a_max > 0 else 1.0`; kernel.cu: a_max > 1e-10)
+    for rule in (0, 1):
+        d, s, q = _q8f_fields(oracle.quantize_q8f(np.zeros((1, 32), np.float32), rule)[0, 0])
+        assert d == 1.0 and s == 0.0 and not q.any()
+
+
+def test_quantize_q8f_tiny_block(oracle):
+    """0 < amax <= 1e-10: the deepseek_v2 rule keeps d = amax/127; the lm_head rule sets d = 1
+    while its scale is 127/1e-10, so the quants stay non-zero (kernel.cu:88-89)."""
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, 0], blk[0, 1] = 1e-12, -4e-13
+    d, _, q = _q8f_fields(oracle.quantize_q8f(blk, 0)[0, 0])
+    assert d == np.float32(1e-12) / np.float32(127.0) and q[0] == 127 and q[1] == -51   # -50.8
+    d, _, q = _q8f_fields(oracle.quantize_q8f(blk, 1)[0, 0])
+    assert d == 1.0 and q[0] == 1 and q[1] == -1                                         # 1.27, -0.508
+
+
+def test_quantize_q8f_fp32_fields_and_sequential_sum(oracle):
+    """d and s are stored as fp32 (no fp16 rounding) and s is the left-to-right fp32 sum: with
+    1e8, seven 1s and -1e8 every 1 is absorbed (the ulp of 1e8 is 8), giving 0 where NumPy's
+    pairwise sum and the exact sum give 7."""
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, :9] = [1e8, 1, 1, 1, 1, 1, 1, 1, -1e8]
+    for rule in (0, 1):
+        _, s, _ = _q8f_fields(oracle.quantize_q8f(blk, rule)[0, 0])
+        assert s == 0.0 and float(np.sum(blk)) == 7.0
+    blk = np.zeros((1, 32), np.float32)
+    blk[0, :2] = [1.0, 0.0001]
+    for rule in (0, 1):
+        d, s, _ = _q8f_fields(oracle.quantize_q8f(blk, rule)[0, 0])
+        assert d != np.float32(np.float16(d)) and s != np.float32(np.float16(s))
+        assert s == np.float32(1.0001) or s == np.float32(1.0) + np.float32(0.0001)
+
+
+def test_quantize_q8f_division_vs_scale(oracle):
+    """The deepseek_v2 rule divides by d (a_val / d_a); the lm_head rule multiplies by 127/amax.
+    Blocks where the two give different integers pin which one each rule uses."""
+    g = np.random.default_rng(61)
+    seen = {0: 0, 1: 0}
+    for _ in range(20000):
+        amax = np.float32(g.uniform(0.5, 2.0))
+        d = np.float32(amax / np.float32(127))
+        scale = np.float32(np.float32(127) / amax)
+        k = int(g.integers(1, 127))
+        x = np.float32((k + 0.5) * d)
+        lo, hi = np.nextafter(x, np.float32(0)), np.nextafter(x, np.float32(9))
+        for cand in (x, lo, hi, np.nextafter(lo, np.float32(0)), np.nextafter(hi, np.float32(9))):
+            by_div = float(np.float32(cand / d))
+            by_mul = float(np.float32(cand * scale))
+            rne_div, away_mul = round(by_div), int(np.floor(by_mul + 0.5))
+            if rne_div != int(np.floor(by_div + 0.5)) or away_mul != round(by_mul):
+                continue   # a tie: covered by the known-answer test
+            b = np.zeros((1, 32), np.float32)
+            b[0, 0], b[0, 1] = amax, cand
+            if round(by_div) != round(by_mul):
+                assert int(_q8f_fields(oracle.quantize_q8f(b, 0)[0, 0])[2][1]) == rne_div
+                assert int(_q8f_fields(oracle.quantize_q8f(b, 1)[0, 0])[2][1]) == away_mul
+                seen[0] += 1
+    assert seen[0] > 0
+
+
+def _int_weights(wtype, g, N, K):
+    """Q4_0 / Q5_0 / Q8_0 weights with d = 1 and their integer values [N, K] decoded by hand
+    from the byte layout (element j < 16 in the low nibble of qs[j], j >= 16 in the high one)."""
+    nb = K // 32
+    if wtype == 0:
+        w = np.zeros((N, nb, 18), np.uint8)
+        w[..., 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+        w[..., 2:18] = g.integers(0, 256, size=(N, nb, 16), dtype=np.uint8)
+        qs = w[..., 2:18].astype(np.int64)
+        vals = np.concatenate([qs & 15, qs >> 4], axis=-1) - 8
+    elif wtype == 5:
+        w = np.zeros((N, nb, 22), np.uint8)
+        w[..., 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+        w[..., 2:22] = g.integers(0, 256, size=(N, nb, 20), dtype=np.uint8)
+        qh = w[..., 2:6].astype(np.int64)
+        hbit = np.stack([(qh[..., j // 8] >> (j % 8)) & 1 for j in range(32)], axis=-1)
+        qs = w[..., 6:22].astype(np.int64)
+        vals = np.concatenate([qs & 15, qs >> 4], axis=-1) + 16 * hbit - 16
+    else:
+        w = np.zeros((N, nb, 34), np.uint8)
+        w[..., 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+        w[..., 2:34] = g.integers(-128, 128, size=(N, nb, 32)).astype(np.int8).view(np.uint8)
+        vals = w[..., 2:34].view(np.int8).astype(np.int64)
+    return w, vals.reshape(N, K)
+
+
+@pytest.mark.parametrize("wtype", [0, 5, 1])
+@pytest.mark.parametrize("rule", [0, 1])
+def test_gemm_q8f_unit_scale_is_integer_matmul(oracle, wtype, rule):
+    """Unit scales (d_w = 1; integer activations with one +-127 per block, so d_a = 1, q_a = x
+    and s_a = sum x exactly): every block term d_w*(d_a*sumi - c*s_a) is the integer
+    sum_k x_k * (q_k - c), so the fp32 oracle must equal x @ values^T exactly."""
+    g = np.random.default_rng(70 + wtype + 10 * rule)
+    M, N, K = 5, 7, 256
+    w, vals = _int_weights(wtype, g, N, K)
+    x = g.integers(-20, 21, size=(M, K // 32, 32)).astype(np.float32)
+    x[:, :, 3] = 127.0
+    x = x.reshape(M, K)
+    a = oracle.quantize_q8f(x, rule)
+    assert np.all(a[..., 0:4].copy().view(np.float32) == 1.0)
+    y = oracle.gemm_q8f(wtype, a, w, M, N, K)
+    want = x.astype(np.int64) @ vals.T
+    assert np.array_equal(y, want.astype(np.float32))
+    assert np.array_equal(oracle.gemm_q8f(wtype, a, w, M, N, K, f64=True), want.astype(np.float64))
+
+
+def test_gemm_q8f_fp32_order_vs_fp64(oracle):
+    """Random scales: the fp32 block-order accumulation stays within fp32 rounding of the fp64 one,
+    and the fp64 one is the dequantised product d_a*q_a . d_w*(q_w - 8) plus the -8*d_w*s_a term
+    computed from the fields in numpy."""
+    from ksq import refcheck
+    g = np.random.default_rng(80)
+    M, N, K = 6, 9, 512
+    x = g.standard_normal((M, K)).astype(np.float32)
+    w = oracle.quantize_q4_0(g.standard_normal((N, K)).astype(np.float32)).reshape(N, K // 32, 18)
+    for rule in (0, 1):
+        a = oracle.quantize_q8f(x, rule)
+        y32 = oracle.gemm_q8f(0, a, w, M, N, K)
+        y64 = oracle.gemm_q8f(0, a, w, M, N, K, f64=True)
+        A, s = refcheck.act_terms(a)
+        d, _, q = refcheck.unpack(0, w)
+        want = A @ (d[..., None] * q).reshape(N, K).T - 8.0 * s @ d.T
+        assert np.allclose(y64, want, rtol=1e-12, atol=1e-9)
+        assert np.max(np.abs(y32 - y64)) <= 1e-5 * np.max(np.abs(y64))
