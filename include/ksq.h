@@ -181,6 +181,28 @@ KSQ_API int ksq_quantize_q8f(int rule, const float* x, uint8_t* y, int M, int K,
 KSQ_API void gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2(const uint8_t* weight, const float* activation, float* output,
                                                      int M, int N, int K);
 
+/* ---- dequantise-then-fp32 GEMM (W4A16 / W8A16) ---------------------------- */
+
+/* C[M][N] = A[M][K] . dequant(B)[N][K]^T with fp32 activations A and Q4_0 (wtype KSQ_W_Q4_0)
+ * or Q8_0 (KSQ_W_Q8_0) weights B [N][K/32], no activation quantisation: the reference's W4A16 /
+ * W8A16 path (gemm_w4a16_naive / gemm_w4a16_tiled / gemm_w8a16_naive, include/gemm_cuda_naive.cuh:
+ * 267-283 and include/gemm_cuda_tiled.cuh:284-291 over the kernels :66-150 and :108-190; CPU
+ * references gemm_w4a16_reference / gemm_w8a16_reference, include/gemm_reference.h:73-147) and
+ * the harness oracle of the fp32-activation definitions (llm_kernel_test/reference/gemm_ref.py:
+ * 51-97).  Every product a * q is exact (bf16 MFMA on a three-term split of each activation);
+ * the fp32 sums round in another order than the reference's loop (agreement within fp32
+ * accumulation error).  Argument order of the reference launchers: A, B, C.  A 16-byte
+ * aligned, finite, |a| < 3.38e38; B and C 4-byte aligned; K % 64 == 0.  workspace: the split-K
+ * partial sums, ksq_gemm_w16_workspace_size(M, N, K) bytes (0 when the grid needs no split), or
+ * NULL for the library's per-device pool.  Returns a ksq_status. */
+KSQ_API size_t ksq_gemm_w16_workspace_size(int M, int N, int K);
+KSQ_API int ksq_gemm_w16(int wtype, const float* A, const uint8_t* B, float* C, int M, int N, int K,
+                         void* workspace, size_t workspace_bytes, void* stream);
+/* The reference launchers' form (stream, pool workspace): gemm_w4a16_naive / gemm_w4a16_tiled
+ * (Q4_0) and gemm_w8a16_naive (Q8_0). */
+KSQ_API int ksq_gemm_w4a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream);
+KSQ_API int ksq_gemm_w8a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream);
+
 /* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the quantised copy of
  * fp32 activations, 0 for pre-quantised activations. */
 KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
@@ -282,6 +304,7 @@ KSQ_API int ksq_set_mmq_config(int config);
 #define KSQ_ENG_MOE_TILE128 (1u << 20)    /* grouped mmq_kernel, 128-row tiles */
 #define KSQ_ENG_MOE_COMBINE (1u << 21)    /* slot-ordered combine of per-entry rows */
 #define KSQ_ENG_TRANSPOSE (1u << 22)      /* output transpose (fused FP16 orientation) */
+#define KSQ_ENG_W16 (1u << 23)            /* w16_kernel (dequantise-then-fp32 GEMM on the bf16 MFMA) */
 KSQ_API uint32_t ksq_debug_last_engines(void);
 
 #ifdef __cplusplus

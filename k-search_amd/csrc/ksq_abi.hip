@@ -335,6 +335,53 @@ int ksq_quantize_q8s(const float* x, uint8_t* y, int M, int K, void* stream) {
     return ok();
 }
 
+size_t ksq_gemm_w16_workspace_size(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int sp = ksq::w16_splits(M, N, K);
+    return sp > 1 ? align256((size_t)sp * (size_t)M * (size_t)N * sizeof(float)) : 0;
+}
+
+int ksq_gemm_w16(int wtype, const float* A, const uint8_t* B, float* C, int M, int N, int K, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+    g_engines = 0;
+    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q8_0)
+        return set_error(KSQ_ERR_TYPE, "the dequantise-then-fp32 GEMM takes Q4_0 or Q8_0 weights (weight type %d)",
+                         wtype);
+    if (M < 0 || N < 0 || K < 0) return set_error(KSQ_ERR_SHAPE, "negative shape M=%d N=%d K=%d", M, N, K);
+    if (K % 64) return set_error(KSQ_ERR_SHAPE, "K=%d is not a multiple of 64", K);
+    if (M == 0 || N == 0) return ok();
+    if (!C) return set_error(KSQ_ERR_NULL, "C is NULL");
+    hipStream_t s = (hipStream_t)stream;
+    if (K == 0) {
+        hipError_t e = ksq::launch_fill_zero(C, (int64_t)M * N, s);
+        return e == hipSuccess ? ok() : hip_error(e, "fill launch");
+    }
+    if (!A || !B) return set_error(KSQ_ERR_NULL, "A or B is NULL");
+    if (((uintptr_t)A & 15u) || ((uintptr_t)B & 3u) || ((uintptr_t)C & 3u))
+        return set_error(KSQ_ERR_ALIGN, "A must be 16-byte aligned, B and C 4-byte aligned");
+    const size_t need = ksq_gemm_w16_workspace_size(M, N, K);
+    void* ws = workspace;
+    if (need) {
+        if (ws) {
+            if (workspace_bytes < need) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", workspace_bytes, need);
+            if ((uintptr_t)ws & 15u) return set_error(KSQ_ERR_ALIGN, "workspace must be 16-byte aligned");
+        } else {
+            int st = pool_get(need, s, &ws);
+            if (st != KSQ_OK) return st;
+        }
+    }
+    hipError_t e = ksq::launch_w16(wtype, A, B, C, M, N, K, need ? (float*)ws : nullptr, s);
+    return e == hipSuccess ? ok() : hip_error(e, "w16 launch");
+}
+
+int ksq_gemm_w4a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream) {
+    return ksq_gemm_w16(KSQ_W_Q4_0, A, B, C, M, N, K, nullptr, 0, stream);
+}
+
+int ksq_gemm_w8a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream) {
+    return ksq_gemm_w16(KSQ_W_Q8_0, A, B, C, M, N, K, nullptr, 0, stream);
+}
+
 int ksq_quantize_q8f(int rule, const float* x, uint8_t* y, int M, int K, void* stream) {
     if (rule != KSQ_Q8F_RNE && rule != KSQ_Q8F_LROUND)
         return set_error(KSQ_ERR_TYPE, "unknown block_q8f quantiser rule %d", rule);

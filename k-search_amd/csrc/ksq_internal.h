@@ -120,6 +120,13 @@ hipError_t launch_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int3
 size_t stream_read_outputs(size_t bytes);
 hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s);
 
+// Dequantise-then-fp32 GEMM (W4A16 / W8A16) on the bf16 MFMA: C[M][N] = A . dequant(W)^T,
+// wtype kWQ40 or kWQ80, K % 64 == 0.  With w16_splits(M, N, K) > 1 it needs `partials`, that
+// many M x N float planes of device scratch.
+int w16_splits(int M, int N, int K);
+hipError_t launch_w16(int wtype, const float* A, const uint8_t* W, float* C, int M, int N, int K, float* partials,
+                      hipStream_t s);
+
 // Fill `n` floats with zero (a kernel, so it can be captured in a graph).
 hipError_t launch_fill_zero(float* p, int64_t n, hipStream_t s);
 

@@ -1,0 +1,289 @@
+// ksq_w16.hip - the dequantise-then-fp32 GEMM (W4A16 / W8A16: fp32 activations, Q4_0 / Q8_0
+// weights, no activation quantisation) on the gfx950 bf16 MFMA.
+//
+// Reference path: gemm_w4a16_naive / gemm_w4a16_tiled / gemm_w8a16_naive
+// (include/gemm_cuda_naive.cuh:66-150, launchers :267-283; include/gemm_cuda_tiled.cuh:108-190,
+// launcher :284-291), CPU references gemm_w4a16_reference / gemm_w8a16_reference
+// (include/gemm_reference.h:73-147) and the harness oracle reference_q4_0_fp32_gemm
+// (llm_kernel_test/reference/gemm_ref.py:51-97): C[m][n] = sum_k A[m][k] * d_w * q_w[n][k] in
+// fp32, with q_w = q - 8 for Q4_0 and the signed quant for Q8_0.
+//
+// gfx950 design:
+//  * Exact products on the bf16 MFMA.  Each fp32 activation is split into three bf16 terms
+//    a = hi + mid + lo (hi = bf16(a), mid = bf16(a - hi), lo = bf16(a - hi - mid)): both
+//    differences are exact in fp32 and the three terms carry all 24 significant bits (finite
+//    |a| below the largest bf16).  The weight quants (q - 8 for Q4_0, q for Q8_0) are integers
+//    of at most 8 bits, exact in bf16.  So every product of v_mfma_f32_32x32x16_bf16 is exact
+//    and only the fp32 sums round, as in the reference's fp32 loop (in another order).  The
+//    terms go in smallest first: lo, mid, hi.
+//  * The K loop steps over two 32-element blocks.  Per block, six MFMAs (two 16-element halves
+//    x three terms) give the block's partial sum P = sum_k a_k q_k for a 32 x 32 patch, then
+//    acc = fma(d_w, P, acc): one VALU op per output and block (the reference multiplies d_w into
+//    every weight element instead; the same value up to rounding).
+//  * Staging: the activation tile is converted to the three bf16 planes and the weight quants
+//    to bf16 once per workgroup and K step, into LDS (row pitch 144 bytes: the 16-byte fragment
+//    reads of 16 consecutive rows hit distinct banks).  The next step's global loads are issued
+//    into registers before the current step's MFMAs.
+//  * Tiles: 128 x 128 (four waves of 64 x 64) for M > 32; 32 x 128 (four waves side by side)
+//    for M <= 32.  Grids below 256 workgroups are split along K; the partial sums are added in
+//    split order by the int8 GEMM's split-K reduction (deterministic).
+//  * Rows / columns past M or N load a clamped in-range row and are not stored.
+#include "ksq_device.h"
+#include "ksq_internal.h"
+
+namespace ksq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+template <int BM_, int BN_, int TM_, int TN_>
+struct W16Tile {
+    static constexpr int BM = BM_, BN = BN_, TM = TM_, TN = TN_;
+    static constexpr int WN = BN / (32 * TN);   // waves along N
+    static constexpr int WM = BM / (32 * TM);   // waves along M
+    static_assert(WN * WM == 4, "four waves per workgroup");
+    static_assert(BN == 128, "the weight staging maps 128 rows x 2 blocks onto 256 threads");
+    static_assert(BM % 16 == 0 && BM * 16 % 256 == 0, "the activation staging maps 16 float4 per row");
+};
+using W16Big = W16Tile<128, 128, 2, 2>;
+using W16Skinny = W16Tile<32, 128, 1, 1>;
+
+constexpr int kW16Pitch = 72;         // bf16 per staged row: 64 values of the step + 8 padding
+
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+__device__ __forceinline__ float bf16_low_f32(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+__device__ __forceinline__ float bf16_high_f32(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
+
+// 32 weight quants of one block as bf16 into dst (32 values), the block's scale into *d.  v: the
+// dwords holding the block, which starts at byte O of v.
+template <int WT, int O>
+__device__ __forceinline__ void w16_stage_block(const uint32_t* v, uint16_t* dst, float* d) {
+    *d = f16_to_f32(half_at(v, O));
+    if constexpr (WT == kWQ40) {
+        // element e < 16: low nibble of qs[e]; e >= 16: high nibble of qs[e - 16]; value q - 8
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t w = word_at(v, O + 2 + 4 * i);
+            float lo[4], hi[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                lo[b] = (float)((w >> (8 * b)) & 0x0Fu) - 8.0f;
+                hi[b] = (float)((w >> (8 * b + 4)) & 0x0Fu) - 8.0f;
+            }
+            *(u32x2*)(dst + 4 * i) = u32x2{bf16_pair(lo[0], lo[1]), bf16_pair(lo[2], lo[3])};
+            *(u32x2*)(dst + 16 + 4 * i) = u32x2{bf16_pair(hi[0], hi[1]), bf16_pair(hi[2], hi[3])};
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t w = word_at(v, O + 2 + 4 * i);
+            float q[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) q[b] = (float)(int8_t)((w >> (8 * b)) & 0xFFu);
+            *(u32x2*)(dst + 4 * i) = u32x2{bf16_pair(q[0], q[1]), bf16_pair(q[2], q[3])};
+        }
+    }
+}
+
+// WT: kWQ40 or kWQ80.  W: [N][K/32] blocks (4-byte aligned); A: fp32 [M][K] (16-byte aligned);
+// C: fp32 [M][N], or split z's partial [M][N] at C + z*M*N.  nb = K/32, even.
+template <class T, int WT>
+__global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__ W, const float* __restrict__ A,
+                                                     float* __restrict__ C, int M, int N, int nb) {
+    constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, P = kW16Pitch;
+    constexpr int BB = block_bytes(WT);                    // 18 or 34
+    constexpr int AC = BM * 16 / 256;                      // activation float4 chunks per thread
+    constexpr int WW = (WT == kWQ40) ? 5 : 9;              // weight dwords a thread loads per step
+    __shared__ __attribute__((aligned(16))) uint16_t sA[3][BM][P];     // lo, mid, hi planes
+    __shared__ __attribute__((aligned(16))) uint16_t sW[BN][P];
+    __shared__ __attribute__((aligned(16))) float sD[2][BN];
+
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = wave / T::WN, wn = wave % T::WN;
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int m0 = (int)blockIdx.y * BM, n0 = (int)blockIdx.x * BN;
+
+    // split z covers K steps [s_lo, s_hi) of two blocks each
+    const int nsteps = nb / 2, Z = (int)gridDim.z, z = (int)blockIdx.z;
+    const int s_lo = (int)((long long)nsteps * z / Z), s_hi = (int)((long long)nsteps * (z + 1) / Z);
+    C += (size_t)z * (size_t)M * (size_t)N;
+    const size_t K = (size_t)nb * 32;
+
+    // staging assignment: activation chunk c = t + 256 i is row c / 16, float4 c % 16 of the
+    // step's 64 floats (16 lanes read 256 contiguous bytes of a row); weight row t % 128,
+    // block t / 128 of the step (wave-uniform)
+    const int wr = t % BN, wb = t / BN;
+    const uint8_t* wrow = W + (size_t)min(n0 + wr, N - 1) * nb * BB;
+    f32x4 pa[AC];
+    uint32_t pw[WW];
+    auto load = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < AC; i++) {
+            const int c = t + 256 * i, r = c >> 4, q = c & 15;
+            pa[i] = *(const f32x4*)(A + (size_t)min(m0 + r, M - 1) * K + (size_t)s * 64 + 4 * q);
+        }
+        // Q4_0: the step's 36 bytes are dwords 0..8 and block wb starts at byte 18 wb, so dwords
+        // 4 wb .. 4 wb + 4 hold it from byte 2 wb on; Q8_0: 68 bytes, block wb at byte 34 wb,
+        // dwords 8 wb .. 8 wb + 8, from byte 2 wb on
+        const uint32_t* src = (const uint32_t*)(wrow + (size_t)s * 2 * BB) + (WT == kWQ40 ? 4 : 8) * wb;
+#pragma unroll
+        for (int i = 0; i < WW; i++) pw[i] = src[i];
+    };
+    auto store = [&]() {
+#pragma unroll
+        for (int i = 0; i < AC; i++) {
+            const int c = t + 256 * i, r = c >> 4, q = c & 15;
+            const float a[4] = {pa[i].x, pa[i].y, pa[i].z, pa[i].w};
+            uint32_t ph[2], pm[2], pl[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                ph[j] = bf16_pair(a[2 * j], a[2 * j + 1]);
+                const float r0 = a[2 * j] - bf16_low_f32(ph[j]), r1 = a[2 * j + 1] - bf16_high_f32(ph[j]);
+                pm[j] = bf16_pair(r0, r1);
+                pl[j] = bf16_pair(r0 - bf16_low_f32(pm[j]), r1 - bf16_high_f32(pm[j]));
+            }
+            *(u32x2*)&sA[0][r][4 * q] = u32x2{pl[0], pl[1]};
+            *(u32x2*)&sA[1][r][4 * q] = u32x2{pm[0], pm[1]};
+            *(u32x2*)&sA[2][r][4 * q] = u32x2{ph[0], ph[1]};
+        }
+        if (wb == 0) w16_stage_block<WT, 0>(pw, &sW[wr][0], &sD[0][wr]);
+        else w16_stage_block<WT, 2>(pw, &sW[wr][32], &sD[1][wr]);
+    };
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    f32x16 zero;
+#pragma unroll
+    for (int r = 0; r < 16; r++) zero[r] = 0.0f;
+    const bool wave_has_rows = M - m0 - wm * 32 * TM > 0;   // wave-uniform
+
+    if (s_lo < s_hi) load(s_lo);
+    for (int s = s_lo; s < s_hi; s++) {
+        store();
+        __syncthreads();
+        if (s + 1 < s_hi) load(s + 1);
+        if (wave_has_rows) {
+#pragma unroll
+            for (int kb = 0; kb < 2; kb++) {
+                bf16x8 wf[TN][2], af[3][TM][2];
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int ko = 32 * kb + 16 * h + 8 * hi;
+#pragma unroll
+                    for (int j = 0; j < TN; j++) wf[j][h] = *(const bf16x8*)&sW[wn * 32 * TN + 32 * j + l32][ko];
+#pragma unroll
+                    for (int e = 0; e < 3; e++)
+#pragma unroll
+                        for (int i = 0; i < TM; i++) af[e][i][h] = *(const bf16x8*)&sA[e][wm * 32 * TM + 32 * i + l32][ko];
+                }
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int nbase = wn * 32 * TN + 32 * j + 4 * hi;
+                    f32x4 dw[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) dw[q] = *(const f32x4*)&sD[kb][nbase + 8 * q];
+#pragma unroll
+                    for (int i = 0; i < TM; i++) {
+                        // the MFMA computes D[n][m]: A operand = weight fragment, B = activations
+                        f32x16 p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][0], af[0][i][0], zero, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][1], af[0][i][1], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][0], af[1][i][0], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][1], af[1][i][1], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][0], af[2][i][0], p, 0, 0, 0);
+                        p = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[j][1], af[2][i][1], p, 0, 0, 0);
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+#pragma unroll
+                            for (int r = 0; r < 4; r++)
+                                acc[i][j][4 * q + r] = fmaf(dw[q][r], p[4 * q + r], acc[i][j][4 * q + r]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // lane l holds activation row m = l % 32 and weight rows n = 8 (r / 4) + 4 (l / 32) + r % 4
+    const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int gm = m0 + wm * 32 * TM + 32 * i + l32;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int nbase = n0 + wn * 32 * TN + 32 * j + 4 * hi;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int gn = nbase + 8 * q;
+                if (vec_ok && gn + 3 < N) {
+                    *(f32x4*)(C + (size_t)gm * N + gn) =
+                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        if (gn + r < N) C[(size_t)gm * N + gn + r] = acc[i][j][4 * q + r];
+                }
+            }
+        }
+    }
+}
+
+namespace {
+constexpr int kW16MinWGs = 256, kW16TargetWGs = 512, kW16MaxSplits = 16;
+
+bool w16_skinny(int M) { return M <= 32; }
+
+int w16_grid_wgs(int M, int N) {
+    const int bm = w16_skinny(M) ? W16Skinny::BM : W16Big::BM;
+    return ((N + 127) / 128) * ((M + bm - 1) / bm);
+}
+}  // namespace
+
+int w16_splits(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 1;
+    const int wgs = w16_grid_wgs(M, N), steps = K / 64;
+    if (wgs >= kW16MinWGs) return 1;
+    int sp = (kW16TargetWGs + wgs - 1) / wgs;
+    sp = sp < steps / 4 ? sp : steps / 4;            // at least 4 K steps per split
+    sp = sp < kW16MaxSplits ? sp : kW16MaxSplits;
+    return sp < 1 ? 1 : sp;
+}
+
+template <int WT>
+static hipError_t w16_launch(const float* A, const uint8_t* W, float* C, int M, int N, int K, int splits,
+                             hipStream_t s) {
+    const int nb = K / 32;
+    if (w16_skinny(M)) {
+        const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32), (unsigned)splits);
+        hipLaunchKernelGGL((w16_kernel<W16Skinny, WT>), grid, dim3(256), 0, s, W, A, C, M, N, nb);
+    } else {
+        const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), (unsigned)splits);
+        hipLaunchKernelGGL((w16_kernel<W16Big, WT>), grid, dim3(256), 0, s, W, A, C, M, N, nb);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_w16(int wtype, const float* A, const uint8_t* W, float* C, int M, int N, int K, float* partials,
+                      hipStream_t s) {
+    if (wtype != kWQ40 && wtype != kWQ80) return hipErrorNotSupported;
+    const int splits = w16_splits(M, N, K);
+    note_engine(KSQ_ENG_W16 | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
+    float* out = C;
+    if (splits > 1) {
+        if (!partials) return hipErrorInvalidValue;
+        out = partials;
+    }
+    hipError_t e = wtype == kWQ40 ? w16_launch<kWQ40>(A, W, out, M, N, K, splits, s)
+                                  : w16_launch<kWQ80>(A, W, out, M, N, K, splits, s);
+    if (e != hipSuccess || splits == 1) return e;
+    return launch_splitk_reduce(partials, C, (int64_t)M * N, splits, s);
+}
+
+}  // namespace ksq

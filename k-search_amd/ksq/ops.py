@@ -56,6 +56,24 @@ def gemm(wtype: int, atype: int, weight: torch.Tensor, activation: torch.Tensor,
     return out
 
 
+def gemm_w16(wtype: int, activation: torch.Tensor, weight: torch.Tensor, M: int, N: int, K: int,
+             out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The dequantise-then-fp32 GEMM (W4A16 / W8A16): output[M, N] = activation[M, K] (fp32) .
+    dequant(weight)[N, K]^T for Q4_0 / Q8_0 weights, through ksq_gemm_w16."""
+    if activation.dtype != torch.float32 or not activation.is_cuda or not weight.is_cuda:
+        raise RuntimeError("gemm_w16 expects a CUDA float32 activation and CUDA uint8 weights")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=weight.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    check(lib().ksq_gemm_w16(wtype, _ptr(activation.contiguous()), _ptr(weight), _ptr(out), M, N, K,
+                             _ptr(workspace), ws_bytes, _stream()))
+    return out
+
+
+def gemm_w16_workspace_size(M: int, N: int, K: int) -> int:
+    return lib().ksq_gemm_w16_workspace_size(M, N, K)
+
+
 def gemm_q4_0_fp16_fused(weight: torch.Tensor, activation: torch.Tensor, M: int, N: int, K: int,
                          out: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """The reference's gemm_q4_0_fp16_fused orientation: Q4_0 weight [M, K/32] (M weight rows),
@@ -223,5 +241,5 @@ def release() -> None:
     lib().ksq_release()
 
 
-__all__ = ["ENTRY_POINTS", "gemm", "forward", "quantize_q8_1", "quantize_q8s", "quantize_q8f", "block_sumi", "last_engines", "set_path",
+__all__ = ["ENTRY_POINTS", "gemm", "gemm_w16", "gemm_w16_workspace_size", "forward", "quantize_q8_1", "quantize_q8s", "quantize_q8f", "block_sumi", "last_engines", "set_path",
            "workspace_size", "moe_gemm", "moe_gemm_routed", "moe_workspace_size", "release", "_lib"]

@@ -30,6 +30,15 @@
  *   Q4_1 / Q5_0 / Q5_1   numpy restatement of the harness formula
  *                        (gemm_ref.py:274-330), dequantise-then-fp64-dot,
  *                        known-answer blocks for the nibble and qh bit order
+ *   W4A16 / W8A16        integer-valued inputs against an exact integer matmul
+ *                        (pins the element order of the nibbles), the reference's
+ *                        interleaved summation order (a cancellation case where
+ *                        k-ascending order differs), fp64 dequantised matmul
+ *   block_q8f quantisers hand-computed blocks: ties (half-even vs away), zero
+ *                        and tiny blocks (the lm_head rule's d = 1 with non-zero
+ *                        quants), fp32 fields, the sequential sum (a block where
+ *                        pairwise and exact sums differ), division vs 127/amax
+ *   block_q8f GEMM       unit scales against the integer matmul, fp64 closed form
  *   native W8A8C8        closed-form quantiser checks (ties, tiny blocks -> d = 1,
  *                        true division vs reciprocal), per-block composition
  *   Q8_1 variants        device kernel: numpy rint/cumsum restatement, ties,
@@ -695,6 +704,64 @@ KSQ_API void ksq_ref_gemm_q8_0_q8s_f64(const uint8_t* A, const uint8_t* W, doubl
                 float d_a;
                 memcpy(&d_a, ab, 4);
                 sum += (double)rd_f16(wb) * (double)d_a * (double)ksq_ref_sumi_q8_0_q8_1(wb, ab);
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Dequantise-then-fp32 GEMMs (W4A16 / W8A16): fp32 activations, no         */
+/* activation quantisation.                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* gemm_w4a16_reference (include/gemm_reference.h:73-112): per output, fp32 sum over the
+ * blocks in order and, inside a block, k = 0..15 adding element k (low nibble of qs[k]) then
+ * element k + 16 (high nibble): w = (q - 8) * d; sum += A * w (product, then sum). */
+KSQ_API void ksq_ref_gemm_w4a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, int nthreads) {
+    const int nb = K / 32;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* blk = B + ((int64_t)j * nb + b) * 18;
+                const float d = rd_f16(blk);
+                const float* a = A + (int64_t)i * K + 32 * b;
+                for (int k = 0; k < 16; k++) {
+                    const float w0 = (float)((blk[2 + k] & 0x0F) - 8) * d;
+                    const float w1 = (float)((blk[2 + k] >> 4) - 8) * d;
+                    sum += a[k] * w0;
+                    sum += a[k + 16] * w1;
+                }
+            }
+            C[(int64_t)i * N + j] = sum;
+        }
+    }
+}
+
+/* gemm_w8a16_reference (include/gemm_reference.h:120-147): w = qs[k] * d; sum += A * w, k
+ * ascending, blocks in order. */
+KSQ_API void ksq_ref_gemm_w8a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, int nthreads) {
+    const int nb = K / 32;
+    (void)nthreads;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) collapse(2)
+#endif
+    for (int i = 0; i < M; i++) {
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            for (int b = 0; b < nb; b++) {
+                const uint8_t* blk = B + ((int64_t)j * nb + b) * 34;
+                const float d = rd_f16(blk);
+                const float* a = A + (int64_t)i * K + 32 * b;
+                for (int k = 0; k < 32; k++) {
+                    const float w = (float)(int8_t)blk[2 + k] * d;
+                    sum += a[k] * w;
+                }
             }
             C[(int64_t)i * N + j] = sum;
         }

@@ -69,6 +69,8 @@ def lib() -> ctypes.CDLL:
         L.ksq_ref_gemm_w8a8c8.argtypes = [P, P, P, i32, i32, i32, i32]
         L.ksq_ref_gemm_q8_0_q8s_f64.argtypes = [P, P, P, i32, i32, i32, i32]
         L.ksq_ref_quantize_row_q8f.argtypes = [i32, P, P, i64]
+        L.ksq_ref_gemm_w4a16.argtypes = [P, P, P, i32, i32, i32, i32]
+        L.ksq_ref_gemm_w8a16.argtypes = [P, P, P, i32, i32, i32, i32]
         L.ksq_ref_gemm_q8f.argtypes = [i32, P, P, P, i32, i32, i32, i32]
         L.ksq_ref_gemm_q8f_f64.argtypes = [i32, P, P, P, i32, i32, i32, i32]
         L.ksq_ref_q4_K_scale_min.argtypes = [i32, P, P, P]
@@ -208,6 +210,17 @@ def gemm_q8s_f64(a_q8s: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthre
 
 
 Q8F_RNE, Q8F_LROUND = 0, 1
+
+
+def gemm_w16(wtype: int, x: np.ndarray, w: np.ndarray, M: int, N: int, K: int, nthreads: int = 0) -> np.ndarray:
+    """gemm_w4a16_reference (wtype 0, Q4_0) / gemm_w8a16_reference (wtype 1, Q8_0): fp32 activations
+    times dequantised weights, the reference's fp32 summation order."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    C = np.empty((M, N), dtype=np.float32)
+    fn = lib().ksq_ref_gemm_w4a16 if wtype == W_Q4_0 else lib().ksq_ref_gemm_w8a16
+    fn(_p(x), _p(w), _p(C), M, N, K, nthreads or max_threads())
+    return C
 
 
 def quantize_q8f(x: np.ndarray, rule: int) -> np.ndarray:

@@ -802,3 +802,46 @@ def test_gemm_q8f_fp32_order_vs_fp64(oracle):
         want = A @ (d[..., None] * q).reshape(N, K).T - 8.0 * s @ d.T
         assert np.allclose(y64, want, rtol=1e-12, atol=1e-9)
         assert np.max(np.abs(y32 - y64)) <= 1e-5 * np.max(np.abs(y64))
+
+
+# ---- W4A16 / W8A16 dequantise-then-fp32 (gemm_reference.h:73-147)
+
+@pytest.mark.parametrize("wtype", [0, 1])
+def test_gemm_w16_integer_inputs_exact(oracle, wtype):
+    """Integer activations and d = 1: every product and partial sum is an exact integer, so the
+    oracle must equal the integer matmul with the weights decoded by hand (pins which nibble is
+    which element: element k < 16 = low nibble of qs[k], k >= 16 = high nibble of qs[k - 16])."""
+    g = np.random.default_rng(90 + wtype)
+    M, N, K = 4, 6, 320
+    w, vals = _int_weights(wtype, g, N, K)
+    x = g.integers(-50, 51, size=(M, K)).astype(np.float32)
+    assert np.array_equal(oracle.gemm_w16(wtype, x, w, M, N, K), (x.astype(np.int64) @ vals.T).astype(np.float32))
+
+
+def test_gemm_w4a16_interleaved_order(oracle):
+    """gemm_w4a16_reference adds element k then element k + 16 (k = 0..15), not k ascending:
+    with A[0] = 1e8, A[16] = 1, A[1] = -1e8 and every dequantised weight 1, its fp32 sum is
+    1e8 + 1 -> 1e8 (absorbed), then - 1e8 -> 0, where ascending order gives 1."""
+    w = np.zeros((1, 1, 18), np.uint8)
+    w[0, 0, 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    w[0, 0, 2:18] = 0x99                      # every quant 9: value 9 - 8 = 1
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0], x[0, 16], x[0, 1] = 1e8, 1.0, -1e8
+    assert oracle.gemm_w16(0, x, w, 1, 1, 32)[0, 0] == 0.0
+    assert float(np.float32(np.float32(1e8) - np.float32(1e8)) + np.float32(1.0)) == 1.0
+
+
+@pytest.mark.parametrize("wtype", [0, 1])
+def test_gemm_w16_vs_dequantised_matmul(oracle, wtype):
+    """Random fp32 activations: the oracle's fp32 loop within fp32 accumulation error of the fp64
+    product of the activations with the weights dequantised in numpy (gemm_ref.py:51-97's form)."""
+    from ksq import refcheck
+    g = np.random.default_rng(95 + wtype)
+    M, N, K = 5, 7, 1024
+    x = g.standard_normal((M, K)).astype(np.float32)
+    quant = oracle.quantize_q4_0 if wtype == 0 else oracle.quantize_q8_0
+    w = quant(g.standard_normal((N, K)).astype(np.float32)).reshape(N, K // 32, -1)
+    ref = x.astype(np.float64) @ refcheck.dequantize(wtype, w).T
+    y = oracle.gemm_w16(wtype, x, w, M, N, K)
+    bound = np.abs(x.astype(np.float64)) @ np.abs(refcheck.dequantize(wtype, w)).T
+    assert np.all(np.abs(y - ref) <= 2.0 ** -24 * K * bound)
