@@ -147,8 +147,12 @@ KSQ_API int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, in
  * 311-338) in its orientation: Q4_0 weight [M][K/32] (M weight rows), fp16 activations [N][K]
  * (uint16 bits, 16-byte aligned), output fp32 [M][N] (weight-row major).  Activations are
  * quantised by its quantize_fp16_to_q8_1_smem rules (KSQ_Q81_FUSED_F16, bit-exact), block
- * dots bit-exact.  workspace: ksq_gemm_q4_0_fp16_fused_workspace_size(M, N, K) bytes of device
- * memory, 256-byte aligned, or NULL for the library's per-device pool (which may allocate). */
+ * dots bit-exact.  For decode shapes (N <= 2 activation rows) the quantisation runs inside the
+ * decode kernel's workgroups, into LDS, as the reference's fused kernel does (one launch, no
+ * workspace used); with the int8 MFMA GEMM the activations are quantised once and the GEMM
+ * writes the [M][N] output directly.  workspace: ksq_gemm_q4_0_fp16_fused_workspace_size(M, N,
+ * K) bytes of device memory (an upper bound), 256-byte aligned, or NULL for the library's
+ * per-device pool (which may allocate). */
 KSQ_API size_t ksq_gemm_q4_0_fp16_fused_workspace_size(int M, int N, int K);
 KSQ_API int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output,
                                      int M, int N, int K, void* workspace, size_t workspace_bytes,

@@ -295,8 +295,12 @@ size_t ksq_gemm_q4_0_fp16_fused_workspace_size(int M, int N, int K) {
 
 int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activation, float* output, int M, int N,
                              int K, void* workspace, size_t workspace_bytes, void* stream) {
-    // the reference's orientation: M weight rows, N activation rows, output [M][N]; computed as
-    // ksq_gemm's [N][M] into the workspace, then transposed
+    // the reference's orientation: M weight rows, N activation rows, output [M][N].  Routes:
+    //  * decode shapes (N <= 2): the decode kernel quantises the fp16 activations in LDS inside
+    //    every workgroup and writes the [M][N] output directly (one launch, no workspace);
+    //  * the int8 MFMA GEMM without split-K: quantise once into the workspace, then the GEMM
+    //    writes its tile transposed, straight into [M][N];
+    //  * otherwise ksq_gemm's [N][M] into the workspace, then a transpose.
     g_engines = 0;
     int st = check_common(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, output, N, M, K);
     if (st != KSQ_OK) return st;
@@ -306,7 +310,12 @@ int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activat
         hipError_t e = ksq::launch_fill_zero(output, (int64_t)M * N, s);
         return e == hipSuccess ? ok() : hip_error(e, "fill launch");
     }
-    const size_t gws = align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K));
+    const bool mmq = use_mmq(KSQ_W_Q4_0, N, M, K, weight, true);
+    if (!mmq && g_path != 3 && ksq::gemv_fused_profitable(KSQ_W_Q4_0, N, M, K, weight, true)) {
+        hipError_t e = ksq::launch_gemv_fused(KSQ_W_Q4_0, ksq::kAQ81, true, weight, fp16_activation, output, N, M, K,
+                                              /*ldc=*/1, /*ldr=*/N, s);
+        return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
+    }
     const size_t need = ksq_gemm_q4_0_fp16_fused_workspace_size(M, N, K);
     void* p = workspace;
     if (p) {
@@ -316,6 +325,15 @@ int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activat
         st = pool_get(need, s, &p);
         if (st != KSQ_OK) return st;
     }
+    if (mmq && ksq::mmq_splits(KSQ_W_Q4_0, N, M, K) == 1) {
+        uint8_t* aq = (uint8_t*)p;
+        hipError_t e = ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, fp16_activation, aq, N, K, s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+        g_engines |= KSQ_ENG_QUANTIZE;
+        e = ksq::launch_mmq(KSQ_W_Q4_0, ksq::kAQ81, weight, aq, output, N, M, K, nullptr, s, /*trans=*/true);
+        return e == hipSuccess ? ok() : hip_error(e, "mmq launch");
+    }
+    const size_t gws = align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K));
     float* tmp = (float*)((uint8_t*)p + gws);
     st = ksq_gemm(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, tmp, N, M, K, gws ? p : nullptr, gws, stream);
     if (st != KSQ_OK) return st;
@@ -415,10 +433,13 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
     }
     const uint8_t* Aq = (const uint8_t*)activation;
     const int afmt = atype_fmt(atype);
-    if (atype_f32(atype) && !atype_q8f(atype) && ksq::gemv_fused_profitable(wtype, M, N, K, weight) &&
+    // decode shapes: the activations are quantised inside every workgroup of the decode kernel
+    // (fp32, or fp16 by the fused FP16 kernels' rules), no quantise launch and no workspace
+    const bool xh = atype == KSQ_A_F16;
+    if (((atype_f32(atype) && !atype_q8f(atype)) || xh) && ksq::gemv_fused_profitable(wtype, M, N, K, weight, xh) &&
         !use_mmq(wtype, M, N, K, weight, true) && g_path != 3) {
-        hipError_t e = ksq::launch_gemv_f32(wtype, afmt, (const uint8_t*)weight, (const float*)activation, output, M,
-                                            N, K, s);
+        hipError_t e = ksq::launch_gemv_fused(wtype, afmt, xh, (const uint8_t*)weight, activation, output, M, N, K, N,
+                                              1, s);
         return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
     }
     // fp32 / fp16 activations are quantised to the start of the (16-byte aligned) workspace,

@@ -159,6 +159,72 @@ __device__ __forceinline__ void quantize_block_q8s(const float* v, uint32_t* out
     }
 }
 
+// Quantise 32 values (fp16 inputs widened to fp32) to one block_q8_1 by the fused FP16 kernels'
+// rules (quantize_fp16_to_q8_1_smem, kernels/gemm/gemm_fused.cuh:76-145): max |x| and the sum
+// by the shared-memory tree (pairs 16, 8, 4, 2 apart, then element 0 with element 1),
+// d = max / 127, ds = (half(d), half(sum)), id = 1 / half(d) (0 when half(d) is 0),
+// q = roundf(x * id) saturated to int8, then clamped to [-127, 127].
+__device__ __forceinline__ void quantize_block_q8_1_f16tree(const float* v, uint32_t* out) {
+#pragma clang fp contract(off)
+    float m[32], t[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) {
+        m[j] = __builtin_fabsf(v[j]);
+        t[j] = v[j];
+    }
+#pragma unroll
+    for (int w = 16; w >= 2; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) {
+            m[j] = __builtin_fmaxf(m[j], m[j + w]);
+            t[j] += t[j + w];
+        }
+    const float d = __builtin_fmaxf(m[0], m[1]) / 127.0f;
+    const float sum = t[0] + t[1];
+    const uint32_t dh = f32_to_f16(d);
+    out[0] = dh | (f32_to_f16(sum) << 16);
+    const float dr = f16_to_f32(dh);
+    const float id = (dr != 0.0f) ? 1.0f / dr : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float r = roundf(v[4 * i + k] * id);
+            int q = (r != r) ? 0 : (int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+            q = q < -127 ? -127 : q;
+            w |= (uint32_t)(q & 0xFF) << (8 * k);
+        }
+        out[1 + i] = w;
+    }
+}
+
+// 32 consecutive activations starting at element `off` of X, as fp32: X holds fp32 values, or
+// fp16 bit patterns when XH (16-byte aligned either way).
+template <bool XH>
+__device__ __forceinline__ void load_x32(const void* X, size_t off, float* x) {
+    if constexpr (XH) {
+        const u32x4* src = (const u32x4*)((const uint16_t*)X + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const u32x4 w = src[i];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                x[8 * i + 2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                x[8 * i + 2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    } else {
+        const f32x4* src = (const f32x4*)((const float*)X + off);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f32x4 q = src[i];
+            x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+        }
+    }
+}
+
 // Quantise 32 floats to one block_q8f (fp32 d and s).  out[0] = d bits, out[1] = s bits,
 // out[2..9] = quants.  s is the sequential fp32 sum in both rules.
 //   RNE (deepseek_v2/w4a32c8_q4_0_fp32_int8/reference.py:50-73, float32 scalar arithmetic

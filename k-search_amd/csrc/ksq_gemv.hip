@@ -224,7 +224,11 @@ __device__ __forceinline__ void wave_copy_to_lds(const uint8_t* __restrict__ g, 
 //   kAFQ   the activations arrive as fp32 and every workgroup quantises the K tile's blocks
 //          itself into LDS while its weight DMA is in flight (the same device quantiser as
 //          ksq_quantize.hip, so the blocks are bit-identical); no separate quantise launch
-constexpr int kAL2 = 0, kADMA = 1, kAFQ = 2;
+//   kAFQH  the same from fp16 activations, by the fused FP16 kernels' quantiser
+//          (kernels/gemm/gemm_fused.cuh:76-145; their kernel :158-310 quantises its activation
+//          columns into shared memory the same way)
+constexpr int kAL2 = 0, kADMA = 1, kAFQ = 2, kAFQH = 3;
+__host__ __device__ constexpr bool is_fq(int amode) { return amode == kAFQ || amode == kAFQH; }
 constexpr int kMaxL2Rows = 2, kMaxFusedRows = 2;
 // With 1-2 activation rows kAL2 reads each row once per wave, i.e. 4x the activation bytes of
 // kADMA, as many bytes again as the weights for M = 1.  Shorter rows are latency-bound and kAL2
@@ -259,10 +263,11 @@ __device__ __forceinline__ void wave_copy_part(const uint8_t* g, uint8_t* dst, i
 // (and its weight copy) and add their partial sums through LDS at the end; with 8 every
 // wave owns 2 rows, so each activation block it reads serves both.
 // AS: the activations are block_q8s (fp32 scale, no sum) instead of block_q8_1.
-// Ain: block_q8_1 / block_q8s bytes [MR][nb] (kAL2, kADMA) or fp32 [MR][32 nb] (kAFQ).
+// Ain: block_q8_1 / block_q8s bytes [MR][nb] (kAL2, kADMA), fp32 [MR][32 nb] (kAFQ) or fp16
+// [MR][32 nb] (kAFQH).  Output C[m * ldc + row * ldr].
 template <int WT, int MR, int AMODE, bool AS, int RPW>
 __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
-                                                       float* __restrict__ C, int N, int nb, int KT, int ldc) {
+                                                       float* __restrict__ C, int N, int nb, int KT, int ldc, int ldr) {
     static_assert(RPW == 1 || RPW == 2 || RPW == 4 || RPW == 8, "1, 2, 4 or 8 rows per workgroup");
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
     constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
@@ -312,20 +317,15 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
                 ashift[m] = (int)((uintptr_t)g & 15);
                 if ((m & 3) == wave) wave_copy_to_lds(g, areg + m * apitch + ashift[m], kt * kQ81Bytes, lane);
             }
-        } else if constexpr (AMODE == kAFQ) {
-            const float* X = (const float*)Ain;
+        } else if constexpr (is_fq(AMODE)) {
             const int K = nb * 32;
             for (int v = threadIdx.x; v < MR * kt; v += 256) {
                 const int m = v / kt, u = v - m * kt;
-                const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)(kt0 + u) * 32);
                 float x[32];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const f32x4 q = src[i];
-                    x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
-                }
+                load_x32<AMODE == kAFQH>(Ain, (size_t)m * K + (size_t)(kt0 + u) * 32, x);
                 uint32_t blk[9];
                 if constexpr (AS) quantize_block_q8s(x, blk);
+                else if constexpr (AMODE == kAFQH) quantize_block_q8_1_f16tree(x, blk);
                 else quantize_block_q8_1(x, blk);
                 uint32_t* dst = (uint32_t*)(areg + m * apitch + u * kQ81Bytes);
 #pragma unroll
@@ -437,7 +437,7 @@ __global__ __launch_bounds__(256) void gemv_row_kernel(const uint8_t* __restrict
         for (int v = 0; v < VR; v++)
             if (row0 + v < N) {
 #pragma unroll
-                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + (size_t)(row0 + v) * ldr] = acc[v][m];
             }
     }
 }
@@ -903,10 +903,11 @@ __global__ __launch_bounds__(256) void gemv_direct_kq_kernel(const uint8_t* __re
 // first issues the loads of its first weight pair, the workgroup then quantises the MR
 // activation rows into LDS (hiding the weight latency), and after one barrier the lanes walk
 // their pairs with the activation blocks read from LDS.  RPW 8: two rows per wave, halving
-// the quantisation each row costs.
-template <int WT, int MR, bool AS, int RPW>
-__global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __restrict__ W, const float* __restrict__ X,
-                                                             float* __restrict__ C, int N, int nb, int ldc) {
+// the quantisation each row costs.  XH: X holds fp16 activations, quantised by the fused FP16
+// kernels' rules.  Output C[m * ldc + row * ldr].
+template <int WT, int MR, bool AS, int RPW, bool XH>
+__global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __restrict__ W, const void* __restrict__ X,
+                                                             float* __restrict__ C, int N, int nb, int ldc, int ldr) {
     static_assert(!is_kquant(WT) && (MR == 1 || MR == 2), "32-element block types, 1-2 activation rows");
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
     constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
@@ -925,15 +926,11 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
     const int K = nb * 32;
     for (int t = threadIdx.x; t < MR * nb; t += 256) {
         const int m = t / nb, u = t - m * nb;
-        const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)u * 32);
         float x[32];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const f32x4 q = src[i];
-            x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
-        }
+        load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x);
         uint32_t blk[9];
         if constexpr (AS) quantize_block_q8s(x, blk);
+        else if constexpr (XH) quantize_block_q8_1_f16tree(x, blk);
         else quantize_block_q8_1(x, blk);
         uint32_t* dst = (uint32_t*)(smem + (size_t)t * kQ81Bytes);
 #pragma unroll
@@ -989,7 +986,7 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
         for (int v = 0; v < VR; v++)
             if (row0 + v < N) {
 #pragma unroll
-                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + (size_t)(row0 + v) * ldr] = acc[v][m];
             }
     }
 }
@@ -1020,7 +1017,7 @@ constexpr int kGemvMinWGs = KSQ_GEMV_MIN_WGS;
 // mode the halved activation traffic did not pay for the halved grid (measured over the 87
 // definitions: neutral at N = 4096, 8-24% slower at N >= 9728 with 8 activation rows).
 #ifndef KSQ_GEMV_RPW8_MODES
-#define KSQ_GEMV_RPW8_MODES 0x4
+#define KSQ_GEMV_RPW8_MODES 0xC
 #endif
 
 static int pick_rpw(int N, int amode) {
@@ -1031,10 +1028,10 @@ static int pick_rpw(int N, int amode) {
 }
 
 template <int WT, int MR, int AMODE, bool AS, int RPW>
-static hipError_t row_launch(const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
+static hipError_t row_launch(const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc, int ldr,
                              hipStream_t s) {
-    if constexpr ((AMODE == kAL2 && MR > kMaxL2Rows) ||
-                  (AMODE == kAFQ && MR > kMaxFusedRows)) {
+    if constexpr ((AMODE == kAL2 && MR > kMaxL2Rows) || (is_fq(AMODE) && MR > kMaxFusedRows) ||
+                  (AMODE == kAFQH && AS)) {
         return hipErrorNotSupported;  // combinations the dispatcher never asks for are not compiled
     } else {
         const size_t lds = gemv_lds_bytes(WT, MR, KT, AMODE, RPW);
@@ -1042,36 +1039,36 @@ static hipError_t row_launch(const uint8_t* W, const void* A, float* C, int N, i
         if (lds > 65536)
             (void)hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         const unsigned grid = (unsigned)((N + RPW - 1) / RPW);
-        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, W, A, C, N, nb, KT, ldc);
+        hipLaunchKernelGGL(k, dim3(grid), dim3(256), lds, s, W, A, C, N, nb, KT, ldc, ldr);
         return hipGetLastError();
     }
 }
 
 template <int WT, int MR, int AMODE, bool AS>
 static hipError_t row_launch_rpw(int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int KT, int ldc,
-                                 hipStream_t s) {
+                                 int ldr, hipStream_t s) {
     switch (rpw) {
         case 8:
-            if constexpr ((KSQ_GEMV_RPW8_MODES >> AMODE) & 1) return row_launch<WT, MR, AMODE, AS, 8>(W, A, C, N, nb, KT, ldc, s);
+            if constexpr ((KSQ_GEMV_RPW8_MODES >> AMODE) & 1) return row_launch<WT, MR, AMODE, AS, 8>(W, A, C, N, nb, KT, ldc, ldr, s);
             else return hipErrorNotSupported;
-        case 4: return row_launch<WT, MR, AMODE, AS, 4>(W, A, C, N, nb, KT, ldc, s);
-        case 2: return row_launch<WT, MR, AMODE, AS, 2>(W, A, C, N, nb, KT, ldc, s);
-        default: return row_launch<WT, MR, AMODE, AS, 1>(W, A, C, N, nb, KT, ldc, s);
+        case 4: return row_launch<WT, MR, AMODE, AS, 4>(W, A, C, N, nb, KT, ldc, ldr, s);
+        case 2: return row_launch<WT, MR, AMODE, AS, 2>(W, A, C, N, nb, KT, ldc, ldr, s);
+        default: return row_launch<WT, MR, AMODE, AS, 1>(W, A, C, N, nb, KT, ldc, ldr, s);
     }
 }
 
 template <int WT, int AMODE, bool AS>
 static hipError_t row_launch_mr(int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int KT,
-                                int ldc, hipStream_t s) {
+                                int ldc, int ldr, hipStream_t s) {
     switch (mr) {
-        case 1: return row_launch_rpw<WT, 1, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 2: return row_launch_rpw<WT, 2, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 3: return row_launch_rpw<WT, 3, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 4: return row_launch_rpw<WT, 4, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 5: return row_launch_rpw<WT, 5, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 6: return row_launch_rpw<WT, 6, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        case 7: return row_launch_rpw<WT, 7, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
-        default: return row_launch_rpw<WT, 8, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, s);
+        case 1: return row_launch_rpw<WT, 1, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 2: return row_launch_rpw<WT, 2, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 3: return row_launch_rpw<WT, 3, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 4: return row_launch_rpw<WT, 4, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 5: return row_launch_rpw<WT, 5, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 6: return row_launch_rpw<WT, 6, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        case 7: return row_launch_rpw<WT, 7, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
+        default: return row_launch_rpw<WT, 8, AMODE, AS>(rpw, W, A, C, N, nb, KT, ldc, ldr, s);
     }
 }
 
@@ -1096,27 +1093,38 @@ static hipError_t direct_launch_rpw(int rpw, const uint8_t* W, const uint8_t* A,
     return hipGetLastError();
 }
 
-template <int WT, bool AS, int MR>
-static hipError_t direct_fq_launch_rpw(int rpw, const uint8_t* W, const float* X, float* C, int N, int nb, int ldc,
-                                       hipStream_t s) {
+template <int WT, bool AS, int MR, bool XH>
+static hipError_t direct_fq_launch_rpw(int rpw, const uint8_t* W, const void* X, float* C, int N, int nb, int ldc,
+                                       int ldr, hipStream_t s) {
     const dim3 blk(256);
     const size_t lds = (size_t)MR * nb * kQ81Bytes;
     switch (rpw) {
-        case 8: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 8>), dim3((N + 7) / 8), blk, lds, s, W, X, C, N, nb, ldc); break;
-        case 4: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 4>), dim3((N + 3) / 4), blk, lds, s, W, X, C, N, nb, ldc); break;
-        case 2: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 2>), dim3((N + 1) / 2), blk, lds, s, W, X, C, N, nb, ldc); break;
-        default: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 1>), dim3(N), blk, lds, s, W, X, C, N, nb, ldc); break;
+        case 8: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 8, XH>), dim3((N + 7) / 8), blk, lds, s, W, X, C, N, nb, ldc, ldr); break;
+        case 4: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 4, XH>), dim3((N + 3) / 4), blk, lds, s, W, X, C, N, nb, ldc, ldr); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 2, XH>), dim3((N + 1) / 2), blk, lds, s, W, X, C, N, nb, ldc, ldr); break;
+        default: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, AS, 1, XH>), dim3(N), blk, lds, s, W, X, C, N, nb, ldc, ldr); break;
     }
     return hipGetLastError();
 }
 
-// QUANT: pre-quantised activations (gemv_direct_kernel), else fp32 (gemv_direct_fq_kernel).
+// QUANT: pre-quantised activations (gemv_direct_kernel), else fp32 or, with xh, fp16
+// (gemv_direct_fq_kernel).
 template <int WT, bool AS>
-static hipError_t direct_launch(bool quant, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb,
-                                int ldc, hipStream_t s) {
-    if (!quant)
-        return mr == 1 ? direct_fq_launch_rpw<WT, AS, 1>(rpw, W, (const float*)A, C, N, nb, ldc, s)
-                       : direct_fq_launch_rpw<WT, AS, 2>(rpw, W, (const float*)A, C, N, nb, ldc, s);
+static hipError_t direct_launch(bool quant, bool xh, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N,
+                                int nb, int ldc, int ldr, hipStream_t s) {
+    if (!quant) {
+        if constexpr (AS) {
+            if (xh) return hipErrorNotSupported;
+            return mr == 1 ? direct_fq_launch_rpw<WT, AS, 1, false>(rpw, W, A, C, N, nb, ldc, ldr, s)
+                           : direct_fq_launch_rpw<WT, AS, 2, false>(rpw, W, A, C, N, nb, ldc, ldr, s);
+        } else {
+            if (xh)
+                return mr == 1 ? direct_fq_launch_rpw<WT, AS, 1, true>(rpw, W, A, C, N, nb, ldc, ldr, s)
+                               : direct_fq_launch_rpw<WT, AS, 2, true>(rpw, W, A, C, N, nb, ldc, ldr, s);
+            return mr == 1 ? direct_fq_launch_rpw<WT, AS, 1, false>(rpw, W, A, C, N, nb, ldc, ldr, s)
+                           : direct_fq_launch_rpw<WT, AS, 2, false>(rpw, W, A, C, N, nb, ldc, ldr, s);
+        }
+    }
     return mr == 1 ? direct_launch_rpw<WT, AS, 1>(rpw, W, (const uint8_t*)A, C, N, nb, ldc, s)
                    : direct_launch_rpw<WT, AS, 2>(rpw, W, (const uint8_t*)A, C, N, nb, ldc, s);
 }
@@ -1197,6 +1205,7 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
         return KSQ_GEMV_DIRECT_MR && (!is_kquant(wtype) || (KSQ_GEMV_DIRECT_KQ && wtype == kWQ4K && (nb & 7) == 0)) &&
                (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 &&
                !(rpw == 4 && (N + 3) / 4 < 512);
+    if (amode == kAFQH && mr >= 3) return false;   // the 3-8 row fused form takes fp32 only
     if (amode == kAFQ && mr >= 3)   // gemv_fused_profitable admitted it: one K tile, no grid exclusion
         return !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && direct_mr_ktp(mr, nb) == (nb >> 1);
     // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
@@ -1205,12 +1214,12 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
         return KSQ_GEMV_DIRECT_KQ && amode == kAL2 && mr <= (wtype == kWQ4K ? 2 : 1) && (nb & 7) == 0 &&
                ((uintptr_t)A & 3) == 0 && ((uintptr_t)W & (wtype == kWQ4K ? 3 : 1)) == 0;
     if (mr > 2 || (nb & 1) || ((uintptr_t)W & 3) || ((uintptr_t)A & 3)) return false;
-    if (amode == kAFQ) return KSQ_GEMV_DIRECT_FQ && (size_t)mr * nb * kQ81Bytes <= kGemvLdsBudget;
+    if (is_fq(amode)) return KSQ_GEMV_DIRECT_FQ && (size_t)mr * nb * kQ81Bytes <= kGemvLdsBudget;
     return amode == kAL2;
 }
 
-static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int rpw, const uint8_t* W, const void* A,
-                                  float* C, int N, int nb, hipStream_t s) {
+static hipError_t direct_dispatch(int wtype, int afmt, bool quant, bool xh, int mr, int rpw, const uint8_t* W,
+                                  const void* A, float* C, int N, int nb, int ldc, int ldr, hipStream_t s) {
     if (mr >= 3 && wtype == kWQ4K) return direct_mr_launch<kWQ4K, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
     if (wtype == kWQ4K || wtype == kWQ6K) {
         const uint8_t* Aq = (const uint8_t*)A;
@@ -1241,62 +1250,69 @@ static hipError_t direct_dispatch(int wtype, int afmt, bool quant, int mr, int r
         }
     }
     switch (wtype) {
-        case kWQ40: return direct_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+        case kWQ40: return direct_launch<kWQ40, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
         case kWQ80:
-            return afmt == kAQ8S ? direct_launch<kWQ80, true>(quant, mr, rpw, W, A, C, N, nb, N, s)
-                                 : direct_launch<kWQ80, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-        case kWQ41: return direct_launch<kWQ41, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-        case kWQ50: return direct_launch<kWQ50, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-        default: return direct_launch<kWQ51, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+            return afmt == kAQ8S ? direct_launch<kWQ80, true>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s)
+                                 : direct_launch<kWQ80, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+        case kWQ41: return direct_launch<kWQ41, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+        case kWQ50: return direct_launch<kWQ50, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+        default: return direct_launch<kWQ51, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
     }
 }
 
 // QUANT: the activations are already quantised (kAL2 / kADMA by row count and length), else fp32 (kAFQ).
 template <int AMODE>
 static hipError_t gemv_dispatch_mode(int wtype, int afmt, int mr, const uint8_t* W, const void* Am, float* Cm,
-                                     int N, int nb, int KT, int rpw, hipStream_t s) {
+                                     int N, int nb, int KT, int rpw, int ldc, int ldr,
+                                     hipStream_t s) {
     switch (wtype) {
-        case kWQ40: return row_launch_mr<kWQ40, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+        case kWQ40: return row_launch_mr<kWQ40, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
         case kWQ80:
-            return (afmt == kAQ8S) ? row_launch_mr<kWQ80, AMODE, true>(mr, rpw, W, Am, Cm, N, nb, KT, N, s)
-                                   : row_launch_mr<kWQ80, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
-        case kWQ4K: return row_launch_mr<kWQ4K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
-        case kWQ6K: return row_launch_mr<kWQ6K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
-        case kWQ41: return row_launch_mr<kWQ41, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
-        case kWQ50: return row_launch_mr<kWQ50, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
-        default: return row_launch_mr<kWQ51, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, N, s);
+            return (afmt == kAQ8S) ? row_launch_mr<kWQ80, AMODE, true>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s)
+                                   : row_launch_mr<kWQ80, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
+        case kWQ4K: return row_launch_mr<kWQ4K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
+        case kWQ6K: return row_launch_mr<kWQ6K, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
+        case kWQ41: return row_launch_mr<kWQ41, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
+        case kWQ50: return row_launch_mr<kWQ50, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
+        default: return row_launch_mr<kWQ51, AMODE, false>(mr, rpw, W, Am, Cm, N, nb, KT, ldc, ldr, s);
     }
 }
 
+// QUANT: pre-quantised activations; else fp32 (or fp16 with xh) quantised in every workgroup.
+// Output element (m, n) at C[m * ldc + n * ldr].
 template <bool QUANT>
-static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const void* A, float* C, int M, int N, int K,
-                                hipStream_t s) {
-    if (afmt == kAQ8S && wtype != kWQ80) return hipErrorNotSupported;
+static hipError_t gemv_dispatch(int wtype, int afmt, bool xh, const uint8_t* W, const void* A, float* C, int M, int N,
+                                int K, int ldc, int ldr, hipStream_t s) {
+    if (afmt == kAQ8S && (wtype != kWQ80 || xh)) return hipErrorNotSupported;
     const int nb = K / 32;
     if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
+    if (!QUANT && xh && M > kMaxFusedRows) return hipErrorNotSupported;
     const int chunk = (QUANT || M > kMaxFusedRows) ? 8 : kMaxFusedRows;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
         const int dma_min = mr == 1 ? kGemvDmaMinBlocks1 : kGemvDmaMinBlocks2;
-        const int AMODE = !QUANT ? kAFQ : (mr <= kMaxL2Rows && nb < dma_min ? kAL2 : kADMA);
+        const int AMODE = !QUANT ? (xh ? kAFQH : kAFQ) : (mr <= kMaxL2Rows && nb < dma_min ? kAL2 : kADMA);
         // K tile: the whole row if it fits the LDS budget, else the largest multiple of 64 blocks
-        const int rpw = pick_rpw(N, (AMODE == kAFQ && mr > kMaxFusedRows) ? kADMA : AMODE);
+        const int rpw = pick_rpw(N, (is_fq(AMODE) && mr > kMaxFusedRows) ? kADMA : AMODE);
         int KT = (nb + 7) & ~7;
         while (KT > 64 && gemv_lds_bytes(wtype, mr, KT, AMODE, rpw) > kGemvLdsBudget) KT = ((KT / 2) + 63) & ~63;
         const void* Am = QUANT ? (const void*)((const uint8_t*)A + (size_t)m0 * nb * kQ81Bytes)
+                       : xh    ? (const void*)((const uint16_t*)A + (size_t)m0 * K)
                                : (const void*)((const float*)A + (size_t)m0 * K);
-        float* Cm = C + (size_t)m0 * N;
+        float* Cm = C + (size_t)m0 * ldc;
         hipError_t e;
         if (direct_eligible(wtype, AMODE, mr, nb, N, rpw, W, Am)) {
             note_engine(is_kquant(wtype) && mr <= 2 ? KSQ_ENG_GEMV_KQ
                         : mr >= 3 ? (QUANT ? KSQ_ENG_GEMV_MR : KSQ_ENG_GEMV_MR_FQ)
                                   : (QUANT ? KSQ_ENG_GEMV_DIRECT : KSQ_ENG_GEMV_DIRECT_FQ));
-            e = direct_dispatch(wtype, afmt, QUANT, mr, rpw, W, Am, Cm, N, nb, s);
+            if (mr >= 3 && (ldc != N || ldr != 1)) return hipErrorNotSupported;   // row-major output only
+            e = direct_dispatch(wtype, afmt, QUANT, xh, mr, rpw, W, Am, Cm, N, nb, ldc, ldr, s);
         } else {
-            note_engine(AMODE == kAFQ ? KSQ_ENG_GEMV_ROW_FQ : KSQ_ENG_GEMV_ROW);
-            if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
-            else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
-            else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, s);
+            note_engine(is_fq(AMODE) ? KSQ_ENG_GEMV_ROW_FQ : KSQ_ENG_GEMV_ROW);
+            if (AMODE == kAL2) e = gemv_dispatch_mode<kAL2>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, ldc, ldr, s);
+            else if (AMODE == kADMA) e = gemv_dispatch_mode<kADMA>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, ldc, ldr, s);
+            else if (AMODE == kAFQH) e = gemv_dispatch_mode<kAFQH>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, ldc, ldr, s);
+            else e = gemv_dispatch_mode<kAFQ>(wtype, afmt, mr, W, Am, Cm, N, nb, KT, rpw, ldc, ldr, s);
         }
         if (e != hipSuccess) return e;
     }
@@ -1305,7 +1321,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, const uint8_t* W, const voi
 
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s) {
-    return gemv_dispatch<true>(wtype, afmt, W, A, C, M, N, K, s);
+    return gemv_dispatch<true>(wtype, afmt, false, W, A, C, M, N, K, N, 1, s);
 }
 
 // The in-workgroup quantisation is repeated by every workgroup; it beats the separate quantise
@@ -1315,8 +1331,8 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 #define KSQ_GEMV_FUSED_MAX_WORK 420000ll
 #endif
 
-bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W) {
-    if (M < 1 || M > 8) return false;
+bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool xh) {
+    if (M < 1 || M > 8 || (xh && M > kMaxFusedRows)) return false;
 #ifndef KSQ_GEMV_FUSED_MR
 #define KSQ_GEMV_FUSED_MR 1
 #endif
@@ -1346,7 +1362,12 @@ bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W) {
 
 hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X, float* C, int M, int N, int K,
                            hipStream_t s) {
-    return gemv_dispatch<false>(wtype, afmt, W, X, C, M, N, K, s);
+    return gemv_dispatch<false>(wtype, afmt, false, W, X, C, M, N, K, N, 1, s);
+}
+
+hipError_t launch_gemv_fused(int wtype, int afmt, bool xh, const uint8_t* W, const void* X, float* C, int M, int N,
+                             int K, int ldc, int ldr, hipStream_t s) {
+    return gemv_dispatch<false>(wtype, afmt, xh, W, X, C, M, N, K, ldc, ldr, s);
 }
 
 // ---------------------------------------------------------------------------

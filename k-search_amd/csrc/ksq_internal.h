@@ -45,9 +45,14 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 // LDS while its weight loads are in flight, so no quantise launch or workspace is needed.
 hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X, float* C, int M, int N, int K,
                            hipStream_t s);
-// Whether launch_gemv_f32 beats quantise + launch_gemv for this shape (M <= 2 and a bounded
-// amount of repeated quantisation).
-bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W);
+// The same from fp32 (xh false) or fp16 (xh true, quantised by the fused FP16 kernels' rules,
+// M <= 2) activations, with output element (m, n) at C[m * ldc + n * ldr] (ldr > 1 only for
+// M <= 2): ldc = 1, ldr = M writes the transposed [N][M] output.
+hipError_t launch_gemv_fused(int wtype, int afmt, bool xh, const uint8_t* W, const void* X, float* C, int M, int N,
+                             int K, int ldc, int ldr, hipStream_t s);
+// Whether the in-workgroup quantisation beats quantise + launch_gemv for this shape (M <= 2, or
+// M <= 8 for fp32, and a bounded amount of repeated quantisation).
+bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool xh = false);
 
 // Small-batch GEMM (1 <= M <= 8) on the 4x4x4 int8 MFMA for the 32-element block types
 // (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1; block_q8s activations with Q8_0).  W and A 4-byte aligned.
@@ -67,8 +72,9 @@ bool mmq_preferred(int wtype, int M, int N, int K);
 // Number of K splits launch_mmq uses for this shape (1: none).  With splits > 1 it needs
 // `partials`, splits * M * N floats of device scratch.
 int mmq_splits(int wtype, int M, int N, int K);
+// trans: write the output transposed, [N][M] (only without split-K: mmq_splits(...) == 1).
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
-                      float* partials, hipStream_t s);
+                      float* partials, hipStream_t s, bool trans = false);
 // In-order sum of `splits` partial [M][N] results (P) into C.
 hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits, hipStream_t s);
 

@@ -123,7 +123,7 @@ template <class T, int WT, bool DUMP, bool MOE, int AF>
 __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
                                                           int32_t* __restrict__ dump, int M, int N, int nb,
-                                                          MoeTiles moe) {
+                                                          MoeTiles moe, int trans) {
     using S = WShape<WT, T::KB>;
     constexpr int BM = T::BM, BN = T::BN, KB = T::KB, TM = T::TM, TN = T::TN;
     constexpr bool AS = AF == kAQ8S, AFS = AF == kAQ8F;
@@ -543,6 +543,24 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
     } else if constexpr (!DUMP) {
         constexpr float out_scale = S::out_scale;
         const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
+        if (trans) {
+            // transposed output [N][M]: for each of its 16 weight rows the 32 lanes of a half-wave
+            // write 32 consecutive activation rows
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int gm = m0 + wm * 32 * TM + i * 32 + l32;
+                    if (gm >= M) continue;
+                    const int nbase = n0 + wn * 32 * TN + j * 32 + 4 * hi;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int gn = nbase + 8 * (r >> 2) + (r & 3);
+                        if (gn < N) C[(size_t)gn * M + gm] = out_scale * acc[i][j][r];
+                    }
+                }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -744,18 +762,18 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ P, float* __restr
 
 template <class T, int WT, bool DUMP, bool MOE, int AF = kAQ81>
 static hipError_t launch_k(dim3 grid, const uint8_t* W, const uint8_t* A, float* C, int32_t* dump, int M, int N,
-                           int nb, const MoeTiles& mt, hipStream_t s) {
+                           int nb, const MoeTiles& mt, hipStream_t s, int trans = 0) {
     if constexpr (is_kquant(WT) && (T::KB != 8 || MOE)) {
         return hipErrorNotSupported;
     } else {
-        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AF>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt);
+        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AF>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt, trans);
         return hipGetLastError();
     }
 }
 
 template <class T, bool DUMP, bool MOE>
 static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, const uint8_t* A, float* C,
-                           int32_t* dump, int M, int N, int nb, const MoeTiles& mt, hipStream_t s) {
+                           int32_t* dump, int M, int N, int nb, const MoeTiles& mt, hipStream_t s, int trans = 0) {
     if (afmt != kAQ81) {
         // the fp32-scale activation blocks: plain GEMM only (no block-dot dump, no MoE)
         if constexpr (DUMP || MOE) {
@@ -763,25 +781,25 @@ static hipError_t launch_t(int wtype, int afmt, dim3 grid, const uint8_t* W, con
         } else {
             if (afmt == kAQ8S) {
                 if (wtype != kWQ80) return hipErrorNotSupported;
-                return launch_k<T, kWQ80, false, false, kAQ8S>(grid, W, A, C, dump, M, N, nb, mt, s);
+                return launch_k<T, kWQ80, false, false, kAQ8S>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
             }
             if (afmt != kAQ8F) return hipErrorNotSupported;
             switch (wtype) {
-                case kWQ40: return launch_k<T, kWQ40, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
-                case kWQ50: return launch_k<T, kWQ50, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
-                case kWQ80: return launch_k<T, kWQ80, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s);
+                case kWQ40: return launch_k<T, kWQ40, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+                case kWQ50: return launch_k<T, kWQ50, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+                case kWQ80: return launch_k<T, kWQ80, false, false, kAQ8F>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
                 default: return hipErrorNotSupported;
             }
         }
     }
     switch (wtype) {
-        case kWQ40: return launch_k<T, kWQ40, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ80: return launch_k<T, kWQ80, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ4K: return launch_k<T, kWQ4K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ6K: return launch_k<T, kWQ6K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ41: return launch_k<T, kWQ41, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ50: return launch_k<T, kWQ50, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
-        case kWQ51: return launch_k<T, kWQ51, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s);
+        case kWQ40: return launch_k<T, kWQ40, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ80: return launch_k<T, kWQ80, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ4K: return launch_k<T, kWQ4K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ6K: return launch_k<T, kWQ6K, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ41: return launch_k<T, kWQ41, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ50: return launch_k<T, kWQ50, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
+        case kWQ51: return launch_k<T, kWQ51, DUMP, MOE>(grid, W, A, C, dump, M, N, nb, mt, s, trans);
         default: return hipErrorNotSupported;
     }
 }
@@ -801,20 +819,20 @@ static int split_cfg(int cfg, int wtype, int M, int N, int K) {
 // splits > 1: C receives splits partial [M][N] results back to back.
 template <bool DUMP>
 static hipError_t launch_cfg(int cfg, int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C,
-                             int32_t* dump, int M, int N, int K, int splits, hipStream_t s) {
+                             int32_t* dump, int M, int N, int K, int splits, hipStream_t s, int trans = 0) {
     const int nb = K / 32;
     const MoeTiles mt{};
     auto grid = [&](int BM, int BN) {
         return dim3((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM), (unsigned)splits);
     };
     switch (cfg) {
-        case 1: return launch_t<TileL, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
-        case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s);
-        case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s);
-        case 5: return launch_t<TileT, DUMP, false>(wtype, afmt, grid(32, 128), W, A, C, dump, M, N, nb, mt, s);
-        case 6: return launch_t<TileP, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
-        case 7: return launch_t<TileW, DUMP, false>(wtype, afmt, grid(64, 128), W, A, C, dump, M, N, nb, mt, s);
-        default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s);
+        case 1: return launch_t<TileL, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s, trans);
+        case 2: return launch_t<TileN, DUMP, false>(wtype, afmt, grid(128, 64), W, A, C, dump, M, N, nb, mt, s, trans);
+        case 3: return launch_t<TileS, DUMP, false>(wtype, afmt, grid(64, 64), W, A, C, dump, M, N, nb, mt, s, trans);
+        case 5: return launch_t<TileT, DUMP, false>(wtype, afmt, grid(32, 128), W, A, C, dump, M, N, nb, mt, s, trans);
+        case 6: return launch_t<TileP, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s, trans);
+        case 7: return launch_t<TileW, DUMP, false>(wtype, afmt, grid(64, 128), W, A, C, dump, M, N, nb, mt, s, trans);
+        default: return launch_t<TileK4, DUMP, false>(wtype, afmt, grid(128, 128), W, A, C, dump, M, N, nb, mt, s, trans);
     }
 }
 
@@ -837,11 +855,12 @@ int mmq_splits(int wtype, int M, int N, int K) {
 }
 
 hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
-                      float* partials, hipStream_t s) {
+                      float* partials, hipStream_t s, bool trans) {
     const int cfg = pick_config(wtype, M, N, K);
     const int splits = split_cfg(cfg, wtype, M, N, K);
+    if (trans && splits > 1) return hipErrorNotSupported;
     note_engine(KSQ_ENG_MMQ_CFG(cfg) | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
-    if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s);
+    if (splits == 1) return launch_cfg<false>(cfg, wtype, afmt, W, A, C, nullptr, M, N, K, 1, s, trans ? 1 : 0);
     if (!partials) return hipErrorInvalidValue;
     hipError_t e = launch_cfg<false>(cfg, wtype, afmt, W, A, partials, nullptr, M, N, K, splits, s);
     if (e != hipSuccess) return e;

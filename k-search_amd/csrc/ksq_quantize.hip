@@ -186,6 +186,10 @@ __device__ __forceinline__ int sat_i8(float r) {
 template <int VAR>
 __device__ __forceinline__ void quantize_block_variant(const float* v, uint32_t* out) {
 #pragma clang fp contract(off)
+    if constexpr (VAR == 3) {
+        quantize_block_q8_1_f16tree(v, out);
+        return;
+    }
     float d, sum;
     if constexpr (VAR == 1) {
         float amax = 0.0f;
@@ -196,7 +200,7 @@ __device__ __forceinline__ void quantize_block_variant(const float* v, uint32_t*
             sum += v[j];
         }
         d = amax / 127.0f;
-    } else if constexpr (VAR == 2) {
+    } else {
         float amax = 0.0f;
         bool nan = false;
 #pragma unroll
@@ -214,44 +218,17 @@ __device__ __forceinline__ void quantize_block_variant(const float* v, uint32_t*
 #pragma unroll
             for (int j = 0; j < 8; j++) r[j] += v[i + j];
         sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-    } else {
-        float m[32], t[32];
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-            m[j] = __builtin_fabsf(v[j]);
-            t[j] = v[j];
-        }
-#pragma unroll
-        for (int w = 16; w >= 2; w >>= 1)
-#pragma unroll
-            for (int j = 0; j < w; j++) {
-                m[j] = __builtin_fmaxf(m[j], m[j + w]);
-                t[j] += t[j + w];
-            }
-        d = __builtin_fmaxf(m[0], m[1]) / 127.0f;
-        sum = t[0] + t[1];
     }
-    const uint32_t dh = f32_to_f16(d);
-    out[0] = dh | (f32_to_f16(sum) << 16);
+    out[0] = f32_to_f16(d) | (f32_to_f16(sum) << 16);
     float id = 0.0f;
     if constexpr (VAR == 1) id = (d > 0.0f) ? 1.0f / d : 0.0f;
-    if constexpr (VAR == 3) {
-        const float dr = f16_to_f32(dh);
-        id = (dr != 0.0f) ? 1.0f / dr : 0.0f;
-    }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         uint32_t w = 0;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const float x = v[4 * i + k];
-            int q;
-            if constexpr (VAR == 1) q = sat_i8(__builtin_rintf(x * id));
-            else if constexpr (VAR == 2) q = sat_i8(__builtin_rintf(x / d));
-            else {
-                q = sat_i8(roundf(x * id));
-                q = q < -127 ? -127 : q;
-            }
+            const int q = (VAR == 1) ? sat_i8(__builtin_rintf(x * id)) : sat_i8(__builtin_rintf(x / d));
             w |= (uint32_t)(q & 0xFF) << (8 * k);
         }
         out[1 + i] = w;

@@ -231,9 +231,12 @@ def _engine_cases():
     for M, path, eng in ((2, 1, {"gemv_direct"}), (6, 3, {"skinny"}), (150, 2, {"mmq3", "splitk"})):
         cases.append((f"q8s_m{M}", 1, M, 256, 1024, 3, path, 0, eng, 0))
     # fp16 activations (quantised by the fused FP16 kernels' rules)
-    for M, path, eng in ((1, 1, {"quantize", "gemv_direct"}), (4, 3, {"quantize", "skinny"}),
+    # (1-2 rows: quantised inside the decode kernel's workgroups, into LDS)
+    for M, path, eng in ((1, 1, {"gemv_direct_fq"}), (2, 0, {"gemv_direct_fq"}), (4, 3, {"quantize", "skinny"}),
                          (150, 2, {"quantize", "mmq3", "splitk"})):
         cases.append((f"f16_m{M}", 0, M, 256, 1024, 4, path, 0, eng, 0))
+    for M in (1, 2):
+        cases.append((f"f16_row_m{M}", 4, M, 256, 1024, 4, 1, 0, {"gemv_row_fq"}, 2))
     return cases
 
 
@@ -278,10 +281,11 @@ def test_exact_engine(dev, oracle, cid, wtype, M, N, K, atype, path, cfg, engine
 
 
 def test_engine_table_covers_every_engine():
-    """The forced cases above (plus the MoE cases below) reach every kernel family ksq_gemm has."""
+    """The forced cases above (plus the MoE and fused FP16 cases below, and the dequantise-then-fp32
+    GEMM of tests/test_gpu_w16.py) reach every kernel family the library has."""
     from ksq import _lib
     seen = set().union(*(c[8] for c in ENGINE_CASES)) | {"moe_tile64", "moe_tile128", "moe_combine",
-                                                          "moe_route", "moe_group", "transpose"}
+                                                          "moe_route", "moe_group", "transpose", "w16"}
     assert seen == set(_lib.ENG), set(_lib.ENG) - seen
 
 
@@ -385,6 +389,27 @@ def test_fp16_fused_orientation_exact(dev):
     torch.cuda.synchronize()
     assert np.array_equal(y1.cpu().numpy(), want)
     assert np.array_equal(y2.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("Mw,Na,K,engines", [
+    (512, 1, 1024, {"gemv_direct_fq"}),          # decode: fp16 quantised in LDS, [M][N] stored directly
+    (4096, 2, 2048, {"gemv_direct_fq"}),
+    (4096, 512, 1024, {"quantize", "mmq3"}),     # MFMA GEMM writing its tiles transposed
+    (384, 40, 1024, {"quantize", "mmq3", "splitk", "transpose"}),   # split-K: [N][M], then transposed
+])
+def test_fp16_fused_routes_exact(dev, Mw, Na, K, engines):
+    """Each route of ksq_gemm_q4_0_fp16_fused gives the exact transposed result and launches the
+    kernels named (no workspace and no transpose for decode shapes and for the unsplit GEMM)."""
+    import torch
+    from ksq import ops, refcheck
+    g = np.random.default_rng(4900 + Na)
+    w, xh, blocks = _inputs(0, g, Na, Mw, K, 4, refcheck.onehot_pattern(Na, K // 32))
+    want = _exact(0, blocks, w).T
+    y = ops.gemm_q4_0_fp16_fused(_t(w, dev), _t(xh, dev), Mw, Na, K)
+    eng = ops.last_engines()
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), want)
+    assert eng == engines, eng
 
 
 def test_dropin_forwarding_module(dev):
