@@ -667,6 +667,16 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
     for (int t0 = 0; t0 < np; t0 += ktp) {
         const int tp = (np - t0) < ktp ? (np - t0) : ktp;
         int p = t0 + part * 64 + lane;
+        // FQ: this thread's first activation block is loaded before the weight pairs, so its
+        // quantisation runs while the weight loads are in flight (loads complete in issue order)
+        float x0[FQ ? 32 : 1];
+        if constexpr (FQ) {
+            const int e = (int)threadIdx.x;
+            if (e < MR * 2 * tp) {
+                const int m = e / (2 * tp), u = e - m * 2 * tp;
+                load_x32<false>(Ain, (size_t)m * nb * 32 + (size_t)(2 * t0 + u) * 32, x0);
+            }
+        }
         uint32_t w[VR][PW];
         if (p < t0 + tp) {
 #pragma unroll
@@ -677,16 +687,15 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
         // wave m % 4 with LDS DMA; its first byte lands at ashift[m] (the source's offset mod 16)
         int ashift[MR];
         if constexpr (FQ) {
-            const float* X = (const float*)Ain;
             const int K = nb * 32;
             for (int e = threadIdx.x; e < MR * 2 * tp; e += 256) {
                 const int m = e / (2 * tp), u = e - m * 2 * tp;   // block u of row m's tile
-                const f32x4* src = (const f32x4*)(X + (size_t)m * K + (size_t)(2 * t0 + u) * 32);
                 float x[32];
+                if (e == (int)threadIdx.x) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const f32x4 q = src[i];
-                    x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+                    for (int i = 0; i < 32; i++) x[i] = x0[i];
+                } else {
+                    load_x32<false>(Ain, (size_t)m * K + (size_t)(2 * t0 + u) * 32, x);
                 }
                 uint32_t blk[9];
                 if constexpr (AS) quantize_block_q8s(x, blk);
@@ -919,15 +928,29 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
     const int row0 = blockIdx.x * RPW + (wave / WPR) * VR;
     const int np = nb >> 1;
     int p = part * 64 + lane;
+    const int K = nb * 32;
+    // this thread's first activation block is loaded before the weight pairs: global loads
+    // complete in issue order, so its quantisation waits only for it and runs while the weight
+    // loads are in flight (loaded after them, the quantisation would wait for the weights too)
+    float x0[32];
+    const bool has0 = (int)threadIdx.x < MR * nb;
+    if (has0) {
+        const int m = (int)threadIdx.x / nb, u = (int)threadIdx.x - m * nb;
+        load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x0);
+    }
     uint32_t w[VR][PW];
 #pragma unroll
     for (int v = 0; v < VR; v++)
         if (p < np && row0 + v < N) load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
-    const int K = nb * 32;
     for (int t = threadIdx.x; t < MR * nb; t += 256) {
         const int m = t / nb, u = t - m * nb;
         float x[32];
-        load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x);
+        if (t == (int)threadIdx.x) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) x[i] = x0[i];
+        } else {
+            load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x);
+        }
         uint32_t blk[9];
         if constexpr (AS) quantize_block_q8s(x, blk);
         else if constexpr (XH) quantize_block_q8_1_f16tree(x, blk);

@@ -624,9 +624,8 @@ static int grid_wgs(int M, int N) {
 //  * Q4_K / Q6_K stage one super-block per K step: 128 x 64 while that grid covers the CUs or
 //    for long rows below M = 256 (Q6_K M = 128, N = 4096, K = 14336: 58.8 vs 70.0 for 64 x 64),
 //    else 64 x 64; Q4_K (nibble-staged) like Q4_0 takes 32 x 128 at M <= 32 (N = 14336,
-//    K = 4096, M = 16: 20.5 vs 26.7) and on grids of 384+ workgroups below M = 256 (M = 128: 45.3
-//    vs 49.3), 128 x 128 from M = 256 while it covers the CUs (M = 2048, N = K = 4096: 114.5 vs
-//    131.9).
+//    K = 4096, M = 16: 20.5 vs 26.7) up to M = 96, 64 x 128 from there to M = 255, 128 x 128
+//    from M = 256 while it covers the CUs (M = 2048, N = K = 4096: 114.5 vs 131.9).
 static int pick_config(int wtype, int M, int N, int K) {
     if (g_mmq_config && !(is_kquant(wtype) && (g_mmq_config == 4 || g_mmq_config == 6))) return g_mmq_config;
     constexpr int kCUs = 256;
@@ -644,9 +643,12 @@ static int pick_config(int wtype, int M, int N, int K) {
         return (gn >= 416 && gn <= 2 * kCUs) ? 2 : 3;
     }
     if (wtype == kWQ4K) {
-        if (M <= 32) return 5;
+        // 33..96 rows: 32 x 128 (N = 14336, K = 4096, M = 96: 36.2 vs 44.8 us for 64 x 64);
+        // 97..255 rows: 64 x 128, split along K while its grid is small (M = 128: 40.8 vs 45.4 for
+        // 32 x 128; M = 192: 53.3 vs 55.0)
+        if (M <= 96) return 5;
         if (M >= 256 && grid_wgs<TileL>(M, N) >= kCUs) return 1;
-        if (M < 256 && grid_wgs<TileT>(M, N) >= 384) return 5;
+        if (M < 256) return 7;
     }
     if (M < 256 && K >= 9728) return 2;
     if (grid_wgs<TileN>(M, N) >= kCUs) return 2;

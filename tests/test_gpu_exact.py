@@ -127,8 +127,8 @@ CONFIG_CASES = [
     ("c1_q8_0_m32_q81", 1, 32, 4096, 4096, "q81", {"mmq3", "splitk"}),
     ("c2_q4_0_m2048_f32", 0, 2048, 4096, 4096, "f32", {"quantize", "mmq1"}),
     ("c2_q4_0_m2048_q81", 0, 2048, 4096, 4096, "q81", {"mmq1"}),
-    ("c3_q4_k_m128_f32", 2, 128, 14336, 4096, "f32", {"quantize", "mmq5"}),
-    ("c3_q4_k_m128_q81", 2, 128, 14336, 4096, "q81", {"mmq5"}),
+    ("c3_q4_k_m128_f32", 2, 128, 14336, 4096, "f32", {"quantize", "mmq7", "splitk"}),
+    ("c3_q4_k_m128_q81", 2, 128, 14336, 4096, "q81", {"mmq7", "splitk"}),
     ("c3_q6_k_m128_f32", 3, 128, 14336, 4096, "f32", {"quantize", "mmq3"}),
     ("c3_q6_k_m128_q81", 3, 128, 14336, 4096, "q81", {"mmq3"}),
 ]
@@ -210,11 +210,13 @@ def _engine_cases():
                       {"quantize", "gemv_row" if wt == 3 else "gemv_mr"} if kq else {"gemv_mr_fq"}, 0))
         # MFMA GEMM, every tile configuration (K-quants take the automatic tile for 4 and 6)
         # (the K-step-4 tiles split this 4-workgroup grid in two along K)
+        # (automatic for M = 150-200: Q4_K the 64 x 128 tile, Q6_K 64 x 64)
+        auto = "mmq7" if wt == 2 else "mmq3"
         for cfg in range(1, 8):
             eng = {f"mmq{cfg}", "splitk"} if cfg in (4, 6) else {f"mmq{cfg}"}
-            cases.append((f"mmq_cfg{cfg}_w{wt}", wt, 150, 136, 512, 1, 2, cfg, {"mmq3"} if kq and cfg in (4, 6) else eng,
+            cases.append((f"mmq_cfg{cfg}_w{wt}", wt, 150, 136, 512, 1, 2, cfg, {auto} if kq and cfg in (4, 6) else eng,
                           0))
-        cases.append((f"mmqf_w{wt}", wt, 200, 384, 1024, 0, 2, 0, {"quantize", "mmq3", "splitk"}, 0))
+        cases.append((f"mmqf_w{wt}", wt, 200, 384, 1024, 0, 2, 0, {"quantize", auto if kq else "mmq3", "splitk"}, 0))
     for wt in LEGACY:
         cases.append((f"dec_oddnb_w{wt}", wt, 1, 200, 1056, 1, 1, 0, {"gemv_row"}, 0))
         cases.append((f"dec_long_w{wt}", wt, 1, 64, 20480, 1, 1, 0, {"gemv_row"}, 0))
