@@ -1353,6 +1353,9 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 #ifndef KSQ_GEMV_FUSED_MAX_WORK
 #define KSQ_GEMV_FUSED_MAX_WORK 420000ll
 #endif
+#ifndef KSQ_GEMV_FUSED_MR_MAX_WORK
+#define KSQ_GEMV_FUSED_MR_MAX_WORK 200000ll
+#endif
 
 bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool xh) {
     if (M < 1 || M > 8 || (xh && M > kMaxFusedRows)) return false;
@@ -1371,7 +1374,7 @@ bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool x
         int rpw = pick_rpw(N, kADMA);
         if (rpw == 4 && M <= 5 && nb >= 384 && (N + 7) / 8 >= kGemvMinWGs) rpw = 8;
         const long long wgs = (N + rpw - 1) / rpw;
-        return (long long)M * wgs * nb <= 200000ll;
+        return (long long)M * wgs * nb <= KSQ_GEMV_FUSED_MR_MAX_WORK;
     }
     const int rpw = pick_rpw(N, kAFQ);
     const int nb = K / 32, KT = (nb + 7) & ~7;

@@ -479,6 +479,10 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         // A wave whose rows all lie past the tile's last row (ragged MoE tiles, the last row
         // tile of a ragged M) skips its MFMAs and epilogues; staging and barriers stay shared.
         if (wave_has_rows) {
+            // the compute phase of this wave goes first at instruction issue: with two workgroups
+            // per CU the other one is usually staging (Q4_K M = 128: 50.0 -> 45.8 us, Q8_0
+            // M = 2048 -2%, the rest level)
+            __builtin_amdgcn_s_setprio(2);
             i32x16 cur = mfma_step(0);
 #pragma unroll
             for (int q = 0; q < NQ; q++) {
@@ -489,6 +493,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 epilogue(b, b * SUBN + h, i, j, cur);
                 cur = nxt;
             }
+            __builtin_amdgcn_s_setprio(0);
         }
 
         if constexpr (SIDE_MFMA && !DUMP) {
