@@ -54,7 +54,9 @@ TRAFFIC = {
                               "profiles/moe_q4_0_t512_e8_top2.md"),
 }
 
-ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe")
+ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
+        "w16_m1", "w16_m2048", "q8f_m2048", "f16_fused_m1")
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, published
 
 
 def log(msg: str) -> None:
@@ -230,6 +232,45 @@ class Workloads:
         return (T, E, N, K, k), fn, copies
 
 
+    def w16(self, M: int, copies: int = 8):
+        """The dequantise-then-fp32 GEMM (W4A16, gemm_w4a16_*): fp32 activations [M, 4096] times
+        dequantised Q4_0 weights [4096, 4096], no activation quantisation."""
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        N, K = 4096, 4096
+        w = synth.weights(ksq.W_Q4_0, g, N, K)
+        copies = 64 if M == 1 else copies
+        W = [self.t(w) for _ in range(copies)]
+        x = self.t(synth.activations(g, M, K))
+        o = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        ws = self.torch.empty(max(256, ops.gemm_w16_workspace_size(M, N, K)), dtype=self.torch.uint8, device=self.dev)
+        return (M, N, K), (lambda i: ops.gemm_w16(ksq.W_Q4_0, x, W[i % copies], M, N, K, out=o, workspace=ws)), copies
+
+    def q8f(self, M: int = 2048, copies: int = 8):
+        """The deepseek_v2 W4A32C8 operator's path (fp32 d_a and s_a, block_q8f) at the config-2
+        shape: fp32 activations quantised by its rules, then the int8 MFMA GEMM."""
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        N, K = 4096, 4096
+        w = synth.weights(ksq.W_Q4_0, g, N, K)
+        W = [self.t(w) for _ in range(copies)]
+        x = self.t(synth.activations(g, M, K))
+        o = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
+        ws = self.torch.empty(ops.workspace_size(0, ksq.A_F32_Q8F_RNE, M, N, K), dtype=self.torch.uint8,
+                              device=self.dev)
+        return (M, N, K), (lambda i: ops.gemm(ksq.W_Q4_0, ksq.A_F32_Q8F_RNE, W[i % copies], x, M, N, K, out=o,
+                                              workspace=ws)), copies
+
+    def f16_fused(self, copies: int = 64):
+        """gemm_q4_0_fp16_fused at decode size (4096 weight rows, one fp16 activation row of 4096):
+        the fp16 activations are quantised inside the decode kernel's workgroups."""
+        ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
+        Mw, Na, K = 4096, 1, 4096
+        w = synth.weights(ksq.W_Q4_0, g, Mw, K)
+        W = [self.t(w) for _ in range(copies)]
+        xh = self.t(synth.activations(g, Na, K).astype(np.float16))
+        o = self.torch.empty((Mw, Na), dtype=self.torch.float32, device=self.dev)
+        return (Mw, Na, K), (lambda i: ops.gemm_q4_0_fp16_fused(W[i % copies], xh, Mw, Na, K, out=o)), copies
+
+
 def other_configs(wl: Workloads, reps: int = 4) -> dict:
     """BASELINE configs 1, 3 and 4, each on rotating weight copies (> 256 MB MALL in total)."""
     out = {}
@@ -249,6 +290,39 @@ def other_configs(wl: Workloads, reps: int = 4) -> dict:
     ms, d = graph_stats(fn, copies, reps)
     moe_bytes = E * N * (K // 32) * 18 + T * K * 4 + T * E * 4 + T * N * 4
     out["moe_q4_0_T512_E8_top2"] = hbm_entry(moe_bytes, ms, d, 2.0 * T * k * N * K, "moe_q4_0_T512_E8_top2")
+    del fn
+    wl.torch.cuda.empty_cache()
+    return out
+
+
+def extra_paths(wl: Workloads, reps: int = 4) -> dict:
+    """The paths beside the headline (not BASELINE configs): the dequantise-then-fp32 GEMM
+    (W4A16) at M = 1 and M = 2048, the deepseek_v2 operator's block_q8f path at the config-2
+    shape, and the fused FP16-activation GEMM at decode size."""
+    out = {}
+    for M in (1, 2048):
+        (M, N, K), fn, copies = wl.w16(M)
+        ms, d = graph_stats(fn, copies, reps)
+        e = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K)
+        if M > 1:
+            # three bf16 MFMA products per fp32 product (exact split of the activations)
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            e["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": round(BF16_PEAK_TFLOPS / 3, 1),
+                             "unit": "TFLOP/s (fp32-exact products: 3 bf16 MFMA terms)",
+                             "frac": round(tf / (BF16_PEAK_TFLOPS / 3), 4)}
+        out[f"w4a16_q4_0_M{M}"] = e
+        del fn
+    (M, N, K), fn, copies = wl.q8f()
+    ms, d = graph_stats(fn, copies, reps)
+    e = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K)
+    top = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    e["roofline"] = {"bound": "mfma", "achieved": round(top, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": round(top / INT8_PEAK_TOPS, 4)}
+    out["deepseek_v2_q8f_q4_0_M2048"] = e
+    del fn
+    (Mw, Na, K), fn, copies = wl.f16_fused()
+    ms, d = graph_stats(fn, copies, reps)
+    out["fp16_fused_q4_0_N1"] = hbm_entry(Mw * (K // 32) * 18 + Na * K * 2 + Mw * Na * 4, ms, d, 2.0 * Mw * Na * K)
     del fn
     wl.torch.cuda.empty_cache()
     return out
@@ -358,6 +432,12 @@ def only(args, dev) -> int:
         _, fn, _ = wl.q8_0(int(args.only[6:]))
     elif args.only in ("q4_k", "q6_k"):
         _, fn, _ = wl.kquant(wl.ksq.W_Q4_K if args.only == "q4_k" else wl.ksq.W_Q6_K)
+    elif args.only.startswith("w16_m"):
+        _, fn, _ = wl.w16(int(args.only[5:]))
+    elif args.only == "q8f_m2048":
+        _, fn, _ = wl.q8f()
+    elif args.only == "f16_fused_m1":
+        _, fn, _ = wl.f16_fused()
     else:
         _, fn, _ = wl.moe()
     for i in range(args.warmup + args.steps):
@@ -391,6 +471,8 @@ def main() -> int:
     # ---- the other BASELINE configs first (this also brings the clocks to their steady state)
     log("bench: BASELINE configs 1, 3, 4")
     configs = other_configs(wl)
+    log("bench: W4A16, deepseek_v2 block_q8f, fused FP16")
+    extra = extra_paths(wl)
 
     # ---- decode GEMV, config 0 shape, and the one-shot read of the same number of bytes
     log("bench: config 0 GEMV")
@@ -477,6 +559,7 @@ def main() -> int:
                     "frac_of_one_shot_read": round(read_ms / gemv_ms, 4),
                     "weight_copies": gcopies},
         "configs": configs,
+        "extra_paths": extra,
     }
     if not args.no_cpu_baseline:
         log("bench: cpu baselines")

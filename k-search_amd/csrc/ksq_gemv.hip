@@ -32,35 +32,6 @@ namespace ksq {
 
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Sum over the 64 lanes, returned in every lane.  Rows of 16 lanes reduce through DPP (quad_perm
-// swaps of 1 and 2 lanes, then rotations by 4 and 8 within the row), and the 4 row sums are read
-// out with v_readlane: register-only steps instead of 6 dependent ds_bpermute round trips
-// through the LDS unit at the tail of every decode wave.
-#ifndef KSQ_WAVE_SUM_DPP
-#define KSQ_WAVE_SUM_DPP 1
-#endif
-template <int CTRL>
-__device__ __forceinline__ float dpp_mov(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#if KSQ_WAVE_SUM_DPP
-    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_mov<0x124>(v);  // row_ror:4
-    v += dpp_mov<0x128>(v);  // row_ror:8
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return (r0 + r1) + (r2 + r3);
-#else
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-#endif
-}
-
 // NW little-endian words starting at byte pointer p (2-byte aligned, LDS or global):
 // NW+1 aligned dword reads re-aligned with v_alignbyte_b32.
 template <int NW>

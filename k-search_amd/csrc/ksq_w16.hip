@@ -235,8 +235,170 @@ __global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__
     }
 }
 
+// ---- decode form (1-4 activation rows) ------------------------------------------------------
+// A GEMV on the VALU: the bf16-MFMA tile wastes 31 of its 32 rows at M = 1 and splits K to fill
+// the chip (13 us at N = K = 4096); here every lane owns pairs of adjacent weight blocks (36 or 68
+// bytes, loaded straight into VGPRs), the workgroup stages the activation rows of a K tile in LDS
+// with each block's fp32 sum, and a lane's block contributes
+//     d_w * (sum_k a_k q_k - 8 * sum_k a_k)      (Q4_0; Q8_0: d_w * sum_k a_k q_k)
+// with q_k converted once per element (v_cvt_f32_ubyte) and one fma per element and activation
+// row: the reference's sum of a_k * (q_k - 8) * d_w regrouped (fp32 rounding differs).  RPW
+// weight rows per 256-thread workgroup, RPW / 4 per wave, every activation value read from LDS
+// serving all of them.
+constexpr int kW16KTile = 4096;   // activation elements per row and K tile
+// LDS layout of a staged activation row: pair p of the tile (64 floats) at p * 68 floats, so the
+// 16-byte reads of 16 lanes (consecutive pairs, 272 bytes apart) hit distinct bank groups
+constexpr int kW16PairPitch = 68;
+
+// NW dwords from p (4-byte aligned) by 16-, 8- and 4-byte loads.
+template <int NW>
+__device__ __forceinline__ void load_dwords_a4(const uint32_t* __restrict__ p, uint32_t* w) {
+#pragma unroll
+    for (int i = 0; i + 4 <= NW; i += 4) {
+        const u32x4a4 v = *(const u32x4a4*)(p + i);
+        w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
+    }
+    constexpr int r0 = NW & ~3;
+    if constexpr (NW - r0 >= 2) {
+        const u32x2a4 v = *(const u32x2a4*)(p + r0);
+        w[r0] = v.x; w[r0 + 1] = v.y;
+    }
+    if constexpr ((NW - r0) & 1) w[NW - 1] = p[NW - 1];
+}
+
+template <int WT, int MR, int RPW>
+__global__ __launch_bounds__(256) void w16_gemv_kernel(const uint8_t* __restrict__ W, const float* __restrict__ A,
+                                                       float* __restrict__ C, int N, int nb) {
+    constexpr int VR = RPW / 4;                                  // weight rows per wave
+    constexpr int BB = block_bytes(WT), PW = BB / 2;             // pair: 36 / 68 bytes = 9 / 17 dwords
+    __shared__ __attribute__((aligned(16))) float sx[MR][kW16KTile / 64 * kW16PairPitch];
+    __shared__ float ssum[MR][kW16KTile / 32];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (int)blockIdx.x * RPW + wave * VR;
+    const size_t K = (size_t)nb * 32;
+    float acc[VR][MR];
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = 0.0f;
+
+    for (int kb0 = 0; kb0 < nb; kb0 += kW16KTile / 32) {
+        const int kbn = min(kW16KTile / 32, nb - kb0);          // blocks in this K tile (even)
+        const int np = kbn / 2;
+        // this lane's first pair of weight blocks for its rows, issued before the staging loads
+        int p = lane;
+        uint32_t w[VR][PW];
+#pragma unroll
+        for (int v = 0; v < VR; v++)
+            if (p < np && row0 + v < N)
+                load_dwords_a4<PW>((const uint32_t*)(W + ((size_t)(row0 + v) * nb + kb0 + 2 * p) * BB), w[v]);
+        // stage the K tile's activations, 8 floats per thread and step, and the block sums
+        for (int e = threadIdx.x; e < MR * kbn * 4; e += 256) {
+            const int m = e / (kbn * 4), c = e - m * kbn * 4;        // c: 8-float chunk of row m
+            const f32x4* src = (const f32x4*)(A + (size_t)m * K + (size_t)kb0 * 32 + 8 * c);
+            const f32x4 x0 = src[0], x1 = src[1];
+            // chunk c = elements 8c .. 8c + 7 of the tile: pair c / 8, offset 8 (c % 8) in it
+            float* dst = &sx[m][(c >> 3) * kW16PairPitch + 8 * (c & 7)];
+            *(f32x4*)dst = x0;
+            *(f32x4*)(dst + 4) = x1;
+            // the 4 chunks of a block sit in 4 consecutive lanes: their partial sums meet by DPP
+            float part = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
+            part += dpp_mov<0xB1>(part);   // quad_perm [1,0,3,2]
+            part += dpp_mov<0x4E>(part);   // quad_perm [2,3,0,1]
+            if ((c & 3) == 0) ssum[m][c >> 2] = part;
+        }
+        __syncthreads();
+        if (row0 < N) {
+            for (bool first = true; p < np; p += 64, first = false) {
+                if (!first) {
+#pragma unroll
+                    for (int v = 0; v < VR; v++)
+                        if (row0 + v < N)
+                            load_dwords_a4<PW>((const uint32_t*)(W + ((size_t)(row0 + v) * nb + kb0 + 2 * p) * BB), w[v]);
+                }
+#pragma unroll
+                for (int h = 0; h < 2; h++) {       // block 2p + h of the tile
+                    const int b = 2 * p + h;
+                    float part[VR][MR];
+#pragma unroll
+                    for (int v = 0; v < VR; v++)
+#pragma unroll
+                        for (int m = 0; m < MR; m++) part[v][m] = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < (WT == kWQ40 ? 4 : 8); i++) {
+                        // 4 quants of each row: Q4_0 elements 4i..4i+3 (low nibbles) and
+                        // 16+4i..16+4i+3 (high nibbles); Q8_0 elements 4i..4i+3
+                        float q[VR][WT == kWQ40 ? 8 : 4];
+#pragma unroll
+                        for (int v = 0; v < VR; v++) {
+                            const uint32_t wd = word_at(w[v], h * BB + 2 + 4 * i);
+                            if constexpr (WT == kWQ40) {
+                                const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+                                for (int j = 0; j < 4; j++) {
+                                    q[v][j] = (float)((lo >> (8 * j)) & 0xFFu);
+                                    q[v][4 + j] = (float)((hi >> (8 * j)) & 0xFFu);
+                                }
+                            } else {
+#pragma unroll
+                                for (int j = 0; j < 4; j++) q[v][j] = (float)(int8_t)((wd >> (8 * j)) & 0xFFu);
+                            }
+                        }
+#pragma unroll
+                        for (int m = 0; m < MR; m++) {
+                            const float* xp = &sx[m][p * kW16PairPitch + 32 * h];
+                            const f32x4 xl = *(const f32x4*)(xp + 4 * i);
+#pragma unroll
+                            for (int v = 0; v < VR; v++) {
+                                part[v][m] = fmaf(xl.x, q[v][0], part[v][m]);
+                                part[v][m] = fmaf(xl.y, q[v][1], part[v][m]);
+                                part[v][m] = fmaf(xl.z, q[v][2], part[v][m]);
+                                part[v][m] = fmaf(xl.w, q[v][3], part[v][m]);
+                            }
+                            if constexpr (WT == kWQ40) {
+                                const f32x4 xh = *(const f32x4*)(xp + 16 + 4 * i);
+#pragma unroll
+                                for (int v = 0; v < VR; v++) {
+                                    part[v][m] = fmaf(xh.x, q[v][4], part[v][m]);
+                                    part[v][m] = fmaf(xh.y, q[v][5], part[v][m]);
+                                    part[v][m] = fmaf(xh.z, q[v][6], part[v][m]);
+                                    part[v][m] = fmaf(xh.w, q[v][7], part[v][m]);
+                                }
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int v = 0; v < VR; v++) {
+                        const float d = f16_to_f32(half_at(w[v], h * BB));
+#pragma unroll
+                        for (int m = 0; m < MR; m++) {
+                            const float t = (WT == kWQ40) ? fmaf(-8.0f, ssum[m][b], part[v][m]) : part[v][m];
+                            acc[v][m] = fmaf(d, t, acc[v][m]);
+                        }
+                    }
+                }
+            }
+        }
+        if (kb0 + kW16KTile / 32 < nb) __syncthreads();   // the next tile overwrites the LDS
+    }
+#pragma unroll
+    for (int v = 0; v < VR; v++)
+#pragma unroll
+        for (int m = 0; m < MR; m++) acc[v][m] = wave_sum(acc[v][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int v = 0; v < VR; v++)
+            if (row0 + v < N) {
+#pragma unroll
+                for (int m = 0; m < MR; m++) C[(size_t)m * N + row0 + v] = acc[v][m];
+            }
+    }
+}
+
 namespace {
 constexpr int kW16MinWGs = 256, kW16TargetWGs = 512, kW16MaxSplits = 16;
+constexpr int kW16GemvMaxRows = 4;
+bool w16_uses_gemv(int M) { return M >= 1 && M <= kW16GemvMaxRows; }
 
 bool w16_skinny(int M) { return M <= 32; }
 
@@ -247,7 +409,7 @@ int w16_grid_wgs(int M, int N) {
 }  // namespace
 
 int w16_splits(int M, int N, int K) {
-    if (M <= 0 || N <= 0 || K <= 0) return 1;
+    if (M <= 0 || N <= 0 || K <= 0 || w16_uses_gemv(M)) return 1;
     const int wgs = w16_grid_wgs(M, N), steps = K / 64;
     if (wgs >= kW16MinWGs) return 1;
     int sp = (kW16TargetWGs + wgs - 1) / wgs;
@@ -270,9 +432,37 @@ static hipError_t w16_launch(const float* A, const uint8_t* W, float* C, int M, 
     return hipGetLastError();
 }
 
+template <int WT, int MR>
+static hipError_t w16_gemv_launch(const float* A, const uint8_t* W, float* C, int N, int K, hipStream_t s) {
+    const int nb = K / 32;
+    // 4 weight rows per wave while that keeps 256 workgroups, else 2 or 1
+    if ((N + 15) / 16 >= kW16MinWGs)
+        hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 16>), dim3((N + 15) / 16), dim3(256), 0, s, W, A, C, N, nb);
+    else if ((N + 7) / 8 >= kW16MinWGs)
+        hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 8>), dim3((N + 7) / 8), dim3(256), 0, s, W, A, C, N, nb);
+    else
+        hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 4>), dim3((N + 3) / 4), dim3(256), 0, s, W, A, C, N, nb);
+    return hipGetLastError();
+}
+
+template <int WT>
+static hipError_t w16_gemv_dispatch(const float* A, const uint8_t* W, float* C, int M, int N, int K, hipStream_t s) {
+    switch (M) {
+        case 1: return w16_gemv_launch<WT, 1>(A, W, C, N, K, s);
+        case 2: return w16_gemv_launch<WT, 2>(A, W, C, N, K, s);
+        case 3: return w16_gemv_launch<WT, 3>(A, W, C, N, K, s);
+        default: return w16_gemv_launch<WT, 4>(A, W, C, N, K, s);
+    }
+}
+
 hipError_t launch_w16(int wtype, const float* A, const uint8_t* W, float* C, int M, int N, int K, float* partials,
                       hipStream_t s) {
     if (wtype != kWQ40 && wtype != kWQ80) return hipErrorNotSupported;
+    if (w16_uses_gemv(M)) {
+        note_engine(KSQ_ENG_W16);
+        return wtype == kWQ40 ? w16_gemv_dispatch<kWQ40>(A, W, C, M, N, K, s)
+                              : w16_gemv_dispatch<kWQ80>(A, W, C, M, N, K, s);
+    }
     const int splits = w16_splits(M, N, K);
     note_engine(KSQ_ENG_W16 | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
     float* out = C;

@@ -67,7 +67,8 @@ def _run(dev, wtype, x, w, M, N, K, workspace=False):
 
 
 @pytest.mark.parametrize("wtype", [0, 1])
-@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (7, 200, 320), (32, 384, 2048), (45, 130, 576),
+@pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (2, 300, 1024), (3, 520, 2048), (4, 130, 8320),
+                                   (1, 4096, 14336), (7, 200, 320), (32, 384, 2048), (45, 130, 576),
                                    (300, 256, 1024), (129, 1024, 4096)])
 def test_w16_integer_inputs_exact(dev, wtype, M, N, K):
     from ksq import ops
@@ -84,7 +85,8 @@ def test_w16_integer_inputs_exact(dev, wtype, M, N, K):
 
 
 @pytest.mark.parametrize("wtype", [0, 1])
-@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 512, 2048), (96, 640, 1536), (512, 512, 4096)])
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (3, 1000, 8192), (16, 512, 2048), (96, 640, 1536),
+                                   (512, 512, 4096)])
 def test_w16_random_vs_oracle(dev, oracle, wtype, M, N, K):
     from ksq import refcheck
     g = np.random.default_rng(600 + M + wtype)
