@@ -648,12 +648,11 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
                 load_x32<false>(Ain, (size_t)m * nb * 32 + (size_t)(2 * t0 + u) * 32, x0);
             }
         }
+        // unconditional loads (row and pair clamped in range), so that the fused quantisation
+        // below waits only for its own activation loads (see gemv_direct_fq_kernel)
         uint32_t w[VR][PW];
-        if (p < t0 + tp) {
 #pragma unroll
-            for (int v = 0; v < VR; v++)
-                if (row0 + v < N) mr_load_w<WT>(W, row0 + v, nb, p, w[v]);
-        }
+        for (int v = 0; v < VR; v++) mr_load_w<WT>(W, min(row0 + v, N - 1), nb, min(p, t0 + tp - 1), w[v]);
         // stage the tile: row m's tp pairs (tp * 72 contiguous bytes from pair t0) are copied by
         // wave m % 4 with LDS DMA; its first byte lands at ashift[m] (the source's offset mod 16)
         int ashift[MR];
@@ -909,10 +908,14 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
         const int m = (int)threadIdx.x / nb, u = (int)threadIdx.x - m * nb;
         load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x0);
     }
+    // unconditional loads (row and pair clamped in range; lanes past them discard the data): with a
+    // conditional load the compiler must assume none is pending on the other path and would wait
+    // for every load, weights included, before the quantisation
     uint32_t w[VR][PW];
 #pragma unroll
     for (int v = 0; v < VR; v++)
-        if (p < np && row0 + v < N) load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
+        load_dwords<PW>((const uint32_t*)(W + (size_t)min(row0 + v, N - 1) * nb * BB) + (size_t)min(p, np - 1) * PW,
+                        w[v]);
     for (int t = threadIdx.x; t < MR * nb; t += 256) {
         const int m = t / nb, u = t - m * nb;
         float x[32];
