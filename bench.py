@@ -43,15 +43,20 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 # copy gives the same counters (reads x2.0, writes x1.0; profiles/copy_calibration.md).  Each
 # figure names the committed summary it comes from.
 TRAFFIC = {
-    "gemm": (int((41688.8 * 2.0 + 33052.6) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
-    "gemv": (int((4641.9 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
+    "gemm": (int((41623.4 * 2.0 + 33206.2) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
+    "gemv": (int((4642.0 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "q8_0_M1": (int((8737.5 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q8_0_M8": (int((8894.7 * 2.0 + 128.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
-    "q8_0_M32": (int(((9337.1 + 2068.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
-    "q4_K_M128": (int((18492.5 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
-    "q6_K_M128": (int((26582.8 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
-    "moe_q4_0_T512_E8_top2": (int(((166837.1 + 4137.5 + 19.0) * 2.0 + 57344.0 + 30976.0 + 12.2) * 1024),
+    "q8_0_M32": (int(((9342.3 + 2068.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q4_K_M128": (int(((19046.2 + 10772.5) * 2.0 + 21504.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "q6_K_M128": (int((26591.4 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "moe_q4_0_T512_E8_top2": (int(((165292.3 + 4144.6 + 19.0) * 2.0 + 57344.0 + 30976.0 + 12.2) * 1024),
                               "profiles/moe_q4_0_t512_e8_top2.md"),
+    "w4a16_q4_0_M1": (int((4732.8 * 2.0 + 16.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
+    "w4a16_q4_0_M2048": (int((142071.9 * 2.0 + 32768.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
+    "deepseek_v2_q8f_q4_0_M2048": (int(((45746.6 + 16439.1) * 2.0 + 32838.0 + 10240.0) * 1024),
+                                   "profiles/q8f_q4_0_m2048_n4096_k4096.md"),
+    "fp16_fused_q4_0_N1": (int((4702.4 * 2.0 + 16.0) * 1024), "profiles/fp16_fused_q4_0_n1_k4096.md"),
 }
 
 ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
@@ -303,13 +308,14 @@ def extra_paths(wl: Workloads, reps: int = 4) -> dict:
     for M in (1, 2048):
         (M, N, K), fn, copies = wl.w16(M)
         ms, d = graph_stats(fn, copies, reps)
-        e = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K)
+        e = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K, f"w4a16_q4_0_M{M}")
         if M > 1:
             # three bf16 MFMA products per fp32 product (exact split of the activations)
             tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
             e["roofline"] = {"bound": "mfma", "achieved": round(tf, 2), "peak": round(BF16_PEAK_TFLOPS / 3, 1),
                              "unit": "TFLOP/s (fp32-exact products: 3 bf16 MFMA terms)",
-                             "frac": round(tf / (BF16_PEAK_TFLOPS / 3), 4)}
+                             "frac": round(tf / (BF16_PEAK_TFLOPS / 3), 4), "traffic": TRAFFIC[f"w4a16_q4_0_M{M}"][0],
+                             "traffic_source": TRAFFIC[f"w4a16_q4_0_M{M}"][1]}
         out[f"w4a16_q4_0_M{M}"] = e
         del fn
     (M, N, K), fn, copies = wl.q8f()
@@ -317,12 +323,14 @@ def extra_paths(wl: Workloads, reps: int = 4) -> dict:
     e = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K)
     top = 2.0 * M * N * K / (ms * 1e-3) / 1e12
     e["roofline"] = {"bound": "mfma", "achieved": round(top, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
-                     "frac": round(top / INT8_PEAK_TOPS, 4)}
+                     "frac": round(top / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC["deepseek_v2_q8f_q4_0_M2048"][0],
+                     "traffic_source": TRAFFIC["deepseek_v2_q8f_q4_0_M2048"][1]}
     out["deepseek_v2_q8f_q4_0_M2048"] = e
     del fn
     (Mw, Na, K), fn, copies = wl.f16_fused()
     ms, d = graph_stats(fn, copies, reps)
-    out["fp16_fused_q4_0_N1"] = hbm_entry(Mw * (K // 32) * 18 + Na * K * 2 + Mw * Na * 4, ms, d, 2.0 * Mw * Na * K)
+    out["fp16_fused_q4_0_N1"] = hbm_entry(Mw * (K // 32) * 18 + Na * K * 2 + Mw * Na * 4, ms, d, 2.0 * Mw * Na * K,
+                                          "fp16_fused_q4_0_N1")
     del fn
     wl.torch.cuda.empty_cache()
     return out
