@@ -5,7 +5,7 @@
 // block formula of gemm_w4a8_reference / gemm_w8a8_reference (include/gemm_reference.h:175-267).
 //
 // gfx950 design:
-//  * A BM x BN workgroup tile, 4 waves each owning TM x TN tiles of 32 x 32 computed
+//  * A BM x BN workgroup tile, four waves each owning TM x TN tiles of 32 x 32 computed
 //    with v_mfma_i32_32x32x32_i8.  One MFMA contracts exactly one 32-element Q block,
 //    so its i32 result IS the reference's integer block dot sumi for a 32 x 32 patch.
 //  * Per K step KB blocks are staged in LDS: Q8_1 quants as int8 rows, Q4_0 / Q4_1
@@ -41,13 +41,19 @@ constexpr float kMagicF = 12582912.0f;
 typedef uint32_t u32x2_a8 __attribute__((ext_vector_type(2), aligned(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
+template <int V>
+struct IntC {
+    static constexpr int value = V;
+};
+
 template <int BM_, int BN_, int KB_, int TM_, int TN_, int OCC_, bool PIPE_ = false>
 struct Tile {
     static constexpr int BM = BM_, BN = BN_, KB = KB_, TM = TM_, TN = TN_, OCC = OCC_;
     static constexpr bool PIPE = PIPE_;   // staging loads of the next K step prefetched into registers
     static constexpr int WN = BN / (32 * TN);          // waves along N
     static constexpr int WM = BM / (32 * TM);          // waves along M
-    static_assert(WN * WM == 4, "four waves per workgroup");
+    static constexpr int NT = 64 * WN * WM;            // threads per workgroup
+    static_assert(WN * WM == 4 || WN * WM == 8, "four or eight waves per workgroup");
     static_assert(KB == 4 || KB == 8, "K step of 4 or 8 blocks");
     static constexpr int APitch = KB * 32 + 16;        // bytes per staged activation row
 };
@@ -120,7 +126,7 @@ __device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
 // global loads of K step k+1 are issued into registers before step k computes (threads 0..127
 // hold an activation chunk, 128..255 a weight chunk), so their latency hides behind the MFMAs.
 template <class T, int WT, bool DUMP, bool MOE, int AF>
-__global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
                                                           int32_t* __restrict__ dump, int M, int N, int nb,
                                                           MoeTiles moe, int trans) {
@@ -193,7 +199,8 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
 #pragma unroll
     for (int r = 0; r < 16; r++) bias[r] = DUMP ? 0 : (int)kMagic;
 
-    const bool wave_has_rows = M - m0 - wm * 32 * TM > 0;   // wave-uniform
+    const int wave_rows = M - m0 - wm * 32 * TM;            // rows of this wave's tiles (wave-uniform)
+    const bool wave_has_rows = wave_rows > 0;
 
     // split-K: workgroup z of gridDim.z covers K steps [z*steps/Z, (z+1)*steps/Z) and writes its
     // partial sums to C + z*M*N (the caller adds the partials)
@@ -286,7 +293,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         }
     };
     constexpr bool PIPE = T::PIPE && !MOE && !is_kquant(WT);
-    static_assert(!PIPE || (KB == 4 && BM == 128 && BN == 128),
+    static_assert(!PIPE || (KB == 4 && BM == 128 && BN == 128 && T::NT == 256),
                   "the pipelined staging covers 128 x 128 tiles with 4-block K steps");
     // PIPE: one chunk per thread and K step; threads 0..127 activation row t, 128..255 weight row t-128
     uint32_t pre[PIPE ? 4 * ABW : 1];
@@ -309,7 +316,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             if (kb0 + KB < kb_hi) pre_load(kb0 + KB);
         } else {
         // ---- stage activations
-        for (int c = t; c < BM * (KB / 4); c += 256) {
+        for (int c = t; c < BM * (KB / 4); c += T::NT) {
             const int sr = c / (KB / 4), g = c % (KB / 4);
             uint32_t v[4 * ABW];
             load_act(sr, g, kb0, v);
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         }
         if constexpr (!is_kquant(WT)) {
             // ---- stage weights
-            for (int c = t; c < BN * (KB / 4); c += 256) {
+            for (int c = t; c < BN * (KB / 4); c += T::NT) {
                 const int sr = c / (KB / 4), g = c % (KB / 4);
                 uint32_t v[WNW + 2];
                 load_w(sr, g, kb0, v);
@@ -326,7 +333,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         } else if constexpr (WT == kWQ4K) {
             // ---- Q4_K: one 144-byte super-block per row and K step (16-byte aligned)
             const int nsb = nb / 8, s0 = kb0 / 8;
-            for (int sr = t; sr < BN; sr += 256) {
+            for (int sr = t; sr < BN; sr += T::NT) {
                 const int wr = min(n0 + sr, N - 1);
                 const uint8_t* p = W + ((size_t)wr * nsb + s0) * kQ4KBytes;
                 uint32_t v[36];
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             // ---- Q6_K: one 210-byte super-block per row and K step (2-byte aligned); two
             // threads per row, each unpacking one 128-element half to int8 (q - 32)
             const int nsb = nb / 8, s0 = kb0 / 8;
-            for (int c = t; c < 2 * BN; c += 256) {
+            for (int c = t; c < 2 * BN; c += T::NT) {
                 const int sr = c >> 1, h = c & 1;
                 const int wr = min(n0 + sr, N - 1);
                 const uint8_t* sb = W + ((size_t)wr * nsb + s0) * kQ6KBytes;
@@ -454,31 +461,30 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             }
         };
 
-        // KB*SUB*TN*TM MFMAs per K step; step q = ((b*SUB + h)*TN + j)*TM + i.  For Q6_K the two
-        // 16-element sub-blocks of a block are separate MFMAs whose weight fragment keeps only the
-        // lanes holding that half (k = 16*hi ..).  The MFMA of step q+1 is issued before the
-        // epilogue of step q.
+        // KB*SUB*TN*TA MFMAs per K step, over the wave's first TA of its TM row tiles; step
+        // q = ((b*SUB + h)*TN + j)*TA + i.  For Q6_K the two 16-element sub-blocks of a block are
+        // separate MFMAs whose weight fragment keeps only the lanes holding that half
+        // (k = 16*hi ..).  The MFMA of step q+1 is issued before the epilogue of step q.
         constexpr int SUBN = S::SUB;
-        constexpr int NQ = KB * SUBN * TM * TN;
-        i32x4 af[TM], bf[TN];
-        auto mfma_step = [&](int q) -> i32x16 {
-            const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
-            const int j = (q / TM) % TN, i = q % TM;
-            if (q % (SUBN * TM * TN) == 0) {
+        auto compute = [&](auto ta) {
+            constexpr int TA = decltype(ta)::value;
+            constexpr int NQ = KB * SUBN * TA * TN;
+            i32x4 af[TA], bf[TN];
+            auto mfma_step = [&](int q) -> i32x16 {
+                const int b = q / (SUBN * TA * TN), h = (q / (TA * TN)) % SUBN;
+                const int j = (q / TA) % TN, i = q % TA;
+                if (q % (SUBN * TA * TN) == 0) {
 #pragma unroll
-                for (int ii = 0; ii < TM; ii++) af[ii] = frag_a(b, ii);
+                    for (int ii = 0; ii < TA; ii++) af[ii] = frag_a(b, ii);
 #pragma unroll
-                for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b(b, jj);
-            }
-            i32x4 bb = bf[j];
-            if constexpr (SUBN == 2) {
-                if (hi != h) bb = i32x4{0, 0, 0, 0};
-            }
-            return __builtin_amdgcn_mfma_i32_32x32x32_i8(bb, af[i], bias, 0, 0, 0);
-        };
-        // A wave whose rows all lie past the tile's last row (ragged MoE tiles, the last row
-        // tile of a ragged M) skips its MFMAs and epilogues; staging and barriers stay shared.
-        if (wave_has_rows) {
+                    for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b(b, jj);
+                }
+                i32x4 bb = bf[j];
+                if constexpr (SUBN == 2) {
+                    if (hi != h) bb = i32x4{0, 0, 0, 0};
+                }
+                return __builtin_amdgcn_mfma_i32_32x32x32_i8(bb, af[i], bias, 0, 0, 0);
+            };
             // the compute phase of this wave goes first at instruction issue: with two workgroups
             // per CU the other one is usually staging (Q4_K M = 128: 50.0 -> 45.8 us, Q8_0
             // M = 2048 -2%, the rest level)
@@ -486,14 +492,34 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             i32x16 cur = mfma_step(0);
 #pragma unroll
             for (int q = 0; q < NQ; q++) {
-                const int b = q / (SUBN * TM * TN), h = (q / (TM * TN)) % SUBN;
-                const int j = (q / TM) % TN, i = q % TM;
+                const int b = q / (SUBN * TA * TN), h = (q / (TA * TN)) % SUBN;
+                const int j = (q / TA) % TN, i = q % TA;
                 i32x16 nxt = bias;
                 if (q + 1 < NQ) nxt = mfma_step(q + 1);
                 epilogue(b, b * SUBN + h, i, j, cur);
                 cur = nxt;
             }
             __builtin_amdgcn_s_setprio(0);
+        };
+        // A wave whose rows all lie past the tile's last row (ragged MoE tiles, the last row
+        // tile of a ragged M) skips its MFMAs and epilogues; staging and barriers stay shared.
+        // In a ragged MoE tile a wave also skips those of its row tiles that hold no row.
+        if (wave_has_rows) {
+            if constexpr (MOE && TM > 1) {
+                const int nta = min(TM, (wave_rows + 31) / 32);   // row tiles with rows, >= 1
+                auto pick = [&](auto self, auto ta) {
+                    constexpr int TA = decltype(ta)::value;
+                    if constexpr (TA == TM) {
+                        compute(ta);
+                    } else {
+                        if (nta == TA) compute(ta);
+                        else self(self, IntC<TA + 1>{});
+                    }
+                };
+                pick(pick, IntC<1>{});
+            } else {
+                compute(IntC<TM>{});
+            }
         }
 
         if constexpr (SIDE_MFMA && !DUMP) {
@@ -502,6 +528,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
             // over 8 block slots, exact products
 #pragma unroll
             for (int i = 0; i < TM; i++) {
+                if (MOE && wave_rows <= 32 * i) continue;   // a row tile without rows (wave-uniform)
                 const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 32 * TM + i * 32 + l32][4 * hi];
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
@@ -523,10 +550,11 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
         // staging buffer is free after the last K step's barrier) so that the atomics of one
         // instruction cover 32 consecutive columns of one token instead of 32 tokens.
         constexpr int kTP = 33;   // padded row pitch (floats) of the [32 m][32 n] transpose
-        static_assert(4 * 32 * kTP * 4 <= BM * T::APitch, "transpose scratch fits the activation tile");
+        static_assert(T::NT / 64 * 32 * kTP * 4 <= BM * T::APitch, "transpose scratch fits the activation tile");
         float* tp = (float*)sA + wave * 32 * kTP;
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++) {
+            if (wave_rows <= 32 * i) break;   // no rows in this or a later row tile (wave-uniform)
 #pragma unroll
             for (int j = 0; j < TN; j++) {
 #pragma unroll
@@ -545,6 +573,7 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
                 }
                 __builtin_amdgcn_wave_barrier();
             }
+        }
     } else if constexpr (!DUMP) {
         constexpr float out_scale = S::out_scale;
         const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
@@ -592,13 +621,20 @@ __global__ __launch_bounds__(256, T::OCC) void mmq_kernel(const uint8_t* __restr
 }
 
 // ---- tile configurations ----------------------------------------------------------
-using TileL = Tile<128, 128, 8, 2, 2, 2>;   // large M: 64 x 64 per wave
+// 128 rows x 32 columns per wave: one weight fragment (the one that needs its nibbles unpacked)
+// per four MFMAs (Q4_0 M = 2048, N = K = 4096: 99 vs 101 us for 64 x 64 per wave)
+using TileL = Tile<128, 128, 8, 4, 1, 2>;   // large M
 using TileN = Tile<128, 64, 8, 2, 1, 2>;    // half the columns per workgroup: twice the workgroups
 using TileS = Tile<64, 64, 8, 1, 1, 3>;     // 32 x 32 per wave, 4x the workgroups of TileL
-using TileK4 = Tile<128, 128, 4, 2, 2, 3>;  // half the K step: smaller LDS, more resident workgroups
+// half the K step without prefetch (selected only explicitly: its exposed load latency makes it
+// the slowest 128 x 128 form, Q4_0 M = 2048, N = K = 4096: 192 us); two workgroups per CU, as
+// three would need more registers than a wave then has
+using TileK4 = Tile<128, 128, 4, 2, 2, 2>;
 using TileT = Tile<32, 128, 8, 1, 1, 3>;    // skinny: M <= 32, the four waves side by side along N
 using TileP = Tile<128, 128, 4, 2, 2, 2, true>;  // 128 x 128, K step 4, next step's loads prefetched
-using TileW = Tile<64, 128, 8, 1, 2, 3>;    // 64 x 128: 32 x 64 per wave, 64-row granularity
+// 64 x 128, 64 x 32 per wave, 64-row granularity (MoE config 4: 294 vs 310 us for 32 x 64 per
+// wave; Q4_K M = 128, N = 14336: 42.8 vs 45.5)
+using TileW = Tile<64, 128, 8, 2, 1, 3>;
 
 static thread_local int g_mmq_config = 0;  // 0 = automatic; set per host thread
 
@@ -773,7 +809,7 @@ static hipError_t launch_k(dim3 grid, const uint8_t* W, const uint8_t* A, float*
     if constexpr (is_kquant(WT) && (T::KB != 8 || MOE)) {
         return hipErrorNotSupported;
     } else {
-        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AF>), grid, dim3(256), 0, s, W, A, C, dump, M, N, nb, mt, trans);
+        hipLaunchKernelGGL((mmq_kernel<T, WT, DUMP, MOE, AF>), grid, dim3(T::NT), 0, s, W, A, C, dump, M, N, nb, mt, trans);
         return hipGetLastError();
     }
 }
