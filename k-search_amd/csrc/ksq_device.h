@@ -295,6 +295,80 @@ __device__ __forceinline__ float wave_sum(float v) {
 #endif
 }
 
+// 16 consecutive fp32 activations starting at element `off` of X (16-byte aligned).
+__device__ __forceinline__ void load_x16(const float* X, size_t off, float* x) {
+    const f32x4* src = (const f32x4*)(X + off);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const f32x4 q = src[i];
+        x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+    }
+}
+
+// One block_q8_1 quantised by a lane pair: lanes 2i and 2i+1 of a wave hold elements 0..15 and
+// 16..31 (h = lane & 1) of the same block in v[0..15].  The bytes are those of
+// quantize_block_q8_1:
+//  * amax is the larger of the two halves' maxima (a max that skips NaN, as both forms there do);
+//  * both lanes compute d = amax / 127 and 1/d;
+//  * the sum stays the left-to-right fp32 sum: the odd lane continues from the even lane's
+//    partial sum of elements 0..15, and hands the total back;
+//  * each lane quantises its own 16 values.
+// The even lane writes words 1..4 of the block at dst, the odd lane words 0 (d, s) and 5..8.
+// Both lanes of every pair must be active.
+__device__ __forceinline__ void quantize_block_q8_1_pair(const float* v, int h, uint32_t* dst) {
+#pragma clang fp contract(off)
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) part += v[j];
+    float sum = dpp_mov<0xB1>(part);                 // quad_perm [1,0,3,2]: the partner's value
+#pragma unroll
+    for (int j = 0; j < 16; j++) sum += v[j];       // the total on the odd lane
+    const float sum_odd = dpp_mov<0xB1>(sum);
+    const float s = h ? sum : sum_odd;
+    const bool finite = __builtin_isfinite(s);
+    float am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float a = fabsf(v[j]);
+        am = (am < a) ? a : am;
+    }
+    const float am_other = dpp_mov<0xB1>(am);
+    const float amax = (am < am_other) ? am_other : am;
+    const float d = amax / 127.0f;
+    const float id = (d > 0.0f) ? 1.0f / d : 0.0f;
+    uint32_t q4[4];
+    if (finite && __builtin_isfinite(id)) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            int q[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float y = v[4 * j + t] * id;
+                q[t] = (int)(y + __builtin_copysignf(0.49999997f, y));
+            }
+            const uint32_t lo = (uint32_t)__builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[0], q[1]));
+            const uint32_t hi = (uint32_t)__builtin_bit_cast(int, __builtin_amdgcn_cvt_pk_i16(q[2], q[3]));
+            q4[j] = __builtin_amdgcn_perm(hi, lo, 0x06040200u);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            uint32_t packed = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) packed |= clamp_i8(round_to_i32(v[4 * j + t] * id)) << (8 * t);
+            q4[j] = packed;
+        }
+    }
+    if (h) {
+        dst[0] = f32_to_f16(d) | (f32_to_f16(s) << 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[5 + j] = q4[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[1 + j] = q4[j];
+    }
+}
+
 // Bits 0..3 of x moved to bit 4 of the four bytes of a word: the fifth bit of four
 // consecutive Q5_0 / Q5_1 quants.  The product places bit k of x at bit 8k (its shifted
 // copies x, x<<7, x<<14, x<<21 do not overlap, so nothing carries).

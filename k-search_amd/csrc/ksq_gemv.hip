@@ -902,11 +902,21 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
     // this thread's first activation block is loaded before the weight pairs: global loads
     // complete in issue order, so its quantisation waits only for it and runs while the weight
     // loads are in flight (loaded after them, the quantisation would wait for the weights too)
-    float x0[32];
-    const bool has0 = (int)threadIdx.x < MR * nb;
+    // fp32 -> block_q8_1: each block is quantised by a lane pair (16 elements a lane), which
+    // spreads the quantisation over all four waves (config 0, fp32 entry: 5.35 -> us); the other
+    // forms quantise a block per lane
+    constexpr bool PAIR = !AS && !XH;
+    const int nq = PAIR ? 2 * MR * nb : MR * nb;   // half blocks or blocks to quantise
+    float x0[PAIR ? 16 : 32];
+    const bool has0 = (int)threadIdx.x < nq;
     if (has0) {
-        const int m = (int)threadIdx.x / nb, u = (int)threadIdx.x - m * nb;
-        load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x0);
+        if constexpr (PAIR) {
+            const int u = (int)threadIdx.x >> 1, m = u / nb, ub = u - m * nb;
+            load_x16((const float*)X, (size_t)m * K + (size_t)ub * 32 + 16 * (threadIdx.x & 1), x0);
+        } else {
+            const int m = (int)threadIdx.x / nb, u = (int)threadIdx.x - m * nb;
+            load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x0);
+        }
     }
     // unconditional loads (row and pair clamped in range; lanes past them discard the data): with a
     // conditional load the compiler must assume none is pending on the other path and would wait
@@ -916,22 +926,35 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
     for (int v = 0; v < VR; v++)
         load_dwords<PW>((const uint32_t*)(W + (size_t)min(row0 + v, N - 1) * nb * BB) + (size_t)min(p, np - 1) * PW,
                         w[v]);
-    for (int t = threadIdx.x; t < MR * nb; t += 256) {
-        const int m = t / nb, u = t - m * nb;
-        float x[32];
-        if (t == (int)threadIdx.x) {
+    for (int t = threadIdx.x; t < nq; t += 256) {
+        if constexpr (PAIR) {
+            // half block t & 1 of block u (the partner lane t ^ 1 holds the other half)
+            const int u = t >> 1, m = u / nb, ub = u - m * nb;
+            float x[16];
+            if (t == (int)threadIdx.x) {
 #pragma unroll
-            for (int i = 0; i < 32; i++) x[i] = x0[i];
+                for (int i = 0; i < 16; i++) x[i] = x0[i];
+            } else {
+                load_x16((const float*)X, (size_t)m * K + (size_t)ub * 32 + 16 * (t & 1), x);
+            }
+            quantize_block_q8_1_pair(x, t & 1, (uint32_t*)(smem + (size_t)u * kQ81Bytes));
         } else {
-            load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x);
-        }
-        uint32_t blk[9];
-        if constexpr (AS) quantize_block_q8s(x, blk);
-        else if constexpr (XH) quantize_block_q8_1_f16tree(x, blk);
-        else quantize_block_q8_1(x, blk);
-        uint32_t* dst = (uint32_t*)(smem + (size_t)t * kQ81Bytes);
+            const int m = t / nb, u = t - m * nb;
+            float x[32];
+            if (t == (int)threadIdx.x) {
 #pragma unroll
-        for (int i = 0; i < 9; i++) dst[i] = blk[i];
+                for (int i = 0; i < 32; i++) x[i] = x0[i];
+            } else {
+                load_x32<XH>(X, (size_t)m * K + (size_t)u * 32, x);
+            }
+            uint32_t blk[9];
+            if constexpr (AS) quantize_block_q8s(x, blk);
+            else if constexpr (XH) quantize_block_q8_1_f16tree(x, blk);
+            else quantize_block_q8_1(x, blk);
+            uint32_t* dst = (uint32_t*)(smem + (size_t)t * kQ81Bytes);
+#pragma unroll
+            for (int i = 0; i < 9; i++) dst[i] = blk[i];
+        }
     }
     __syncthreads();
     float acc[VR][MR];

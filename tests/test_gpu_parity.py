@@ -258,6 +258,66 @@ def test_prequantized_entry_matches_fp32_entry(dev, oracle, wtype):
     assert np.array_equal(y32, yq)
 
 
+def _order_sensitive_rows(g, M, K):
+    """fp32 activation rows whose every block has its left-to-right fp32 sum and the sum of its two
+    16-element halves' partial sums rounding to different fp16 values (so the s field of
+    block_q8_1 pins the reference's summation order), with |d| and |s| inside fp16's range."""
+    f16 = np.float16
+    out = np.empty((M * K // 32, 32), np.float32)
+    n = 0
+    while n < out.shape[0]:
+        c = (g.standard_normal((4096, 32)) * 10.0 ** g.uniform(-3, 0, (4096, 1))).astype(np.float32)
+        i = np.arange(4096)
+        big = g.uniform(1e3, 3e4, 4096).astype(np.float32)
+        c[i, g.integers(0, 16, 4096)] = big
+        c[i, g.integers(16, 32, 4096)] = -big * np.float32(1.0 + 1e-4) * g.choice([1, -1], 4096).astype(np.float32)
+        seq = np.add.accumulate(c, axis=1, dtype=np.float32)[:, -1]
+        halves = (np.add.accumulate(c[:, :16], axis=1, dtype=np.float32)[:, -1]
+                  + np.add.accumulate(c[:, 16:], axis=1, dtype=np.float32)[:, -1]).astype(np.float32)
+        keep = c[(seq.astype(f16) != halves.astype(f16)) & np.isfinite(seq.astype(f16))]
+        take = min(len(keep), out.shape[0] - n)
+        out[n:n + take] = keep[:take]
+        n += take
+    return out.reshape(M, K)
+
+
+# (weight type, activation type (0 fp32, 4 fp16), M, N, K, the engines that must quantise in-kernel)
+IN_KERNEL_QUANT_CASES = [
+    (0, 0, 1, 512, 4096, {"gemv_direct_fq"}),      # lane-pair quantiser, one round
+    (0, 0, 2, 512, 4096, {"gemv_direct_fq"}),      # lane pairs, two rounds
+    (0, 0, 1, 256, 14336, {"gemv_direct_fq"}),     # lane pairs, 3.5 rounds
+    (1, 0, 1, 384, 2048, {"gemv_direct_fq"}),
+    (5, 0, 1, 384, 2048, {"gemv_direct_fq"}),
+    (0, 0, 4, 512, 2048, {"gemv_mr_fq"}),          # 3-8 rows: a block per lane
+    (0, 4, 1, 512, 4096, {"gemv_direct_fq"}),      # fp16 by the fused FP16 kernels' rules
+    (0, 4, 2, 512, 2048, {"gemv_direct_fq"}),
+]
+
+
+@pytest.mark.parametrize("wtype,atype,M,N,K,engines", IN_KERNEL_QUANT_CASES)
+def test_in_kernel_quantisers_bit_exact(dev, oracle, wtype, atype, M, N, K, engines):
+    """The fused fp32 / fp16 entries quantise inside the GEMV workgroups; on blocks whose s field
+    depends on the summation order (see _order_sensitive_rows) their output equals, bit for bit,
+    the pre-quantised entry's output on the oracle's blocks (quantize_row_q8_1_ref, or the fused
+    FP16 quantiser for fp16): the same block bytes went in, and the per-row arithmetic after the
+    quantisation is the same code (types without a min term, so no fma contraction differs)."""
+    from ksq import ops, synth
+    g = np.random.default_rng(2300 + 17 * wtype + M + K + atype)
+    w = synth.weights(wtype, g, N, K)
+    x = _order_sensitive_rows(g, M, K)
+    if atype == 4:
+        x = x.astype(np.float16)
+        blocks = oracle.quantize_q8_1_variant(x, 3)
+    else:
+        blocks = oracle.quantize_q8_1(x)
+    y = _gpu_gemm(dev, wtype, w, x, M, N, K, atype=atype)
+    eng = ops.last_engines()
+    yq = _gpu_gemm(dev, wtype, w, blocks, M, N, K, atype=1)
+    assert eng == engines, eng
+    assert np.isfinite(y).all()
+    assert np.array_equal(y, yq)
+
+
 def test_unaligned_weight_uses_generic_path(dev, oracle):
     """A weight tensor starting 2 bytes into its buffer (blocks are only 2-byte aligned)."""
     import torch
