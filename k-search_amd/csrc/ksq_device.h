@@ -295,13 +295,29 @@ __device__ __forceinline__ float wave_sum(float v) {
 #endif
 }
 
-// 16 consecutive fp32 activations starting at element `off` of X (16-byte aligned).
-__device__ __forceinline__ void load_x16(const float* X, size_t off, float* x) {
-    const f32x4* src = (const f32x4*)(X + off);
+// 16 consecutive activations starting at element `off` of X, as fp32: X holds fp32 values, or
+// fp16 bit patterns when XH (16-byte aligned either way).
+template <bool XH>
+__device__ __forceinline__ void load_x16(const void* X, size_t off, float* x) {
+    if constexpr (XH) {
+        const u32x4* src = (const u32x4*)((const uint16_t*)X + off);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const f32x4 q = src[i];
-        x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+        for (int i = 0; i < 2; i++) {
+            const u32x4 w = src[i];
+            const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                x[8 * i + 2 * k] = f16_to_f32(ws[k] & 0xFFFFu);
+                x[8 * i + 2 * k + 1] = f16_to_f32(ws[k] >> 16);
+            }
+        }
+    } else {
+        const f32x4* src = (const f32x4*)((const float*)X + off);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const f32x4 q = src[i];
+            x[4 * i] = q.x; x[4 * i + 1] = q.y; x[4 * i + 2] = q.z; x[4 * i + 3] = q.w;
+        }
     }
 }
 
@@ -361,6 +377,56 @@ __device__ __forceinline__ void quantize_block_q8_1_pair(const float* v, int h, 
     }
     if (h) {
         dst[0] = f32_to_f16(d) | (f32_to_f16(s) << 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[5 + j] = q4[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[1 + j] = q4[j];
+    }
+}
+
+// The fused FP16 kernels' quantiser (quantize_block_q8_1_f16tree) on a lane pair laid out as for
+// quantize_block_q8_1_pair.  Its reduction tree first combines elements j and j + 16, which sit
+// in the two lanes of the pair: each lane takes its partner's 16 values, and both lanes run the
+// same tree, so both hold d and the sum; each lane then quantises its own 16 values.  Same words
+// to dst as quantize_block_q8_1_pair.
+__device__ __forceinline__ void quantize_block_q8_1_f16tree_pair(const float* v, int h, uint32_t* dst) {
+#pragma clang fp contract(off)
+    float m[16], t[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float o = dpp_mov<0xB1>(v[j]);        // the partner's element: j + 16 or j
+        const float lo = h ? o : v[j], hi = h ? v[j] : o;
+        m[j] = __builtin_fmaxf(__builtin_fabsf(lo), __builtin_fabsf(hi));
+        t[j] = lo + hi;
+    }
+#pragma unroll
+    for (int w = 8; w >= 2; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) {
+            m[j] = __builtin_fmaxf(m[j], m[j + w]);
+            t[j] += t[j + w];
+        }
+    const float d = __builtin_fmaxf(m[0], m[1]) / 127.0f;
+    const float sum = t[0] + t[1];
+    const uint32_t dh = f32_to_f16(d);
+    const float dr = f16_to_f32(dh);
+    const float id = (dr != 0.0f) ? 1.0f / dr : 0.0f;
+    uint32_t q4[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float r = roundf(v[4 * i + k] * id);
+            int q = (r != r) ? 0 : (int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+            q = q < -127 ? -127 : q;
+            w |= (uint32_t)(q & 0xFF) << (8 * k);
+        }
+        q4[i] = w;
+    }
+    if (h) {
+        dst[0] = dh | (f32_to_f16(sum) << 16);
 #pragma unroll
         for (int j = 0; j < 4; j++) dst[5 + j] = q4[j];
     } else {
