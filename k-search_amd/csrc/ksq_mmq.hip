@@ -466,7 +466,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         // separate MFMAs whose weight fragment keeps only the lanes holding that half
         // (k = 16*hi ..).  The MFMA of step q+1 is issued before the epilogue of step q.
         constexpr int SUBN = S::SUB;
-        auto compute = [&](auto ta) {
+        auto compute = [&](auto ta) __attribute__((always_inline)) {
             constexpr int TA = decltype(ta)::value;
             constexpr int NQ = KB * SUBN * TA * TN;
             i32x4 af[TA], bf[TN];
@@ -506,17 +506,18 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         // In a ragged MoE tile a wave also skips those of its row tiles that hold no row.
         if (wave_has_rows) {
             if constexpr (MOE && TM > 1) {
+                // explicit cases (a recursive dispatch was not inlined: the accumulators then
+                // went to scratch memory, 15x slower)
+                static_assert(TM <= 4, "row tiles per wave");
                 const int nta = min(TM, (wave_rows + 31) / 32);   // row tiles with rows, >= 1
-                auto pick = [&](auto self, auto ta) {
-                    constexpr int TA = decltype(ta)::value;
-                    if constexpr (TA == TM) {
-                        compute(ta);
-                    } else {
-                        if (nta == TA) compute(ta);
-                        else self(self, IntC<TA + 1>{});
-                    }
-                };
-                pick(pick, IntC<1>{});
+                if (nta >= TM) {
+                    compute(IntC<TM>{});
+                } else if (nta == 1) {
+                    compute(IntC<1>{});
+                } else if constexpr (TM >= 3) {
+                    if (nta == 2) compute(IntC<2>{});
+                    else if constexpr (TM >= 4) compute(IntC<3>{});
+                }
             } else {
                 compute(IntC<TM>{});
             }
@@ -910,10 +911,12 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
     return launch_splitk_reduce(partials, C, (int64_t)M * N, splits, s);
 }
 
-// 64 x 64 tiles (64-row granularity: an expert's rows split into tiles with little padding) until
-// the experts average 384+ rows, then for the nibble types 128 x 128 (measured on MI355X, Q4_0,
-// N = 4096, K = 14336, 2048 tokens top-2 of 8 experts: 989 vs 1184 us; 512 tokens: 486 vs 396 us
-// the other way).
+// 64-row tiles (64 x 128, little padding per expert).  The 128 x 128 form (empty 32-row tiles of a
+// ragged tile skipped) measured slower at every routed size but one on MI355X (Q4_0, top-2 of 8
+// experts, us, 64- vs 128-row tiles): 512 tokens N = 14336, K = 4096: 257 vs 301; 1024 tokens:
+// 450 vs 470; 2048 tokens N = 4096, K = 14336: 808 vs 885; 4096 tokens N = K = 4096: 487 vs 514;
+// 2048 tokens N = 14336, K = 4096: 842 vs 830.  It stays selectable through this build-time
+// threshold (rows per expert).
 #ifndef KSQ_MOE_TILE128_MIN_ROWS
 #define KSQ_MOE_TILE128_MIN_ROWS 100000
 #endif
