@@ -442,6 +442,13 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
                                               1, s);
         return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
     }
+    // block_q8f rules on 1-2 fp32 rows: the decode kernel quantises them in every workgroup too
+    if ((atype == KSQ_A_F32_Q8F_RNE || atype == KSQ_A_F32_Q8F_LROUND) && g_path != 2 && g_path != 3 &&
+        ksq::gemv_q8f_profitable(wtype, M, N, K, weight)) {
+        hipError_t e = ksq::launch_gemv_q8f(atype == KSQ_A_F32_Q8F_RNE ? KSQ_Q8F_RNE : KSQ_Q8F_LROUND, wtype,
+                                            (const uint8_t*)weight, (const float*)activation, output, M, N, K, s);
+        return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
+    }
     // fp32 / fp16 activations are quantised to the start of the (16-byte aligned) workspace,
     // which is what the GEMM then reads
     const bool f32 = atype_f32(atype), f16 = atype == KSQ_A_F16;

@@ -385,6 +385,54 @@ __device__ __forceinline__ void quantize_block_q8_1_pair(const float* v, int h, 
     }
 }
 
+// block_q8f (quantize_block_q8f, either rule) on a lane pair laid out as for
+// quantize_block_q8_1_pair: the larger of the halves' fmaxf maxima, the left-to-right sum
+// continued by the odd lane, d and the scale on both lanes, 16 quants a lane.  The even lane
+// writes words 2..5 of the 10-word block at dst, the odd lane words 0 (d), 1 (s) and 6..9.
+template <int RULE>
+__device__ __forceinline__ void quantize_block_q8f_pair(const float* v, int h, uint32_t* dst) {
+#pragma clang fp contract(off)
+    float part = 0.0f, am = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        am = __builtin_fmaxf(am, __builtin_fabsf(v[j]));
+        part += v[j];
+    }
+    float sum = dpp_mov<0xB1>(part);                 // quad_perm [1,0,3,2]: the partner's value
+#pragma unroll
+    for (int j = 0; j < 16; j++) sum += v[j];       // the total on the odd lane
+    const float amax = __builtin_fmaxf(am, dpp_mov<0xB1>(am));
+    float d, scale = 0.0f;
+    if constexpr (RULE == kQ8FRne) {
+        d = amax > 0.0f ? amax / 127.0f : 1.0f;
+    } else {
+        d = amax > 1e-10f ? amax / 127.0f : 1.0f;
+        scale = 127.0f / __builtin_fmaxf(amax, 1e-10f);
+    }
+    uint32_t q4[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const float x = v[4 * j + t];
+            const float r = (RULE == kQ8FRne) ? __builtin_rintf(x / d) : roundf(x * scale);
+            const int q = (r != r) ? 0 : (int)__builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);
+            packed |= ((uint32_t)q & 0xFFu) << (8 * t);
+        }
+        q4[j] = packed;
+    }
+    if (h) {
+        dst[0] = __builtin_bit_cast(uint32_t, d);
+        dst[1] = __builtin_bit_cast(uint32_t, sum);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[6 + j] = q4[j];
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) dst[2 + j] = q4[j];
+    }
+}
+
 // The fused FP16 kernels' quantiser (quantize_block_q8_1_f16tree) on a lane pair laid out as for
 // quantize_block_q8_1_pair.  Its reduction tree first combines elements j and j + 16, which sit
 // in the two lanes of the pair: each lane takes its partner's 16 values, and both lanes run the

@@ -486,6 +486,39 @@ __device__ __forceinline__ float reg_block_dot(const uint32_t* raw, const uint32
     else return dw * da * (float)s + f16_to_f32(half_at<OFF + 2>(raw)) * f16_to_f32(a[0] >> 16);
 }
 
+// The block at byte OFF of raw dotted with a block_q8f activation block a[10] (fp32 d, fp32 s, 32
+// quants): the integer dot, then the deepseek_v2 operator's block term d_w * (d_a * sumi - c * s_a)
+// (c = 8 for Q4_0, 16 for Q5_0; none for Q8_0), as ksq_ref_gemm_q8f states it.
+template <int WT, int OFF>
+__device__ __forceinline__ float reg_block_dot_q8f(const uint32_t* raw, const uint32_t* a) {
+    static_assert(WT == kWQ40 || WT == kWQ50 || WT == kWQ80, "block_q8f pairs with Q4_0, Q5_0 and Q8_0");
+    int s = 0;
+    if constexpr (WT == kWQ40) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = word_at<OFF + 2>(raw, i);
+            s = dot4((int)(q & 0x0F0F0F0Fu), (int)a[2 + i], s);
+            s = dot4((int)((q >> 4) & 0x0F0F0F0Fu), (int)a[6 + i], s);
+        }
+    } else if constexpr (WT == kWQ80) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s = dot4((int)word_at<OFF + 2>(raw, i), (int)a[2 + i], s);
+    } else {
+        const uint32_t h = word_at<OFF + 2>(raw, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t q = word_at<OFF + 6>(raw, i);
+            s = dot4((int)((q & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i))), (int)a[2 + i], s);
+            s = dot4((int)(((q >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i))), (int)a[6 + i], s);
+        }
+    }
+    const float dw = f16_to_f32(half_at<OFF>(raw));
+    const float da = __builtin_bit_cast(float, a[0]), sa = __builtin_bit_cast(float, a[1]);
+    if constexpr (WT == kWQ40) return dw * (da * (float)s - 8.0f * sa);
+    else if constexpr (WT == kWQ50) return dw * (da * (float)s - 16.0f * sa);
+    else return dw * (da * (float)s);
+}
+
 // C[m][row] for m < MR (1 or 2); RPW rows per 256-thread workgroup: 8 = two rows per wave (each
 // activation pair a lane loads serves both), 4 = one, 2 or 1 = 4 / RPW waves per row (their
 // partial sums meet in LDS).  A: block_q8_1 (or block_q8s when AS) [MR][nb], nb even.
@@ -883,11 +916,15 @@ __global__ __launch_bounds__(256) void gemv_direct_kq_kernel(const uint8_t* __re
 // activation rows into LDS (hiding the weight latency), and after one barrier the lanes walk
 // their pairs with the activation blocks read from LDS.  RPW 8: two rows per wave, halving
 // the quantisation each row costs.  XH: X holds fp16 activations, quantised by the fused FP16
-// kernels' rules.  Output C[m * ldc + row * ldr].
-template <int WT, int MR, bool AS, int RPW, bool XH>
+// kernels' rules.  QF 1 / 2: the rows are quantised to block_q8f by the deepseek_v2 (RNE) /
+// lm_head (LROUND) rule instead.  Output C[m * ldc + row * ldr].
+template <int WT, int MR, bool AS, int RPW, bool XH, int QF = 0>
 __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __restrict__ W, const void* __restrict__ X,
                                                              float* __restrict__ C, int N, int nb, int ldc, int ldr) {
     static_assert(!is_kquant(WT) && (MR == 1 || MR == 2), "32-element block types, 1-2 activation rows");
+    static_assert(!QF || (!AS && !XH && (WT == kWQ40 || WT == kWQ50 || WT == kWQ80)),
+                  "block_q8f: fp32 rows against Q4_0, Q5_0 or Q8_0 weights");
+    constexpr int QW = QF ? 10 : 9, QB = 4 * QW;   // words / bytes per staged activation block
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
     constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
     constexpr int BB = block_bytes(WT), PW = BB / 2;
@@ -902,9 +939,9 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
     // this thread's first activation block is loaded before the weight pairs: global loads
     // complete in issue order, so its quantisation waits only for it and runs while the weight
     // loads are in flight (loaded after them, the quantisation would wait for the weights too)
-    // fp32 or fp16 -> block_q8_1: each block is quantised by a lane pair (16 elements a lane),
-    // which spreads the quantisation over all four waves (config 0, fp32 entry: 5.40 -> 4.57 us);
-    // block_q8s quantises a block per lane
+    // fp32 or fp16 -> block_q8_1 (or block_q8f): each block is quantised by a lane pair (16
+    // elements a lane), which spreads the quantisation over all four waves (config 0, fp32 entry:
+    // 5.40 -> 4.57 us); block_q8s quantises a block per lane
     constexpr bool PAIR = !AS;
     const int nq = PAIR ? 2 * MR * nb : MR * nb;   // half blocks or blocks to quantise
     float x0[PAIR ? 16 : 32];
@@ -937,8 +974,9 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
             } else {
                 load_x16<XH>(X, (size_t)m * K + (size_t)ub * 32 + 16 * (t & 1), x);
             }
-            uint32_t* dst = (uint32_t*)(smem + (size_t)u * kQ81Bytes);
-            if constexpr (XH) quantize_block_q8_1_f16tree_pair(x, t & 1, dst);
+            uint32_t* dst = (uint32_t*)(smem + (size_t)u * QB);
+            if constexpr (QF) quantize_block_q8f_pair<QF - 1>(x, t & 1, dst);
+            else if constexpr (XH) quantize_block_q8_1_f16tree_pair(x, t & 1, dst);
             else quantize_block_q8_1_pair(x, t & 1, dst);
         } else {
             const int m = t / nb, u = t - m * nb;
@@ -972,17 +1010,22 @@ __global__ __launch_bounds__(256) void gemv_direct_fq_kernel(const uint8_t* __re
                     if (row0 + v < N)
                         load_dwords<PW>((const uint32_t*)(W + (size_t)(row0 + v) * nb * BB) + (size_t)p * PW, w[v]);
             }
-            uint32_t a[MR][18];
+            uint32_t a[MR][2 * QW];
 #pragma unroll
             for (int m = 0; m < MR; m++)
-                load_dwords<18>((const uint32_t*)(smem + ((size_t)m * nb + 2 * p) * kQ81Bytes), a[m]);
+                load_dwords<2 * QW>((const uint32_t*)(smem + ((size_t)m * nb + 2 * p) * QB), a[m]);
 #pragma unroll
             for (int v = 0; v < VR; v++)
                 if (row0 + v < N) {
 #pragma unroll
                     for (int m = 0; m < MR; m++) {
-                        acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a[m]);
-                        acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a[m] + 9);
+                        if constexpr (QF) {
+                            acc[v][m] += reg_block_dot_q8f<WT, 0>(w[v], a[m]);
+                            acc[v][m] += reg_block_dot_q8f<WT, BB>(w[v], a[m] + QW);
+                        } else {
+                            acc[v][m] += reg_block_dot<WT, AS, 0>(w[v], a[m]);
+                            acc[v][m] += reg_block_dot<WT, AS, BB>(w[v], a[m] + 9);
+                        }
                     }
                 }
         }
@@ -1393,6 +1436,53 @@ hipError_t launch_gemv_f32(int wtype, int afmt, const uint8_t* W, const float* X
 hipError_t launch_gemv_fused(int wtype, int afmt, bool xh, const uint8_t* W, const void* X, float* C, int M, int N,
                              int K, int ldc, int ldr, hipStream_t s) {
     return gemv_dispatch<false>(wtype, afmt, xh, W, X, C, M, N, K, ldc, ldr, s);
+}
+
+// ---- block_q8f decode (the deepseek_v2 / lm_head operators at 1-2 activation rows) ----------
+template <int WT, int MR, int QF>
+static hipError_t q8f_launch_rpw(int rpw, const uint8_t* W, const float* X, float* C, int N, int nb, hipStream_t s) {
+    const dim3 blk(256);
+    const size_t lds = (size_t)MR * nb * 40;
+    switch (rpw) {
+        case 8: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, false, 8, false, QF>), dim3((N + 7) / 8), blk, lds, s, W, X, C, N, nb, N, 1); break;
+        case 4: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, false, 4, false, QF>), dim3((N + 3) / 4), blk, lds, s, W, X, C, N, nb, N, 1); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, false, 2, false, QF>), dim3((N + 1) / 2), blk, lds, s, W, X, C, N, nb, N, 1); break;
+        default: hipLaunchKernelGGL((gemv_direct_fq_kernel<WT, MR, false, 1, false, QF>), dim3(N), blk, lds, s, W, X, C, N, nb, N, 1); break;
+    }
+    return hipGetLastError();
+}
+
+template <int WT, int QF>
+static hipError_t q8f_launch(int M, int rpw, const uint8_t* W, const float* X, float* C, int N, int nb, hipStream_t s) {
+    return M == 1 ? q8f_launch_rpw<WT, 1, QF>(rpw, W, X, C, N, nb, s) : q8f_launch_rpw<WT, 2, QF>(rpw, W, X, C, N, nb, s);
+}
+
+// The fused decode kernel applies: 1-2 rows of a Q4_0 / Q5_0 / Q8_0 matrix with an even block
+// count, dword-aligned weights, the rows' block_q8f blocks within the LDS budget, and the work
+// the workgroups repeat (every one quantises the rows) under the fused kernels' limit.  The MFMA
+// GEMM with split-K took 2.4x as long at M = 1 (N = K = 5120: 17.2 us; the block_q8_1 fused path
+// 7.0 us on the same box).
+bool gemv_q8f_profitable(int wtype, int M, int N, int K, const void* W) {
+    if (M < 1 || M > 2 || !(wtype == kWQ40 || wtype == kWQ50 || wtype == kWQ80)) return false;
+    const int nb = K / 32;
+    if ((nb & 1) || ((uintptr_t)W & 3) || (size_t)M * nb * 40 > kGemvLdsBudget) return false;
+    const int rpw = pick_rpw(N, kAFQ);
+    return (long long)M * ((N + rpw - 1) / rpw) * nb <= KSQ_GEMV_FUSED_MAX_WORK;
+}
+
+hipError_t launch_gemv_q8f(int rule, int wtype, const uint8_t* W, const float* X, float* C, int M, int N, int K,
+                           hipStream_t s) {
+    if (!gemv_q8f_profitable(wtype, M, N, K, W) || (rule != kQ8FRne && rule != kQ8FLround)) return hipErrorNotSupported;
+    const int nb = K / 32, rpw = pick_rpw(N, kAFQ);
+    note_engine(KSQ_ENG_GEMV_DIRECT_FQ);
+    switch (wtype) {
+        case kWQ40: return rule == kQ8FRne ? q8f_launch<kWQ40, 1>(M, rpw, W, X, C, N, nb, s)
+                                           : q8f_launch<kWQ40, 2>(M, rpw, W, X, C, N, nb, s);
+        case kWQ50: return rule == kQ8FRne ? q8f_launch<kWQ50, 1>(M, rpw, W, X, C, N, nb, s)
+                                           : q8f_launch<kWQ50, 2>(M, rpw, W, X, C, N, nb, s);
+        default: return rule == kQ8FRne ? q8f_launch<kWQ80, 1>(M, rpw, W, X, C, N, nb, s)
+                                        : q8f_launch<kWQ80, 2>(M, rpw, W, X, C, N, nb, s);
+    }
 }
 
 // ---------------------------------------------------------------------------

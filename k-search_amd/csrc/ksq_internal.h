@@ -53,6 +53,11 @@ hipError_t launch_gemv_fused(int wtype, int afmt, bool xh, const uint8_t* W, con
 // Whether the in-workgroup quantisation beats quantise + launch_gemv for this shape (M <= 2, or
 // M <= 8 for fp32, and a bounded amount of repeated quantisation).
 bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool xh = false);
+// fp32 [M][K] activations (M = 1, 2) quantised to block_q8f by `rule` (kQ8FRne / kQ8FLround)
+// inside every workgroup of the decode kernel, against Q4_0 / Q5_0 / Q8_0 weights; C [M][N].
+bool gemv_q8f_profitable(int wtype, int M, int N, int K, const void* W);
+hipError_t launch_gemv_q8f(int rule, int wtype, const uint8_t* W, const float* X, float* C, int M, int N, int K,
+                           hipStream_t s);
 
 // Small-batch GEMM (1 <= M <= 8) on the 4x4x4 int8 MFMA for the 32-element block types
 // (Q4_0, Q8_0, Q4_1, Q5_0, Q5_1; block_q8s activations with Q8_0).  W and A 4-byte aligned.

@@ -99,15 +99,79 @@ def _run(dev, wtype, atype, w, a, M, N, K, cfg=0):
 
 @pytest.mark.parametrize("wtype", [0, 5, 1])
 @pytest.mark.parametrize("atype", [A_Q8F, A_F32_RNE, A_F32_LROUND])
-@pytest.mark.parametrize("M", [1, 8, 33, 300])
+@pytest.mark.parametrize("M", [1, 2, 8, 33, 300])
 def test_gemm_q8f_unit_scale_exact(dev, wtype, atype, M):
     g = np.random.default_rng(1000 * wtype + 10 * atype + M)
     N, K = 384, 1024
     w, a, ref = _unit_case(g, wtype, M, N, K, atype)
     y, eng = _run(dev, wtype, atype, w, a, M, N, K)
     assert np.array_equal(y, ref), (wtype, atype, M, float(np.abs(y - ref).max()))
-    assert any(e.startswith("mmq") for e in eng), eng
-    assert ("quantize" in eng) == (atype != A_Q8F), eng
+    if atype != A_Q8F and M <= 2:
+        # fp32 rows at decode sizes: quantised to block_q8f inside the decode kernel
+        assert eng == {"gemv_direct_fq"}, eng
+    else:
+        assert any(e.startswith("mmq") for e in eng), eng
+        assert ("quantize" in eng) == (atype != A_Q8F), eng
+
+
+def _order_sensitive_blocks(g, M, K):
+    """fp32 rows whose every block has a left-to-right fp32 sum different from the sum of its two
+    16-element halves' partial sums (so the s field pins the summation order)."""
+    out = np.empty((M * K // 32, 32), np.float32)
+    n = 0
+    while n < out.shape[0]:
+        c = (g.standard_normal((4096, 32)) * 10.0 ** g.uniform(-3, 0, (4096, 1))).astype(np.float32)
+        i = np.arange(4096)
+        big = g.uniform(1e3, 3e4, 4096).astype(np.float32)
+        c[i, g.integers(0, 16, 4096)] = big
+        c[i, g.integers(16, 32, 4096)] = -big * np.float32(1.0 + 1e-4)
+        seq = np.add.accumulate(c, axis=1, dtype=np.float32)[:, -1]
+        halves = (np.add.accumulate(c[:, :16], axis=1, dtype=np.float32)[:, -1]
+                  + np.add.accumulate(c[:, 16:], axis=1, dtype=np.float32)[:, -1]).astype(np.float32)
+        keep = c[seq != halves]
+        take = min(len(keep), out.shape[0] - n)
+        out[n:n + take] = keep[:take]
+        n += take
+    return out.reshape(M, K)
+
+
+@pytest.mark.parametrize("atype", [A_F32_RNE, A_F32_LROUND])
+@pytest.mark.parametrize("M", [1, 2])
+def test_q8f_decode_quantiser_readout(dev, oracle, atype, M):
+    """The decode kernel's in-workgroup block_q8f quantiser, read back bit for bit:
+    * Q4_0 weights whose quants are all 8 (value 0) with d_w = 1 in block r of row r only:
+      output (m, r) = d_w * (d_a * 0 - 8 * s_a) = -8 * s_a of activation block r, exactly;
+    * Q8_0 weights with one quant 1 at element k of block b in row 32 b + k (d_w = 1, others 0):
+      output = d_a * q_a[k], the reference's own single rounding of that product.
+    On blocks whose sequential and split sums differ, against the oracle's block_q8f bytes."""
+    import torch
+    from ksq import ops
+    K = 4096
+    nb = K // 32
+    g = np.random.default_rng(5000 + 10 * atype + M)
+    x = _order_sensitive_blocks(g, M, K)
+    blocks = oracle.quantize_q8f(x, RULE_OF[atype]).reshape(M, nb, 40)
+    s_ref = blocks[:, :, 4:8].copy().view(np.float32)[:, :, 0]
+    # Q4_0 readout of s
+    w4 = np.zeros((nb, nb, 18), np.uint8)
+    w4[:, :, 2:] = 0x88
+    w4[np.arange(nb), np.arange(nb), 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    y4 = ops.gemm(0, atype, _t(w4, dev), _t(x, dev), M, nb, K)
+    eng = ops.last_engines()
+    torch.cuda.synchronize()
+    assert eng == {"gemv_direct_fq"}, eng
+    assert np.array_equal(y4.cpu().numpy(), (np.float32(-8.0) * s_ref).astype(np.float32))
+    # Q8_0 readout of d_a * q_a
+    w8 = np.zeros((nb * 32, nb, 34), np.uint8)
+    r = np.arange(nb * 32)
+    w8[r, r // 32, 0:2] = np.frombuffer(np.float16(1).tobytes(), np.uint8)
+    w8[r, r // 32, 2 + r % 32] = 1
+    y8 = ops.gemm(1, atype, _t(w8, dev), _t(x, dev), M, nb * 32, K)
+    eng = ops.last_engines()
+    torch.cuda.synchronize()
+    assert eng == {"gemv_direct_fq"}, eng
+    ref8 = oracle.gemm_q8f(1, blocks.reshape(M, nb * 40), w8, M, nb * 32, K)
+    assert np.array_equal(y8.cpu().numpy(), ref8)
 
 
 @pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
