@@ -214,8 +214,9 @@ KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K
 /* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype (the block_q8s forms pair
  * with Q8_0 weights only, KSQ_ERR_TYPE otherwise; KSQ_A_F16 takes fp16 activations, 16-byte
  * aligned, quantised by the fused FP16 kernels' rules as KSQ_Q81_FUSED_F16; the block_q8f forms
- * pair with Q4_0, Q5_0 and Q8_0 weights, need K % 256 == 0 and run on the int8 MFMA GEMM at
- * every M, block contribution d_w*(d_a*sumi - c*s_a) with c = 8 / 16 / 0 in fp32).  workspace may be
+ * pair with Q4_0, Q5_0 and Q8_0 weights and need K % 256 == 0; fp32 rows take the decode kernel
+ * (quantising in every workgroup) at M <= 2 where it applies, else the int8 MFMA GEMM, block
+ * contribution d_w*(d_a*sumi - c*s_a) with c = 8 / 16 / 0 in fp32).  workspace may be
  * NULL (then a per-device pool owned by the library is used, which makes the call
  * allocate on first use and when sizes grow).  Returns a ksq_status. */
 KSQ_API int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, float* output,

@@ -194,7 +194,8 @@ GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
 int run_matmul(int wtype, int afmt, const uint8_t* W, const uint8_t* Aq, float* C, int M, int N, int K,
                float* partials, hipStream_t s) {
     hipError_t e;
-    // block_q8f runs on the MFMA GEMM only (check_common has checked its shape and alignment)
+    // pre-quantised block_q8f runs on the MFMA GEMM (check_common has checked its shape and
+    // alignment); fp32 rows at decode sizes were taken by the fused decode kernel before
     const bool mmq = afmt == ksq::kAQ8F || use_mmq(wtype, M, N, K, W, aligned16(Aq));
     if (mmq) {
         e = ksq::launch_mmq(wtype, afmt, W, Aq, C, M, N, K, partials, s);
