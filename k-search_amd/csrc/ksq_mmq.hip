@@ -136,14 +136,16 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
     constexpr int ABW = AFS ? 10 : 9;                  // dwords per activation block
     constexpr int AQ = AFS ? 2 : 1;                    // dword offset of the quants in a block
     // the s_a term: f16 MFMA for block_q8_1, an epilogue subtraction for block_q8f
-    constexpr bool SIDE_MFMA = S::side && AF == kAQ81, SIDE_SUB = S::side && AFS;
+    constexpr bool SIDE_MFMA = S::side && AF == kAQ81, SIDE_BF = S::side && AFS;
     __shared__ __attribute__((aligned(16))) uint8_t sA[BM * T::APitch];
     __shared__ __attribute__((aligned(16))) uint8_t sW[BN * S::WPitch];
     __shared__ __attribute__((aligned(16))) float sDa[KB][BM];     // d_a' (d_a/8 for Q4_0)
     __shared__ __attribute__((aligned(16))) float sNc[KB][BM];     // -12582912 * d_a'
     __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
     __shared__ __attribute__((aligned(16))) uint16_t sSaH[BM][8];  // -s_a, fp16 bits (side term)
-    __shared__ __attribute__((aligned(16))) float sNs[SIDE_SUB ? KB : 1][SIDE_SUB ? BM : 1];  // -s_a, fp32
+    // block_q8f: -s_a as three bf16 parts (hi + mid + lo, exact), d_w as two (hi + lo, exact)
+    __shared__ __attribute__((aligned(16))) uint16_t sSaB[SIDE_BF ? 3 : 1][SIDE_BF ? BM : 1][8];
+    __shared__ __attribute__((aligned(16))) uint16_t sDwB[SIDE_BF ? 2 : 1][SIDE_BF ? BN : 1][8];
     __shared__ __attribute__((aligned(16))) uint16_t sDwH[BN][8];  // side-term weight factor, fp16 bits
     __shared__ __attribute__((aligned(16))) uint16_t sDwL[WT == kWQ4K ? BN : 1][8];  // Q4_K: its low part
     __shared__ int32_t sRows[MOE ? BM : 1];                        // MoE: entry index of each tile row
@@ -169,6 +171,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         // the f16 side-term MFMA contracts 8 block slots; slots 4..7 stay zero
         if (t < BM) *(uint4*)&sSaH[t][0] = uint4{0, 0, 0, 0};
         if (t < BN) *(uint4*)&sDwH[t][0] = uint4{0, 0, 0, 0};
+        if constexpr (SIDE_BF) {
+            if (t < BM)
+                for (int e = 0; e < 3; e++) *(uint4*)&sSaB[e][t][0] = uint4{0, 0, 0, 0};
+            if (t < BN)
+                for (int e = 0; e < 2; e++) *(uint4*)&sDwB[e][t][0] = uint4{0, 0, 0, 0};
+        }
     }
     if constexpr (MOE) {
         const int tile = blockIdx.y;
@@ -236,7 +244,17 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
             sNc[kb][sr] = -kMagicF * da;
             // block_q8f: the term -c*s_a in the main term's units (c = out_scale: 8 for Q4_0,
             // 16 for Q5_0), i.e. -s_a
-            if constexpr (SIDE_SUB) sNs[kb][sr] = -__builtin_bit_cast(float, bv[1]);
+            if constexpr (SIDE_BF) {
+                // -s_a in the main term's units (the factor c cancels against d_a / c), split into
+                // bf16 parts whose sum is exact: hi = bf16(x), mid = bf16(x - hi), lo = the rest
+                const float x = -__builtin_bit_cast(float, bv[1]);
+                const __bf16 h = (__bf16)x;
+                const float r = x - (float)h;
+                const __bf16 m = (__bf16)r;
+                sSaB[0][sr][kb] = __builtin_bit_cast(uint16_t, h);
+                sSaB[1][sr][kb] = __builtin_bit_cast(uint16_t, m);
+                sSaB[2][sr][kb] = __builtin_bit_cast(uint16_t, (__bf16)(r - (float)m));
+            }
             if constexpr (SIDE_MFMA) sSaH[sr][kb] = (uint16_t)((bv[0] >> 16) ^ 0x8000u);
         }
     };
@@ -264,6 +282,13 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 // side factor against -s_a: d_w (Q4_0, Q5_0) or -m (Q4_1, Q5_1)
                 if constexpr (WT == kWQ41 || WT == kWQ51) sDwH[sr][kb] = (uint16_t)(half_at(v, off + 2) ^ 0x8000u);
                 else sDwH[sr][kb] = (uint16_t)dwb;
+                if constexpr (SIDE_BF) {
+                    // d_w (11 significant bits) as bf16 hi + lo, exact
+                    const float dwf = f16_to_f32(dwb);
+                    const __bf16 h = (__bf16)dwf;
+                    sDwB[0][sr][kb] = __builtin_bit_cast(uint16_t, h);
+                    sDwB[1][sr][kb] = __builtin_bit_cast(uint16_t, (__bf16)(dwf - (float)h));
+                }
                 if constexpr (WT == kWQ40 || WT == kWQ41) {
                     constexpr int q = (WT == kWQ40) ? 2 : 4;  // offset of qs
                     *(u32x4*)(sW + sr * S::WPitch + kb * 16) =
@@ -444,7 +469,6 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                     for (int q = 0; q < 4; q++) edw[q] = *(const f32x4*)&sDw[u][nbase + 8 * q];
                 }
                 const float da = sDa[b][lm], nc = sNc[b][lm];
-                const float ns = SIDE_SUB ? sNs[b][lm] : 0.0f;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
 #pragma unroll
@@ -453,8 +477,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                         // reads element 0 with this compiler
                         const int e = res[4 * q + p];
                         const float f = __builtin_bit_cast(float, e);
-                        float x = fmaf(f, da, nc);              // sumi * d_a'
-                        if constexpr (SIDE_SUB) x = x + ns;     // (d_a*sumi - c*s_a) / c, one rounding
+                        const float x = fmaf(f, da, nc);        // sumi * d_a'
                         acc[i][j][4 * q + p] = fmaf(edw[q][p], x, acc[i][j][4 * q + p]);
                     }
                 }
@@ -539,6 +562,28 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                     if constexpr (WT == kWQ4K) {
                         const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * hi];
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(dl4, sa4, acc[i][j], 0, 0, 0);
+                    }
+                }
+            }
+        }
+        if constexpr (SIDE_BF && !DUMP) {
+            // block_q8f side term: acc[n][m] += sum over the staged blocks of d_w * (-s_a), as the six
+            // exact products of the bf16 parts (d_w hi, lo) x (-s_a hi, mid, lo) on the bf16 MFMA:
+            // MFMA e covers part pairs 2e (k = 0..7, the lanes with hi = 0) and 2e + 1 (k = 8..15)
+            // over the 8 block slots, pair p = (d_w part p / 3, s_a part p % 3)
+            typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int arow = wm * 32 * TM + i * 32 + l32;
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int wrow = wn * 32 * TN + j * 32 + l32;
+#pragma unroll
+                    for (int e = 0; e < 3; e++) {
+                        const int pr = 2 * e + hi;
+                        const bf16x8 wv = *(const bf16x8*)&sDwB[pr / 3][wrow][0];
+                        const bf16x8 av = *(const bf16x8*)&sSaB[pr % 3][arow][0];
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wv, av, acc[i][j], 0, 0, 0);
                     }
                 }
             }
