@@ -45,24 +45,25 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 # copy gives the same counters (reads x2.0, writes x1.0; profiles/copy_calibration.md).  Each
 # figure names the committed summary it comes from.
 TRAFFIC = {
-    "gemm": (int((41623.4 * 2.0 + 33206.2) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
-    "gemv": (int((4642.0 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
+    "gemm": (int((41619.8 * 2.0 + 32768.4) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
+    "gemv": (int((4641.9 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "q8_0_M1": (int((8737.5 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q8_0_M8": (int((8894.7 * 2.0 + 128.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
-    "q8_0_M32": (int(((9342.3 + 2068.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
-    "q4_K_M128": (int(((19046.2 + 10772.5) * 2.0 + 21504.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
-    "q6_K_M128": (int((26591.4 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
-    "moe_q4_0_T512_E8_top2": (int(((165292.3 + 4144.6 + 19.0) * 2.0 + 57344.0 + 30976.0 + 12.2) * 1024),
+    "q8_0_M32": (int(((9336.5 + 2068.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q4_K_M128": (int(((19077.8 + 10772.5) * 2.0 + 21504.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "q6_K_M128": (int((26590.7 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
+    "moe_q4_0_T512_E8_top2": (int(((165936.2 + 4144.5 + 19.0) * 2.0 + 57344.0 + 30976.0 + 12.2) * 1024),
                               "profiles/moe_q4_0_t512_e8_top2.md"),
     "w4a16_q4_0_M1": (int((4732.8 * 2.0 + 16.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
-    "w4a16_q4_0_M2048": (int((142071.9 * 2.0 + 32768.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
-    "deepseek_v2_q8f_q4_0_M2048": (int(((45746.6 + 16439.1) * 2.0 + 32838.0 + 10240.0) * 1024),
+    "w4a16_q4_0_M2048": (int((141346.1 * 2.0 + 32768.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
+    "deepseek_v2_q8f_q4_0_M2048": (int(((45714.6 + 16439.1) * 2.0 + 32768.0 + 10240.0) * 1024),
                                    "profiles/q8f_q4_0_m2048_n4096_k4096.md"),
-    "fp16_fused_q4_0_N1": (int((4702.4 * 2.0 + 16.0) * 1024), "profiles/fp16_fused_q4_0_n1_k4096.md"),
+    "deepseek_v2_q8f_q4_0_M1": (int((4727.9 * 2.0 + 16.0) * 1024), "profiles/q8f_q4_0_m2048_n4096_k4096.md"),
+    "fp16_fused_q4_0_N1": (int((4698.1 * 2.0 + 16.0) * 1024), "profiles/fp16_fused_q4_0_n1_k4096.md"),
 }
 
 ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
-        "w16_m1", "w16_m2048", "q8f_m2048", "f16_fused_m1")
+        "w16_m1", "w16_m2048", "q8f_m1", "q8f_m2048", "f16_fused_m1")
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, published
 
 
@@ -266,8 +267,9 @@ class Workloads:
         return (M, N, K), (lambda i: ops.gemm_w16(ksq.W_Q4_0, x, W[i % copies], M, N, K, out=o, workspace=ws)), copies
 
     def q8f(self, M: int = 2048, copies: int = 8):
-        """The deepseek_v2 W4A32C8 operator's path (fp32 d_a and s_a, block_q8f) at the config-2
-        shape: fp32 activations quantised by its rules, then the int8 MFMA GEMM."""
+        """The deepseek_v2 W4A32C8 operator's path (fp32 d_a and s_a, block_q8f) at N = K = 4096:
+        fp32 activations quantised by its rules, then the int8 MFMA GEMM (M = 2048), or quantised
+        inside the decode kernel's workgroups (M = 1; 64 weight copies)."""
         ksq, ops, synth, g = self.ksq, self.ops, self.synth, self.g
         N, K = 4096, 4096
         w = synth.weights(ksq.W_Q4_0, g, N, K)
@@ -318,7 +320,7 @@ def other_configs(wl: Workloads, reps: int = 4) -> dict:
 def extra_paths(wl: Workloads, reps: int = 4) -> dict:
     """The paths beside the headline (not BASELINE configs): the dequantise-then-fp32 GEMM
     (W4A16) at M = 1 and M = 2048, the deepseek_v2 operator's block_q8f path at the config-2
-    shape, and the fused FP16-activation GEMM at decode size."""
+    shape and at M = 1, and the fused FP16-activation GEMM at decode size."""
     out = {}
     for M in (1, 2048):
         (M, N, K), fn, copies = wl.w16(M)
@@ -341,6 +343,12 @@ def extra_paths(wl: Workloads, reps: int = 4) -> dict:
                      "frac": round(top / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC["deepseek_v2_q8f_q4_0_M2048"][0],
                      "traffic_source": TRAFFIC["deepseek_v2_q8f_q4_0_M2048"][1]}
     out["deepseek_v2_q8f_q4_0_M2048"] = e
+    del fn
+    # the same operator at decode size: block_q8f quantised inside the decode kernel's workgroups
+    (M, N, K), fn, copies = wl.q8f(1, 64)
+    ms, d = graph_stats(fn, copies, reps)
+    out["deepseek_v2_q8f_q4_0_M1"] = hbm_entry(N * (K // 32) * 18 + M * K * 4 + M * N * 4, ms, d, 2.0 * M * N * K,
+                                               "deepseek_v2_q8f_q4_0_M1")
     del fn
     (Mw, Na, K), fn, copies = wl.f16_fused()
     ms, d = graph_stats(fn, copies, reps)
@@ -457,8 +465,9 @@ def only(args, dev) -> int:
         _, fn, _ = wl.kquant(wl.ksq.W_Q4_K if args.only == "q4_k" else wl.ksq.W_Q6_K)
     elif args.only.startswith("w16_m"):
         _, fn, _ = wl.w16(int(args.only[5:]))
-    elif args.only == "q8f_m2048":
-        _, fn, _ = wl.q8f()
+    elif args.only.startswith("q8f_m"):
+        m = int(args.only[5:])
+        _, fn, _ = wl.q8f(m, 8 if m > 2 else 64)
     elif args.only == "f16_fused_m1":
         _, fn, _ = wl.f16_fused()
     else:
