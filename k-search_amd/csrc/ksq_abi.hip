@@ -182,9 +182,17 @@ struct GemmWs {
     size_t q, p, total;
 };
 
+// Whether fp32 activations are quantised to planar block_q8_1 for the LDS-DMA GEMM (given that
+// the MFMA GEMM runs).
+bool use_planar(int wtype, int atype, int M, int N, int K, bool mmq) {
+    return mmq && atype == KSQ_A_F32 && (K % 256) == 0 && ksq::mmq_planar_preferred(wtype, M, N, K);
+}
+
 GemmWs gemm_ws(int wtype, int atype, int M, int N, int K, bool mmq) {
     GemmWs w{};
-    w.q = atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * atype_block_bytes(atype)) : 0;
+    w.q = use_planar(wtype, atype, M, N, K, mmq)
+              ? align256(ksq::planar_bytes(M, K))
+              : atype_raw(atype) ? align256((size_t)M * (size_t)(K / 32) * atype_block_bytes(atype)) : 0;
     const int splits = mmq ? ksq::mmq_splits(wtype, M, N, K) : 1;
     w.p = splits > 1 ? align256((size_t)splits * (size_t)M * (size_t)N * sizeof(float)) : 0;
     w.total = w.q + w.p;
@@ -469,6 +477,16 @@ int ksq_gemm(int wtype, int atype, const void* weight, const void* activation, f
         }
     }
     float* partials = L.p ? (float*)(ws + L.q) : nullptr;
+    if (use_planar(wtype, atype, M, N, K, mmq)) {
+        // the LDS-DMA GEMM's own activation layout (same blocks, split into planes)
+        const ksq::PlanarQ81 P = ksq::planar_at(ws, M, K);
+        hipError_t e = ksq::launch_quantize_planar((const float*)activation, P, M, K, ksq::planar_da_scale(wtype), s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+        g_engines |= KSQ_ENG_QUANTIZE;
+        e = ksq::launch_mmq_planar(wtype, (const uint8_t*)weight, P, output, M, N, K, partials, s);
+        if (e != hipSuccess) return hip_error(e, "mmq launch");
+        return ok();
+    }
     if (f32 || f16) {
         // fp16 input takes the fused FP16 kernels' quantiser (kernels/gemm/gemm_fused.cuh:76-145)
         hipError_t e;

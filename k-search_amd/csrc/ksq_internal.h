@@ -31,6 +31,31 @@ hipError_t launch_quantize_q8f(int rule, const float* x, uint8_t* y, int64_t row
 // the same launch.
 hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, int K, float* zero, int64_t nzero,
                                      hipStream_t s);
+// Planar block_q8_1: the blocks of quantize_row_q8_1 split into planes, so that every piece
+// the LDS-DMA GEMM stages is a 16-byte-aligned run it copies into LDS without VGPRs.
+//   q  [M][K]          int8 quants (block kb of row m at q + m*K + 32*kb)
+//   dn [K/32][mp][2]   fp32 pairs (d, nc): d = d_a * da_scale (d_a the block's fp16 scale,
+//                      da_scale a power of two), nc = -12582912 * d
+//   sa [K/128][mp][4]  fp16 bits of -s_a
+// mp = M rounded up to a multiple of 128; rows M .. mp-1 of dn and sa hold zeros.
+struct PlanarQ81 {
+    int8_t* q;
+    float* dn;
+    uint16_t* sa;
+    int mp;
+};
+// Workspace bytes of the planes (each 256-byte aligned) and their addresses in a workspace.
+size_t planar_bytes(int M, int K);
+PlanarQ81 planar_at(void* ws, int M, int K);
+// fp32 [M][K] (16-byte aligned, K % 128 == 0) -> planar block_q8_1.
+hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int K, float da_scale, hipStream_t s);
+// The LDS-DMA GEMM (Q4_0 / Q4_1 weights, K % 256 == 0, W 16-byte aligned) on planar
+// activations quantised with da_scale = planar_da_scale(wtype); whether it is the pick for this
+// shape (fp32 activations); partials as launch_mmq (mmq_splits(...) > 1).
+bool mmq_planar_preferred(int wtype, int M, int N, int K);
+float planar_da_scale(int wtype);
+hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int M, int N, int K,
+                             float* partials, hipStream_t s);
 // variant 0-3 of ksq_quantize_q8_1_variant (x fp32, or fp16 bits for variant 3)
 hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
 // out [cols][rows] = in [rows][cols], fp32
@@ -83,8 +108,9 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
 // In-order sum of `splits` partial [M][N] results (P) into C.
 hipError_t launch_splitk_reduce(const float* P, float* C, int64_t mn, int splits, hipStream_t s);
 
-// Force one of the MFMA tile configurations (1..6) or automatic choice (0) for the calling host
-// thread; -1 if out of range.
+// Force one of the MFMA tile configurations (1..7; 8: the LDS-DMA GEMM where it applies, the
+// 128 x 128 tile elsewhere) or automatic choice (0) for the calling host thread; -1 if out of
+// range.
 int mmq_set_config(int c);
 
 // Expert-grouped prefill GEMM (MoE).  Arrays are device arrays produced by launch_moe_route /

@@ -666,6 +666,244 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
     }
 }
 
+// ---- the LDS-DMA GEMM: planar block_q8_1 activations, nibble weights --------------------------
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane (no VGPRs); the
+// caller waits with s_waitcnt vmcnt before the data is read.
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// 128 x 128 tiles of Q4_0 / Q4_1 weights against planar block_q8_1 activations, the same
+// arithmetic as mmq_kernel (magic-bias epilogue, f16-MFMA side term) in K steps of 4 blocks
+// with every LDS array double-buffered, so the loads of step k+1 run under the MFMAs of step k:
+//  * every wave copies its share of step k+1's activation planes into the other buffer by DMA
+//    (21 wave instructions per step: 16 KiB of quants, 4 KiB of (d, nc) pairs, 1 KiB of sa)
+//    and loads half a weight row of step k+1 per thread (2 blocks) into VGPRs;
+//  * all four waves compute step k (each 128 rows x 32 columns, as the 128 x 128 tile of
+//    mmq_kernel); then the weight halves are unpacked into the other buffer, the DMA is waited
+//    for, and one barrier ends the step.
+// (Every wave does the same work: splitting the roles between waves left a register copy of
+// the weight words at the branches' join that made every wave wait for its loads before
+// computing.)
+// The quants are stored without padding, with the 16-byte pieces of a row XOR-swizzled (piece p
+// of row r at slot p ^ (r & 7)), so that the fragment reads of 8 consecutive rows fall into 8
+// different bank groups.  With the slots of one DMA instruction being 8 consecutive rows, lane
+// l's source piece is (l & 7) ^ (l >> 3) for every instruction.
+template <int WT>
+__global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __restrict__ W, PlanarQ81 A,
+                                                           float* __restrict__ C, int M, int N, int nb) {
+    static_assert(WT == kWQ40 || WT == kWQ41, "nibble-staged weights");
+    constexpr int KB = 4, BM = 128, BN = 128, TM = 4;
+    using S = WShape<WT, KB>;
+    constexpr int WNW = S::Chunk / 4;   // weight words per row and step
+    __shared__ __attribute__((aligned(16))) uint8_t sA0[BM * 128], sA1[BM * 128];
+    __shared__ __attribute__((aligned(16))) uint8_t sW0[BN * S::WPitch], sW1[BN * S::WPitch];
+    __shared__ __attribute__((aligned(16))) float sDn0[KB * BM * 2], sDn1[KB * BM * 2];   // (d, nc) pairs
+    __shared__ __attribute__((aligned(16))) float sDw0[KB * BN], sDw1[KB * BN];
+    __shared__ __attribute__((aligned(16))) uint16_t sSa0[BM * 4], sSa1[BM * 4];
+    // side-term weight factor per row and block; row BN stays zero (read by the lanes holding
+    // the f16 MFMA's k = 4..7, for which a step has no blocks)
+    __shared__ __attribute__((aligned(16))) uint16_t sDh0[(BN + 1) * 4], sDh1[(BN + 1) * 4];
+
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int l32 = lane & 31, hi = lane >> 5;
+    const int m0 = (int)blockIdx.y * BM, n0 = (int)blockIdx.x * BN;
+    const int K = nb * 32;
+    const int nsteps = nb / KB, Z = (int)gridDim.z, z = (int)blockIdx.z;
+    const int kb_lo = (int)((long long)nsteps * z / Z) * KB, kb_hi = (int)((long long)nsteps * (z + 1) / Z) * KB;
+    C += (size_t)z * (size_t)M * (size_t)N;
+
+    // ---- per-lane DMA source offsets ----
+    // quants: wave w fills slots 256 w .. 256 w + 255 (rows 32 w .. 32 w + 31; rows past M read
+    // row M-1); (d, nc): wave w copies block w of the step, lane -> rows 2 lane, 2 lane + 1; sa:
+    // one instruction of wave 3, lane -> rows 2 lane, 2 lane + 1
+    const int8_t* qtile = A.q + (size_t)m0 * K;
+    uint32_t qoff[4];
+    {
+        const int p = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) {
+            const int r = min(m0 + 32 * wave + 8 * ii + (lane >> 3), M - 1) - m0;
+            qoff[ii] = (uint32_t)r * (uint32_t)K + 16u * p;
+        }
+    }
+    auto dma_act = [&](auto par, int kb0) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        uint8_t* dA = P ? sA1 : sA0;
+        const int8_t* qs = qtile + (size_t)kb0 * 32;
+#pragma unroll
+        for (int ii = 0; ii < 4; ii++) dma16(qs + qoff[ii], dA + (4 * wave + ii) * 1024);
+        dma16(A.dn + 2 * ((size_t)(kb0 + wave) * A.mp + m0 + 2 * lane), (P ? sDn1 : sDn0) + 256 * wave);
+        if (wave == 3) dma16(A.sa + ((size_t)(kb0 >> 2) * A.mp + m0 + 2 * lane) * 4, P ? sSa1 : sSa0);
+    };
+
+    // ---- weights: thread t stages blocks 2h, 2h + 1 (h = t % 2) of row t / 2 ----
+    // (4-byte loads of the 36- / 40-byte half chunk: 8-byte loads from the 8-byte boundary below,
+    // with Q4_0's second half re-aligned by a word, measured 1% slower on the whole call)
+    constexpr int HW = WNW / 2;   // words per half chunk
+    const int wsr = t >> 1, wh = t & 1;
+    uint32_t pre[HW + 1];
+    auto load_w = [&](int kb0) __attribute__((always_inline)) {
+        const int wr = min(n0 + wsr, N - 1);
+        const uint32_t* p = (const uint32_t*)(W + (size_t)wr * nb * S::BB + (size_t)(kb0 + 2 * wh) * S::BB);
+#pragma unroll
+        for (int i = 0; i < HW; i++) pre[i] = p[i];
+        pre[HW] = 0;
+    };
+    auto store_w = [&](auto par) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        uint8_t* dW = P ? sW1 : sW0;
+        float* dDw = P ? sDw1 : sDw0;
+        uint16_t* dDh = P ? sDh1 : sDh0;
+        uint32_t dh[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int kb = 2 * wh + j, off = j * S::BB;
+            const uint32_t dwb = half_at(pre, off);
+            dDw[kb * BN + wsr] = f16_to_f32(dwb);
+            // side factor against -s_a: d_w (Q4_0) or -m (Q4_1)
+            dh[j] = (WT == kWQ41) ? (half_at(pre, off + 2) ^ 0x8000u) : dwb;
+            constexpr int q = (WT == kWQ40) ? 2 : 4;   // offset of qs
+            *(u32x4*)(dW + wsr * S::WPitch + kb * 16) =
+                u32x4{word_at(pre, off + q), word_at(pre, off + q + 4), word_at(pre, off + q + 8),
+                      word_at(pre, off + q + 12)};
+        }
+        *(uint32_t*)(dDh + 4 * wsr + 2 * wh) = dh[0] | (dh[1] << 16);
+    };
+
+    // ---- compute ----
+    f32x16 acc[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[i][r] = 0.0f;
+    i32x16 bias;
+#pragma unroll
+    for (int r = 0; r < 16; r++) bias[r] = (int)kMagic;
+    const int wn = wave;   // four waves side by side along N, each over all 128 rows
+    int aoff[KB];          // swizzled byte offset of piece 2b + hi of row l32
+#pragma unroll
+    for (int b = 0; b < KB; b++) aoff[b] = l32 * 128 + ((((2 * b + hi) ^ (l32 & 7))) << 4);
+    const int woff = (wn * 32 + l32) * S::WPitch;
+    const int dh_idx = hi ? BN * 4 : (wn * 32 + l32) * 4;
+    const int nbase = wn * 32 + 4 * hi;   // local weight row of r = 0
+
+    auto compute = [&](auto par) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        const uint8_t* cA = P ? sA1 : sA0;
+        const uint8_t* cW = P ? sW1 : sW0;
+        const float* cDn = P ? sDn1 : sDn0;
+        const float* cDw = P ? sDw1 : sDw0;
+        const uint16_t* cSa = P ? sSa1 : sSa0;
+        const uint16_t* cDh = P ? sDh1 : sDh0;
+        constexpr int NQ = KB * TM;
+        i32x4 af[TM], bf;
+        f32x4 edw[4];
+        auto mfma_step = [&](int q) -> i32x16 {
+            const int b = q / TM, i = q % TM;
+            if (i == 0) {
+#pragma unroll
+                for (int ii = 0; ii < TM; ii++) af[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[b]);
+                const u32x4 x = *(const u32x4*)(cW + woff + b * 16);
+                const int s4 = 4 * hi;
+                bf = i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
+                           (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
+            }
+            return __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i], bias, 0, 0, 0);
+        };
+        __builtin_amdgcn_s_setprio(2);
+        i32x16 cur = mfma_step(0);
+#pragma unroll
+        for (int q = 0; q < NQ; q++) {
+            const int b = q / TM, i = q % TM;
+            i32x16 nxt = bias;
+            if (q + 1 < NQ) nxt = mfma_step(q + 1);
+            if (i == 0) {
+#pragma unroll
+                for (int qq = 0; qq < 4; qq++) edw[qq] = *(const f32x4*)&cDw[b * BN + nbase + 8 * qq];
+            }
+            const int lm = i * 32 + l32;
+            const f32x2 dn = *(const f32x2*)&cDn[2 * (b * BM + lm)];
+            const float da = dn.x, nc = dn.y;
+#pragma unroll
+            for (int qq = 0; qq < 4; qq++) {
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int e = cur[4 * qq + p];
+                    const float f = __builtin_bit_cast(float, e);
+                    const float x = fmaf(f, da, nc);   // sumi * d_a'
+                    acc[i][4 * qq + p] = fmaf(edw[qq][p], x, acc[i][4 * qq + p]);
+                }
+            }
+            cur = nxt;
+        }
+        __builtin_amdgcn_s_setprio(0);
+        // side term over the step's 4 blocks (f16 MFMA, exact products; k = 4..7 read zeros)
+        const f16x4 dw4 = *(const f16x4*)&cDh[dh_idx];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const f16x4 sa4 = *(const f16x4*)&cSa[(i * 32 + l32) * 4];
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x8f16(dw4, sa4, acc[i], 0, 0, 0);
+        }
+    };
+
+    // ---- pipeline ----
+    if (t < 4) {
+        sDh0[BN * 4 + t] = 0;
+        sDh1[BN * 4 + t] = 0;
+    }
+    if (kb_lo < kb_hi) {
+        dma_act(IntC<0>{}, kb_lo);
+        load_w(kb_lo);
+        store_w(IntC<0>{});
+        wait_vmem_all();
+    }
+    __syncthreads();
+    auto step = [&](auto par, int kb0) __attribute__((always_inline)) {
+        constexpr int P = decltype(par)::value;
+        const bool more = kb0 + KB < kb_hi;
+        if (more) {
+            dma_act(IntC<1 - P>{}, kb0 + KB);
+            load_w(kb0 + KB);
+        }
+        compute(par);
+        if (more) {
+            store_w(IntC<1 - P>{});
+            wait_vmem_all();
+        }
+        __syncthreads();
+    };
+    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += 2 * KB) {
+        step(IntC<0>{}, kb0);
+        if (kb0 + KB < kb_hi) step(IntC<1>{}, kb0 + KB);
+    }
+
+    // ---- output ----
+    constexpr float out_scale = S::out_scale;
+    const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const int gm = m0 + i * 32 + l32;
+        if (gm >= M) continue;
+#pragma unroll
+        for (int qq = 0; qq < 4; qq++) {
+            const int gn = n0 + nbase + 8 * qq;   // this lane's 4 consecutive outputs gn .. gn + 3
+            if (vec_ok && gn + 3 < N) {
+                *(f32x4*)(C + (size_t)gm * N + gn) =
+                    f32x4{out_scale * acc[i][4 * qq], out_scale * acc[i][4 * qq + 1], out_scale * acc[i][4 * qq + 2],
+                          out_scale * acc[i][4 * qq + 3]};
+            } else {
+#pragma unroll
+                for (int p = 0; p < 4; p++)
+                    if (gn + p < N) C[(size_t)gm * N + gn + p] = out_scale * acc[i][4 * qq + p];
+            }
+        }
+    }
+}
+
 // ---- tile configurations ----------------------------------------------------------
 // 128 rows x 32 columns per wave: one weight fragment (the one that needs its nibbles unpacked)
 // per four MFMAs (Q4_0 M = 2048, N = K = 4096: 99 vs 101 us for 64 x 64 per wave)
@@ -685,7 +923,7 @@ using TileW = Tile<64, 128, 8, 2, 1, 3>;
 static thread_local int g_mmq_config = 0;  // 0 = automatic; set per host thread
 
 int mmq_set_config(int c) {
-    if (c < 0 || c > 7) return -1;
+    if (c < 0 || c > 8) return -1;
     g_mmq_config = c;
     return 0;
 }
@@ -714,6 +952,8 @@ static int grid_wgs(int M, int N) {
 //    K = 4096, M = 16: 20.5 vs 26.7) up to M = 96, 64 x 128 from there to M = 255, 128 x 128
 //    from M = 256 while it covers the CUs (M = 2048, N = K = 4096: 114.5 vs 131.9).
 static int pick_config(int wtype, int M, int N, int K) {
+    // configuration 8 (the LDS-DMA GEMM, mmq_planar_preferred) is the 128 x 128 tile elsewhere
+    if (g_mmq_config == 8) return 1;
     if (g_mmq_config && !(is_kquant(wtype) && (g_mmq_config == 4 || g_mmq_config == 6))) return g_mmq_config;
     constexpr int kCUs = 256;
     const bool nib = (wtype == kWQ40 || wtype == kWQ41), kq = is_kquant(wtype);
@@ -953,6 +1193,38 @@ hipError_t launch_mmq(int wtype, int afmt, const uint8_t* W, const uint8_t* A, f
     if (!partials) return hipErrorInvalidValue;
     hipError_t e = launch_cfg<false>(cfg, wtype, afmt, W, A, partials, nullptr, M, N, K, splits, s);
     if (e != hipSuccess) return e;
+    return launch_splitk_reduce(partials, C, (int64_t)M * N, splits, s);
+}
+
+// The LDS-DMA GEMM takes fp32 activations against Q4_0 / Q4_1 wherever the 128 x 128 tile is
+// the automatic pick (or configuration 8 forces it).
+#ifndef KSQ_MMQ_PLANAR
+#define KSQ_MMQ_PLANAR 1
+#endif
+bool mmq_planar_preferred(int wtype, int M, int N, int K) {
+    if (wtype != kWQ40 && wtype != kWQ41) return false;
+    if (g_mmq_config == 8) return true;
+    return KSQ_MMQ_PLANAR && g_mmq_config == 0 && pick_config(wtype, M, N, K) == 1;
+}
+
+float planar_da_scale(int wtype) { return wtype == kWQ40 ? 1.0f / WShape<kWQ40, 4>::out_scale : 1.0f; }
+
+hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int M, int N, int K,
+                             float* partials, hipStream_t s) {
+    if (K % 256) return hipErrorInvalidValue;
+    const int splits = split_for<TileL>(wtype, M, N, K);
+    if (splits > 1 && !partials) return hipErrorInvalidValue;
+    note_engine(KSQ_ENG_MMQ_PLANAR | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
+    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), (unsigned)splits);
+    float* out = splits > 1 ? partials : C;
+    if (wtype == kWQ40)
+        hipLaunchKernelGGL(mmq_planar_kernel<kWQ40>, grid, dim3(256), 0, s, W, A, out, M, N, K / 32);
+    else if (wtype == kWQ41)
+        hipLaunchKernelGGL(mmq_planar_kernel<kWQ41>, grid, dim3(256), 0, s, W, A, out, M, N, K / 32);
+    else
+        return hipErrorNotSupported;
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splits == 1) return e;
     return launch_splitk_reduce(partials, C, (int64_t)M * N, splits, s);
 }
 

@@ -167,6 +167,75 @@ hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, i
     return hipGetLastError();
 }
 
+// ---- planar block_q8_1 (the LDS-DMA GEMM's input) ---------------------------------------
+// The same blocks as quantize_q8_1_kernel<kQF81> (same device quantiser, bit for bit), written
+// as the planes of PlanarQ81.  A workgroup owns 64 rows x 4 blocks: it reads the 64 row
+// segments of 512 bytes with coalesced 16-byte loads into LDS ([row][block] with a 33-float
+// pitch, so the per-lane block reads are conflict free), and lane t quantises block t % 4 of row
+// t / 4, so that the 4 lanes of a row write its 128 quant bytes, its (d, nc) pairs and its 4 sa
+// halves side by side.  Rows M .. mp-1 quantise zeros: their dn and sa entries are written,
+// their quants are not.
+__global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __restrict__ x, PlanarQ81 y, int M, int K,
+                                                              float da_scale) {
+    __shared__ float stage[64 * 4 * kQPitch];
+    const int t = threadIdx.x;
+    const int r0 = (int)blockIdx.x * 64, kb0 = (int)blockIdx.y * 4;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+        const int idx = p * 256 + t, row = idx >> 5, c = idx & 31;   // c: float4 of the row segment
+        f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (r0 + row < M) v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)(r0 + row) * K + kb0 * 32) + c);
+        float* dst = stage + (row * 4 + (c >> 3)) * kQPitch + (c & 7) * 4;
+        dst[0] = v.x;
+        dst[1] = v.y;
+        dst[2] = v.z;
+        dst[3] = v.w;
+    }
+    __syncthreads();
+    const int row = t >> 2, blk = t & 3, m = r0 + row, kb = kb0 + blk;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = stage[t * kQPitch + j];
+    uint32_t q[9];
+    quantize_block_q8_1(v, q);
+    if (m < M) {
+        u32x4* dq = (u32x4*)(y.q + (size_t)m * K + (size_t)kb * 32);
+        dq[0] = u32x4{q[1], q[2], q[3], q[4]};
+        dq[1] = u32x4{q[5], q[6], q[7], q[8]};
+    }
+    const float d = f16_to_f32(q[0] & 0xFFFFu) * da_scale;
+    *(f32x2*)(y.dn + 2 * ((size_t)kb * y.mp + m)) = f32x2{d, -12582912.0f * d};
+    y.sa[((size_t)(kb0 >> 2) * y.mp + m) * 4 + blk] = (uint16_t)((q[0] >> 16) ^ 0x8000u);
+}
+
+size_t planar_bytes(int M, int K) {
+    auto a256 = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t mp = (size_t)((M + 127) / 128) * 128, nb = (size_t)(K / 32);
+    return a256((size_t)M * K) + a256(nb * mp * 8) + a256(nb / 4 * mp * 8);
+}
+
+PlanarQ81 planar_at(void* ws, int M, int K) {
+    auto a256 = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    const size_t mp = (size_t)((M + 127) / 128) * 128, nb = (size_t)(K / 32);
+    uint8_t* p = (uint8_t*)ws;
+    PlanarQ81 y;
+    y.q = (int8_t*)p;
+    p += a256((size_t)M * K);
+    y.dn = (float*)p;
+    p += a256(nb * mp * 8);
+    y.sa = (uint16_t*)p;
+    y.mp = (int)mp;
+    return y;
+}
+
+hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int K, float da_scale, hipStream_t s) {
+    if (M <= 0 || K <= 0) return hipSuccess;
+    if (K % 128) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(y.mp / 64), (unsigned)(K / 128));
+    hipLaunchKernelGGL(quantize_planar_kernel, grid, dim3(256), 0, s, x, y, M, K, da_scale);
+    return hipGetLastError();
+}
+
 // ---- the reference's other Q8_1 quantisers (ksq_quantize_q8_1_variant) -----------------
 // One lane per 32-value block, as the reference's own device quantiser runs; block_q8_1 out.
 //   1 quantize_q8_1_kernel (include/quantize.h:301-336): fmaxf/sequential-sum, id = 1/d,

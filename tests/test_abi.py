@@ -115,10 +115,17 @@ def test_quantize_q8f_rejects_bad_arguments():
 
 
 def test_workspace_size():
-    """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K)."""
+    """fp32 input needs its block_q8_1 copy, quantised input none (M = 2048: no split-K).  Q4_0 / Q4_1
+    at this shape take the LDS-DMA GEMM, whose activations are planar: [M][K] int8 quants, d and nc
+    as [K/32][Mp] floats, -s_a as [K/128][Mp][4] fp16 (Mp = M rounded up to 128)."""
     from ksq import _lib
     L = _lib.lib()
-    assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == 2048 * 128 * 36
+    planar = 2048 * 4096 + 2 * 128 * 2048 * 4 + 32 * 2048 * 8
+    assert L.ksq_gemm_workspace_size(0, 0, 2048, 4096, 4096) == planar
+    assert L.ksq_gemm_workspace_size(4, 0, 2048, 4096, 4096) == planar
+    # M = 1100 (Mp = 1152; each plane 256-byte aligned), split in two along K: the partial sums follow
+    assert L.ksq_gemm_workspace_size(0, 0, 1100, 4096, 4096) == (1100 * 4096 + 2 * 128 * 1152 * 4 + 32 * 1152 * 8
+                                                                 + 2 * 1100 * 4096 * 4)
     assert L.ksq_gemm_workspace_size(0, 1, 2048, 4096, 4096) == 0
     assert L.ksq_gemm_workspace_size(1, 0, 2048, 4096, 4096) == 2048 * 128 * 36
     # block_q8f (fp32 d and s): 40-byte blocks

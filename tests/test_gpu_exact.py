@@ -125,7 +125,7 @@ CONFIG_CASES = [
     ("c1_q8_0_m8_q81", 1, 8, 4096, 4096, "q81", {"skinny"}),
     ("c1_q8_0_m32_f32", 1, 32, 4096, 4096, "f32", {"quantize", "mmq3", "splitk"}),
     ("c1_q8_0_m32_q81", 1, 32, 4096, 4096, "q81", {"mmq3", "splitk"}),
-    ("c2_q4_0_m2048_f32", 0, 2048, 4096, 4096, "f32", {"quantize", "mmq1"}),
+    ("c2_q4_0_m2048_f32", 0, 2048, 4096, 4096, "f32", {"quantize", "mmq_planar"}),
     ("c2_q4_0_m2048_q81", 0, 2048, 4096, 4096, "q81", {"mmq1"}),
     ("c3_q4_k_m128_f32", 2, 128, 14336, 4096, "f32", {"quantize", "mmq7", "splitk"}),
     ("c3_q4_k_m128_q81", 2, 128, 14336, 4096, "q81", {"mmq7", "splitk"}),
@@ -224,6 +224,11 @@ def _engine_cases():
         cases.append((f"decf_oddnb_w{wt}", wt, 1, 100, 1056, 0, 1, 0, {"gemv_row_fq"}, 0))
         for M in (1, 3, 8):
             cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1024, 1, 3, 0, {"skinny"}, 0))
+    # the LDS-DMA GEMM (fp32 activations quantised to planar block_q8_1; Q4_0 / Q4_1): split in
+    # two along K, with an even (4) and an odd (5) number of 4-block steps per split; ragged M, N
+    for wt in (0, 4):
+        for K in (1024, 1280):
+            cases.append((f"mmqp_k{K}_w{wt}", wt, 200, 330, K, 0, 2, 8, {"quantize", "mmq_planar", "splitk"}, 0))
     cases.append(("splitk_w0", 0, 32, 1024, 8192, 1, 0, 0, {"mmq5", "splitk"}, 0))
     cases.append(("splitk_w1", 1, 32, 1024, 8192, 1, 0, 0, {"mmq3", "splitk"}, 0))
     # the native W8A8C8 operator's block_q8s activations: fp32 (its quantiser) and pre-quantised

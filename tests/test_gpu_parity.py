@@ -427,10 +427,11 @@ def test_moe_config4_sampled(dev, oracle):
     assert np.isfinite(y).all()
 
 
-@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7])
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5, 6, 7, 8])
 @pytest.mark.parametrize("wtype", ALL_WTYPES)
 def test_mfma_tile_configs(dev, oracle, cfg, wtype):
-    """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile)."""
+    """Every MFMA tile configuration (K step 4 is not used for K-quants: they take the automatic tile;
+    configuration 8 is the LDS-DMA GEMM for Q4_0 / Q4_1, the 128 x 128 tile for the rest)."""
     from ksq import _lib, synth
     g = np.random.default_rng(1500 + 10 * cfg + wtype)
     M, N, K = 150, 136, 512
@@ -479,7 +480,7 @@ def test_skinny_q8s_native(dev, oracle, M):
 
 ENGINE_FAMILIES = {"decode": {"gemv_row", "gemv_row_fq", "gemv_direct", "gemv_direct_fq", "gemv_mr", "gemv_mr_fq",
                                "gemv_kq"},
-                   "skinny": {"skinny"}, "mmq": {f"mmq{c}" for c in range(1, 8)}}
+                   "skinny": {"skinny"}, "mmq": {f"mmq{c}" for c in range(1, 8)} | {"mmq_planar"}}
 
 
 def _family(engines):
