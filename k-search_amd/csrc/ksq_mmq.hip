@@ -688,9 +688,12 @@ __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(
 // the weight words at the branches' join that made every wave wait for its loads before
 // computing.)
 // The quants are stored without padding, with the 16-byte pieces of a row XOR-swizzled (piece p
-// of row r at slot p ^ (r & 7)), so that the fragment reads of 8 consecutive rows fall into 8
-// different bank groups.  With the slots of one DMA instruction being 8 consecutive rows, lane
-// l's source piece is (l & 7) ^ (l >> 3) for every instruction.
+// of row r at slot p ^ ((r / 2) % 8)): a 128-byte row spans half of the 64 banks, so rows of
+// one parity share a bank half, and the swizzle spreads the 8 rows of each parity among a
+// fragment read's 16 consecutive rows over the 8 slots; the 16 lanes served together then hit
+// 16 different bank groups (the plain p ^ (r % 8) left 2-way conflicts: 5.5e6 conflict cycles
+// per launch).  The slots of one DMA instruction are 8 consecutive rows, so lane l of
+// instruction i sources piece (l % 8) ^ ((4 i + l / 16) % 8).
 template <int WT>
 __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __restrict__ W, PlanarQ81 A,
                                                            float* __restrict__ C, int M, int N, int nb) {
@@ -723,9 +726,9 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
     const int8_t* qtile = A.q + (size_t)m0 * K;
     uint32_t qoff[4];
     {
-        const int p = (lane & 7) ^ (lane >> 3);
 #pragma unroll
         for (int ii = 0; ii < 4; ii++) {
+            const int p = (lane & 7) ^ ((4 * ii + (lane >> 4)) & 7);
             const int r = min(m0 + 32 * wave + 8 * ii + (lane >> 3), M - 1) - m0;
             qoff[ii] = (uint32_t)r * (uint32_t)K + 16u * p;
         }
@@ -786,7 +789,7 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
     const int wn = wave;   // four waves side by side along N, each over all 128 rows
     int aoff[KB];          // swizzled byte offset of piece 2b + hi of row l32
 #pragma unroll
-    for (int b = 0; b < KB; b++) aoff[b] = l32 * 128 + ((((2 * b + hi) ^ (l32 & 7))) << 4);
+    for (int b = 0; b < KB; b++) aoff[b] = l32 * 128 + (((2 * b + hi) ^ ((l32 >> 1) & 7)) << 4);
     const int woff = (wn * 32 + l32) * S::WPitch;
     const int dh_idx = hi ? BN * 4 : (wn * 32 + l32) * 4;
     const int nbase = wn * 32 + 4 * hi;   // local weight row of r = 0
