@@ -62,7 +62,7 @@ TRAFFIC = {
     "fp16_fused_q4_0_N1": (int((4698.1 * 2.0 + 16.0) * 1024), "profiles/fp16_fused_q4_0_n1_k4096.md"),
 }
 
-ONLY = ("copy", "read", "gemm", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
+ONLY = ("copy", "read", "gemm", "gemm_q81", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
         "w16_m1", "w16_m2048", "q8f_m1", "q8f_m2048", "f16_fused_m1")
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, published
 
@@ -180,15 +180,22 @@ class Workloads:
         out = self.torch.empty((M, N), dtype=self.torch.float32, device=self.dev)
         ws = self.torch.empty(ops.workspace_size(0, 0, M, N, K), dtype=self.torch.uint8, device=self.dev)
         AQ = [ops.quantize_q8_1(X[i]) for i in range(copies)]
+        PQ = [ops.quantize_planar(ksq.W_Q4_0, X[i]) for i in range(copies)]
         self.torch.cuda.synchronize()
 
         def step(i):
             ops.gemm(ksq.W_Q4_0, ksq.A_F32, W[i % copies], X[i % copies], M, N, K, out=out, workspace=ws)
 
         def gemm_only(i):
+            # the step's GEMM launch alone: the LDS-DMA GEMM on the planar activations the step's
+            # quantise launch writes
+            ops.gemm_planar(ksq.W_Q4_0, W[i % copies], PQ[i % copies], M, N, K, out=out)
+
+        def gemm_q81(i):
+            # pre-quantised block_q8_1 input (ksq_gemm_q4_0_q8_1): the 128 x 128 register-staged tile
             ops.gemm(ksq.W_Q4_0, ksq.A_Q8_1, W[i % copies], AQ[i % copies], M, N, K, out=out)
 
-        return (M, N, K), step, gemm_only
+        return (M, N, K), step, gemm_only, gemm_q81
 
     def gemv(self, copies: int = 64):
         """Config 0: 64 weight copies (604 MB, > 2x the MALL)."""
@@ -453,9 +460,9 @@ def only(args, dev) -> int:
         fn = lambda i: dst.copy_(src)  # noqa: E731
     elif args.only == "read":
         fn, _ = wl.read()
-    elif args.only in ("gemm", "step"):
-        _, step, gemm_only = wl.config2()
-        fn = gemm_only if args.only == "gemm" else step
+    elif args.only in ("gemm", "step", "gemm_q81"):
+        _, step, gemm_only, gemm_q81 = wl.config2()
+        fn = {"gemm": gemm_only, "step": step, "gemm_q81": gemm_q81}[args.only]
     elif args.only in ("gemv", "gemv_f32"):
         _, q81, f32, _ = wl.gemv()
         fn = q81 if args.only == "gemv" else f32
@@ -523,7 +530,7 @@ def main() -> int:
     read_gbs = 9437184 / (read_ms * 1e-3) / 1e9
 
     # ---- headline: config 2 steps
-    (M, N, K), step, gemm_only = wl.config2()
+    (M, N, K), step, gemm_only, gemm_q81 = wl.config2()
     log(f"bench: config 2 inputs M={M} N={N} K={K}, 8 rotating copies")
     n_eager = min(args.warmup, 2)            # sizes the library's workspace pool before capture
     for i in range(n_eager):
@@ -557,6 +564,7 @@ def main() -> int:
     settle(g1)
     gemm_d = dist(replay_samples(g1, 48))
     del g1
+    q81_ms, q81_d = graph_stats(gemm_q81, args.steps, 1)
 
     result = {
         "metric": "Q4_0×Q8_1 GEMM TOPS at M=2048; GEMV HBM GB/s at M=1 (N=K=4096)",
@@ -572,18 +580,22 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic, seeded (Q4_0 nibbles U[0,15], d=|N(0,0.02)|; activations N(0,1))",
         "config": {"workload": "q4_0_q8_1_prefill_gemm (BASELINE config 2)", "M": M, "N": N, "K": K,
-                   "entry": "gemm_w4a32c8_q4_0_fp32_int8: quantize_q8_1 + int8-MFMA GEMM",
+                   "entry": "gemm_w4a32c8_q4_0_fp32_int8: quantize_q8_1 (planar layout) + int8-MFMA GEMM "
+                            "(LDS-DMA staging)",
                    "rotating_copies": 8, "warmup_settle_ms": SETTLE_MS,
                    "host_wall_ms_per_step": round(wall, 5),
                    "step_distribution": step_d},
-        "roofline": {"bound": "mfma", "kernel": "mmq_kernel<0> (Q4_0 x Q8_1, v_mfma_i32_32x32x32_i8)",
+        "roofline": {"bound": "mfma", "kernel": "mmq_planar_kernel<0> (Q4_0 x planar Q8_1, v_mfma_i32_32x32x32_i8)",
                      "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                      "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC["gemm"][0],
                      "traffic_source": TRAFFIC["gemm"][1],
-                     "traffic_unit": "bytes per launch (algorithmic: %d)" % (
-                         N * (K // 32) * 18 + M * (K // 32) * 36 + M * N * 4),
+                     "traffic_unit": "bytes per launch (algorithmic: %d; planar activations 42 bytes per "
+                                     "block)" % (N * (K // 32) * 18 + M * (K // 32) * 42 + M * N * 4),
                      "avg_kernel_ms": round(gemm_ms, 5), "kernel_distribution": gemm_d,
-                     "note": "int8 ops = 2*M*N*K per launch over the HIP-event time of graph-replayed launches"},
+                     "note": "int8 ops = 2*M*N*K per launch over the HIP-event time of graph-replayed launches",
+                     "q8_1_input_kernel": {"kernel": "mmq_kernel<TileL, Q4_0> (ksq_gemm_q4_0_q8_1)",
+                                           "avg_kernel_ms": round(q81_ms, 5),
+                                           "TOPS": round(ops_per_step / (q81_ms * 1e-3) / 1e12, 3), **q81_d}},
         "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(gemv_gbs, 1), "unit": "GB/s",
                     "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6), **gemv_d,
                     "algorithmic_bytes": gemv_bytes,

@@ -240,6 +240,21 @@ KSQ_API int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const voi
 KSQ_API size_t ksq_debug_stream_read_outputs(size_t bytes);
 KSQ_API int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream);
 
+/* Debug / measurement: the two launches of an fp32 ksq_gemm call that takes the LDS-DMA GEMM
+ * (Q4_0 / Q4_1 weights, K % 256 == 0, the 128 x 128-tile shapes), run separately so that the
+ * GEMM kernel can be timed alone.  ksq_debug_quantize_planar writes the planar block_q8_1
+ * activations of x [M][K] (fp32, 16-byte aligned) for weight type wtype into `planar`
+ * (ksq_debug_planar_bytes(M, K) bytes, 256-byte aligned): the same blocks as
+ * ksq_quantize_q8_1, split into an int8 quant plane [M][K], (d, -12582912 d) fp32 pairs
+ * [K/32][Mp] (d = the fp16 scale, divided by 8 for Q4_0) and -s fp16 bits [K/128][Mp][4]
+ * (Mp = M rounded up to 128).  ksq_debug_gemm_planar runs the GEMM on them; it splits along K
+ * where ksq_gemm would, with its partial sums in the library's workspace pool.  The two in a
+ * row write what ksq_gemm writes for the same fp32 input. */
+KSQ_API size_t ksq_debug_planar_bytes(int M, int K);
+KSQ_API int ksq_debug_quantize_planar(int wtype, const float* x, void* planar, int M, int K, void* stream);
+KSQ_API int ksq_debug_gemm_planar(int wtype, const void* weight, const void* planar, float* output, int M, int N,
+                                  int K, void* stream);
+
 /* Debug: per-block integer dot products out[M][N][nblk] (nblk = K/32, or K/16 for
  * Q6_K) computed by the device block-dot code of the decode kernels. */
 KSQ_API int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out,

@@ -524,6 +524,49 @@ int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const void* activ
     return ksq_gemm(wtype, atype, weight, activation, output, M, N, K, p, (size_t)KSQ_NOALLOC_SCRATCH_BYTES, stream);
 }
 
+size_t ksq_debug_planar_bytes(int M, int K) {
+    if (M <= 0 || K <= 0 || K % 256) return 0;
+    return ksq::planar_bytes(M, K);
+}
+
+int ksq_debug_quantize_planar(int wtype, const float* x, void* planar, int M, int K, void* stream) {
+    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q4_1)
+        return set_error(KSQ_ERR_TYPE, "the LDS-DMA GEMM takes Q4_0 and Q4_1 weights (weight type %d)", wtype);
+    if (M < 0 || K < 0 || K % 256) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d K=%d (K %% 256 == 0)", M, K);
+    if (M == 0 || K == 0) return ok();
+    if (!x || !planar) return set_error(KSQ_ERR_NULL, "x or planar is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)planar & 255u))
+        return set_error(KSQ_ERR_ALIGN, "x must be 16-byte and planar 256-byte aligned");
+    hipError_t e = ksq::launch_quantize_planar(x, ksq::planar_at(planar, M, K), M, K, ksq::planar_da_scale(wtype),
+                                               (hipStream_t)stream);
+    return e == hipSuccess ? ok() : hip_error(e, "quantize launch");
+}
+
+int ksq_debug_gemm_planar(int wtype, const void* weight, const void* planar, float* output, int M, int N, int K,
+                          void* stream) {
+    g_engines = 0;
+    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q4_1)
+        return set_error(KSQ_ERR_TYPE, "the LDS-DMA GEMM takes Q4_0 and Q4_1 weights (weight type %d)", wtype);
+    if (M < 0 || N < 0 || K < 0 || K % 256) return set_error(KSQ_ERR_SHAPE, "bad shape M=%d N=%d K=%d", M, N, K);
+    if (M == 0 || N == 0 || K == 0) return ok();
+    if (!weight || !planar || !output) return set_error(KSQ_ERR_NULL, "weight, planar or output is NULL");
+    if (((uintptr_t)weight & 15u) || ((uintptr_t)planar & 255u) || ((uintptr_t)output & 3u))
+        return set_error(KSQ_ERR_ALIGN, "weight must be 16-byte, planar 256-byte and output 4-byte aligned");
+    hipStream_t s = (hipStream_t)stream;
+    float* partials = nullptr;
+    const int splits = ksq::mmq_planar_splits(wtype, M, N, K);
+    if (splits > 1) {
+        void* p = nullptr;
+        int st = pool_get((size_t)splits * (size_t)M * (size_t)N * sizeof(float), s, &p);
+        if (st != KSQ_OK) return st;
+        partials = (float*)p;
+    }
+    // the planes are only read: the const view is the layout of planar_at
+    const ksq::PlanarQ81 P = ksq::planar_at(const_cast<void*>(planar), M, K);
+    hipError_t e = ksq::launch_mmq_planar(wtype, (const uint8_t*)weight, P, output, M, N, K, partials, s);
+    return e == hipSuccess ? ok() : hip_error(e, "mmq launch");
+}
+
 size_t ksq_debug_stream_read_outputs(size_t bytes) { return ksq::stream_read_outputs(bytes); }
 
 int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream) {

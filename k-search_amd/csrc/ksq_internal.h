@@ -53,6 +53,7 @@ hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int
 // activations quantised with da_scale = planar_da_scale(wtype); whether it is the pick for this
 // shape (fp32 activations); partials as launch_mmq (mmq_splits(...) > 1).
 bool mmq_planar_preferred(int wtype, int M, int N, int K);
+int mmq_planar_splits(int wtype, int M, int N, int K);
 float planar_da_scale(int wtype);
 hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int M, int N, int K,
                              float* partials, hipStream_t s);

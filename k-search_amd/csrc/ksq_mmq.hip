@@ -1210,6 +1210,8 @@ bool mmq_planar_preferred(int wtype, int M, int N, int K) {
     return KSQ_MMQ_PLANAR && g_mmq_config == 0 && pick_config(wtype, M, N, K) == 1;
 }
 
+int mmq_planar_splits(int wtype, int M, int N, int K) { return split_for<TileL>(wtype, M, N, K); }
+
 float planar_da_scale(int wtype) { return wtype == kWQ40 ? 1.0f / WShape<kWQ40, 4>::out_scale : 1.0f; }
 
 hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int M, int N, int K,

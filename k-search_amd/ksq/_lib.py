@@ -65,6 +65,9 @@ SIGNATURES = {
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),
     "ksq_gemm": ([_I, _I, _P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_gemm_noalloc": ([_I, _I, _P, _P, _P, _I, _I, _I, _P], _I),
+    "ksq_debug_planar_bytes": ([_I, _I], _SZ),
+    "ksq_debug_quantize_planar": ([_I, _P, _P, _I, _I, _P], _I),
+    "ksq_debug_gemm_planar": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_stream_read_outputs": ([_SZ], _SZ),
     "ksq_debug_stream_read": ([_P, _SZ, _P, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),

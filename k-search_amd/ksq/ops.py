@@ -178,6 +178,30 @@ def block_sumi(wtype: int, weight: torch.Tensor, act_q8_1: torch.Tensor, M: int,
     return out
 
 
+def quantize_planar(wtype: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The planar block_q8_1 activations the LDS-DMA GEMM reads (debug / measurement): a uint8
+    buffer of ksq_debug_planar_bytes(M, K) bytes holding the int8 quant plane [M][K], the
+    (d, -12582912 d) fp32 pairs [K/32][Mp] and the -s fp16 bits [K/128][Mp][4], each plane
+    256-byte aligned (Mp = M rounded up to 128)."""
+    if not (x.is_cuda and x.dtype == torch.float32):
+        raise RuntimeError("quantize_planar expects a CUDA float32 tensor")
+    x = x.contiguous()
+    M, K = x.shape
+    if out is None:
+        out = torch.empty(max(1, lib().ksq_debug_planar_bytes(M, K)), dtype=torch.uint8, device=x.device)
+    check(lib().ksq_debug_quantize_planar(wtype, _ptr(x), _ptr(out), M, K, _stream()))
+    return out
+
+
+def gemm_planar(wtype: int, weight: torch.Tensor, planar: torch.Tensor, M: int, N: int, K: int,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """The LDS-DMA GEMM alone on quantize_planar's output (debug / measurement)."""
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=weight.device)
+    check(lib().ksq_debug_gemm_planar(wtype, _ptr(weight), _ptr(planar), _ptr(out), M, N, K, _stream()))
+    return out
+
+
 def stream_read(buf: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """Calibration read of every byte of buf (ksq_debug_stream_read); returns the XOR words."""
     nbytes = buf.numel() * buf.element_size()

@@ -72,6 +72,66 @@ def test_quantize_q8_1_bit_exact(dev, oracle):
         assert np.array_equal(q.cpu().numpy(), oracle.quantize_q8_1(x)), (M, K)
 
 
+def _planar_planes(buf, M, K):
+    """(quants [M][K] int8, (d, nc) [K/32][Mp][2] float32, -s bits [K/128][Mp][4] uint16) of a
+    planar block_q8_1 buffer (each plane 256-byte aligned, Mp = M rounded up to 128)."""
+    a256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    mp, nb = (M + 127) // 128 * 128, K // 32
+    q = buf[:M * K].view(np.int8).reshape(M, K)
+    o = a256(M * K)
+    dn = buf[o:o + nb * mp * 8].view(np.float32).reshape(nb, mp, 2)
+    o += a256(nb * mp * 8)
+    sa = buf[o:o + nb // 4 * mp * 8].view(np.uint16).reshape(nb // 4, mp, 4)
+    return q, dn, sa
+
+
+@pytest.mark.parametrize("wtype,M,K", [(0, 2048, 4096), (4, 300, 1024), (0, 1, 256)])
+def test_quantize_planar_bit_exact(dev, oracle, wtype, M, K):
+    """The LDS-DMA GEMM's planar activations hold exactly the oracle's block_q8_1 blocks: quants,
+    d (divided by 8 for Q4_0) with -12582912 d beside it, and -s; rows past M are zeros."""
+    import torch
+    from ksq import ops
+    g = np.random.default_rng(120 + M)
+    x = g.standard_normal((M, K), dtype=np.float32)
+    x[0, 64] = np.inf                      # the general path of the device quantiser
+    x[M // 2, 96:128] *= 1e-39
+    buf = ops.quantize_planar(wtype, _t(x, dev))
+    torch.cuda.synchronize()
+    q, dn, sa = _planar_planes(buf.cpu().numpy(), M, K)
+    blk = oracle.quantize_q8_1(x)                               # [M][K/32][36]
+    d16 = blk[:, :, 0:2].copy().view(np.float16)[:, :, 0]
+    s16 = blk[:, :, 2:4].copy().view(np.uint16)[:, :, 0]
+    assert np.array_equal(q, blk[:, :, 4:].reshape(M, K).view(np.int8))
+    d = d16.astype(np.float32) * np.float32(0.125 if wtype == 0 else 1.0)
+    assert np.array_equal(dn[:, :M, 0], d.T)
+    assert np.array_equal(dn[:, :M, 1], (np.float32(-12582912.0) * d).T)
+    want_sa = (s16 ^ 0x8000).T.reshape(K // 128, 4, M).transpose(0, 2, 1)
+    assert np.array_equal(sa[:, :M, :], want_sa)
+    assert not dn[:, M:, 0].any() and not dn[:, M:, 1].any()
+
+
+@pytest.mark.parametrize("wtype,M,N,K", [(0, 2048, 4096, 4096), (4, 300, 520, 1280)])
+def test_planar_halves_equal_fp32_call(dev, wtype, M, N, K):
+    """ksq_debug_quantize_planar + ksq_debug_gemm_planar write what the fp32 ksq_gemm call writes,
+    bit for bit (the bench times the GEMM half alone)."""
+    import torch
+    from ksq import _lib, ops, synth
+    g = np.random.default_rng(130 + M)
+    w = _t(synth.weights(wtype, g, N, K), dev)
+    x = _t(synth.activations(g, M, K), dev)
+    L = _lib.lib()
+    assert L.ksq_set_mmq_config(8) == 0
+    try:
+        y = ops.gemm(wtype, 0, w, x, M, N, K)
+        assert "mmq_planar" in ops.last_engines()
+        y2 = ops.gemm_planar(wtype, w, ops.quantize_planar(wtype, x), M, N, K)
+        assert ops.last_engines() & {"mmq_planar"}
+        torch.cuda.synchronize()
+    finally:
+        L.ksq_set_mmq_config(0)
+    assert torch.equal(y, y2)
+
+
 @pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_quantize_q8_1_variants_bit_exact(dev, oracle, variant):
     """ksq_quantize_q8_1_variant: the reference's device quantiser (1), the NumPy harness
