@@ -743,11 +743,13 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
         if (wave == 3) dma16(A.sa + ((size_t)(kb0 >> 2) * A.mp + m0 + 2 * lane) * 4, P ? sSa1 : sSa0);
     };
 
-    // ---- weights: thread t stages blocks 2h, 2h + 1 (h = t % 2) of row t / 2 ----
-    // (4-byte loads of the 36- / 40-byte half chunk: 8-byte loads from the 8-byte boundary below,
-    // with Q4_0's second half re-aligned by a word, measured 1% slower on the whole call)
+    // ---- weights: thread t stages blocks 2h, 2h + 1 (h = t / 128) of row t % 128 ----
+    // (consecutive lanes write consecutive rows' scales and quants, free of LDS bank conflicts;
+    // lane pairs sharing a row left 2-way conflicts on every scale write: 1.3e6 conflict cycles
+    // per launch.  4-byte loads of the 36- / 40-byte half chunk: 8-byte loads from the 8-byte
+    // boundary below, with Q4_0's second half re-aligned by a word, measured 1% slower.)
     constexpr int HW = WNW / 2;   // words per half chunk
-    const int wsr = t >> 1, wh = t & 1;
+    const int wsr = t & 127, wh = t >> 7;
     uint32_t pre[HW + 1];
     auto load_w = [&](int kb0) __attribute__((always_inline)) {
         const int wr = min(n0 + wsr, N - 1);
