@@ -805,27 +805,40 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
         const uint16_t* cSa = P ? sSa1 : sSa0;
         const uint16_t* cDh = P ? sDh1 : sDh0;
         constexpr int NQ = KB * TM;
-        i32x4 af[TM], bf;
+        i32x4 af[TM], afn[TM], bf;
+        u32x4 bxn;
         f32x4 edw[4];
-        auto mfma_step = [&](int q) -> i32x16 {
-            const int b = q / TM, i = q % TM;
-            if (i == 0) {
-#pragma unroll
-                for (int ii = 0; ii < TM; ii++) af[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[b]);
-                const u32x4 x = *(const u32x4*)(cW + woff + b * 16);
-                const int s4 = 4 * hi;
-                bf = i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
-                           (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
-            }
-            return __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i], bias, 0, 0, 0);
+        auto unpack = [&](const u32x4& x) -> i32x4 {
+            const int s4 = 4 * hi;
+            return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
+                         (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
         };
+#pragma unroll
+        for (int ii = 0; ii < TM; ii++) af[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[0]);
+        bf = unpack(*(const u32x4*)(cW + woff));
         __builtin_amdgcn_s_setprio(2);
-        i32x16 cur = mfma_step(0);
+        i32x16 cur = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[0], bias, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
             const int b = q / TM, i = q % TM;
+            if (i == 0 && b + 1 < KB) {
+                // the next block's fragments, a block ahead of their MFMAs
+#pragma unroll
+                for (int ii = 0; ii < TM; ii++) afn[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[b + 1]);
+                bxn = *(const u32x4*)(cW + woff + (b + 1) * 16);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             i32x16 nxt = bias;
-            if (q + 1 < NQ) nxt = mfma_step(q + 1);
+            if (q + 1 < NQ) {
+                if (i + 1 < TM) {
+                    nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i + 1], bias, 0, 0, 0);
+                } else {
+                    bf = unpack(bxn);
+#pragma unroll
+                    for (int ii = 0; ii < TM; ii++) af[ii] = afn[ii];
+                    nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[0], bias, 0, 0, 0);
+                }
+            }
             if (i == 0) {
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++) edw[qq] = *(const f32x4*)&cDw[b * BN + nbase + 8 * qq];
