@@ -368,6 +368,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                     v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
                 }
                 const float d = f16_to_f32(v[0] & 0xFFFFu), dmin = f16_to_f32(v[0] >> 16);
+                // the row's 8 side factors leave as one 16-byte write per plane (8 two-byte
+                // writes per row 16 bytes apart were 4-way LDS bank conflicts)
+                uint32_t hh[4], ll[4];
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
                     int sc, mn;
@@ -377,9 +380,17 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                     const float f = dmin * (float)mn * 0.125f;
                     const _Float16 h = (_Float16)f;
                     const _Float16 l = (_Float16)(f - (float)h);
-                    sDwH[sr][j] = __builtin_bit_cast(uint16_t, h);
-                    sDwL[sr][j] = __builtin_bit_cast(uint16_t, l);
+                    const uint32_t hb = __builtin_bit_cast(uint16_t, h), lb = __builtin_bit_cast(uint16_t, l);
+                    if (j & 1) {
+                        hh[j >> 1] |= hb << 16;
+                        ll[j >> 1] |= lb << 16;
+                    } else {
+                        hh[j >> 1] = hb;
+                        ll[j >> 1] = lb;
+                    }
                 }
+                *(u32x4*)&sDwH[sr][0] = u32x4{hh[0], hh[1], hh[2], hh[3]};
+                *(u32x4*)&sDwL[sr][0] = u32x4{ll[0], ll[1], ll[2], ll[3]};
 #pragma unroll
                 for (int i = 0; i < 8; i++)
                     *(u32x4*)(sW + sr * S::WPitch + 16 * i) =
@@ -387,10 +398,13 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
             }
         } else {
             // ---- Q6_K: one 210-byte super-block per row and K step (2-byte aligned); two
-            // threads per row, each unpacking one 128-element half to int8 (q - 32)
+            // threads per row, each unpacking one 128-element half to int8 (q - 32): threads
+            // c < BN take the first halves of rows c, the next BN the second halves (consecutive
+            // lanes write consecutive rows; lane pairs sharing a row were 2-way LDS bank
+            // conflicts on every scale write)
             const int nsb = nb / 8, s0 = kb0 / 8;
             for (int c = t; c < 2 * BN; c += T::NT) {
-                const int sr = c >> 1, h = c & 1;
+                const int sr = c % BN, h = c / BN;
                 const int wr = min(n0 + sr, N - 1);
                 const uint8_t* sb = W + ((size_t)wr * nsb + s0) * kQ6KBytes;
                 uint32_t ql[16], qh[8], scw[2];
