@@ -229,6 +229,9 @@ def _engine_cases():
     for wt in (0, 4):
         for K in (1024, 1280):
             cases.append((f"mmqp_k{K}_w{wt}", wt, 200, 330, K, 0, 2, 8, {"quantize", "mmq_planar", "splitk"}, 0))
+        # a single row and a ragged 33 rows in one 128-row tile (rows past M read row M-1)
+        for M in (1, 33):
+            cases.append((f"mmqp_m{M}_w{wt}", wt, M, 136, 512, 0, 2, 8, {"quantize", "mmq_planar"}, 0))
     cases.append(("splitk_w0", 0, 32, 1024, 8192, 1, 0, 0, {"mmq5", "splitk"}, 0))
     cases.append(("splitk_w1", 1, 32, 1024, 8192, 1, 0, 0, {"mmq3", "splitk"}, 0))
     # the native W8A8C8 operator's block_q8s activations: fp32 (its quantiser) and pre-quantised
