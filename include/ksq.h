@@ -207,8 +207,10 @@ KSQ_API int ksq_gemm_w16(int wtype, const float* A, const uint8_t* B, float* C, 
 KSQ_API int ksq_gemm_w4a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream);
 KSQ_API int ksq_gemm_w8a16(const float* A, const uint8_t* B, float* C, int M, int N, int K, void* stream);
 
-/* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the quantised copy of
- * fp32 activations, 0 for pre-quantised activations. */
+/* Workspace bytes ksq_gemm needs for (wtype, atype, M, N, K): the quantised copy of fp32 or
+ * fp16 activations (block_q8_1 rows, or the LDS-DMA GEMM's planar form for fp32 x Q4_0 / Q4_1
+ * at large M, 42 bytes per block), plus the split-K partial sums of small MFMA grids (so it can
+ * be non-zero for pre-quantised activations too).  The workspace must be 16-byte aligned. */
 KSQ_API size_t ksq_gemm_workspace_size(int wtype, int atype, int M, int N, int K);
 
 /* General entry: wtype = enum ksq_wtype, atype = enum ksq_atype (the block_q8s forms pair
