@@ -49,9 +49,13 @@ using W16Skinny = W16Tile<32, 128, 1, 1>;
 
 constexpr int kW16Pitch = 72;         // bf16 per staged row: 64 values of the step + 8 padding
 
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values as a bf16 pair (round to nearest even), lo in the low half: one packed
+// conversion (v_cvt_pk_bf16_f32) instead of two single ones and the shift and or that merge them.
 __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2v{lo, hi}, bf16x2));
 }
 __device__ __forceinline__ float bf16_low_f32(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
 __device__ __forceinline__ float bf16_high_f32(uint32_t p) { return __builtin_bit_cast(float, p & 0xFFFF0000u); }
