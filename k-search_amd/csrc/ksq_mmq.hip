@@ -35,6 +35,10 @@
 
 namespace ksq {
 
+#ifndef KSQ_KQ_PIPE
+#define KSQ_KQ_PIPE 1   // K-quant staging loads of the next K step prefetched into registers
+#endif
+
 constexpr uint32_t kMagic = 0x4B400000u;  // 12582912.0f
 constexpr float kMagicF = 12582912.0f;
 
@@ -317,19 +321,135 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
             }
         }
     };
+    // ---- K-quant super-blocks, split into the global loads and the LDS writes.  Work item c is
+    // weight row c (Q4_K: 144 bytes, 16-byte aligned) or, for Q6_K (210 bytes, 2-byte aligned),
+    // half h = c / BN of row c % BN: items c < BN take the first halves (consecutive lanes write
+    // consecutive rows; lane pairs sharing a row were 2-way LDS bank conflicts on every scale
+    // write).  The loads keep raw words: Q6_K's are re-aligned with v_alignbyte_b32 when stored.
+    constexpr int KQW = (WT == kWQ6K) ? 2 * BN : BN;     // weight work items per K step
+    auto load_kq = [&](int c, int kb0, uint32_t* v) {
+        const int nsb = nb / 8, s0 = kb0 / 8;
+        if constexpr (WT == kWQ4K) {
+            const int wr = min(n0 + c, N - 1);
+            const uint8_t* p = W + ((size_t)wr * nsb + s0) * kQ4KBytes;
+#pragma unroll
+            for (int i = 0; i < 9; i++) {
+                const u32x4 x = *(const u32x4*)(p + 16 * i);
+                v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+            }
+        } else if constexpr (WT == kWQ6K) {
+            // v[0..16] the ql half (64 B at 64h), v[17..25] the qh half (32 B at 128 + 32h),
+            // v[26..28] the 8 scales (at 192 + 8h), v[29] d, v[30] the byte shift; the last raw
+            // word of each field is read only when the super-block is not 4-byte aligned, so no
+            // byte past the field is touched
+            const int sr = c % BN, h = c / BN;
+            const int wr = min(n0 + sr, N - 1);
+            const uint8_t* sb = W + ((size_t)wr * nsb + s0) * kQ6KBytes;
+            const int sh = (int)((uintptr_t)sb & 3u);
+            const uint32_t* q = (const uint32_t*)(sb - sh);
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = q[16 * h + i];
+            v[16] = sh ? q[16 * h + 16] : 0u;
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[17 + i] = q[32 + 8 * h + i];
+            v[25] = sh ? q[40 + 8 * h] : 0u;
+            v[26] = q[48 + 2 * h];
+            v[27] = q[49 + 2 * h];
+            v[28] = sh ? q[50 + 2 * h] : 0u;
+            v[29] = *(const uint16_t*)(sb + 208);
+            v[30] = (uint32_t)sh;
+        }
+    };
+    auto store_kq = [&](int c, const uint32_t* v) {
+        if constexpr (WT == kWQ4K) {
+            const int sr = c;
+            const float d = f16_to_f32(v[0] & 0xFFFFu), dmin = f16_to_f32(v[0] >> 16);
+            // the row's 8 side factors leave as one 16-byte write per plane (8 two-byte
+            // writes per row 16 bytes apart were 4-way LDS bank conflicts)
+            uint32_t hh[4], ll[4];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                int sc, mn;
+                q4_K_scale_min_regs(j, v + 1, sc, mn);
+                sDw[j][sr] = d * (float)sc;                     // exact: 11 x 6 bits
+                // side factor dmin*m/8 (17 significant bits) as an fp16 hi + lo pair
+                const float f = dmin * (float)mn * 0.125f;
+                const _Float16 h = (_Float16)f;
+                const _Float16 l = (_Float16)(f - (float)h);
+                const uint32_t hb = __builtin_bit_cast(uint16_t, h), lb = __builtin_bit_cast(uint16_t, l);
+                if (j & 1) {
+                    hh[j >> 1] |= hb << 16;
+                    ll[j >> 1] |= lb << 16;
+                } else {
+                    hh[j >> 1] = hb;
+                    ll[j >> 1] = lb;
+                }
+            }
+            *(u32x4*)&sDwH[sr][0] = u32x4{hh[0], hh[1], hh[2], hh[3]};
+            *(u32x4*)&sDwL[sr][0] = u32x4{ll[0], ll[1], ll[2], ll[3]};
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                *(u32x4*)(sW + sr * S::WPitch + 16 * i) =
+                    u32x4{v[4 + 4 * i], v[5 + 4 * i], v[6 + 4 * i], v[7 + 4 * i]};
+        } else if constexpr (WT == kWQ6K) {
+            // unpack one 128-element half to int8 (q - 32)
+            const int sr = c % BN, h = c / BN;
+            const int sh = (int)v[30];
+            uint32_t ql[16], qh[8], scw[2];
+#pragma unroll
+            for (int i = 0; i < 16; i++) ql[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], sh);
+#pragma unroll
+            for (int i = 0; i < 8; i++) qh[i] = __builtin_amdgcn_alignbyte(v[18 + i], v[17 + i], sh);
+#pragma unroll
+            for (int i = 0; i < 2; i++) scw[i] = __builtin_amdgcn_alignbyte(v[27 + i], v[26 + i], sh);
+            const float d = f16_to_f32(v[29]);
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int sc = (int)(int8_t)((scw[u >> 2] >> (8 * (u & 3))) & 0xFFu);
+                sDw[8 * h + u][sr] = d * (float)sc;              // exact: 11 x 8 bits
+            }
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                uint32_t o[8];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t lo = (ql[8 * (g & 1) + i] >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
+                    const uint32_t hb = ((qh[i] >> (2 * g)) << 4) & 0x30303030u;
+                    // 6-bit values b, one per byte; (b + 96) ^ 128 = b - 32 as int8, and b + 96
+                    // <= 159 carries into no neighbouring byte
+                    o[i] = ((lo | hb) + 0x60606060u) ^ 0x80808080u;
+                }
+                // elements 128h + 32g .. +31 = block 4h + g of this K step
+                u32x4* dst = (u32x4*)(sW + sr * S::WPitch + (4 * h + g) * 32);
+                dst[0] = u32x4{o[0], o[1], o[2], o[3]};
+                dst[1] = u32x4{o[4], o[5], o[6], o[7]};
+            }
+        }
+    };
     constexpr bool PIPE = T::PIPE && !MOE && !is_kquant(WT);
     static_assert(!PIPE || (KB == 4 && BM == 128 && BN == 128 && T::NT == 256),
                   "the pipelined staging covers 128 x 128 tiles with 4-block K steps");
+    // KPIPE (Q6_K, no MoE, tiles whose K step is at most 128 weight items and 128 activation
+    // chunks): threads 0..127 hold weight item t, 128..255 activation chunk t - 128 of the next K
+    // step, the same way (Q6_K M = 128, N = 14336, K = 4096 on 64 x 64: 70.9 -> 62.5 us with the
+    // quantiser).  Q4_K's prefetched form spills at three workgroups per CU (64 x 128: 42.9 ->
+    // 50.9 us) and stays unprefetched.
+    constexpr int ACH = BM * (KB / 4);                   // activation chunks per K step
+    constexpr bool KPIPE = KSQ_KQ_PIPE && WT == kWQ6K && !MOE && T::NT == 256 && KQW <= 128 && ACH <= 128;
     // PIPE: one chunk per thread and K step; threads 0..127 activation row t, 128..255 weight row t-128
-    uint32_t pre[PIPE ? 4 * ABW : 1];
+    uint32_t pre[(PIPE || KPIPE) ? 4 * ABW : 1];
+    static_assert(!KPIPE || 4 * ABW >= 36, "a prefetched super-block fits the chunk registers");
     const bool pre_act = t < 128;
     auto pre_load = [&](int kb0) {
         if constexpr (PIPE) {
             if (pre_act) load_act(t, 0, kb0, pre);
             else load_w(t - 128, 0, kb0, pre);
+        } else if constexpr (KPIPE) {
+            if (t < KQW) load_kq(t, kb0, pre);
+            else if (t >= 128 && t - 128 < ACH) load_act((t - 128) / (KB / 4), (t - 128) % (KB / 4), kb0, pre);
         }
     };
-    if constexpr (PIPE) {
+    if constexpr (PIPE || KPIPE) {
         if (kb_lo < kb_hi) pre_load(kb_lo);
     }
 
@@ -337,6 +457,11 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         if constexpr (PIPE) {
             if (pre_act) store_act(t, 0, pre);
             else store_w(t - 128, 0, pre);
+            __syncthreads();
+            if (kb0 + KB < kb_hi) pre_load(kb0 + KB);
+        } else if constexpr (KPIPE) {
+            if (t < KQW) store_kq(t, pre);
+            else if (t >= 128 && t - 128 < ACH) store_act((t - 128) / (KB / 4), (t - 128) % (KB / 4), pre);
             __syncthreads();
             if (kb0 + KB < kb_hi) pre_load(kb0 + KB);
         } else {
@@ -355,85 +480,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 load_w(sr, g, kb0, v);
                 store_w(sr, g, v);
             }
-        } else if constexpr (WT == kWQ4K) {
-            // ---- Q4_K: one 144-byte super-block per row and K step (16-byte aligned)
-            const int nsb = nb / 8, s0 = kb0 / 8;
-            for (int sr = t; sr < BN; sr += T::NT) {
-                const int wr = min(n0 + sr, N - 1);
-                const uint8_t* p = W + ((size_t)wr * nsb + s0) * kQ4KBytes;
-                uint32_t v[36];
-#pragma unroll
-                for (int i = 0; i < 9; i++) {
-                    const u32x4 x = *(const u32x4*)(p + 16 * i);
-                    v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
-                }
-                const float d = f16_to_f32(v[0] & 0xFFFFu), dmin = f16_to_f32(v[0] >> 16);
-                // the row's 8 side factors leave as one 16-byte write per plane (8 two-byte
-                // writes per row 16 bytes apart were 4-way LDS bank conflicts)
-                uint32_t hh[4], ll[4];
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    int sc, mn;
-                    q4_K_scale_min_regs(j, v + 1, sc, mn);
-                    sDw[j][sr] = d * (float)sc;                     // exact: 11 x 6 bits
-                    // side factor dmin*m/8 (17 significant bits) as an fp16 hi + lo pair
-                    const float f = dmin * (float)mn * 0.125f;
-                    const _Float16 h = (_Float16)f;
-                    const _Float16 l = (_Float16)(f - (float)h);
-                    const uint32_t hb = __builtin_bit_cast(uint16_t, h), lb = __builtin_bit_cast(uint16_t, l);
-                    if (j & 1) {
-                        hh[j >> 1] |= hb << 16;
-                        ll[j >> 1] |= lb << 16;
-                    } else {
-                        hh[j >> 1] = hb;
-                        ll[j >> 1] = lb;
-                    }
-                }
-                *(u32x4*)&sDwH[sr][0] = u32x4{hh[0], hh[1], hh[2], hh[3]};
-                *(u32x4*)&sDwL[sr][0] = u32x4{ll[0], ll[1], ll[2], ll[3]};
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-                    *(u32x4*)(sW + sr * S::WPitch + 16 * i) =
-                        u32x4{v[4 + 4 * i], v[5 + 4 * i], v[6 + 4 * i], v[7 + 4 * i]};
-            }
         } else {
-            // ---- Q6_K: one 210-byte super-block per row and K step (2-byte aligned); two
-            // threads per row, each unpacking one 128-element half to int8 (q - 32): threads
-            // c < BN take the first halves of rows c, the next BN the second halves (consecutive
-            // lanes write consecutive rows; lane pairs sharing a row were 2-way LDS bank
-            // conflicts on every scale write)
-            const int nsb = nb / 8, s0 = kb0 / 8;
-            for (int c = t; c < 2 * BN; c += T::NT) {
-                const int sr = c % BN, h = c / BN;
-                const int wr = min(n0 + sr, N - 1);
-                const uint8_t* sb = W + ((size_t)wr * nsb + s0) * kQ6KBytes;
-                uint32_t ql[16], qh[8], scw[2];
-                read_words_g<16>(sb + 64 * h, ql);
-                read_words_g<8>(sb + 128 + 32 * h, qh);
-                read_words_g<2>(sb + 192 + 8 * h, scw);
-                const float d = f16_to_f32(*(const uint16_t*)(sb + 208));
-#pragma unroll
-                for (int u = 0; u < 8; u++) {
-                    const int sc = (int)(int8_t)((scw[u >> 2] >> (8 * (u & 3))) & 0xFFu);
-                    sDw[8 * h + u][sr] = d * (float)sc;              // exact: 11 x 8 bits
-                }
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    uint32_t o[8];
-#pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        const uint32_t lo = (ql[8 * (g & 1) + i] >> (4 * (g >> 1))) & 0x0F0F0F0Fu;
-                        const uint32_t hb = ((qh[i] >> (2 * g)) << 4) & 0x30303030u;
-                        const uint32_t b6 = lo | hb;                 // 6-bit values, one per byte
-                        const uint32_t x = b6 ^ 0x20202020u;         // b - 32 for b >= 32
-                        const uint32_t neg = x & 0x20202020u;        // b < 32: sign-extend
-                        o[i] = x | (neg << 1) | (neg << 2);
-                    }
-                    // elements 128h + 32g .. +31 = block 4h + g of this K step
-                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + (4 * h + g) * 32);
-                    dst[0] = u32x4{o[0], o[1], o[2], o[3]};
-                    dst[1] = u32x4{o[4], o[5], o[6], o[7]};
-                }
+            // ---- K-quants: one super-block per weight row (Q4_K) or half-row (Q6_K) and K step
+            for (int c = t; c < KQW; c += T::NT) {
+                uint32_t v[36];
+                load_kq(c, kb0, v);
+                store_kq(c, v);
             }
         }
         __syncthreads();
@@ -501,7 +553,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         // KB*SUB*TN*TA MFMAs per K step, over the wave's first TA of its TM row tiles; step
         // q = ((b*SUB + h)*TN + j)*TA + i.  For Q6_K the two 16-element sub-blocks of a block are
         // separate MFMAs whose weight fragment keeps only the lanes holding that half
-        // (k = 16*hi ..).  The MFMA of step q+1 is issued before the epilogue of step q.
+        // (k = 16*hi ..); one K = 16 MFMA per sub-block instead measured slower (M = 128,
+        // N = 14336, K = 4096: 65.6 vs 63.0 us, its fragments cost registers the 64 x 64 tile
+        // then spills).  The MFMA of step q+1 is issued before the epilogue of step q.
         constexpr int SUBN = S::SUB;
         auto compute = [&](auto ta) __attribute__((always_inline)) {
             constexpr int TA = decltype(ta)::value;
