@@ -142,7 +142,8 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
     // the s_a term: f16 MFMA for block_q8_1, an epilogue subtraction for block_q8f
     constexpr bool SIDE_MFMA = S::side && AF == kAQ81, SIDE_BF = S::side && AFS;
     __shared__ __attribute__((aligned(16))) uint8_t sA[BM * T::APitch];
-    __shared__ __attribute__((aligned(16))) uint8_t sW[BN * S::WPitch];
+    // Q6_K: one more row, all zeros, that the lanes outside a sub-block read
+    __shared__ __attribute__((aligned(16))) uint8_t sW[(BN + (S::SUB == 2 ? 1 : 0)) * S::WPitch];
     __shared__ __attribute__((aligned(16))) float sDa[KB][BM];     // d_a' (d_a/8 for Q4_0)
     __shared__ __attribute__((aligned(16))) float sNc[KB][BM];     // -12582912 * d_a'
     __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
@@ -171,6 +172,9 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                   "block_q8f activations pair with Q4_0, Q5_0 and Q8_0 weights");
     static_assert(!(AFS && MOE), "the grouped GEMM reads block_q8_1 activations");
 
+    if constexpr (S::SUB == 2) {
+        for (int i = t; i < S::WPitch / 16; i += T::NT) *(u32x4*)(sW + BN * S::WPitch + 16 * i) = u32x4{0, 0, 0, 0};
+    }
     if constexpr (KB == 4) {
         // the f16 side-term MFMA contracts 8 block slots; slots 4..7 stay zero
         if (t < BM) *(uint4*)&sSaH[t][0] = uint4{0, 0, 0, 0};
@@ -512,6 +516,12 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
             }
         };
+        // Q6_K sub-block h of block b: the lanes holding the other half (hi != h) read the zero
+        // row, so the MFMA sums only this sub-block's 16 products
+        auto frag_b_sub = [&](int b, int j, int h) -> i32x4 {
+            const int row = (hi == h) ? wn * 32 * TN + j * 32 + l32 : BN;
+            return *(const i32x4*)(sW + row * S::WPitch + b * 32 + 16 * hi);
+        };
         // The MFMA computes the transposed tile D[n][m] (A operand = weight fragment, B operand =
         // activation fragment): lane l holds activation row m = l % 32 and the 16 weight rows
         // n = 8*(r/4) + 4*(l/32) + r%4, so its activation scales are two scalars and its weight
@@ -553,7 +563,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         // KB*SUB*TN*TA MFMAs per K step, over the wave's first TA of its TM row tiles; step
         // q = ((b*SUB + h)*TN + j)*TA + i.  For Q6_K the two 16-element sub-blocks of a block are
         // separate MFMAs whose weight fragment keeps only the lanes holding that half
-        // (k = 16*hi ..); one K = 16 MFMA per sub-block instead measured slower (M = 128,
+        // (k = 16*hi ..; the others read the zero row); one K = 16 MFMA per sub-block instead measured slower (M = 128,
         // N = 14336, K = 4096: 65.6 vs 63.0 us, its fragments cost registers the 64 x 64 tile
         // then spills).  The MFMA of step q+1 is issued before the epilogue of step q.
         constexpr int SUBN = S::SUB;
@@ -567,14 +577,18 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 if (q % (SUBN * TA * TN) == 0) {
 #pragma unroll
                     for (int ii = 0; ii < TA; ii++) af[ii] = frag_a(b, ii);
+                    if constexpr (SUBN == 1) {
 #pragma unroll
-                    for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b(b, jj);
+                        for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b(b, jj);
+                    }
                 }
-                i32x4 bb = bf[j];
                 if constexpr (SUBN == 2) {
-                    if (hi != h) bb = i32x4{0, 0, 0, 0};
+                    if (q % (TA * TN) == 0) {
+#pragma unroll
+                        for (int jj = 0; jj < TN; jj++) bf[jj] = frag_b_sub(b, jj, h);
+                    }
                 }
-                return __builtin_amdgcn_mfma_i32_32x32x32_i8(bb, af[i], bias, 0, 0, 0);
+                return __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], bias, 0, 0, 0);
             };
             // the compute phase of this wave goes first at instruction issue: with two workgroups
             // per CU the other one is usually staging (Q4_K M = 128: 50.0 -> 45.8 us, Q8_0
