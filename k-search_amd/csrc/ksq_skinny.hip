@@ -333,6 +333,10 @@ hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A
     const long long wave_target = M <= 4 ? 4096 : 1024;
     int nwv = 4;
     while (nwv < max_nwv && (long long)wgs * nwv < wave_target && steps >= 2 * nwv) nwv *= 2;
+    // 5-8 rows on a grid of at most one workgroup per CU: 8 waves (whole call, us: Q8_0 N = K =
+    // 4096, M = 8 14.3 -> 13.6, M = 6 13.8 -> 12.7; Q4_0 M = 8 13.1 -> 12.4); with 448 workgroups
+    // 4 stay better (Q8_0 N = K = 7168, M = 8: 27.2 vs 29.6)
+    if (M > 4 && wgs <= 256 && nwv < 8 && steps >= 16) nwv = 8;
     note_engine(KSQ_ENG_SKINNY);
     switch (wtype) {
         case kWQ40: return skinny_launch_mp<kWQ40, false>(nwv, W, A, C, M, N, nb, s);
