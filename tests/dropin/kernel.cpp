@@ -1,5 +1,6 @@
 // kernel.cpp - the forwarding file a KernelEvalPlus maintainer compiles in place of a quant_gemm
-// definition's kernel.cu to run it on libksq (the binding of INTEGRATION.md, section 1).
+// definition's kernel.cu to run it on libksq: each entry point forwards to the libksq symbol of
+// the same name.
 //
 // The reference harness generates a pybind wrapper around the definition's entry point
 // (kernelevalplus-main/llm_kernel_test/op_test_handler.py:298-349) which declares
