@@ -439,10 +439,13 @@ static hipError_t w16_launch(const float* A, const uint8_t* W, float* C, int M, 
 template <int WT, int MR>
 static hipError_t w16_gemv_launch(const float* A, const uint8_t* W, float* C, int N, int K, hipStream_t s) {
     const int nb = K / 32;
-    // 4 weight rows per wave while that keeps 256 workgroups, else 2 or 1
-    if ((N + 15) / 16 >= kW16MinWGs)
+    // 4 weight rows per wave while that keeps 512 workgroups, else 2 or 1 (whole call, us, with 256
+    // in place of 512: N = K = 4096 M = 1 6.84 -> 5.6, M = 2 8.66 -> 6.56; N = 4096, K = 14336,
+    // M = 4 33.4 -> 26.3; N = 14336 level; 1024 loses at M = 4: 35.6)
+    constexpr int kGemvMinWGs = 512;
+    if ((N + 15) / 16 >= kGemvMinWGs)
         hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 16>), dim3((N + 15) / 16), dim3(256), 0, s, W, A, C, N, nb);
-    else if ((N + 7) / 8 >= kW16MinWGs)
+    else if ((N + 7) / 8 >= kGemvMinWGs)
         hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 8>), dim3((N + 7) / 8), dim3(256), 0, s, W, A, C, N, nb);
     else
         hipLaunchKernelGGL((w16_gemv_kernel<WT, MR, 4>), dim3((N + 3) / 4), dim3(256), 0, s, W, A, C, N, nb);
