@@ -47,6 +47,7 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 TRAFFIC = {
     "gemm": (int((47754.3 * 2.0 + 32768.7) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
     "gemv": (int((4641.9 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
+    "gemv_f32": (int((4723.9 * 2.0 + 16.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "q8_0_M1": (int((8737.4 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q8_0_M8": (int((8889.7 * 2.0 + 128.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q8_0_M32": (int(((9342.9 + 2062.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
@@ -62,7 +63,7 @@ TRAFFIC = {
     "fp16_fused_q4_0_N1": (int((4697.9 * 2.0 + 16.0) * 1024), "profiles/fp16_fused_q4_0_n1_k4096.md"),
 }
 
-ONLY = ("copy", "read", "gemm", "gemm_q81", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
+ONLY = ("read_curve", "copy", "read", "gemm", "gemm_q81", "step", "gemv", "gemv_f32", "q8_0_m1", "q8_0_m8", "q8_0_m32", "q4_k", "q6_k", "moe",
         "w16_m1", "w16_m2048", "q8f_m1", "q8f_m2048", "f16_fused_m1")
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, published
 
@@ -152,6 +153,30 @@ def hbm_entry(bytes_, ms, d, ops=None, name=None):
         e["roofline"]["traffic"], e["roofline"]["traffic_source"] = TRAFFIC[name]
     if ops is not None:
         e["TOPS"] = round(ops / (ms * 1e-3) / 1e12, 3)
+    return e
+
+
+# Ceiling that the per-block scale epilogue puts on int8 MFMA use, as a fraction of the int8 peak:
+# per v_mfma_i32_32x32x32_i8 (32 cycles at peak) each lane applies 16 outputs' block scales with
+# 2 fp32 VALU ops each, at 4 cycles per wave64 op (packed fp32 off): 128 VALU cycles, so MFMA use
+# is capped at 32 / 128 = 25% for the 32-element block types (Q4_0, Q8_0, Q4_K sub-blocks of 32).
+# Q6_K's 16-element sub-blocks take two masked MFMAs and two epilogues per 32 elements: 12.5%.
+EPILOGUE_CEILING = {"q4_K": 0.25, "q6_K": 0.125, "q4_0": 0.25, "q8_0": 0.25}
+
+
+def mfma_entry(bytes_, ms, d, ops, name, ceiling):
+    """A compute-bound config: the roofline is the int8 MFMA peak, with the fraction of the epilogue
+    ceiling beside it; the HBM rate is kept as a secondary figure."""
+    e = hbm_entry(bytes_, ms, d, ops, name)
+    hbm = e.pop("roofline")
+    top = ops / (ms * 1e-3) / 1e12
+    e["roofline"] = {"bound": "mfma", "achieved": round(top, 2), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": round(top / INT8_PEAK_TOPS, 4), "epilogue_ceiling_frac": ceiling,
+                     "frac_of_epilogue_ceiling": round(top / INT8_PEAK_TOPS / ceiling, 4),
+                     "hbm": {"achieved": hbm["achieved"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": hbm["frac"]}}
+    if "traffic" in hbm:
+        e["roofline"]["traffic"], e["roofline"]["traffic_source"] = hbm["traffic"], hbm["traffic_source"]
     return e
 
 
@@ -312,13 +337,14 @@ def other_configs(wl: Workloads, reps: int = 4) -> dict:
     for wt, name, sb in ((wl.ksq.W_Q4_K, "q4_K", 144), (wl.ksq.W_Q6_K, "q6_K", 210)):
         (M, N, K), fn, copies = wl.kquant(wt)
         ms, d = graph_stats(fn, copies, reps)
-        out[f"{name}_M128"] = hbm_entry(N * (K // 256) * sb + M * (K // 32) * 36 + M * N * 4, ms, d, 2.0 * M * N * K,
-                                        f"{name}_M128")
+        out[f"{name}_M128"] = mfma_entry(N * (K // 256) * sb + M * (K // 32) * 36 + M * N * 4, ms, d,
+                                         2.0 * M * N * K, f"{name}_M128", EPILOGUE_CEILING[name])
         del fn
     (T, E, N, K, k), fn, copies = wl.moe()
     ms, d = graph_stats(fn, copies, reps)
     moe_bytes = E * N * (K // 32) * 18 + T * K * 4 + T * E * 4 + T * N * 4
-    out["moe_q4_0_T512_E8_top2"] = hbm_entry(moe_bytes, ms, d, 2.0 * T * k * N * K, "moe_q4_0_T512_E8_top2")
+    out["moe_q4_0_T512_E8_top2"] = mfma_entry(moe_bytes, ms, d, 2.0 * T * k * N * K, "moe_q4_0_T512_E8_top2",
+                                              EPILOGUE_CEILING["q4_0"])
     del fn
     wl.torch.cuda.empty_cache()
     return out
@@ -364,6 +390,84 @@ def extra_paths(wl: Workloads, reps: int = 4) -> dict:
     del fn
     wl.torch.cuda.empty_cache()
     return out
+
+
+# ---------------------------------------------------------------- HBM read-size curve
+CURVE_BASE = 9437184                          # the config-0 weight matrix, bytes
+CURVE_SIZES = [CURVE_BASE >> 2, CURVE_BASE >> 1] + [CURVE_BASE << j for j in range(7)]   # 2.4 MB .. 604 MB
+CURVE_POOL = CURVE_BASE << 7                  # 1.21 GB of rotating buffers (> 4x the 256 MB MALL)
+
+
+def _wg_candidates(nbytes: int) -> list[int]:
+    """Per-workgroup byte counts (multiples of 4096) giving grids of about 256 j workgroups (one
+    to 64 per CU) for a read of nbytes."""
+    out = []
+    for j in (1, 2, 3, 4, 6, 8, 16, 32, 64):
+        wg = max(4096, -(-(-(-nbytes // (256 * j))) // 4096) * 4096)
+        if wg not in out:
+            out.append(wg)
+    return out
+
+
+def fit_line(x, y) -> tuple[float, float]:
+    """(intercept, slope) of y = a + b x by least squares on relative residuals (weights 1 / y), so
+    the small reads, whose times are mostly the fixed cost, count as much as the large ones."""
+    x, y = np.asarray(x, dtype=np.float64), np.asarray(y, dtype=np.float64)
+    b, a = np.polyfit(x, y, 1, w=1.0 / y)
+    return float(a), float(b)
+
+
+def read_curve(reps: int = 4) -> dict:
+    """Time a plain streaming read (ksq_debug_stream_read_wg, the best of several launch shapes per
+    size) and torch's dst.copy_(src) at 2.4 MB .. 604 MB, each over rotating slices of a 1.21 GB
+    pool, and fit t = t0 + bytes / BW to each.  BW is the sustained on-box rate, t0 the fixed cost
+    of one launch's ramp; t(9.47 MB) is what a bandwidth-bound GEMV of config 0's size can reach."""
+    import torch
+
+    from ksq import ops
+    dev = torch.device("cuda:0")
+    pool = torch.ones(CURVE_POOL, dtype=torch.uint8, device=dev)
+    dst = torch.empty(CURVE_POOL, dtype=torch.uint8, device=dev)
+    pts, cpts = [], []
+    for nb in CURVE_SIZES:
+        copies = int(min(256, max(2, CURVE_POOL // nb)))
+        bufs = [pool[i * nb:(i + 1) * nb] for i in range(copies)]
+        best = None
+        for wg in _wg_candidates(nb):
+            r = ops.stream_read(bufs[0], wg_bytes=wg)
+
+            def rd(i, wg=wg, r=r):
+                ops.stream_read(bufs[i % copies], out=r, wg_bytes=wg)
+            ms, d = graph_stats(rd, copies, reps)
+            if best is None or ms < best[0]:
+                best = (ms, d, wg)
+        ms, d, wg = best
+        pts.append({"bytes": nb, "ms": round(ms, 6), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1), "wg_bytes": wg,
+                    "workgroups": -(-nb // wg), "median_ms": d["median_ms"], "copies": copies})
+        dsts = [dst[i * nb:(i + 1) * nb] for i in range(copies)]
+        ms, d = graph_stats(lambda i: dsts[i % copies].copy_(bufs[i % copies]), copies, reps)
+        cpts.append({"bytes_read": nb, "ms": round(ms, 6), "GB/s_read_plus_write": round(2 * nb / (ms * 1e-3) / 1e9, 1),
+                     "median_ms": d["median_ms"]})
+        log(f"bench: read curve {nb / 1e6:.1f} MB: read {pts[-1]['ms'] * 1e3:.2f} us ({pts[-1]['GB/s']} GB/s), "
+            f"copy {cpts[-1]['ms'] * 1e3:.2f} us")
+    del pool, dst
+    torch.cuda.empty_cache()
+    t0, inv_bw = fit_line([p["bytes"] for p in pts], [p["ms"] * 1e-3 for p in pts])
+    ct0, cinv = fit_line([2 * p["bytes_read"] for p in cpts], [p["ms"] * 1e-3 for p in cpts])
+    for p in pts:
+        p["fit_ms"] = round((t0 + inv_bw * p["bytes"]) * 1e3, 6)
+    return {"read": pts, "copy": cpts,
+            "read_fit": {"t0_us": round(t0 * 1e6, 3), "sustained_GBps": round(1 / inv_bw / 1e9, 1),
+                         "sustained_frac_of_peak": round(1 / inv_bw / 1e9 / HBM_PEAK_GBS, 4)},
+            "copy_fit": {"t0_us": round(ct0 * 1e6, 3), "sustained_GBps_read_plus_write": round(1 / cinv / 1e9, 1)},
+            "how": "ksq_debug_stream_read_wg (16-byte loads, best of ~9 launch shapes per size) and torch "
+                   "dst.copy_(src), HIP-graph replays over rotating slices of a 1.21 GB pool; "
+                   "t = t0 + bytes / BW fitted over all sizes by least squares on relative residuals"}
+
+
+def fitted_read_ms(curve: dict, nbytes: int) -> float:
+    f = curve["read_fit"]
+    return f["t0_us"] * 1e-3 + nbytes / (f["sustained_GBps"] * 1e9) * 1e3
 
 
 # ---------------------------------------------------------------- CPU baselines
@@ -452,6 +556,9 @@ def cpu_baselines(budget_s: float = 1.2) -> dict:
 def only(args, dev) -> int:
     """Launch just one kernel sequence --warmup + --steps times, eagerly (for rocprofv3)."""
     import torch
+    if args.only == "read_curve":
+        print(json.dumps(read_curve()), flush=True)
+        return 0
     wl = Workloads(dev)
     if args.only == "copy":
         # calibration for the FETCH_SIZE / WRITE_SIZE counters: a plain copy of 256 MiB
@@ -513,6 +620,10 @@ def main() -> int:
     log("bench: W4A16, deepseek_v2 block_q8f, fused FP16")
     extra = extra_paths(wl)
 
+    # ---- HBM read-size curve: the on-box sustained read rate and a launch's fixed cost
+    log("bench: HBM read-size curve")
+    curve = read_curve()
+
     # ---- decode GEMV, config 0 shape, and the one-shot read of the same number of bytes
     log("bench: config 0 GEMV")
     (Mv, Nv, Kv), gemv_q81, gemv_f32, gcopies = wl.gemv()
@@ -527,6 +638,7 @@ def main() -> int:
     gemv_bytes = Nv * (Kv // 32) * 18 + Mv * (Kv // 32) * 36 + Mv * Nv * 4
     gemv_gbs = gemv_bytes / (gemv_ms * 1e-3) / 1e9
     f32_bytes = Nv * (Kv // 32) * 18 + Mv * Kv * 4 + Mv * Nv * 4
+    f32_gbs = f32_bytes / (gemv_f32_ms * 1e-3) / 1e9
     read_gbs = 9437184 / (read_ms * 1e-3) / 1e9
 
     # ---- headline: config 2 steps
@@ -586,8 +698,10 @@ def main() -> int:
                    "host_wall_ms_per_step": round(wall, 5),
                    "step_distribution": step_d},
         "roofline": {"bound": "mfma", "kernel": "mmq_planar_kernel<0> (Q4_0 x planar Q8_1, v_mfma_i32_32x32x32_i8)",
-                     "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": TRAFFIC["gemm"][0],
+                     "achieved": round(gemm_tops, 3), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+                     "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "epilogue_ceiling_frac": EPILOGUE_CEILING["q4_0"],
+                     "frac_of_epilogue_ceiling": round(gemm_tops / INT8_PEAK_TOPS / EPILOGUE_CEILING["q4_0"], 4),
+                     "traffic": TRAFFIC["gemm"][0],
                      "traffic_source": TRAFFIC["gemm"][1],
                      "traffic_unit": "bytes per launch (algorithmic: %d; planar activations 42 bytes per "
                                      "block)" % (N * (K // 32) * 18 + M * (K // 32) * 42 + M * N * 4),
@@ -596,18 +710,26 @@ def main() -> int:
                      "q8_1_input_kernel": {"kernel": "mmq_kernel<TileL, Q4_0> (ksq_gemm_q4_0_q8_1)",
                                            "avg_kernel_ms": round(q81_ms, 5),
                                            "TOPS": round(ops_per_step / (q81_ms * 1e-3) / 1e12, 3), **q81_d}},
-        "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(gemv_gbs, 1), "unit": "GB/s",
-                    "entry": "ksq_gemm_q4_0_q8_1 (Q8_1 activations)", "avg_ms": round(gemv_ms, 6), **gemv_d,
-                    "algorithmic_bytes": gemv_bytes,
-                    "roofline": {"bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": HBM_PEAK_GBS,
-                                 "unit": "GB/s", "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
-                                 "traffic": TRAFFIC["gemv"][0], "traffic_source": TRAFFIC["gemv"][1]},
-                    "fp32_entry_ms": round(gemv_f32_ms, 6), "fp32_entry_distribution": gemv_f32_d,
-                    "fp32_entry_gbs": round(f32_bytes / (gemv_f32_ms * 1e-3) / 1e9, 1),
+        "gemv_m1": {"metric": "GEMV HBM GB/s at M=1 (N=K=4096)", "value": round(f32_gbs, 1), "unit": "GB/s",
+                    "entry": "gemm_w4a32c8_q4_0_fp32_int8 (config 0 as defined: fp32 activations, quantised to "
+                             "Q8_1 inside the decode kernel's workgroups)",
+                    "avg_ms": round(gemv_f32_ms, 6), **gemv_f32_d, "algorithmic_bytes": f32_bytes,
+                    "roofline": {"bound": "hbm", "achieved": round(f32_gbs, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(f32_gbs / HBM_PEAK_GBS, 4),
+                                 "traffic": TRAFFIC["gemv_f32"][0], "traffic_source": TRAFFIC["gemv_f32"][1],
+                                 "fitted_read_ms": round(fitted_read_ms(curve, f32_bytes), 6),
+                                 "frac_of_fitted_read": round(fitted_read_ms(curve, f32_bytes) / gemv_f32_ms, 4),
+                                 "sustained_read_GBps": curve["read_fit"]["sustained_GBps"],
+                                 "read_t0_us": curve["read_fit"]["t0_us"]},
+                    "q8_1_entry": {"entry": "ksq_gemm_q4_0_q8_1 (pre-quantised Q8_1 activations)",
+                                   "avg_ms": round(gemv_ms, 6), **gemv_d, "algorithmic_bytes": gemv_bytes,
+                                   "GB/s": round(gemv_gbs, 1), "frac": round(gemv_gbs / HBM_PEAK_GBS, 4),
+                                   "traffic": TRAFFIC["gemv"][0], "traffic_source": TRAFFIC["gemv"][1],
+                                   "frac_of_fitted_read": round(fitted_read_ms(curve, gemv_bytes) / gemv_ms, 4)},
                     "one_shot_read_9437184B": {"ms": round(read_ms, 6), **read_d, "GB/s": round(read_gbs, 1),
                                                "how": "ksq_debug_stream_read of 9,437,184 bytes, 64 rotating copies"},
-                    "frac_of_one_shot_read": round(read_ms / gemv_ms, 4),
                     "weight_copies": gcopies},
+        "hbm_read_curve": curve,
         "configs": configs,
         "extra_paths": extra,
     }

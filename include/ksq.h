@@ -241,6 +241,11 @@ KSQ_API int ksq_gemm_noalloc(int wtype, int atype, const void* weight, const voi
  * a given byte count, the ceiling a bandwidth-bound kernel of that size is measured against. */
 KSQ_API size_t ksq_debug_stream_read_outputs(size_t bytes);
 KSQ_API int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream);
+/* The same read with wg_bytes (a positive multiple of 4096, at most 1 GiB) per workgroup instead
+ * of 32 KiB, so a read-size curve can pick the launch shape that covers the CUs evenly; writes
+ * ksq_debug_stream_read_wg_outputs(bytes, wg_bytes) XOR words (0 for an invalid wg_bytes). */
+KSQ_API size_t ksq_debug_stream_read_wg_outputs(size_t bytes, size_t wg_bytes);
+KSQ_API int ksq_debug_stream_read_wg(const void* p, size_t bytes, size_t wg_bytes, uint32_t* out, void* stream);
 
 /* Debug / measurement: the two launches of an fp32 ksq_gemm call that takes the LDS-DMA GEMM
  * (Q4_0 / Q4_1 weights, K % 256 == 0, the 128 x 128-tile shapes), run separately so that the

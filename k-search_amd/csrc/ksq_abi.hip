@@ -567,15 +567,27 @@ int ksq_debug_gemm_planar(int wtype, const void* weight, const void* planar, flo
     return e == hipSuccess ? ok() : hip_error(e, "mmq launch");
 }
 
-size_t ksq_debug_stream_read_outputs(size_t bytes) { return ksq::stream_read_outputs(bytes); }
+size_t ksq_debug_stream_read_outputs(size_t bytes) { return ksq::stream_read_outputs(bytes, 32768); }
 
-int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream) {
+size_t ksq_debug_stream_read_wg_outputs(size_t bytes, size_t wg_bytes) {
+    return (wg_bytes == 0 || wg_bytes % 4096) ? 0 : ksq::stream_read_outputs(bytes, wg_bytes);
+}
+
+int ksq_debug_stream_read_wg(const void* p, size_t bytes, size_t wg_bytes, uint32_t* out, void* stream) {
+    if (wg_bytes == 0 || wg_bytes % 4096 || wg_bytes > ((size_t)1 << 30))
+        return set_error(KSQ_ERR_SHAPE, "wg_bytes must be a positive multiple of 4096, at most 1 GiB");
     if (bytes == 0) return ok();
     if (!p || !out) return set_error(KSQ_ERR_NULL, "p or out is NULL");
     if (((uintptr_t)p & 15u) || (bytes & 15u) || ((uintptr_t)out & 3u))
         return set_error(KSQ_ERR_ALIGN, "p must be 16-byte aligned, bytes a multiple of 16, out 4-byte aligned");
-    hipError_t e = ksq::launch_stream_read(p, bytes, out, (hipStream_t)stream);
+    if (ksq::stream_read_outputs(bytes, wg_bytes) > 0x7FFFFFFFu)
+        return set_error(KSQ_ERR_SHAPE, "too many workgroups for this wg_bytes");
+    hipError_t e = ksq::launch_stream_read(p, bytes, wg_bytes, out, (hipStream_t)stream);
     return e == hipSuccess ? ok() : hip_error(e, "stream read launch");
+}
+
+int ksq_debug_stream_read(const void* p, size_t bytes, uint32_t* out, void* stream) {
+    return ksq_debug_stream_read_wg(p, bytes, 32768, out, stream);
 }
 
 int ksq_debug_block_sumi(int wtype, const void* weight, const uint8_t* act_q8_1, int32_t* out, int M, int N,

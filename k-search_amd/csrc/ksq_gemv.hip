@@ -1530,22 +1530,26 @@ __global__ void block_sumi_kernel(int wtype, const uint8_t* __restrict__ W, cons
 }
 
 // Calibration: a plain streaming read of `bytes` (16-byte aligned, a multiple of 16) with the
-// decode kernels' load width, 32 KiB per workgroup, each workgroup XOR-folding what it read into
-// one word of out (so the loads cannot be elided).
+// decode kernels' load width.  Workgroup g reads the per16 16-byte words from g * per16 (per16 a
+// multiple of 256) in rounds of 8 loads per thread, XOR-folding what it read into one word of
+// out (so the loads cannot be elided).
 constexpr int kReadBytesPerWG = 32768;
 
-__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16,
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restrict__ p, int64_t n16, int64_t per16,
                                                           uint32_t* __restrict__ out) {
-    const int64_t base = (int64_t)blockIdx.x * (kReadBytesPerWG / 16);
-    u32x4 v[kReadBytesPerWG / 16 / 256];
-#pragma unroll
-    for (int i = 0; i < kReadBytesPerWG / 16 / 256; i++) {
-        const int64_t k = base + i * 256 + threadIdx.x;
-        v[i] = k < n16 ? p[k] : u32x4{0, 0, 0, 0};
-    }
+    const int64_t beg = (int64_t)blockIdx.x * per16;
+    const int64_t end = beg + per16 < n16 ? beg + per16 : n16;
     uint32_t x = 0;
+    for (int64_t k0 = beg; k0 < end; k0 += 8 * 256) {
+        u32x4 v[8];
 #pragma unroll
-    for (int i = 0; i < kReadBytesPerWG / 16 / 256; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+        for (int i = 0; i < 8; i++) {
+            const int64_t k = k0 + i * 256 + threadIdx.x;
+            v[i] = k < end ? p[k] : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) x ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
     for (int o = 32; o > 0; o >>= 1) x ^= __shfl_xor(x, o);
     __shared__ uint32_t red[4];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = x;
@@ -1553,13 +1557,14 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
     if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
 }
 
-size_t stream_read_outputs(size_t bytes) { return (bytes + kReadBytesPerWG - 1) / kReadBytesPerWG; }
+size_t stream_read_outputs(size_t bytes, size_t wg_bytes) { return (bytes + wg_bytes - 1) / wg_bytes; }
 
-hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s) {
+hipError_t launch_stream_read(const void* p, size_t bytes, size_t wg_bytes, uint32_t* out, hipStream_t s) {
     const int64_t n16 = (int64_t)(bytes / 16);
-    const size_t grid = stream_read_outputs(bytes);
+    const size_t grid = stream_read_outputs(bytes, wg_bytes);
     if (grid == 0) return hipSuccess;
-    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4*)p, n16, out);
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)grid), dim3(256), 0, s, (const u32x4*)p, n16,
+                       (int64_t)(wg_bytes / 16), out);
     return hipGetLastError();
 }
 

@@ -153,10 +153,10 @@ hipError_t launch_moe_combine(const float* scratch, const int32_t* ids, float* o
 hipError_t launch_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N,
                              int K, hipStream_t s);
 
-// Calibration read of `bytes` bytes at p (16-byte aligned, bytes % 16 == 0); writes
-// stream_read_outputs(bytes) words to out.
-size_t stream_read_outputs(size_t bytes);
-hipError_t launch_stream_read(const void* p, size_t bytes, uint32_t* out, hipStream_t s);
+// Calibration read of `bytes` bytes at p (16-byte aligned, bytes % 16 == 0), wg_bytes (a multiple
+// of 4096) per workgroup; writes stream_read_outputs(bytes, wg_bytes) words to out.
+size_t stream_read_outputs(size_t bytes, size_t wg_bytes);
+hipError_t launch_stream_read(const void* p, size_t bytes, size_t wg_bytes, uint32_t* out, hipStream_t s);
 
 // Dequantise-then-fp32 GEMM (W4A16 / W8A16) on the bf16 MFMA: C[M][N] = A . dequant(W)^T,
 // wtype kWQ40 or kWQ80, K % 64 == 0.  With w16_splits(M, N, K) > 1 it needs `partials`, that

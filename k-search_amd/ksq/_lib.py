@@ -70,6 +70,8 @@ SIGNATURES = {
     "ksq_debug_gemm_planar": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_stream_read_outputs": ([_SZ], _SZ),
     "ksq_debug_stream_read": ([_P, _SZ, _P, _P], _I),
+    "ksq_debug_stream_read_wg_outputs": ([_SZ, _SZ], _SZ),
+    "ksq_debug_stream_read_wg": ([_P, _SZ, _SZ, _P, _P], _I),
     "ksq_debug_block_sumi": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_debug_block_sumi_mfma": ([_I, _P, _P, _P, _I, _I, _I, _P], _I),
     "ksq_set_path": ([_I], _I),

@@ -202,12 +202,20 @@ def gemm_planar(wtype: int, weight: torch.Tensor, planar: torch.Tensor, M: int, 
     return out
 
 
-def stream_read(buf: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Calibration read of every byte of buf (ksq_debug_stream_read); returns the XOR words."""
+def stream_read(buf: torch.Tensor, out: torch.Tensor | None = None, wg_bytes: int | None = None) -> torch.Tensor:
+    """Calibration read of every byte of buf (ksq_debug_stream_read, or ksq_debug_stream_read_wg
+    with wg_bytes per workgroup); returns the XOR words, one per workgroup."""
     nbytes = buf.numel() * buf.element_size()
+    if wg_bytes is None:
+        if out is None:
+            out = torch.empty(max(1, lib().ksq_debug_stream_read_outputs(nbytes)), dtype=torch.int32,
+                              device=buf.device)
+        check(lib().ksq_debug_stream_read(_ptr(buf), nbytes, _ptr(out), _stream()))
+        return out
     if out is None:
-        out = torch.empty(max(1, lib().ksq_debug_stream_read_outputs(nbytes)), dtype=torch.int32, device=buf.device)
-    check(lib().ksq_debug_stream_read(_ptr(buf), nbytes, _ptr(out), _stream()))
+        out = torch.empty(max(1, lib().ksq_debug_stream_read_wg_outputs(nbytes, wg_bytes)), dtype=torch.int32,
+                          device=buf.device)
+    check(lib().ksq_debug_stream_read_wg(_ptr(buf), nbytes, wg_bytes, _ptr(out), _stream()))
     return out
 
 

@@ -132,6 +132,35 @@ def quantize_q8s(x: np.ndarray) -> np.ndarray:
     return out
 
 
+def quantize_q8f(x: np.ndarray, rule: int = 0) -> np.ndarray:
+    """fp32 [M, K] -> block_q8f bytes [M, K/32, 40] (fp32 d, fp32 s, 32 int8).
+    rule 0, the deepseek_v2 W4A32C8 operator (core/operators/quant_gemm/variants/deepseek_v2/
+    w4a32c8_q4_0_fp32_int8/reference.py:50-73): d = amax / 127 in fp32 (1.0 when amax is 0),
+    s = the left-to-right fp32 sum, q = round half to even of the fp32 quotient x / d, clamped.
+    rule 1, the lm_head kernel (best_kernels_GLM-5/quant_gemm/..._lm_head_n128256_k4096/
+    kernel.cu:85-107): d = amax / 127 (1.0 when amax <= 1e-10), q = lroundf(x * (127 / amax)),
+    half away from zero, wrapped to int8."""
+    x = np.asarray(x, dtype=np.float32)
+    M, K = x.shape
+    xb = x.reshape(M, K // 32, 32)
+    amax = np.abs(xb).max(axis=-1)
+    ssum = np.cumsum(xb, axis=-1, dtype=np.float32)[..., -1]
+    if rule == 0:
+        d = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+        v = (xb / d[..., None]).astype(np.float32)
+        q = np.clip(np.rint(v), -128, 127).astype(np.int8)
+    else:
+        d = np.where(amax > np.float32(1e-10), amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+        sc = (np.float32(127.0) / np.maximum(amax, np.float32(1e-10))).astype(np.float32)
+        v = (xb * sc[..., None]).astype(np.float32).astype(np.float64)
+        q = (np.sign(v) * np.floor(np.abs(v) + 0.5)).astype(np.int64).astype(np.uint8).view(np.int8)
+    out = np.empty((M, K // 32, 40), dtype=np.uint8)
+    out[..., 0:4] = d[..., None].view(np.uint8)
+    out[..., 4:8] = ssum.astype(np.float32)[..., None].view(np.uint8)
+    out[..., 8:] = q.view(np.uint8)
+    return out
+
+
 def gemm_q8s_f64(a: np.ndarray, w: np.ndarray) -> np.ndarray:
     """Q8_0 weights x block_q8s activations: sum_b d_w d_a S in fp64."""
     dw, _, _ = unpack(1, w)

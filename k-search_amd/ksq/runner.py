@@ -21,6 +21,8 @@ and write test_results.json.  This module does the same for libksq:
                (data/ggml_baseline_quant_gemm.json), for one chosen hardware
 
     python -m ksq.runner --definition path/to/def.json [--attempt-path DIR]
+    python -m ksq.runner --definition path/to/variants/<model>/<variant> [--attempt-path DIR]
+    python -m ksq.runner --operators path/to/core/operators [--attempt-path DIR]
     python -m ksq.runner --sweep [--filter TEXT] [--all-configs] [--out results.json]
 
 --all-configs uses the definition's own test_configs (M = 1, 2, 3, 4, 5, 8, 512) instead
@@ -52,19 +54,74 @@ WEIGHT_ENTRIES = {
     "q5_0": (_lib.W_Q5_0, "gemm_w5a32c8_q5_0_fp32_int8"),
     "q5_1": (_lib.W_Q5_1, "gemm_w5a32c8_q5_1_fp32_int8"),
 }
+# activation types of the fp32-input entries, and the device / numpy quantiser of each
+FP32_ACTIVATIONS = (_lib.A_F32, _lib.A_F32_Q8S, _lib.A_F32_Q8F_RNE, _lib.A_F32_Q8F_LROUND)
 BLOCK_BYTES = {_lib.W_Q4_0: 18, _lib.W_Q8_0: 34, _lib.W_Q4_1: 20, _lib.W_Q5_0: 22, _lib.W_Q5_1: 24}
 HANDLER_CONFIGS = ((1, "single_token"), (8, "small_batch"), (512, "large_batch"))
 
 
 # ---------------------------------------------------------------- spec handling
 def load_spec(path: str) -> dict:
-    """A definition JSON (or an operator spec.json) as the runner's spec dict."""
+    """A definition JSON, an operator spec.json, or an operator variant directory (its spec.json
+    plus impl.json) as the runner's spec dict.  For spec.json files the variant directory and
+    its impl.json are recorded too (core/operators/registry.py:97-136 reads a variant's spec.json
+    from its directory; impl.json carries the kernel's file and entry point)."""
+    vdir = None
+    if os.path.isdir(path):
+        vdir, path = path, os.path.join(path, "spec.json")
     with open(path) as f:
         spec = json.load(f)
+    if vdir is None and os.path.basename(path) == "spec.json":
+        vdir = os.path.dirname(os.path.abspath(path))
+    if vdir is not None:
+        spec["_variant_dir"] = os.path.abspath(vdir)
+        ipath = os.path.join(vdir, "impl.json")
+        if os.path.exists(ipath):
+            with open(ipath) as f:
+                impl = json.load(f)
+            spec["_impl"] = impl
+            if "kernel" not in spec and isinstance(impl.get("kernel"), dict):
+                spec["kernel"] = impl["kernel"]
     if "params" not in spec and "axes" in spec:   # unified_test_runner.py:111-126
         spec["params"] = {k: ({"value": v.get("value")} if v.get("type") == "const" else {"default": 1})
                           for k, v in spec["axes"].items() if isinstance(v, dict)}
     return spec
+
+
+def discover(operators_dir: str, family: str = "quant_gemm") -> list[dict]:
+    """Every variant of an operator family, as the reference's OperatorRegistry finds them
+    (core/operators/registry.py:71-136: <family>/manifest.json, then variants/<variant>/spec.json),
+    also one level further down (variants/<model>/<variant>/spec.json, where the reference keeps
+    its deepseek_v2 and deepseek_v3 operators).  Each entry is a loaded spec (load_spec) with its
+    variant path relative to variants/ in "_variant"."""
+    fdir = os.path.join(operators_dir, family)
+    if not os.path.exists(os.path.join(fdir, "manifest.json")):
+        raise FileNotFoundError(f"{fdir}: no manifest.json (not an operator family directory)")
+    vroot = os.path.join(fdir, "variants")
+    found = []
+    for root, dirs, files in os.walk(vroot):
+        dirs.sort()
+        if "spec.json" in files:
+            spec = load_spec(root)
+            spec["_variant"] = os.path.relpath(root, vroot)
+            found.append(spec)
+    return found
+
+
+def _arch_tags(spec: dict) -> list[str]:
+    """Model-architecture qualifiers of a spec: its model_architectures ("deepseek-v2" ->
+    "deepseek_v2") and the model directory its variant sits under (variants/deepseek_v2/...)."""
+    tags = [a.lower().replace("-", "_").replace(".", "_") for a in spec.get("model_architectures") or []]
+    rel = spec.get("_variant")
+    if rel is None and spec.get("_variant_dir"):
+        parts = os.path.normpath(spec["_variant_dir"]).split(os.sep)
+        if "variants" in parts:
+            rel = os.sep.join(parts[parts.index("variants") + 1:])
+    if rel:
+        parts = os.path.normpath(rel).split(os.sep)
+        if len(parts) > 1:
+            tags.append(parts[0].lower().replace("-", "_"))
+    return list(dict.fromkeys(tags))
 
 
 def spec_from_table(d: dict) -> dict:
@@ -90,15 +147,35 @@ def _dim(spec: dict, cfg: dict, name: str, default: int) -> int:
     return int(p.get("value", p.get("default", default))) if isinstance(p, dict) else default
 
 
+def entry_candidates(spec: dict) -> list[str]:
+    """libksq symbols that may implement a spec, in the order they are tried.  First the
+    variant-qualified names gemm_{name}_{arch} for the spec's model architectures (a variant
+    whose arithmetic differs from the generic operator of the same name, such as the deepseek_v2
+    W4A32C8 operator with its fp32 activation scales, is exported under that name); then the
+    reference's own order (core/run_tests.py:218-234): kernel.entry_point, gemm_{name}, name."""
+    name = spec.get("name", "")
+    entry = (spec.get("kernel") or {}).get("entry_point") or name
+    out = []
+    for tag in _arch_tags(spec):
+        out += [f"gemm_{name}_{tag}", f"{entry}_{tag}"]
+    out += [entry, f"gemm_{name}", name]
+    return list(dict.fromkeys(c for c in out if c))
+
+
 def resolve(spec: dict) -> tuple[int, int, str]:
-    """(weight type, activation type, entry point) for a spec."""
+    """(weight type, activation type, entry point) for a spec: the first entry_candidates() name
+    that libksq implements, else (definition JSONs, whose names are shapes) the entry of the
+    weight dtype."""
     wd = spec["inputs"]["weight"]["dtype"].replace("block_", "")
     ad = spec["inputs"]["activation"]["dtype"]
     if ad not in ("float32", "fp32"):
         raise ValueError(f"activation dtype {ad!r}: only fp32-activation definitions are defined for quant_gemm")
-    entry = (spec.get("kernel") or {}).get("entry_point")
-    if entry == "gemm_w8a8c8_q8_0_q8_1" or spec.get("name") == "w8a8c8_q8_0_q8_1":
-        return _lib.W_Q8_0, _lib.A_F32_Q8S, "gemm_w8a8c8_q8_0_q8_1"
+    for c in entry_candidates(spec):
+        if c in ops.ENTRY_POINTS and ops.ENTRY_POINTS[c][1] in FP32_ACTIVATIONS:
+            wt, at = ops.ENTRY_POINTS[c]
+            if WEIGHT_ENTRIES.get(wd, (wt,))[0] != wt:
+                raise ValueError(f"entry {c} takes weight type {wt}, the spec's weight is {wd!r}")
+            return wt, at, c
     if wd not in WEIGHT_ENTRIES:
         raise ValueError(f"weight dtype {wd!r} has no libksq entry")
     wt, e = WEIGHT_ENTRIES[wd]
@@ -206,6 +283,17 @@ def ggml_baseline(wtype: int, N: int, M: int, K: int, hardware: str):
     return (_BASELINE.get(key) or {}).get(hardware)
 
 
+def _quantisers(atype: int):
+    """(device quantiser, numpy quantiser) of the activation blocks an fp32 entry of type atype
+    forms: block_q8_1, block_q8s (the native W8A8C8 operator) or block_q8f (deepseek_v2 / lm_head)."""
+    if atype == _lib.A_F32_Q8S:
+        return ops.quantize_q8s, refcheck.quantize_q8s
+    if atype in (_lib.A_F32_Q8F_RNE, _lib.A_F32_Q8F_LROUND):
+        rule = _lib.Q8F_RNE if atype == _lib.A_F32_Q8F_RNE else _lib.Q8F_LROUND
+        return (lambda x: ops.quantize_q8f(x, rule)), (lambda x: refcheck.quantize_q8f(x, rule))
+    return ops.quantize_q8_1, refcheck.quantize_q8_1
+
+
 # ---------------------------------------------------------------- one definition
 class DefinitionRunner:
     def __init__(self, warmup: int = 10, iterations: int = 100, baseline_hardware: str = "RTX4090",
@@ -218,13 +306,18 @@ class DefinitionRunner:
     def run(self, spec: dict, attempt_dir: str | None = None) -> dict:
         name = spec.get("name", "definition")
         res = {"attempt_id": name, "variant": "libksq", "op_type": "quant_gemm",
-               "tested_at": datetime.now().isoformat(), "spec": spec,
+               "tested_at": datetime.now().isoformat(),
+               "spec": {k: v for k, v in spec.items() if not k.startswith("_")},
                "compilation": {}, "correctness": {}, "performance": {}}
         try:
             wtype, atype, entry = resolve(spec)
             getattr(_lib.lib(), entry)
             res["compilation"] = {"success": True, "errors": [], "warnings": [], "diagnostics": [],
-                                  "library": _lib.LIB_PATH, "entry_point": entry}
+                                  "library": _lib.LIB_PATH, "entry_point": entry,
+                                  "candidates": entry_candidates(spec), "weight_type": wtype,
+                                  "activation_type": atype}
+            if spec.get("_variant_dir"):
+                res["variant_dir"] = spec["_variant_dir"]
         except Exception as e:  # noqa: BLE001 - reported in the results like a compile error
             res["compilation"] = {"success": False, "errors": [str(e)], "warnings": [], "diagnostics": []}
             return self._save(res, attempt_dir)
@@ -283,13 +376,18 @@ class DefinitionRunner:
         rows = sorted({0, M - 1, *torch.randint(0, M, (2,), generator=g, device=self.dev).tolist()})
         cols = sorted(set(torch.randint(0, N, (64,), generator=g, device=self.dev).tolist()) | {0, N - 1})
         xr = x[rows].contiguous()
-        q8s = atype == _lib.A_F32_Q8S
-        a_dev = (ops.quantize_q8s if q8s else ops.quantize_q8_1)(xr)
+        dev_q, np_q = _quantisers(atype)
+        a_dev = dev_q(xr)
         torch.cuda.synchronize()
         x_np, w_np = xr.cpu().numpy(), w[cols].contiguous().cpu().numpy()
-        a_ref = (refcheck.quantize_q8s if q8s else refcheck.quantize_q8_1)(x_np)
+        a_ref = np_q(x_np)
         q_ok = bool(np.array_equal(a_dev.cpu().numpy(), a_ref))
-        ref64 = refcheck.gemm_q8s_f64(a_ref, w_np) if q8s else refcheck.gemm_f64(wtype, a_ref, w_np)
+        if atype == _lib.A_F32_Q8S:
+            ref64 = refcheck.gemm_q8s_f64(a_ref, w_np)
+        elif atype in (_lib.A_F32_Q8F_RNE, _lib.A_F32_Q8F_LROUND):
+            ref64, _ = refcheck.exact_gemm(wtype, a_ref, w_np)   # block_q8f: fp32 d_a and s_a
+        else:
+            ref64 = refcheck.gemm_f64(wtype, a_ref, w_np)
         err = refcheck.max_rel_err(y[rows][:, cols].cpu().numpy(), ref64)
         s_ok, engines = self._unit_scale(wtype, atype, M, N, K, cols)
         return {"passed": q_ok and s_ok and err <= 1e-3, "quantize_bit_exact": q_ok, "block_dots_bit_exact": s_ok,
@@ -303,7 +401,7 @@ class DefinitionRunner:
         q8s = atype == _lib.A_F32_Q8S
         yu = ops.gemm(wtype, atype, torch.from_numpy(wu).to(self.dev), torch.from_numpy(xu).to(self.dev), M, N, K)
         engines = sorted(ops.last_engines())
-        au = (refcheck.quantize_q8s if q8s else refcheck.quantize_q8_1)(xu)
+        au = _quantisers(atype)[1](xu)
         ref, bound = refcheck.exact_gemm(wtype, au, wu[cols], q8s=q8s)
         ok = bool(bound.max() < 2.0 ** 24 and np.array_equal(yu[:, cols].cpu().numpy(), ref.astype(np.float32)))
         del wu, yu
@@ -411,7 +509,9 @@ def sweep(filter_text: str | None, runner: DefinitionRunner, out: str | None) ->
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--definition", help="definition JSON (or operator spec.json)")
+    ap.add_argument("--definition", help="definition JSON, operator spec.json or operator variant directory")
+    ap.add_argument("--operators", help="operators directory (core/operators): run every discovered variant of "
+                                        "its quant_gemm family, each in <attempt-path>/<variant>/")
     ap.add_argument("--attempt-path", help="directory for test_results.json")
     ap.add_argument("--sweep", action="store_true", help="run every definition of the built-in table")
     ap.add_argument("--filter", help="sweep only definitions whose name contains this text")
@@ -431,8 +531,18 @@ def main(argv=None) -> int:
         r = sweep(args.filter, runner, args.out)
         print(json.dumps({k: v for k, v in r.items() if k != "results"}), flush=True)
         return 0 if not r["failed"] else 1
+    if args.operators:
+        ok = True
+        for v in discover(args.operators):
+            out = os.path.join(args.attempt_path, v["_variant"]) if args.attempt_path else None
+            r = runner.run(v, out)
+            ok &= bool(r["correctness"].get("passed"))
+            print(json.dumps({"variant": v["_variant"], "entry_point": r["compilation"].get("entry_point"),
+                              "correctness": r["correctness"].get("passed"),
+                              "benchmarks": r["performance"].get("benchmarks")}), flush=True)
+        return 0 if ok else 1
     if not args.definition:
-        ap.error("--definition or --sweep is required")
+        ap.error("--definition, --operators or --sweep is required")
     r = runner.run(load_spec(args.definition), args.attempt_path)
     print(json.dumps({"compilation": r["compilation"].get("success"), "correctness": r["correctness"].get("passed"),
                       "benchmarks": r["performance"].get("benchmarks")}), flush=True)

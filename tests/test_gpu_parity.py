@@ -911,3 +911,12 @@ def test_stream_read_calibration(dev):
         words = np.pad(a, (0, (-nbytes) % 32768)).view(np.uint32).reshape(-1, 8192)
         want = np.bitwise_xor.reduce(words, axis=1)
         assert np.array_equal(got.cpu().numpy().view(np.uint32), want), nbytes
+    # the per-workgroup size of the read-size curve: 4 KiB (one load per thread) to 256 KiB (rounds of
+    # 8 loads per thread), ragged last workgroup included
+    for nbytes, wg in ((9437184, 4096), (9437184, 36864), (100000 - 100000 % 16, 65536), (1 << 22, 262144)):
+        a = g.integers(0, 256, nbytes, dtype=np.uint8)
+        got = ops.stream_read(_t(a, dev), wg_bytes=wg)
+        torch.cuda.synchronize()
+        words = np.pad(a, (0, (-nbytes) % wg)).view(np.uint32).reshape(-1, wg // 4)
+        want = np.bitwise_xor.reduce(words, axis=1)
+        assert np.array_equal(got.cpu().numpy().view(np.uint32), want), (nbytes, wg)

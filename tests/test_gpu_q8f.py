@@ -227,3 +227,30 @@ def test_deepseek_v2_dropin_spec_configs(dev, oracle, M):
     ref = oracle.gemm_q8f(0, blocks, w, len(rows), N, K)
     got = y.cpu().numpy()[rows]
     assert _rel_err(got, ref) < TOL
+
+
+def test_runner_deepseek_v2_spec(dev, tmp_path):
+    """The deepseek_v2 W4A32C8 operator run through the definition runner from its spec.json
+    fields (name w4a32c8_q4_0_fp32_int8, entry "forward", model_architectures deepseek-v2,
+    threshold 0.1, test_configs M = 1..5, 8, 512, N = K = 5120): it resolves to the block_q8f entry,
+    and the runner's exact checks compare against the fp32-scale quantiser and block formula."""
+    from ksq import _lib, runner
+    spec = {"name": "w4a32c8_q4_0_fp32_int8", "variant": "W4A32C8", "family": "quant_gemm",
+            "model_architectures": ["deepseek-v2"], "kernel": {"file": "kernel.cu", "entry_point": "forward"},
+            "inputs": {"weight": {"dtype": "block_q4_0"}, "activation": {"dtype": "float32"}},
+            "params": {"M": {"type": "int"}, "N": {"type": "int", "default": 5120},
+                       "K": {"type": "int", "default": 5120}},
+            "test_configs": [{"name": f"batch_{m}", "M": m} for m in (1, 2, 3, 4, 5, 8, 512)],
+            "accuracy": {"metric": "nmse", "threshold": 0.1}}
+    r = runner.DefinitionRunner(warmup=1, iterations=2, all_configs=True, log=lambda s: None).run(spec, str(tmp_path))
+    assert r["compilation"]["entry_point"] == "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2"
+    assert r["compilation"]["activation_type"] == _lib.A_F32_Q8F_RNE
+    assert r["correctness"]["threshold"] == 0.1
+    cases = r["correctness"]["test_cases"]
+    assert [c["config"] for c in cases] == [f"batch_{m}" for m in (1, 2, 3, 4, 5, 8, 512)]
+    for c in cases:
+        ex = c["exact"]
+        assert c["passed"] and ex["quantize_bit_exact"] and ex["block_dots_bit_exact"], c
+        assert ex["max_rel_err_vs_fp64"] <= 1e-3, c
+        assert ex["engines"], c
+    assert (tmp_path / "test_results.json").exists()

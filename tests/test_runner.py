@@ -109,6 +109,111 @@ def test_runner_spec_handling(tmp_path):
         runner.resolve({"inputs": {"weight": {"dtype": "q4_0"}, "activation": {"dtype": "block_q8_1"}}})
 
 
+# the deepseek_v2 operator's identifying fields (core/operators/quant_gemm/variants/deepseek_v2/
+# w4a32c8_q4_0_fp32_int8/spec.json): the generic operator's name, entry "forward", one architecture
+DSV2_SPEC = {"name": "w4a32c8_q4_0_fp32_int8", "variant": "W4A32C8", "family": "quant_gemm",
+             "model_architectures": ["deepseek-v2"], "kernel": {"file": "kernel.cu", "entry_point": "forward"},
+             "inputs": {"weight": {"dtype": "block_q4_0"}, "activation": {"dtype": "float32"}},
+             "params": {"M": {"type": "int"}, "N": {"type": "int", "default": 5120},
+                        "K": {"type": "int", "default": 5120}},
+             "test_configs": [{"name": f"batch_{m}", "M": m} for m in (1, 2, 3, 4, 5, 8, 512)],
+             "accuracy": {"metric": "nmse", "threshold": 0.1}}
+
+
+def test_runner_resolves_variant_identity():
+    """The entry a spec resolves to follows its identity, not its weight dtype alone: the
+    deepseek_v2 W4A32C8 spec (entry "forward") runs the block_q8f entry with fp32 d_a and s_a; the
+    same name without the architecture runs the generic gemm_{name}; the reference's order
+    (entry_point, gemm_{name}, name) picks the native W8A8C8 entry either way."""
+    from ksq import _lib, runner
+    assert runner.entry_candidates(DSV2_SPEC)[:2] == ["gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2", "forward_deepseek_v2"]
+    assert runner.resolve(DSV2_SPEC) == (_lib.W_Q4_0, _lib.A_F32_Q8F_RNE, "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2")
+    generic = {k: v for k, v in DSV2_SPEC.items() if k != "model_architectures"}
+    assert runner.resolve(generic) == (_lib.W_Q4_0, _lib.A_F32, "gemm_w4a32c8_q4_0_fp32_int8")
+    # the architecture can also come from the variant directory the spec was found under
+    by_dir = dict(generic, _variant_dir="/x/quant_gemm/variants/deepseek_v2/w4a32c8_q4_0_fp32_int8")
+    assert runner.resolve(by_dir)[2] == "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2"
+    native = {"name": "w8a8c8_q8_0_q8_1", "model_architectures": ["deepseek-v3"],
+              "kernel": {"entry_point": "forward"},
+              "inputs": {"weight": {"dtype": "block_q8_0"}, "activation": {"dtype": "float32"}}}
+    assert runner.resolve(native) == (_lib.W_Q8_0, _lib.A_F32_Q8S, "gemm_w8a8c8_q8_0_q8_1")
+    # an entry whose weight type contradicts the spec's weight dtype is refused
+    with pytest.raises(ValueError):
+        runner.resolve(dict(native, inputs={"weight": {"dtype": "block_q4_0"}, "activation": {"dtype": "float32"}}))
+
+
+def _write_family(root, variants):
+    fam = root / "quant_gemm"
+    (fam / "variants").mkdir(parents=True)
+    (fam / "manifest.json").write_text(json.dumps({"name": "quant_gemm", "op_type": "gemm"}))
+    for rel, spec, impl in variants:
+        d = fam / "variants" / rel
+        d.mkdir(parents=True)
+        (d / "spec.json").write_text(json.dumps(spec))
+        if impl is not None:
+            (d / "impl.json").write_text(json.dumps(impl))
+    return fam
+
+
+def test_runner_discovers_variant_directories(tmp_path):
+    """discover() walks <family>/manifest.json and variants/**/spec.json as the reference's
+    OperatorRegistry does (plus the nested variants/<model>/<variant>/ layout), merges impl.json's
+    kernel entry, and each discovered variant resolves to its own libksq entry."""
+    from ksq import _lib, runner
+    dsv2 = {k: v for k, v in DSV2_SPEC.items() if k != "model_architectures"}   # identity from the path only
+    dsv3 = {"name": "w8a8c8_q8_0_q8_1", "inputs": {"weight": {"dtype": "block_q8_0"},
+                                                    "activation": {"dtype": "float32"}}}
+    plain = {"name": "w8a32c8_q8_0_fp32_int8", "inputs": {"weight": {"dtype": "block_q8_0"},
+                                                          "activation": {"dtype": "float32"}}}
+    _write_family(tmp_path, [
+        ("deepseek_v2/w4a32c8_q4_0_fp32_int8", dsv2, {"name": "w4a32c8_q4_0_fp32_int8"}),
+        ("deepseek_v3/w8a8c8_q8_0_q8_1", dsv3, {"kernel": {"file": "kernel.cu", "entry_point": "gemm_w8a8c8_q8_0_q8_1"}}),
+        ("w8a32c8_q8_0_fp32_int8", plain, None)])
+    found = runner.discover(str(tmp_path))
+    got = {v["_variant"]: runner.resolve(v) for v in found}
+    assert got == {
+        "deepseek_v2/w4a32c8_q4_0_fp32_int8": (_lib.W_Q4_0, _lib.A_F32_Q8F_RNE, "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2"),
+        "deepseek_v3/w8a8c8_q8_0_q8_1": (_lib.W_Q8_0, _lib.A_F32_Q8S, "gemm_w8a8c8_q8_0_q8_1"),
+        "w8a32c8_q8_0_fp32_int8": (_lib.W_Q8_0, _lib.A_F32, "gemm_w8a32c8_q8_0_fp32_int8")}
+    v3 = next(v for v in found if v["_variant"].startswith("deepseek_v3"))
+    assert v3["kernel"]["entry_point"] == "gemm_w8a8c8_q8_0_q8_1" and "_impl" in v3
+    # a variant directory given directly loads the same spec
+    d = runner.load_spec(str(tmp_path / "quant_gemm" / "variants" / "deepseek_v2" / "w4a32c8_q4_0_fp32_int8"))
+    assert runner.resolve(d)[2] == "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2"
+    with pytest.raises(FileNotFoundError):
+        runner.discover(str(tmp_path / "quant_gemm"))
+
+
+REF_OPERATORS = "/root/reference/kernelevalplus-main/core/operators"
+
+
+@pytest.mark.skipif(not os.path.isdir(REF_OPERATORS), reason="the reference tree is not on this machine")
+def test_runner_resolves_reference_operator_specs():
+    """The reference's own quant_gemm operator variants (read as JSON data) resolve to the libksq
+    entries with their arithmetic: deepseek_v2 to the block_q8f entry, deepseek_v3 to the native
+    W8A8C8 symbol."""
+    from ksq import _lib, runner
+    got = {v["_variant"]: runner.resolve(v) for v in runner.discover(REF_OPERATORS)}
+    assert got["deepseek_v2/w4a32c8_q4_0_fp32_int8"] == (_lib.W_Q4_0, _lib.A_F32_Q8F_RNE,
+                                                         "gemm_w4a32c8_q4_0_fp32_int8_deepseek_v2")
+    assert got["deepseek_v3/w8a8c8_q8_0_q8_1"] == (_lib.W_Q8_0, _lib.A_F32_Q8S, "gemm_w8a8c8_q8_0_q8_1")
+
+
+@pytest.mark.parametrize("rule", [0, 1])
+def test_refcheck_quantize_q8f_matches_oracle(oracle, rule):
+    """The runner's numpy block_q8f quantiser equals the oracle's C restatement bit for bit, on
+    random rows, exact ties of x / d (x = k + 0.5 with amax 127: d = 1), a zero block and tiny
+    blocks."""
+    from ksq import refcheck
+    g = np.random.default_rng(31 + rule)
+    x = g.standard_normal((6, 256), dtype=np.float32) * np.float32(3.0)
+    x[1, :32] = np.arange(-16, 16, dtype=np.float32) + np.float32(0.5)
+    x[1, 31] = np.float32(127.0)
+    x[2, 32:64] = 0.0
+    x[3, 64:96] *= np.float32(1e-12)
+    assert np.array_equal(refcheck.quantize_q8f(x, rule), oracle.quantize_q8f(x, rule))
+
+
 def test_runner_ggml_table():
     from ksq import _lib, runner
     # the GGML rows quoted for config 0 and config 1 (RTX 4090 / H800)
