@@ -647,12 +647,16 @@ __device__ __forceinline__ void mr_pair_acc(float& acc, const MrCtx<WT>& c, cons
 }
 
 // FQ: the activations arrive as fp32 [MR][32 nb] and the workgroup quantises the (single) K
-// tile into the same LDS layout instead (the device quantiser, bit-identical blocks).
-template <int WT, int MR, bool AS, int RPW, bool FQ>
+// tile into the same LDS layout instead (the device quantiser, bit-identical blocks); with XH they
+// arrive as fp16 and are quantised by the fused FP16 kernels' rules (kernels/gemm/gemm_fused.cuh:
+// 76-145, quantize_block_q8_1_f16tree).  Output element (m, row) at C[m * ldc + row * ldr].
+template <int WT, int MR, bool AS, int RPW, bool FQ, bool XH = false>
 __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __restrict__ W, const void* __restrict__ Ain,
-                                                             float* __restrict__ C, int N, int nb, int ktp, int ldc) {
+                                                             float* __restrict__ C, int N, int nb, int ktp, int ldc,
+                                                             int ldr) {
     static_assert((!is_kquant(WT) || WT == kWQ4K) && MR >= 1 && MR <= 8 && !(FQ && is_kquant(WT)),
                   "32-element block types or Q4_K, 1-8 activation rows");
+    static_assert(!XH || (FQ && !AS), "fp16 rows are quantised to block_q8_1 inside the workgroup");
     constexpr int WPR = RPW >= 4 ? 1 : 4 / RPW;  // waves per row
     constexpr int VR = RPW >= 4 ? RPW / 4 : 1;   // rows per wave
     constexpr int PW = MrW<WT>::NW;
@@ -678,7 +682,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
             const int e = (int)threadIdx.x;
             if (e < MR * 2 * tp) {
                 const int m = e / (2 * tp), u = e - m * 2 * tp;
-                load_x32<false>(Ain, (size_t)m * nb * 32 + (size_t)(2 * t0 + u) * 32, x0);
+                load_x32<XH>(Ain, (size_t)m * nb * 32 + (size_t)(2 * t0 + u) * 32, x0);
             }
         }
         // unconditional loads (row and pair clamped in range), so that the fused quantisation
@@ -698,10 +702,11 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
 #pragma unroll
                     for (int i = 0; i < 32; i++) x[i] = x0[i];
                 } else {
-                    load_x32<false>(Ain, (size_t)m * K + (size_t)(2 * t0 + u) * 32, x);
+                    load_x32<XH>(Ain, (size_t)m * K + (size_t)(2 * t0 + u) * 32, x);
                 }
                 uint32_t blk[9];
                 if constexpr (AS) quantize_block_q8s(x, blk);
+                else if constexpr (XH) quantize_block_q8_1_f16tree(x, blk);
                 else quantize_block_q8_1(x, blk);
                 uint32_t* dst = (uint32_t*)((uint8_t*)sact + (size_t)m * apitch + (size_t)u * kQ81Bytes);
 #pragma unroll
@@ -766,7 +771,7 @@ __global__ __launch_bounds__(256) void gemv_direct_mr_kernel(const uint8_t* __re
         for (int v = 0; v < VR; v++)
             if (row0 + v < N) {
 #pragma unroll
-                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + row0 + v] = acc[v][m];
+                for (int m = 0; m < MR; m++) C[(size_t)m * ldc + (size_t)(row0 + v) * ldr] = acc[v][m];
             }
     }
 }
@@ -1204,9 +1209,9 @@ static int direct_mr_ktp(int mr, int nb) {
     return ktp;
 }
 
-template <int WT, bool AS, int MR, bool FQ>
+template <int WT, bool AS, int MR, bool FQ, bool XH = false>
 static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const void* A, float* C, int N, int nb, int ldc,
-                                       hipStream_t s) {
+                                       int ldr, hipStream_t s) {
     const int ktp = direct_mr_ktp(MR, nb);
     if (FQ && ktp != (nb >> 1)) return hipErrorNotSupported;   // fused quantisation: one K tile
     const size_t lds = (size_t)MR * direct_mr_apitch(ktp);
@@ -1218,23 +1223,27 @@ static hipError_t direct_mr_launch_rpw(int rpw, const uint8_t* W, const void* A,
     switch (rpw) {
         case 8:
             if constexpr (MR <= 5)
-                hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 8, FQ>), dim3((N + 7) / 8), blk, lds, s, W, A, C, N, nb, ktp, ldc);
+                hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 8, FQ, XH>), dim3((N + 7) / 8), blk, lds, s, W, A, C, N, nb, ktp, ldc, ldr);
             break;
-        case 4: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 4, FQ>), dim3((N + 3) / 4), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
-        case 2: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 2, FQ>), dim3((N + 1) / 2), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
-        default: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 1, FQ>), dim3(N), blk, lds, s, W, A, C, N, nb, ktp, ldc); break;
+        case 4: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 4, FQ, XH>), dim3((N + 3) / 4), blk, lds, s, W, A, C, N, nb, ktp, ldc, ldr); break;
+        case 2: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 2, FQ, XH>), dim3((N + 1) / 2), blk, lds, s, W, A, C, N, nb, ktp, ldc, ldr); break;
+        default: hipLaunchKernelGGL((gemv_direct_mr_kernel<WT, MR, AS, 1, FQ, XH>), dim3(N), blk, lds, s, W, A, C, N, nb, ktp, ldc, ldr); break;
     }
     return hipGetLastError();
 }
 
 template <int WT, bool AS>
-static hipError_t direct_mr_launch(bool quant, int mr, int rpw, const uint8_t* W, const void* A, float* C, int N, int nb,
-                                   int ldc, hipStream_t s) {
-#define KSQ_MR_CASE(MRV)                                                                  \
-    if constexpr (is_kquant(WT)) return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s) \
+static hipError_t direct_mr_launch(bool quant, bool xh, int mr, int rpw, const uint8_t* W, const void* A, float* C,
+                                   int N, int nb, int ldc, int ldr, hipStream_t s) {
+#define KSQ_MR_CASE(MRV)                                                                                          \
+    if constexpr (is_kquant(WT)) return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, ldr, s) \
                                               : hipErrorNotSupported;                                             \
-    else return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, s)                   \
-                      : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, s);
+    else if constexpr (AS) return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, ldr, s)    \
+                                        : xh ? hipErrorNotSupported                                               \
+                                             : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, ldr, s); \
+    else return quant ? direct_mr_launch_rpw<WT, AS, MRV, false>(rpw, W, A, C, N, nb, ldc, ldr, s)                     \
+                : xh  ? direct_mr_launch_rpw<WT, AS, MRV, true, true>(rpw, W, A, C, N, nb, ldc, ldr, s)               \
+                      : direct_mr_launch_rpw<WT, AS, MRV, true>(rpw, W, A, C, N, nb, ldc, ldr, s);
     switch (mr) {
         case 3: KSQ_MR_CASE(3)
         case 4: KSQ_MR_CASE(4)
@@ -1270,8 +1279,7 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
         return KSQ_GEMV_DIRECT_MR && (!is_kquant(wtype) || (KSQ_GEMV_DIRECT_KQ && wtype == kWQ4K && (nb & 7) == 0)) &&
                (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && ((uintptr_t)A & 3) == 0 && direct_mr_ktp(mr, nb) > 0 &&
                !(rpw == 4 && (N + 3) / 4 < 512);
-    if (amode == kAFQH && mr >= 3) return false;   // the 3-8 row fused form takes fp32 only
-    if (amode == kAFQ && mr >= 3)   // gemv_fused_profitable admitted it: one K tile, no grid exclusion
+    if (is_fq(amode) && mr >= 3)   // gemv_fused_profitable admitted it: one K tile, no grid exclusion
         return !is_kquant(wtype) && (nb & 1) == 0 && ((uintptr_t)W & 3) == 0 && direct_mr_ktp(mr, nb) == (nb >> 1);
     // Q6_K with 2 activation rows measured level with gemv_row_kernel (N = 14336, K = 4096: 17.3
     // vs 17.0 us), 1 row 13-18% faster; Q4_K 10-20% faster with 1 or 2
@@ -1285,7 +1293,7 @@ static bool direct_eligible(int wtype, int amode, int mr, int nb, int N, int rpw
 
 static hipError_t direct_dispatch(int wtype, int afmt, bool quant, bool xh, int mr, int rpw, const uint8_t* W,
                                   const void* A, float* C, int N, int nb, int ldc, int ldr, hipStream_t s) {
-    if (mr >= 3 && wtype == kWQ4K) return direct_mr_launch<kWQ4K, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+    if (mr >= 3 && wtype == kWQ4K) return direct_mr_launch<kWQ4K, false>(quant, false, mr, rpw, W, A, C, N, nb, N, 1, s);
     if (wtype == kWQ4K || wtype == kWQ6K) {
         const uint8_t* Aq = (const uint8_t*)A;
         const dim3 blk(256);
@@ -1305,13 +1313,13 @@ static hipError_t direct_dispatch(int wtype, int afmt, bool quant, bool xh, int 
     }
     if (mr >= 3) {
         switch (wtype) {
-            case kWQ40: return direct_mr_launch<kWQ40, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+            case kWQ40: return direct_mr_launch<kWQ40, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
             case kWQ80:
-                return afmt == kAQ8S ? direct_mr_launch<kWQ80, true>(quant, mr, rpw, W, A, C, N, nb, N, s)
-                                     : direct_mr_launch<kWQ80, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-            case kWQ41: return direct_mr_launch<kWQ41, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-            case kWQ50: return direct_mr_launch<kWQ50, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
-            default: return direct_mr_launch<kWQ51, false>(quant, mr, rpw, W, A, C, N, nb, N, s);
+                return afmt == kAQ8S ? direct_mr_launch<kWQ80, true>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s)
+                                     : direct_mr_launch<kWQ80, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+            case kWQ41: return direct_mr_launch<kWQ41, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+            case kWQ50: return direct_mr_launch<kWQ50, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
+            default: return direct_mr_launch<kWQ51, false>(quant, xh, mr, rpw, W, A, C, N, nb, ldc, ldr, s);
         }
     }
     switch (wtype) {
@@ -1351,7 +1359,6 @@ static hipError_t gemv_dispatch(int wtype, int afmt, bool xh, const uint8_t* W, 
     if (afmt == kAQ8S && (wtype != kWQ80 || xh)) return hipErrorNotSupported;
     const int nb = K / 32;
     if (M <= 0 || N <= 0 || nb == 0) return hipSuccess;
-    if (!QUANT && xh && M > kMaxFusedRows) return hipErrorNotSupported;
     const int chunk = (QUANT || M > kMaxFusedRows) ? 8 : kMaxFusedRows;
     for (int m0 = 0; m0 < M; m0 += chunk) {
         const int mr = (M - m0) < chunk ? (M - m0) : chunk;
@@ -1370,7 +1377,7 @@ static hipError_t gemv_dispatch(int wtype, int afmt, bool xh, const uint8_t* W, 
             note_engine(is_kquant(wtype) && mr <= 2 ? KSQ_ENG_GEMV_KQ
                         : mr >= 3 ? (QUANT ? KSQ_ENG_GEMV_MR : KSQ_ENG_GEMV_MR_FQ)
                                   : (QUANT ? KSQ_ENG_GEMV_DIRECT : KSQ_ENG_GEMV_DIRECT_FQ));
-            if (mr >= 3 && (ldc != N || ldr != 1)) return hipErrorNotSupported;   // row-major output only
+            if (mr >= 3 && QUANT && (ldc != N || ldr != 1)) return hipErrorNotSupported;   // row-major output only
             e = direct_dispatch(wtype, afmt, QUANT, xh, mr, rpw, W, Am, Cm, N, nb, ldc, ldr, s);
         } else {
             note_engine(is_fq(AMODE) ? KSQ_ENG_GEMV_ROW_FQ : KSQ_ENG_GEMV_ROW);
@@ -1400,7 +1407,7 @@ hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, 
 #endif
 
 bool gemv_fused_profitable(int wtype, int M, int N, int K, const void* W, bool xh) {
-    if (M < 1 || M > 8 || (xh && M > kMaxFusedRows)) return false;
+    if (M < 1 || M > 8) return false;
 #ifndef KSQ_GEMV_FUSED_MR
 #define KSQ_GEMV_FUSED_MR 1
 #endif

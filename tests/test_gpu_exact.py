@@ -247,6 +247,10 @@ def _engine_cases():
         cases.append((f"f16_m{M}", 0, M, 256, 1024, 4, path, 0, eng, 0))
     for M in (1, 2):
         cases.append((f"f16_row_m{M}", 4, M, 256, 1024, 4, 1, 0, {"gemv_row_fq"}, 2))
+    # 3-8 fp16 rows: quantised inside the multi-row decode kernel's workgroups (no quantise launch)
+    for wt in LEGACY:
+        for M in (3, 8):
+            cases.append((f"f16_mr_m{M}_w{wt}", wt, M, 256, 1024, 4, 0, 0, {"gemv_mr_fq"}, 0))
     return cases
 
 
@@ -404,6 +408,11 @@ def test_fp16_fused_orientation_exact(dev):
 @pytest.mark.parametrize("Mw,Na,K,engines", [
     (512, 1, 1024, {"gemv_direct_fq"}),          # decode: fp16 quantised in LDS, [M][N] stored directly
     (4096, 2, 2048, {"gemv_direct_fq"}),
+    # 3-8 activation rows: fp16 quantised in LDS by the multi-row decode kernel, [M][N] stored
+    # directly (the reference tiles 4 activation columns per block: gemm_fused.cuh:157-162)
+    (768, 3, 4096, {"gemv_mr_fq"}),
+    (1024, 4, 2048, {"gemv_mr_fq"}),
+    (1024, 8, 1024, {"gemv_mr_fq"}),
     (4096, 512, 1024, {"quantize", "mmq3"}),     # MFMA GEMM writing its tiles transposed
     (384, 40, 1024, {"quantize", "mmq3", "splitk", "transpose"}),   # split-K: [N][M], then transposed
 ])

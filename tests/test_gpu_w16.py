@@ -69,7 +69,11 @@ def _run(dev, wtype, x, w, M, N, K, workspace=False):
 @pytest.mark.parametrize("wtype", [0, 1])
 @pytest.mark.parametrize("M,N,K", [(1, 256, 1024), (2, 300, 1024), (3, 520, 2048), (4, 130, 8320),
                                    (1, 4096, 14336), (7, 200, 320), (32, 384, 2048), (45, 130, 576),
-                                   (300, 256, 1024), (129, 1024, 4096)])
+                                   (300, 256, 1024), (129, 1024, 4096),
+                                   # the decode form's 16 and 8 weight rows per workgroup (512+ workgroups)
+                                   # with ragged last workgroups: 16 rows at N = 14336 and N = 8200
+                                   # (8 rows past N), 8 rows at N = 4100 (4 past N)
+                                   (1, 14336, 4096), (4, 8200, 1024), (2, 4100, 2048)])
 def test_w16_integer_inputs_exact(dev, wtype, M, N, K):
     from ksq import ops
     g = np.random.default_rng(500 + 7 * M + wtype)
