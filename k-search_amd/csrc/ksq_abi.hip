@@ -644,6 +644,18 @@ MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
     return L;
 }
 
+// Routing inside the grouping workgroup (one launch, 1024 threads routing T / 1024 tokens each)
+// while T * E stays under this threshold; from it on routing takes its own launch over the chip
+// (one thread per token) before the grouping workgroup.  Measured on MI355X, whole ksq_moe_gemm
+// call at N = K = 256, top-2 (us, one launch vs two): E = 8: T = 512 22.4 vs 22.1, T = 1024
+// 26.5 vs 24.5, T = 8192 98.5 vs 72.1, T = 16384 187.5 vs 130.8; E = 64: T = 512 44.4 vs 38.7,
+// T = 4096 189.3 vs 92.2, T = 16384 695.2 vs 283.9.  The grouping workgroup's counting sort stays
+// on one CU and is what grows with T past that.
+#ifndef KSQ_MOE_ROUTE_SPLIT_TE
+#define KSQ_MOE_ROUTE_SPLIT_TE 8192
+#endif
+static bool moe_route_in_group(int T, int E) { return (long long)T * E < (long long)KSQ_MOE_ROUTE_SPLIT_TE; }
+
 int moe_run(int wtype, const void* weights, const float* activation, const float* logits, const int32_t* ids_in,
             const float* wts_in, float* output, int T, int N, int K, int E, int top_k, int renorm, int32_t* ids_out,
             float* wts_out, void* workspace, size_t ws_bytes, hipStream_t s) {
@@ -690,10 +702,17 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     int32_t* ntiles = (int32_t*)(base + L.ntiles);
     int32_t* texp = (int32_t*)(base + L.texp);
     int32_t* trow0 = (int32_t*)(base + L.trow0);
-    if (logits) {
+    if (logits && moe_route_in_group(T, E)) {
         e = ksq::launch_moe_route_group(logits, T, E, top_k, renorm, ids, wts, tile_rows, rows, eend, ntiles, texp,
                                         trow0, s);
         if (e != hipSuccess) return hip_error(e, "route launch");
+        g_engines |= KSQ_ENG_MOE_ROUTE;
+    } else if (logits) {
+        // many tokens: one thread per token over the whole chip, then the grouping workgroup
+        e = ksq::launch_moe_route(logits, T, E, top_k, renorm, ids, wts, s);
+        if (e != hipSuccess) return hip_error(e, "route launch");
+        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
+        if (e != hipSuccess) return hip_error(e, "group launch");
         g_engines |= KSQ_ENG_MOE_ROUTE;
     } else {
         ids = (int32_t*)ids_in;

@@ -463,6 +463,25 @@ def test_moe_small(dev, oracle, T, E, N, K, top_k, renorm):
     assert _rel_err(y, ref) <= TOL
 
 
+@pytest.mark.parametrize("T,E,N,K,top_k,renorm", [(1100, 8, 128, 256, 2, False), (200, 64, 96, 256, 2, True),
+                                                  (300, 40, 64, 256, 3, False)])
+def test_moe_routing_own_launch(dev, oracle, T, E, N, K, top_k, renorm):
+    """From T * E = 8192 on, routing runs as its own launch over the chip before the grouping
+    workgroup: the same routing as the oracle (ids exact, weights to 1e-6) and the same output as
+    the caller-routed entry given those ids (bit for bit at top_k = 2, whose two additions onto zero
+    are order-free), within the tolerance of the oracle."""
+    import torch
+    from ksq import ops
+    assert T * E >= 8192   # past the library's threshold (KSQ_MOE_ROUTE_SPLIT_TE)
+    W, x, logits, y, ids, wts = _moe_case(dev, oracle, T, E, N, K, top_k, renorm, 1400 + T)
+    ref = oracle.moe_q4_0_f64(W, oracle.quantize_q8_1(x), ids, wts, T, N, K)
+    assert _rel_err(y, ref) <= TOL
+    if top_k == 2:
+        y2 = ops.moe_gemm_routed(0, _t(W, dev), _t(x, dev), _t(ids, dev), _t(wts, dev), T, N, K, E)
+        torch.cuda.synchronize()
+        assert np.array_equal(y, y2.cpu().numpy())
+
+
 def test_moe_routed_matches_routing_entry(dev, oracle):
     """Caller-supplied routing reproduces the routed entry bit for bit (top_k = 2 sums are order-free)."""
     import torch
