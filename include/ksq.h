@@ -333,6 +333,7 @@ KSQ_API int ksq_set_mmq_config(int config);
 #define KSQ_ENG_TRANSPOSE (1u << 22)      /* output transpose (fused FP16 orientation) */
 #define KSQ_ENG_W16 (1u << 23)            /* w16_kernel (dequantise-then-fp32 GEMM on the bf16 MFMA) */
 #define KSQ_ENG_MMQ_PLANAR (1u << 24)     /* mmq_planar_kernel (planar block_q8_1 staged by LDS DMA) */
+#define KSQ_ENG_MOE_PLANAR (1u << 25)     /* grouped mmq_planar_kernel (128-row tiles, expert-sorted planar rows) */
 KSQ_API uint32_t ksq_debug_last_engines(void);
 
 #ifdef __cplusplus

@@ -625,13 +625,25 @@ struct MoeLayout {
     int max_tiles;
 };
 
+// Rows per tile of the grouped GEMM's schedule: 128 for the LDS-DMA form, else mmq_kernel's.
+static int moe_tile_rows(int wtype, int T, int N, int K, int E, int top_k) {
+    (void)N;
+    return ksq::mmq_moe_planar(wtype, T, E, top_k, K) ? 128 : ksq::mmq_moe_tile_rows(wtype, T, E, top_k);
+}
+
+// Planar rows of the LDS-DMA form's activations: one per entry, plus one tile's worth so that a
+// tile starting at any entry reads its (d, nc) and -s rows inside the planes.
+static int moe_planar_rows(int T, int top_k) { return T * top_k + 128; }
+
 MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
     MoeLayout L{};
     const size_t ent = (size_t)T * top_k;
-    const int tile_rows = ksq::mmq_moe_tile_rows(wtype, T, E, top_k);
+    const int tile_rows = moe_tile_rows(wtype, T, N, K, E, top_k);
     L.max_tiles = (int)((ent + tile_rows - 1) / tile_rows) + E;
     size_t off = 0;
-    L.aq = off; off = align256(off + (size_t)T * (K / 32) * 36);
+    L.aq = off;
+    off = align256(off + (ksq::mmq_moe_planar(wtype, T, E, top_k, K) ? ksq::planar_bytes(moe_planar_rows(T, top_k), K)
+                                                                     : (size_t)T * (K / 32) * 36));
     L.ids = off; off = align256(off + ent * 4);
     L.wts = off; off = align256(off + ent * 4);
     L.rows = off; off = align256(off + ent * 4);
@@ -671,7 +683,8 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     if (((uintptr_t)weights & 15u) || ((uintptr_t)activation & 15u) || ((uintptr_t)output & 3u))
         return set_error(KSQ_ERR_ALIGN, "MoE weights/activation must be 16-byte aligned, output 4-byte");
     const MoeLayout L = moe_layout(wtype, T, N, K, E, top_k);
-    const int tile_rows = ksq::mmq_moe_tile_rows(wtype, T, E, top_k);
+    const int tile_rows = moe_tile_rows(wtype, T, N, K, E, top_k);
+    const bool planar = ksq::mmq_moe_planar(wtype, T, E, top_k, K);
     void* ws = workspace;
     if (ws) {
         if (ws_bytes < L.total) return set_error(KSQ_ERR_WORKSPACE, "workspace %zu < %zu bytes", ws_bytes, L.total);
@@ -690,9 +703,13 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     float* scratch = moe_uses_scratch(top_k) ? (float*)(base + L.scratch) : nullptr;
     const int64_t nout = (int64_t)T * N;
     const bool zero_fused = !scratch && ((uintptr_t)output & 15u) == 0 && (nout & 3) == 0;
-    hipError_t e = zero_fused ? ksq::launch_quantize_q8_1_zero(activation, aq, T, K, output, nout, s)
-                              : ksq::launch_quantize_q8_1(activation, aq, T, K, s);
-    if (e != hipSuccess) return hip_error(e, "quantize launch");
+    hipError_t e = hipSuccess;
+    if (!planar) {
+        // mmq_kernel's form: quantise the tokens first (rows are gathered inside the GEMM)
+        e = zero_fused ? ksq::launch_quantize_q8_1_zero(activation, aq, T, K, output, nout, s)
+                       : ksq::launch_quantize_q8_1(activation, aq, T, K, s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+    }
     if (!scratch && !zero_fused) {
         e = ksq::launch_fill_zero(output, nout, s);
         if (e != hipSuccess) return hip_error(e, "fill launch");
@@ -722,7 +739,17 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
     }
     g_engines |= KSQ_ENG_QUANTIZE | KSQ_ENG_MOE_GROUP;
     ksq::MoeTilesArgs a{ntiles, texp, trow0, eend, rows, wts, scratch, top_k};
-    e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, tile_rows, a, s);
+    if (planar) {
+        // the LDS-DMA form: the entries' rows quantised in expert-sorted order (the output zeroed in
+        // the same launch), then 128-row tiles of each expert
+        const ksq::PlanarQ81 P = ksq::planar_at(aq, moe_planar_rows(T, top_k), K);
+        e = ksq::launch_quantize_planar_gather(activation, P, T * top_k, K, ksq::planar_da_scale(wtype), rows, top_k,
+                                               zero_fused ? output : nullptr, zero_fused ? nout : 0, s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+        e = ksq::launch_mmq_planar_moe(wtype, (const uint8_t*)weights, P, output, N, K, L.max_tiles, a, s);
+    } else {
+        e = ksq::launch_mmq_moe(wtype, (const uint8_t*)weights, aq, output, N, K, L.max_tiles, tile_rows, a, s);
+    }
     if (e != hipSuccess) return hip_error(e, "grouped gemm launch");
     if (scratch) {
         e = ksq::launch_moe_combine(scratch, ids, output, T, N, top_k, E, s);

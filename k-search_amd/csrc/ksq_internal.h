@@ -49,6 +49,11 @@ size_t planar_bytes(int M, int K);
 PlanarQ81 planar_at(void* ws, int M, int K);
 // fp32 [M][K] (16-byte aligned, K % 128 == 0) -> planar block_q8_1.
 hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int K, float da_scale, hipStream_t s);
+// The same for the grouped MoE GEMM: planar row m (m < entries) holds x row rows[m] / top_k; rows
+// entries .. y.mp - 1 hold zero blocks (their quants are not written).  With zero non-null the
+// same launch also clears nzero floats there (16-byte aligned, nzero % 4 == 0).
+hipError_t launch_quantize_planar_gather(const float* x, const PlanarQ81& y, int entries, int K, float da_scale,
+                                         const int32_t* rows, int top_k, float* zero, int64_t nzero, hipStream_t s);
 // The LDS-DMA GEMM (Q4_0 / Q4_1 weights, K % 256 == 0, W 16-byte aligned) on planar
 // activations quantised with da_scale = planar_da_scale(wtype); whether it is the pick for this
 // shape (fp32 activations); partials as launch_mmq (mmq_splits(...) > 1).
@@ -128,6 +133,11 @@ struct MoeTilesArgs {
 };
 // Rows per grouped-GEMM tile (the MoE tile schedule's granularity) for a routing shape.
 int mmq_moe_tile_rows(int wtype, int T, int E, int top_k);
+// Whether the grouped GEMM runs on the LDS-DMA kernel (128-row tiles over planar activations in
+// expert-sorted order, launch_quantize_planar_gather), and that launch.
+bool mmq_moe_planar(int wtype, int T, int E, int top_k, int K);
+hipError_t launch_mmq_planar_moe(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int N, int K,
+                                 int max_tiles, const MoeTilesArgs& a, hipStream_t s);
 hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float* C, int N, int K, int max_tiles,
                           int tile_rows, const MoeTilesArgs& a, hipStream_t s);
 

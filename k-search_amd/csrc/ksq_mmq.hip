@@ -776,9 +776,16 @@ __device__ __forceinline__ void wait_vmem_all() { asm volatile("s_waitcnt vmcnt(
 // 16 different bank groups (the plain p ^ (r % 8) left 2-way conflicts: 5.5e6 conflict cycles
 // per launch).  The slots of one DMA instruction are 8 consecutive rows, so lane l of
 // instruction i sources piece (l % 8) ^ ((4 i + l / 16) % 8).
-template <int WT>
+// MOE (the expert-grouped GEMM): workgroup y is entry y of the tile schedule (128-row tiles of one
+// expert; surplus workgroups of the worst-case grid return at once).  Its planar rows are the
+// tile's rows of the expert-sorted entries (the gathered planar quantiser wrote them), the weights
+// are its expert's, a tile of at most 32 or 64 rows runs a K loop over that many rows (the others
+// stage no activation quants), and the output is added, weighted by the routing probability, into
+// C[token][n] through an LDS transpose (coalesced atomics; per-entry rows into moe.scratch when
+// top_k > 2).
+template <int WT, bool MOE = false>
 __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __restrict__ W, PlanarQ81 A,
-                                                           float* __restrict__ C, int M, int N, int nb) {
+                                                           float* __restrict__ C, int M, int N, int nb, MoeTiles moe) {
     static_assert(WT == kWQ40 || WT == kWQ41, "nibble-staged weights");
     constexpr int KB = 4, BM = 128, BN = 128, TM = 4;
     using S = WShape<WT, KB>;
@@ -792,10 +799,33 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
     // the f16 MFMA's k = 4..7, for which a step has no blocks)
     __shared__ __attribute__((aligned(16))) uint16_t sDh0[(BN + 1) * 4], sDh1[(BN + 1) * 4];
 
+    __shared__ int32_t sRows[MOE ? BM : 1];   // MoE: entry index of each tile row
+    __shared__ int32_t sTok[MOE ? BM : 1];    // MoE: its token (output row)
+    __shared__ float sWt[MOE ? BM : 1];       // MoE: its routing weight * out_scale
+
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int l32 = lane & 31, hi = lane >> 5;
-    const int m0 = (int)blockIdx.y * BM, n0 = (int)blockIdx.x * BN;
+    int m0 = (int)blockIdx.y * BM;
+    const int n0 = (int)blockIdx.x * BN;
+    int rows_here = BM;   // MoE: rows of this tile
+    if constexpr (MOE) {
+        // schedule values are wave-uniform (read once, broadcast), so the row-count dispatch below
+        // is a scalar branch
+        const int tile = blockIdx.y;
+        if (tile >= __builtin_amdgcn_readfirstlane(moe.num_tiles[0])) return;   // surplus workgroups
+        const int e = __builtin_amdgcn_readfirstlane(moe.tile_expert[tile]);
+        m0 = __builtin_amdgcn_readfirstlane(moe.tile_row0[tile]);
+        rows_here = min(BM, __builtin_amdgcn_readfirstlane(moe.expert_end[e]) - m0);
+        M = m0 + rows_here;                              // DMA sources past the tile's rows read its last row
+        W += (size_t)e * moe.expert_stride;
+        if (t < BM) {
+            const int ent = moe.rows[m0 + min(t, rows_here - 1)];
+            sRows[t] = ent;
+            sTok[t] = ent / moe.top_k;
+            sWt[t] = moe.weights[ent] * S::out_scale;
+        }
+    }
     const int K = nb * 32;
     const int nsteps = nb / KB, Z = (int)gridDim.z, z = (int)blockIdx.z;
     const int kb_lo = (int)((long long)nsteps * z / Z) * KB, kb_hi = (int)((long long)nsteps * (z + 1) / Z) * KB;
@@ -815,12 +845,14 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
             qoff[ii] = (uint32_t)r * (uint32_t)K + 16u * p;
         }
     }
-    auto dma_act = [&](auto par, int kb0) __attribute__((always_inline)) {
+    auto dma_act = [&](auto par, int kb0, bool qa) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;
         uint8_t* dA = P ? sA1 : sA0;
         const int8_t* qs = qtile + (size_t)kb0 * 32;
+        if (qa) {
 #pragma unroll
-        for (int ii = 0; ii < 4; ii++) dma16(qs + qoff[ii], dA + (4 * wave + ii) * 1024);
+            for (int ii = 0; ii < 4; ii++) dma16(qs + qoff[ii], dA + (4 * wave + ii) * 1024);
+        }
         dma16(A.dn + 2 * ((size_t)(kb0 + wave) * A.mp + m0 + 2 * lane), (P ? sDn1 : sDn0) + 256 * wave);
         if (wave == 3) dma16(A.sa + ((size_t)(kb0 >> 2) * A.mp + m0 + 2 * lane) * 4, P ? sSa1 : sSa0);
     };
@@ -878,16 +910,20 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
     const int dh_idx = hi ? BN * 4 : (wn * 32 + l32) * 4;
     const int nbase = wn * 32 + 4 * hi;   // local weight row of r = 0
 
-    auto compute = [&](auto par) __attribute__((always_inline)) {
+    // TA: the row sub-tiles a K loop computes (TM, or fewer for a ragged MoE tile; each value
+    // is a K loop of its own, free of per-sub-tile branches: a wave-uniform branch around each
+    // sub-tile's epilogue inside the loop cost 10% on full tiles)
+    auto compute = [&](auto par, auto tav) __attribute__((always_inline)) {
         constexpr int P = decltype(par)::value;
+        constexpr int TA = decltype(tav)::value;
         const uint8_t* cA = P ? sA1 : sA0;
         const uint8_t* cW = P ? sW1 : sW0;
         const float* cDn = P ? sDn1 : sDn0;
         const float* cDw = P ? sDw1 : sDw0;
         const uint16_t* cSa = P ? sSa1 : sSa0;
         const uint16_t* cDh = P ? sDh1 : sDh0;
-        constexpr int NQ = KB * TM;
-        i32x4 af[TM], afn[TM], bf;
+        constexpr int NQ = KB * TA;
+        i32x4 af[TA], afn[TA], bf;
         u32x4 bxn;
         f32x4 edw[4];
         auto unpack = [&](const u32x4& x) -> i32x4 {
@@ -896,28 +932,28 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
                          (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
         };
 #pragma unroll
-        for (int ii = 0; ii < TM; ii++) af[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[0]);
+        for (int ii = 0; ii < TA; ii++) af[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[0]);
         bf = unpack(*(const u32x4*)(cW + woff));
         __builtin_amdgcn_s_setprio(2);
         i32x16 cur = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[0], bias, 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
-            const int b = q / TM, i = q % TM;
+            const int b = q / TA, i = q % TA;
             if (i == 0 && b + 1 < KB) {
                 // the next block's fragments, a block ahead of their MFMAs
 #pragma unroll
-                for (int ii = 0; ii < TM; ii++) afn[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[b + 1]);
+                for (int ii = 0; ii < TA; ii++) afn[ii] = *(const i32x4*)(cA + ii * 32 * 128 + aoff[b + 1]);
                 bxn = *(const u32x4*)(cW + woff + (b + 1) * 16);
                 __builtin_amdgcn_sched_barrier(0);
             }
             i32x16 nxt = bias;
             if (q + 1 < NQ) {
-                if (i + 1 < TM) {
+                if (i + 1 < TA) {
                     nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[i + 1], bias, 0, 0, 0);
                 } else {
                     bf = unpack(bxn);
 #pragma unroll
-                    for (int ii = 0; ii < TM; ii++) af[ii] = afn[ii];
+                    for (int ii = 0; ii < TA; ii++) af[ii] = afn[ii];
                     nxt = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf, af[0], bias, 0, 0, 0);
                 }
             }
@@ -925,17 +961,19 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
 #pragma unroll
                 for (int qq = 0; qq < 4; qq++) edw[qq] = *(const f32x4*)&cDw[b * BN + nbase + 8 * qq];
             }
-            const int lm = i * 32 + l32;
-            const f32x2 dn = *(const f32x2*)&cDn[2 * (b * BM + lm)];
-            const float da = dn.x, nc = dn.y;
+            {
+                const int lm = i * 32 + l32;
+                const f32x2 dn = *(const f32x2*)&cDn[2 * (b * BM + lm)];
+                const float da = dn.x, nc = dn.y;
 #pragma unroll
-            for (int qq = 0; qq < 4; qq++) {
+                for (int qq = 0; qq < 4; qq++) {
 #pragma unroll
-                for (int p = 0; p < 4; p++) {
-                    const int e = cur[4 * qq + p];
-                    const float f = __builtin_bit_cast(float, e);
-                    const float x = fmaf(f, da, nc);   // sumi * d_a'
-                    acc[i][4 * qq + p] = fmaf(edw[qq][p], x, acc[i][4 * qq + p]);
+                    for (int p = 0; p < 4; p++) {
+                        const int e = cur[4 * qq + p];
+                        const float f = __builtin_bit_cast(float, e);
+                        const float x = fmaf(f, da, nc);   // sumi * d_a'
+                        acc[i][4 * qq + p] = fmaf(edw[qq][p], x, acc[i][4 * qq + p]);
+                    }
                 }
             }
             cur = nxt;
@@ -944,7 +982,7 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
         // side term over the step's 4 blocks (f16 MFMA, exact products; k = 4..7 read zeros)
         const f16x4 dw4 = *(const f16x4*)&cDh[dh_idx];
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+        for (int i = 0; i < TA; i++) {
             const f16x4 sa4 = *(const f16x4*)&cSa[(i * 32 + l32) * 4];
             acc[i] = __builtin_amdgcn_mfma_f32_32x32x8f16(dw4, sa4, acc[i], 0, 0, 0);
         }
@@ -955,33 +993,75 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
         sDh0[BN * 4 + t] = 0;
         sDh1[BN * 4 + t] = 0;
     }
-    if (kb_lo < kb_hi) {
-        dma_act(IntC<0>{}, kb_lo);
-        load_w(kb_lo);
-        store_w(IntC<0>{});
-        wait_vmem_all();
-    }
-    __syncthreads();
-    auto step = [&](auto par, int kb0) __attribute__((always_inline)) {
-        constexpr int P = decltype(par)::value;
-        const bool more = kb0 + KB < kb_hi;
-        if (more) {
-            dma_act(IntC<1 - P>{}, kb0 + KB);
-            load_w(kb0 + KB);
-        }
-        compute(par);
-        if (more) {
-            store_w(IntC<1 - P>{});
+    auto run = [&](auto tav) __attribute__((always_inline)) {
+        constexpr int TA = decltype(tav)::value;
+        // waves past the computed sub-tiles stage no activation quants (no wave reads them)
+        const bool qa = wave < TA;
+        if (kb_lo < kb_hi) {
+            dma_act(IntC<0>{}, kb_lo, qa);
+            load_w(kb_lo);
+            store_w(IntC<0>{});
             wait_vmem_all();
         }
         __syncthreads();
+        auto step = [&](auto par, int kb0) __attribute__((always_inline)) {
+            constexpr int P = decltype(par)::value;
+            const bool more = kb0 + KB < kb_hi;
+            if (more) {
+                dma_act(IntC<1 - P>{}, kb0 + KB, qa);
+                load_w(kb0 + KB);
+            }
+            compute(par, tav);
+            if (more) {
+                store_w(IntC<1 - P>{});
+                wait_vmem_all();
+            }
+            __syncthreads();
+        };
+        for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += 2 * KB) {
+            step(IntC<0>{}, kb0);
+            if (kb0 + KB < kb_hi) step(IntC<1>{}, kb0 + KB);
+        }
     };
-    for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += 2 * KB) {
-        step(IntC<0>{}, kb0);
-        if (kb0 + KB < kb_hi) step(IntC<1>{}, kb0 + KB);
+    if constexpr (MOE) {
+        // wave-uniform: the tile's row count comes from the broadcast schedule
+        const int ta = (rows_here + 31) >> 5;
+        if (ta >= 3) run(IntC<TM>{});
+        else if (ta == 2) run(IntC<2>{});
+        else run(IntC<1>{});
+    } else {
+        run(IntC<TM>{});
     }
 
     // ---- output ----
+    if constexpr (MOE) {
+        // the staging buffers are free after the last K step's barrier: each wave transposes its
+        // [32 rows][32 columns] sub-tiles through a 33-float-pitch scratch, so that one atomic
+        // instruction covers 32 consecutive columns of one token
+        constexpr int kTP = 33;
+        static_assert(2 * 32 * kTP * 4 <= BM * 128, "two waves' transpose scratch fits one activation buffer");
+        float* tp = (float*)(wave < 2 ? sA0 : sA1) + (wave & 1) * 32 * kTP;
+        const int gn = n0 + nbase - 4 * hi + l32;   // this lane's column after the transpose
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            if (32 * i >= rows_here) break;   // no rows in this or a later sub-tile (wave-uniform)
+#pragma unroll
+            for (int r = 0; r < 16; r++) tp[l32 * kTP + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[i][r];
+            __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes done
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int p = 0; p < 16; p++) {
+                const int lm = i * 32 + 2 * p + hi;   // tile row
+                if (lm < rows_here && gn < N) {
+                    const float v = tp[(2 * p + hi) * kTP + l32] * sWt[lm];
+                    if (moe.scratch) moe.scratch[(size_t)sRows[lm] * N + gn] = v;
+                    else unsafeAtomicAdd(C + (size_t)sTok[lm] * N + gn, v);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
     constexpr float out_scale = S::out_scale;
     const bool vec_ok = (N % 4) == 0 && (((uintptr_t)C & 15u) == 0);
 #pragma unroll
@@ -1320,9 +1400,9 @@ hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, fl
     const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), (unsigned)splits);
     float* out = splits > 1 ? partials : C;
     if (wtype == kWQ40)
-        hipLaunchKernelGGL(mmq_planar_kernel<kWQ40>, grid, dim3(256), 0, s, W, A, out, M, N, K / 32);
+        hipLaunchKernelGGL((mmq_planar_kernel<kWQ40, false>), grid, dim3(256), 0, s, W, A, out, M, N, K / 32, MoeTiles{});
     else if (wtype == kWQ41)
-        hipLaunchKernelGGL(mmq_planar_kernel<kWQ41>, grid, dim3(256), 0, s, W, A, out, M, N, K / 32);
+        hipLaunchKernelGGL((mmq_planar_kernel<kWQ41, false>), grid, dim3(256), 0, s, W, A, out, M, N, K / 32, MoeTiles{});
     else
         return hipErrorNotSupported;
     hipError_t e = hipGetLastError();
@@ -1373,6 +1453,40 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
     }
     const dim3 grid((unsigned)((N + TileS::BN - 1) / TileS::BN), (unsigned)max_tiles);
     return launch_t<TileS, false, true>(wtype, kAQ81, grid, W, Aq, C, nullptr, 0, N, nb, mt, s);
+}
+
+// The grouped GEMM on the LDS-DMA kernel (Q4_0 / Q4_1, fp32 activations quantised to planar
+// rows in expert-sorted order): from an average of KSQ_MOE_PLANAR_MIN_ROWS entries per expert on.
+#ifndef KSQ_MOE_PLANAR_MIN_ROWS
+#define KSQ_MOE_PLANAR_MIN_ROWS 96
+#endif
+bool mmq_moe_planar(int wtype, int T, int E, int top_k, int K) {
+    return (wtype == kWQ40 || wtype == kWQ41) && K % 256 == 0 &&
+           (long long)T * top_k >= (long long)KSQ_MOE_PLANAR_MIN_ROWS * E;
+}
+
+hipError_t launch_mmq_planar_moe(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int N, int K,
+                                 int max_tiles, const MoeTilesArgs& a, hipStream_t s) {
+    if (K % 256) return hipErrorInvalidValue;
+    MoeTiles mt;
+    mt.num_tiles = a.num_tiles;
+    mt.tile_expert = a.tile_expert;
+    mt.tile_row0 = a.tile_row0;
+    mt.expert_end = a.expert_end;
+    mt.rows = a.rows;
+    mt.weights = a.weights;
+    mt.scratch = a.scratch;
+    mt.top_k = a.top_k;
+    mt.expert_stride = (size_t)N * (K / 32) * block_bytes(wtype);
+    note_engine(KSQ_ENG_MOE_PLANAR);
+    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)max_tiles);
+    if (wtype == kWQ40)
+        hipLaunchKernelGGL((mmq_planar_kernel<kWQ40, true>), grid, dim3(256), 0, s, W, A, C, 0, N, K / 32, mt);
+    else if (wtype == kWQ41)
+        hipLaunchKernelGGL((mmq_planar_kernel<kWQ41, true>), grid, dim3(256), 0, s, W, A, C, 0, N, K / 32, mt);
+    else
+        return hipErrorNotSupported;
+    return hipGetLastError();
 }
 
 hipError_t launch_mmq_block_sumi(int wtype, const uint8_t* W, const uint8_t* A, int32_t* out, int M, int N, int K,

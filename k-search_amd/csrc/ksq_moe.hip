@@ -129,16 +129,25 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
     }
     __syncthreads();
     if (t == 0) {
+        // full tiles first, then each expert's ragged last tile: the cheaper ragged workgroups
+        // are dispatched last, where they fill the grid's final partial wave
         int acc = 0, nt = 0;
         for (int e = 0; e < E; e++) {
             cursor[e] = acc;
-            for (int r = 0; r < count[e]; r += tile_rows) {
+            for (int r = 0; r + tile_rows <= count[e]; r += tile_rows) {
                 tile_expert[nt] = e;
                 tile_row0[nt] = acc + r;
                 nt++;
             }
             acc += count[e];
             expert_end[e] = acc;
+        }
+        for (int e = 0; e < E; e++) {
+            if (count[e] % tile_rows) {
+                tile_expert[nt] = e;
+                tile_row0[nt] = expert_end[e] - count[e] % tile_rows;
+                nt++;
+            }
         }
         num_tiles[0] = nt;
     }
@@ -168,6 +177,10 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
         }
         __syncthreads();
     }
+    // entries with an expert id outside [0, E) were not placed: the list's tail past the placed
+    // ones gets entry 0, so that every rows[j] < total names a real token
+    const int placed = E > 0 ? cursor[E - 1] : 0;
+    for (int j = placed + t; j < total; j += kGroupThreads) rows[j] = 0;
 }
 
 __global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,

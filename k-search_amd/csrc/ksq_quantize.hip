@@ -175,16 +175,39 @@ hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, i
 // t / 4, so that the 4 lanes of a row write its 128 quant bytes, its (d, nc) pairs and its 4 sa
 // halves side by side.  Rows M .. mp-1 quantise zeros: their dn and sa entries are written,
 // their quants are not.
+// GATHER (the grouped MoE GEMM's input): planar row m holds x row rows[m] / top_k (rows = the
+// expert-sorted (token, slot) entries, M of them), and workgroups from x = mp / 64 on clear 32 KiB
+// each of `zero` (n4 16-byte groups; chunk (x - mp / 64) * gridDim.y + y), so that the output the
+// grouped GEMM accumulates into needs no launch of its own.
+template <bool GATHER>
 __global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __restrict__ x, PlanarQ81 y, int M, int K,
-                                                              float da_scale) {
+                                                              float da_scale, const int32_t* __restrict__ rows,
+                                                              int top_k, float* __restrict__ zero, int64_t n4) {
     __shared__ float stage[64 * 4 * kQPitch];
     const int t = threadIdx.x;
+    if constexpr (GATHER) {
+        if ((int)blockIdx.x >= y.mp / 64) {
+            const int64_t chunk = ((int64_t)blockIdx.x - y.mp / 64) * gridDim.y + blockIdx.y;
+            const int64_t base = chunk * (kZeroBytesPerWG / 16);
+            if (base >= n4) return;
+            f32x4* z = (f32x4*)zero;
+#pragma unroll
+            for (int i = 0; i < kZeroBytesPerWG / 16 / 256; i++) {
+                const int64_t k = base + i * 256 + t;
+                if (k < n4) z[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+            return;
+        }
+    }
     const int r0 = (int)blockIdx.x * 64, kb0 = (int)blockIdx.y * 4;
 #pragma unroll
     for (int p = 0; p < 8; p++) {
         const int idx = p * 256 + t, row = idx >> 5, c = idx & 31;   // c: float4 of the row segment
         f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (r0 + row < M) v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)(r0 + row) * K + kb0 * 32) + c);
+        if (r0 + row < M) {
+            const int src = GATHER ? rows[r0 + row] / top_k : r0 + row;
+            v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)src * K + kb0 * 32) + c);
+        }
         float* dst = stage + (row * 4 + (c >> 3)) * kQPitch + (c & 7) * 4;
         dst[0] = v.x;
         dst[1] = v.y;
@@ -232,7 +255,21 @@ hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int
     if (M <= 0 || K <= 0) return hipSuccess;
     if (K % 128) return hipErrorInvalidValue;
     const dim3 grid((unsigned)(y.mp / 64), (unsigned)(K / 128));
-    hipLaunchKernelGGL(quantize_planar_kernel, grid, dim3(256), 0, s, x, y, M, K, da_scale);
+    hipLaunchKernelGGL(quantize_planar_kernel<false>, grid, dim3(256), 0, s, x, y, M, K, da_scale, nullptr, 1,
+                       nullptr, (int64_t)0);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_planar_gather(const float* x, const PlanarQ81& y, int entries, int K, float da_scale,
+                                         const int32_t* rows, int top_k, float* zero, int64_t nzero, hipStream_t s) {
+    if (K <= 0 || K % 128) return hipErrorInvalidValue;
+    if (entries < 0 || y.mp < entries || y.mp % 64) return hipErrorInvalidValue;
+    const int64_t n4 = zero ? nzero / 4 : 0;
+    const int64_t zchunks = (n4 * 16 + kZeroBytesPerWG - 1) / kZeroBytesPerWG;
+    const int64_t zgrid = (zchunks + K / 128 - 1) / (K / 128);   // chunks spread over grid y too
+    const dim3 grid((unsigned)(y.mp / 64 + zgrid), (unsigned)(K / 128));
+    hipLaunchKernelGGL(quantize_planar_kernel<true>, grid, dim3(256), 0, s, x, y, entries, K, da_scale, rows, top_k,
+                       zero, n4);
     return hipGetLastError();
 }
 

@@ -24,7 +24,7 @@ ENG = {"quantize": 1 << 0, "gemv_row": 1 << 1, "gemv_row_fq": 1 << 2, "gemv_dire
        "gemv_direct_fq": 1 << 4, "gemv_mr": 1 << 5, "gemv_mr_fq": 1 << 6, "gemv_kq": 1 << 7, "skinny": 1 << 8,
        **{f"mmq{c}": 1 << (8 + c) for c in range(1, 8)}, "splitk": 1 << 16, "moe_route": 1 << 17,
        "moe_group": 1 << 18, "moe_tile64": 1 << 19, "moe_tile128": 1 << 20, "moe_combine": 1 << 21,
-       "transpose": 1 << 22, "w16": 1 << 23, "mmq_planar": 1 << 24}
+       "transpose": 1 << 22, "w16": 1 << 23, "mmq_planar": 1 << 24, "moe_planar": 1 << 25}
 STATUS = {0: "KSQ_OK", 1: "KSQ_ERR_NULL", 2: "KSQ_ERR_SHAPE", 3: "KSQ_ERR_ALIGN",
           4: "KSQ_ERR_TYPE", 5: "KSQ_ERR_WORKSPACE", 6: "KSQ_ERR_HIP"}
 

@@ -174,7 +174,8 @@ def test_exact_moe_config4(dev, oracle):
     y = ops.moe_gemm_routed(0, _t(w, dev), _t(x, dev), _t(ids, dev), _t(wts, dev), T, N, K, E)
     eng = ops.last_engines()
     torch.cuda.synchronize()
-    assert eng == {"quantize", "moe_group", "moe_tile64"}, eng
+    # ~128 rows per expert: the LDS-DMA kernel's 128-row tiles over expert-sorted planar rows
+    assert eng == {"quantize", "moe_group", "moe_planar"}, eng
     a = oracle.quantize_q8_1(x)
     ref = np.zeros((T, N))
     for e in range(E):
@@ -298,7 +299,7 @@ def test_engine_table_covers_every_engine():
     """The forced cases above (plus the MoE and fused FP16 cases below, and the dequantise-then-fp32
     GEMM of tests/test_gpu_w16.py) reach every kernel family the library has."""
     from ksq import _lib
-    seen = set().union(*(c[8] for c in ENGINE_CASES)) | {"moe_tile64", "moe_tile128", "moe_combine",
+    seen = set().union(*(c[8] for c in ENGINE_CASES)) | {"moe_tile64", "moe_tile128", "moe_planar", "moe_combine",
                                                           "moe_route", "moe_group", "transpose", "w16"}
     assert seen == set(_lib.ENG), set(_lib.ENG) - seen
 
@@ -306,12 +307,15 @@ def test_engine_table_covers_every_engine():
 # ------------------------------------------------------------------ MoE engines
 @pytest.mark.parametrize("wtype", LEGACY)
 @pytest.mark.parametrize("T,E,top_k,tile,skew", [(96, 4, 2, 64, False), (96, 4, 3, 64, False),
-                                                 (800, 4, 2, 64, False), (300, 4, 2, 64, True)])
+                                                 (800, 4, 2, 64, False), (300, 4, 2, 64, True),
+                                                 (260, 4, 3, 64, True)])
 def test_exact_moe_engines(dev, wtype, T, E, top_k, tile, skew):
-    """Grouped GEMM in 64- and 128-row tiles, and the top_k > 2 combine, per block type; with
-    top_k = 3 one slot of one token carries an out-of-range expert id, which contributes
-    nothing.  Skewed routing (expert shares 0.55 / 0.3 / 0.1 / 0.05) leaves 128-row tiles whose
-    waves hold 0, 1 or 2 of their 32-row sub-tiles."""
+    """Grouped GEMM per block type, and the top_k > 2 combine; with top_k = 3 one slot of one
+    token carries an out-of-range expert id, which contributes nothing.  From 96 entries per
+    expert on, Q4_0 / Q4_1 run the LDS-DMA kernel on 128-row tiles of expert-sorted planar rows;
+    skewed routing (expert shares 0.55 / 0.3 / 0.1 / 0.05) leaves tiles with 1-4 of their 32-row
+    sub-tiles holding rows, and experts whose rows end mid-tile.  The other types (and fewer
+    rows) take mmq_kernel's 64-row tiles."""
     import torch
     from ksq import ops, refcheck
     from oracle import oracle
@@ -329,7 +333,8 @@ def test_exact_moe_engines(dev, wtype, T, E, top_k, tile, skew):
     y = ops.moe_gemm_routed(wtype, _t(w, dev), _t(x, dev), _t(ids, dev), _t(wts, dev), T, N, K, E)
     eng = ops.last_engines()
     torch.cuda.synchronize()
-    want_eng = {"quantize", "moe_group", f"moe_tile{tile}"} | ({"moe_combine"} if top_k > 2 else set())
+    grouped = "moe_planar" if wtype in (0, 4) and T * top_k >= 96 * E else f"moe_tile{tile}"
+    want_eng = {"quantize", "moe_group", grouped} | ({"moe_combine"} if top_k > 2 else set())
     assert eng == want_eng, eng
     a = oracle.quantize_q8_1(x)
     ref = np.zeros((T, N))
