@@ -21,6 +21,17 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
+// LDS written by some lanes of a wave and read by other lanes of the same wave.  The
+// wavefront-scope release / acquire pair keeps the compiler from moving LDS accesses across
+// the point or reusing a value read before it (a lane that wrote nothing may otherwise keep its
+// earlier read of the same address); LDS operations of one wave complete in order, so no
+// wait instruction is needed for the hardware.
+__device__ __forceinline__ void wave_lds_exchange() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 constexpr int kQ40Bytes = 18;
 constexpr int kQ80Bytes = 34;
 constexpr int kQ81Bytes = 36;

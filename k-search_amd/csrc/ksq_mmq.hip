@@ -688,7 +688,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
 #pragma unroll
                 for (int r = 0; r < 16; r++) tp[l32 * kTP + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[i][j][r];
                 __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes done
-                __builtin_amdgcn_wave_barrier();
+                wave_lds_exchange();
                 const int gn = n0 + wn * 32 * TN + j * 32 + l32;
 #pragma unroll
                 for (int p = 0; p < 16; p++) {
@@ -699,7 +699,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                         else unsafeAtomicAdd(C + (size_t)sTok[lm] * N + gn, v);
                     }
                 }
-                __builtin_amdgcn_wave_barrier();
+                wave_lds_exchange();
             }
         }
     } else if constexpr (!DUMP) {
@@ -1048,7 +1048,7 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
 #pragma unroll
             for (int r = 0; r < 16; r++) tp[l32 * kTP + 8 * (r >> 2) + 4 * hi + (r & 3)] = acc[i][r];
             __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): this wave's LDS writes done
-            __builtin_amdgcn_wave_barrier();
+            wave_lds_exchange();
 #pragma unroll
             for (int p = 0; p < 16; p++) {
                 const int lm = i * 32 + 2 * p + hi;   // tile row
@@ -1058,7 +1058,7 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
                     else unsafeAtomicAdd(C + (size_t)sTok[lm] * N + gn, v);
                 }
             }
-            __builtin_amdgcn_wave_barrier();
+            wave_lds_exchange();
         }
         return;
     }

@@ -25,7 +25,7 @@ constexpr int kQPitch = 33;  // floats per staged block
 // operations, then keep the compiler from moving LDS accesses across the point.
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_exchange();
 }
 
 // Output formats: kQF81 block_q8_1 (quantize_row_q8_1_ref), kQF8S block_q8s (the native W8A8C8
