@@ -91,9 +91,18 @@ __device__ __forceinline__ void w16_stage_block(const uint32_t* v, uint16_t* dst
     }
 }
 
+// Linear tile of workgroup x in a grid of gx (a multiple of 8) workgroups: workgroups are handed to
+// the 8 XCDs round robin (XCD = x % 8), so XCD j takes tiles j * gx / 8 .. (j + 1) * gx / 8 - 1,
+// whole rows of row-major tiles: its L2 then holds its activation rows for every column tile
+// (the plain grid spreads each 128-row tile's column tiles over all 8 XCDs, whose L2s each
+// fetch the rows).
+__device__ __forceinline__ int w16_tile(int x, int gx) { return (x % 8) * (gx / 8) + x / 8; }
+
 // WT: kWQ40 or kWQ80.  W: [N][K/32] blocks (4-byte aligned); A: fp32 [M][K] (16-byte aligned);
 // C: fp32 [M][N], or split z's partial [M][N] at C + z*M*N.  nb = K/32, even.
-template <class T, int WT>
+// XG: workgroup x is a linear tile index whose tiles each XCD takes as one contiguous run in
+// row-major tile order (see w16_tile).
+template <class T, int WT, bool XG = false>
 __global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__ W, const float* __restrict__ A,
                                                      float* __restrict__ C, int M, int N, int nb) {
     constexpr int BM = T::BM, BN = T::BN, TM = T::TM, TN = T::TN, P = kW16Pitch;
@@ -107,7 +116,15 @@ __global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int wm = wave / T::WN, wn = wave % T::WN;
     const int l32 = lane & 31, hi = lane >> 5;
-    const int m0 = (int)blockIdx.y * BM, n0 = (int)blockIdx.x * BN;
+    int tm = (int)blockIdx.y, tn = (int)blockIdx.x;
+    if constexpr (XG) {
+        const int gn = (N + BN - 1) / BN, tiles = gn * ((M + BM - 1) / BM);
+        const int L = w16_tile((int)blockIdx.x, (int)gridDim.x);
+        if (L >= tiles) return;   // padding of the grid to a multiple of 8 (whole workgroup)
+        tm = L / gn;
+        tn = L % gn;
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
 
     // split z covers K steps [s_lo, s_hi) of two blocks each
     const int nsteps = nb / 2, Z = (int)gridDim.z, z = (int)blockIdx.z;
@@ -430,8 +447,9 @@ static hipError_t w16_launch(const float* A, const uint8_t* W, float* C, int M, 
         const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 31) / 32), (unsigned)splits);
         hipLaunchKernelGGL((w16_kernel<W16Skinny, WT>), grid, dim3(256), 0, s, W, A, C, M, N, nb);
     } else {
-        const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), (unsigned)splits);
-        hipLaunchKernelGGL((w16_kernel<W16Big, WT>), grid, dim3(256), 0, s, W, A, C, M, N, nb);
+        const int tiles = ((N + 127) / 128) * ((M + 127) / 128);
+        const dim3 grid((unsigned)((tiles + 7) / 8 * 8), 1u, (unsigned)splits);
+        hipLaunchKernelGGL((w16_kernel<W16Big, WT, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb);
     }
     return hipGetLastError();
 }
