@@ -21,6 +21,11 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
 
+// Linear tile of workgroup x in a 1-D grid of gx (a multiple of 8) workgroups: workgroups go to
+// the 8 XCDs round robin (XCD = x % 8), so XCD j takes tiles j * gx / 8 .. (j + 1) * gx / 8 - 1,
+// a contiguous run of the row-major tile order (whole rows of tiles for grids of 8 rows or more).
+__device__ __forceinline__ int xcd_tile(int x, int gx) { return (x % 8) * (gx / 8) + x / 8; }
+
 // LDS written by some lanes of a wave and read by other lanes of the same wave.  The
 // wavefront-scope release / acquire pair keeps the compiler from moving LDS accesses across
 // the point or reusing a value read before it (a lane that wrote nothing may otherwise keep its

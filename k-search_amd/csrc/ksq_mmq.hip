@@ -807,7 +807,16 @@ __global__ __launch_bounds__(256, 2) void mmq_planar_kernel(const uint8_t* __res
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int l32 = lane & 31, hi = lane >> 5;
     int m0 = (int)blockIdx.y * BM;
-    const int n0 = (int)blockIdx.x * BN;
+    int n0 = (int)blockIdx.x * BN;
+    if constexpr (!MOE) {
+        // workgroup x is a linear tile index, each XCD (x % 8) taking a contiguous run of row-major
+        // tiles: whole rows of tiles per XCD, so each XCD's L2 fetches its activation rows once
+        const int gn = (N + BN - 1) / BN, tiles = gn * ((M + BM - 1) / BM);
+        const int L = xcd_tile((int)blockIdx.x, (int)gridDim.x);
+        if (L >= tiles) return;   // padding of the grid to a multiple of 8 (whole workgroup)
+        m0 = (L / gn) * BM;
+        n0 = (L % gn) * BN;
+    }
     int rows_here = BM;   // MoE: rows of this tile
     if constexpr (MOE) {
         // schedule values are wave-uniform (read once, broadcast), so the row-count dispatch below
@@ -1397,7 +1406,8 @@ hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, fl
     const int splits = split_for<TileL>(wtype, M, N, K);
     if (splits > 1 && !partials) return hipErrorInvalidValue;
     note_engine(KSQ_ENG_MMQ_PLANAR | (splits > 1 ? KSQ_ENG_SPLITK : 0u));
-    const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128), (unsigned)splits);
+    const int tiles = ((N + 127) / 128) * ((M + 127) / 128);
+    const dim3 grid((unsigned)((tiles + 7) / 8 * 8), 1u, (unsigned)splits);   // tile order: xcd_tile
     float* out = splits > 1 ? partials : C;
     if (wtype == kWQ40)
         hipLaunchKernelGGL((mmq_planar_kernel<kWQ40, false>), grid, dim3(256), 0, s, W, A, out, M, N, K / 32, MoeTiles{});

@@ -91,17 +91,11 @@ __device__ __forceinline__ void w16_stage_block(const uint32_t* v, uint16_t* dst
     }
 }
 
-// Linear tile of workgroup x in a grid of gx (a multiple of 8) workgroups: workgroups are handed to
-// the 8 XCDs round robin (XCD = x % 8), so XCD j takes tiles j * gx / 8 .. (j + 1) * gx / 8 - 1,
-// whole rows of row-major tiles: its L2 then holds its activation rows for every column tile
-// (the plain grid spreads each 128-row tile's column tiles over all 8 XCDs, whose L2s each
-// fetch the rows).
-__device__ __forceinline__ int w16_tile(int x, int gx) { return (x % 8) * (gx / 8) + x / 8; }
-
 // WT: kWQ40 or kWQ80.  W: [N][K/32] blocks (4-byte aligned); A: fp32 [M][K] (16-byte aligned);
 // C: fp32 [M][N], or split z's partial [M][N] at C + z*M*N.  nb = K/32, even.
 // XG: workgroup x is a linear tile index whose tiles each XCD takes as one contiguous run in
-// row-major tile order (see w16_tile).
+// row-major tile order (xcd_tile): whole rows of tiles per XCD, so each XCD's L2 fetches its
+// activation rows once (the plain grid spreads each 128-row tile's column tiles over all 8 XCDs).
 template <class T, int WT, bool XG = false>
 __global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__ W, const float* __restrict__ A,
                                                      float* __restrict__ C, int M, int N, int nb) {
@@ -119,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void w16_kernel(const uint8_t* __restrict__
     int tm = (int)blockIdx.y, tn = (int)blockIdx.x;
     if constexpr (XG) {
         const int gn = (N + BN - 1) / BN, tiles = gn * ((M + BM - 1) / BM);
-        const int L = w16_tile((int)blockIdx.x, (int)gridDim.x);
+        const int L = xcd_tile((int)blockIdx.x, (int)gridDim.x);
         if (L >= tiles) return;   // padding of the grid to a multiple of 8 (whole workgroup)
         tm = L / gn;
         tn = L % gn;
