@@ -342,6 +342,19 @@ int ksq_gemm_q4_0_fp16_fused(const uint8_t* weight, const uint16_t* fp16_activat
         e = ksq::launch_mmq(KSQ_W_Q4_0, ksq::kAQ81, weight, aq, output, N, M, K, nullptr, s, /*trans=*/true);
         return e == hipSuccess ? ok() : hip_error(e, "mmq launch");
     }
+    if (N <= 8 && g_path != 2 && g_path != 3) {
+        // up to 8 activation rows: quantise once, then the decode kernels write [M][N] directly.
+        // Two launches; the small-batch MFMA kernel or the split MFMA GEMM would add a transpose
+        // (and a reduction), measured slower at every shape tried (whole call, us: 4096 weight
+        // rows, K = 4096, 8 rows 14.0 -> 11.8; 14336 x 4096, 7 rows 26.5 -> 23.6; 2048 x 4096,
+        // 6 rows 12.8 -> 8.5; 4096 x 14336, 8 rows 26.1 vs 26.4 the one tie)
+        uint8_t* aq = (uint8_t*)p;
+        hipError_t e = ksq::launch_quantize_variant(KSQ_Q81_FUSED_F16, fp16_activation, aq, N, K, s);
+        if (e != hipSuccess) return hip_error(e, "quantize launch");
+        g_engines |= KSQ_ENG_QUANTIZE;
+        e = ksq::launch_gemv_strided(KSQ_W_Q4_0, ksq::kAQ81, weight, aq, output, N, M, K, /*ldc=*/1, /*ldr=*/N, s);
+        return e == hipSuccess ? ok() : hip_error(e, "gemv launch");
+    }
     const size_t gws = align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K));
     float* tmp = (float*)((uint8_t*)p + gws);
     st = ksq_gemm(KSQ_W_Q4_0, KSQ_A_F16, weight, fp16_activation, tmp, N, M, K, gws ? p : nullptr, gws, stream);

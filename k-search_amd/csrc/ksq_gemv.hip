@@ -1377,7 +1377,8 @@ static hipError_t gemv_dispatch(int wtype, int afmt, bool xh, const uint8_t* W, 
             note_engine(is_kquant(wtype) && mr <= 2 ? KSQ_ENG_GEMV_KQ
                         : mr >= 3 ? (QUANT ? KSQ_ENG_GEMV_MR : KSQ_ENG_GEMV_MR_FQ)
                                   : (QUANT ? KSQ_ENG_GEMV_DIRECT : KSQ_ENG_GEMV_DIRECT_FQ));
-            if (mr >= 3 && QUANT && (ldc != N || ldr != 1)) return hipErrorNotSupported;   // row-major output only
+            // the K-quant multi-row form writes a row-major output only
+            if (mr >= 3 && QUANT && wtype == kWQ4K && (ldc != N || ldr != 1)) return hipErrorNotSupported;
             e = direct_dispatch(wtype, afmt, QUANT, xh, mr, rpw, W, Am, Cm, N, nb, ldc, ldr, s);
         } else {
             note_engine(is_fq(AMODE) ? KSQ_ENG_GEMV_ROW_FQ : KSQ_ENG_GEMV_ROW);
@@ -1394,6 +1395,11 @@ static hipError_t gemv_dispatch(int wtype, int afmt, bool xh, const uint8_t* W, 
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s) {
     return gemv_dispatch<true>(wtype, afmt, false, W, A, C, M, N, K, N, 1, s);
+}
+
+hipError_t launch_gemv_strided(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N,
+                               int K, int ldc, int ldr, hipStream_t s) {
+    return gemv_dispatch<true>(wtype, afmt, false, W, A, C, M, N, K, ldc, ldr, s);
 }
 
 // The in-workgroup quantisation is repeated by every workgroup; it beats the separate quantise

@@ -70,6 +70,9 @@ hipError_t launch_transpose_f32(const float* in, float* out, int rows, int cols,
 // wtype: 0 Q4_0, 1 Q8_0, 2 Q4_K, 3 Q6_K, 4 Q4_1, 5 Q5_0, 6 Q5_1.
 hipError_t launch_gemv(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
                        hipStream_t s);
+// The same with output element (m, n) at C[m * ldc + n * ldr] (not for Q4_K at 3-8 rows).
+hipError_t launch_gemv_strided(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N,
+                               int K, int ldc, int ldr, hipStream_t s);
 
 // The same decode kernels on fp32 activations [M][K] (16-byte aligned): every workgroup
 // quantises the activation blocks it needs (block_q8_1, or block_q8s for afmt kAQ8S) into

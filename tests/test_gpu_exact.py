@@ -418,6 +418,13 @@ def test_fp16_fused_orientation_exact(dev):
     (768, 3, 4096, {"gemv_mr_fq"}),
     (1024, 4, 2048, {"gemv_mr_fq"}),
     (1024, 8, 1024, {"gemv_mr_fq"}),
+    # past the in-workgroup quantisation's work limit: one quantise launch, then the multi-row
+    # decode kernel storing [M][N] directly (no transpose; ksq_gemm itself would take the
+    # small-batch MFMA kernel at 8 rows and the split MFMA GEMM at 14336 x 4096 x 8)
+    (4096, 5, 4096, {"quantize", "gemv_mr"}),
+    (14336, 3, 4096, {"quantize", "gemv_mr"}),
+    (4096, 8, 4096, {"quantize", "gemv_mr"}),
+    (14336, 8, 4096, {"quantize", "gemv_mr"}),
     (4096, 512, 1024, {"quantize", "mmq3"}),     # MFMA GEMM writing its tiles transposed
     (384, 40, 1024, {"quantize", "mmq3", "splitk", "transpose"}),   # split-K: [N][M], then transposed
 ])

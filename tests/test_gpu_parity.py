@@ -178,12 +178,18 @@ def test_fp16_activation_entries(dev, oracle, wtype):
         ref = oracle.gemm_f64(wtype, oracle.quantize_q8_1_variant(xh, 3), w, M, N, K)
         wt = _t(w, dev)
         y = ops.gemm(wtype, A_F16, wt, _t(xh, dev), M, N, K)
+        eng = ops.last_engines() - {"quantize"}
         torch.cuda.synchronize()
         assert _rel_err(y.cpu().numpy(), ref) <= TOL, (M, N, K)
         if wtype == 0:
             yt = ops.gemm_q4_0_fp16_fused(wt, _t(xh, dev), N, M, K)
+            eng_t = ops.last_engines() - {"quantize", "transpose"}
             torch.cuda.synchronize()
-            assert np.array_equal(yt.cpu().numpy(), y.cpu().numpy().T), (M, N, K)
+            assert _rel_err(yt.cpu().numpy().T, ref) <= TOL, (M, N, K)
+            # the same kernels give the same bits (up to 8 rows the fused entry takes the decode
+            # kernels where ksq_gemm may take the small-batch MFMA kernel)
+            if eng_t == eng:
+                assert np.array_equal(yt.cpu().numpy(), y.cpu().numpy().T), (M, N, K)
 
 
 def test_golden_fixture_on_gpu(dev):
