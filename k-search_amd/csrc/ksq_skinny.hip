@@ -312,9 +312,18 @@ bool skinny_preferred(int wtype, int M, int N, int K) {
     // N = 14336 (0.6% above the per-shape best over 81 shapes; Q4_0 N = 14336, K = 4096, M = 4:
     // 13.0 decode vs 15.8; N = 3584, K = 3584: 4.8 vs 6.1 the other way)
     if (M <= 5) return N >= 2048 && N < 14336 && K <= 3584;
+    // 6-8 rows (fp32 entry over the definition shapes and BASELINE-like ones, whole call, us, the
+    // register-direct decode kernel against this one): rows of up to 3584 elements stay here
+    // (N = 7168, K = 512, M = 8: 7.2 vs 12.6); at K = 4096 only 4096 <= N < 14336 (Q8_0 N = 14336:
+    // 25.0 vs 29.8 at M = 6, 29.3 vs 32.9 at M = 8; N = 128256: 151 vs 179; N = 2048, Q8_1 input:
+    // 6.3 vs 8.4); rows of up to 6144 elements from N = 7168 on (N = 12288, K = 5120, M = 8: 29.4
+    // vs 37.4); longer rows only below N = 14336 (N = K = 7168: 27.5 vs 28.4; N = 18432, K = 7168:
+    // 46.5 vs 50.5 the other way)
     if (N < 2048) return false;
-    if (K <= 4096) return true;
-    if (K <= 8192) return N >= 7168;
+    if (K <= 3584) return true;
+    if (K <= 4096) return N >= 4096 && N < 14336;
+    if (K <= 6144) return N >= 7168;
+    if (K <= 8192) return N >= 7168 && N < 14336;
     return false;
 }
 
