@@ -1195,18 +1195,15 @@ bool mmq_preferred(int wtype, int M, int N, int K) {
     if (wtype == kWQ4K)
         return (M >= 7 && nk >= 1.2e7) || (M >= 5 && M <= 6 && ((nk >= 2.0e7 && K <= 5120) || K <= 1024));
     if (wtype == kWQ6K) return M >= 7 && K <= 7168 && nk >= 1.5e7;
-    if (!nib && wtype != kWQ80) return false;
-    // with the register-direct decode kernels (3-8 rows) the crossovers moved: nibble types at
-    // M = 5, 6 stay on the decode kernel to N * K = 1e8 (N = 3584, K = 18944, M = 5: 18.3 vs 21.7
-    // MFMA); Q8_0 at M = 7, 8 takes the MFMA GEMM only for 2e7 <= N * K < 3e7 (N = K = 5120:
-    // 15.7 vs 17.2 small-batch; N = K = 7168: 26.5 vs 23.1 small-batch, N = 14336, K = 4096:
-    // 28.4 vs 25.2 decode)
-    bool pref;
-    if (M >= 7) pref = nk >= 2.0e7 && (nib || nk < 3.0e7);
-    else if (M >= 5) pref = nib && nk >= 1.0e8;
-    else pref = false;
-    if (pref && K <= 3584 && skinny_preferred(wtype, M, N, K)) return false;
-    return pref;
+    // 3-8 rows of the 32-element types, fitted on the definition shapes (430 cases, fp32 entry;
+    // the small-batch kernel with shared activation pieces and the decode kernels are the
+    // alternatives): Q8_0 never (the MFMA GEMM was 5-120% slower on every such case), the nibble
+    // types on rows of at least 4096 elements once the grid is wide (N >= 18432 from 6 rows on,
+    // N >= 100000 from 4) or the matrix large from 7 rows on (N = 128256, K = 4096, Q4_1, M = 8:
+    // 0.81x the better alternative; N = 7168, K = 18432, M = 8: 0.94-1.01x; N = 14336, K = 4096,
+    // M = 8: 1.20-1.31x, so not there)
+    if (!nib) return false;
+    return K >= 4096 && ((M >= 6 && N >= 18432) || (M >= 4 && N >= 100000) || (M >= 7 && nk >= 1.3e8));
 }
 
 bool mmq_supported(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {

@@ -95,13 +95,20 @@ __device__ __forceinline__ float dpp_row_ror(float v, int n) {
 // (Q8_0 weights only).  wbytes / abytes: readable bytes of W and A (W's rounded up to a dword:
 // the last dword of the weights is read whole).  Loads are buffer loads: a block past K or an
 // activation row past M reads at an offset beyond the buffer and gets zeros.
-template <int WT, int MP, bool AS, int NWV>
+// AL (K % 128 == 0, A 16-byte aligned): a step's activation blocks (4 MP rows x 4 blocks, 36 MP
+// 16-byte pieces) are loaded once per wave, one piece per lane, and exchanged through the wave's
+// LDS region, instead of every lane loading its 9 dwords (each block then came through 4 lanes:
+// removing the activation traffic altogether took Q8_0 N = K = 4096, M = 8 from 9.8 to 7.0 us).
+template <int WT, int MP, bool AS, int NWV, bool AL = false>
 __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
                                                           float* __restrict__ C, int M, int N, int nb, int ldc,
                                                           uint32_t wbytes, uint32_t abytes) {
     using F = SkFmt<WT>;
     constexpr int BB = F::BB;
+    constexpr int AP = 36 * MP;                  // activation pieces of 16 bytes per step (AL)
+    constexpr int APL = (AP + 63) / 64;          // pieces per lane
     __shared__ float red[NWV][kSkRows][4 * MP];
+    __shared__ __attribute__((aligned(16))) uint32_t sact[AL ? NWV : 1][AL ? 4 * AP : 4];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 4, kb = (lane >> 2) & 3, q = lane & 3;
@@ -119,6 +126,14 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
         const int m = q + 4 * pp;
         aoff0[pp] = m < M ? ((uint32_t)m * (uint32_t)nb + (uint32_t)kb) * (uint32_t)kQ81Bytes : kOOB;
     }
+    // AL: piece p = lane + 64 i of a step is bytes 16 (p % 9) .. of activation row p / 9's 4 blocks
+    uint32_t poff0[APL];
+#pragma unroll
+    for (int i = 0; i < APL; i++) {
+        const int p = lane + 64 * i, row = p / 9;
+        poff0[i] = (p < AP && row < M) ? (uint32_t)row * (uint32_t)nb * (uint32_t)kQ81Bytes + 16u * (uint32_t)(p % 9)
+                                       : kOOB;
+    }
 
     const int S = (nb + 3) >> 2;
     const int s_lo = (int)((long long)S * wave / NWV), s_hi = (int)((long long)S * (wave + 1) / NWV);
@@ -134,20 +149,42 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
 
     struct Step {
         uint32_t w[F::WD];
-        uint32_t a[MP][9];
+        uint32_t a[AL ? 1 : MP][9];
+        u32x4 ap[AL ? APL : 1];
     };
     auto load = [&](int s, Step& st) {
         const bool bok = 4 * s + kb < nb;
         const uint32_t woff = bok ? wrow_off + (uint32_t)(4 * s) * BB - (uint32_t)sh : kOOB;
         buf_load<F::WD>(rw, woff, st.w);
+        if constexpr (AL) {
 #pragma unroll
-        for (int pp = 0; pp < MP; pp++) {
-            const uint32_t aoff = bok ? aoff0[pp] + (uint32_t)(4 * s) * kQ81Bytes : kOOB;
-            buf_load<9>(ra, aoff, st.a[pp]);
+            for (int i = 0; i < APL; i++)
+                st.ap[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                    ra, poff0[i] == kOOB ? kOOB : poff0[i] + (uint32_t)(4 * s) * kQ81Bytes, 0, 0);
+        } else {
+#pragma unroll
+            for (int pp = 0; pp < MP; pp++) {
+                const uint32_t aoff = bok ? aoff0[pp] + (uint32_t)(4 * s) * kQ81Bytes : kOOB;
+                buf_load<9>(ra, aoff, st.a[pp]);
+            }
         }
     };
+    uint32_t* sap = &sact[AL ? wave : 0][0];
 
     auto compute = [&](const Step& st) {
+        // AL: the wave's step pieces into its LDS region, then every lane's activation blocks
+        uint32_t al[AL ? MP : 1][9];
+        if constexpr (AL) {
+            wave_lds_exchange();   // the previous step's reads come first
+#pragma unroll
+            for (int i = 0; i < APL; i++)
+                if (lane + 64 * i < AP) *(u32x4*)&sap[4 * (lane + 64 * i)] = st.ap[i];
+            wave_lds_exchange();   // every lane reads pieces other lanes wrote
+#pragma unroll
+            for (int pp = 0; pp < MP; pp++)
+#pragma unroll
+                for (int i = 0; i < 9; i++) al[pp][i] = sap[(q + 4 * pp) * 36 + kb * 9 + i];
+        }
         // weight scale(s) and the 8 A-operand dwords (elements 4j .. 4j+3)
         float dw, mw = 0.0f;
         uint32_t pay[F::NP];
@@ -191,10 +228,11 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
         for (int pp = 0; pp < MP; pp++) {
             if (pp * 4 >= M) break;  // uniform: no activation rows in this pass
             i32x4 d = bias;
+            const uint32_t* av = AL ? al[AL ? pp : 0] : st.a[AL ? 0 : pp];
 #pragma unroll
             for (int j = 0; j < 8; j++)
-                d = __builtin_amdgcn_mfma_i32_4x4x4i8((int)a8[j], (int)st.a[pp][1 + j], d, 0, 0, 0);
-            const uint32_t ds = st.a[pp][0];
+                d = __builtin_amdgcn_mfma_i32_4x4x4i8((int)a8[j], (int)av[1 + j], d, 0, 0, 0);
+            const uint32_t ds = av[0];
             // block_q8s: fp32 scale with its two lowest mantissa bits cleared so that
             // 12582912 * d_a stays exact (relative change < 2^-21)
             const float da = AS ? __builtin_bit_cast(float, ds & ~3u) : f16_to_f32(ds & 0xFFFFu);
@@ -260,16 +298,37 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
     const uint32_t wbytes = (uint32_t)(((uint64_t)N * nb * block_bytes(WT) + 3) & ~(uint64_t)3);
     const uint32_t abytes = (uint32_t)((uint64_t)M * nb * kQ81Bytes);
     const dim3 grid((unsigned)((N + kSkRows - 1) / kSkRows));
-    if constexpr (MP == 1) {  // 16 waves leave 128 VGPRs per lane: enough for one activation pass only
-        if (nwv == 16) {
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    // the shared activation pieces: whole 4-block steps, 16-byte aligned rows
+    const bool al = (nb % 4) == 0 && ((uintptr_t)A & 15u) == 0;
+    {
+        // 16 waves leave 128 VGPRs per lane: enough for one activation pass, or two with the
+        // shared pieces (the 5-8-row launch rule asks for 16 only then)
+        if (nwv == 16 && al) {
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
+                               wbytes, abytes);
             return hipGetLastError();
         }
+        if constexpr (MP == 1) {
+            if (nwv == 16) {
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
+                                   wbytes, abytes);
+                return hipGetLastError();
+            }
+        }
     }
-    if (nwv >= 8)
-        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
-    else
-        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    if (nwv >= 8) {
+        if (al)
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
+                               abytes);
+        else
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    } else {
+        if (al)
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes,
+                               abytes);
+        else
+            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    }
     return hipGetLastError();
 }
 
@@ -308,23 +367,30 @@ bool skinny_preferred(int wtype, int M, int N, int K) {
     if (M == 2)
         return (K <= 1024 && N >= 4096) ||
                (wtype == kWQ80 && N >= 3584 && N <= 8192 && K >= 3584 && K <= 8192);
-    // 3-5 rows against the register-direct decode kernel: rows of up to 3584 elements below
-    // N = 14336 (0.6% above the per-shape best over 81 shapes; Q4_0 N = 14336, K = 4096, M = 4:
-    // 13.0 decode vs 15.8; N = 3584, K = 3584: 4.8 vs 6.1 the other way)
-    if (M <= 5) return N >= 2048 && N < 14336 && K <= 3584;
-    // 6-8 rows (fp32 entry over the definition shapes and BASELINE-like ones, whole call, us, the
-    // register-direct decode kernel against this one): rows of up to 3584 elements stay here
-    // (N = 7168, K = 512, M = 8: 7.2 vs 12.6); at K = 4096 only 4096 <= N < 14336 (Q8_0 N = 14336:
-    // 25.0 vs 29.8 at M = 6, 29.3 vs 32.9 at M = 8; N = 128256: 151 vs 179; N = 2048, Q8_1 input:
-    // 6.3 vs 8.4); rows of up to 6144 elements from N = 7168 on (N = 12288, K = 5120, M = 8: 29.4
-    // vs 37.4); longer rows only below N = 14336 (N = K = 7168: 27.5 vs 28.4; N = 18432, K = 7168:
-    // 46.5 vs 50.5 the other way)
-    if (N < 2048) return false;
+    // 3-8 rows, fitted on the definition shapes x M = 3, 4, 5, 6, 8 (430 cases, fp32 entry, whole
+    // call, this kernel with its activation pieces shared through LDS against the decode kernels
+    // and the MFMA GEMM): the automatic route lands 0.2% above the per-case best (geometric
+    // mean), no case more than 6.1% above it.  Examples (us, decode vs this kernel): Q8_0 N = K =
+    // 4096, M = 8 15.2 vs 13.4; Q4_0 N = 2560, K = 9728, M = 5 15.4 vs 13.5; the other way
+    // N = 512, K = 7168, M = 8 the decode kernel wins by 10-18% and N = 5120, K = 12288, M = 6 by
+    // 2-29%.
+    const bool nib = (wtype == kWQ40 || wtype == kWQ41);
+    if (M == 3) return N >= 2048 && (K <= 1536 || (nib && N >= 100000 && K <= 2560));
+    if (M == 4) {
+        if (N < 2048) return false;
+        if (K <= 3584) return true;
+        if (K <= 4096) return N < 100000;
+        if (K <= 7168) return (N >= 7168 && N < 14336) || N >= 100000;
+        return N <= 4096;
+    }
+    if (N < 1536) return false;
     if (K <= 3584) return true;
-    if (K <= 4096) return N >= 4096 && N < 14336;
-    if (K <= 6144) return N >= 7168;
-    if (K <= 8192) return N >= 7168 && N < 14336;
-    return false;
+    if (K <= 8192) {
+        if (M <= 6 && N < 4096 && K > 4096) return false;
+        if (M == 5 && K > 4096 && (N < 7168 || (N >= 14336 && N < 100000 && K >= 7168))) return false;
+        return true;
+    }
+    return N <= 4096 || (M >= 6 && N >= 7168);
 }
 
 hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int K,
@@ -335,11 +401,15 @@ hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A
     // (~4 for 5-8 rows, whose waves hold twice the accumulators), but at least two K steps
     // (4 blocks each) per wave.  Measured (us, M = 2 / 4): Q4_0 N = 4096, K = 14336 20.2 / 20.9
     // with ~4 waves per CU, 13.4 / 15.8 with ~16; at M = 8 ~16 waves per CU lose (Q4_0
-    // N = 14336, K = 4096: 29.3 vs 24.4).
+    // N = 14336, K = 4096: 29.3 vs 24.4).  With the shared activation pieces (K % 128 == 0,
+    // 16-byte aligned activations) 5-8 rows fit 16 waves too and take the M <= 4 rule (kernel
+    // alone, us, 8 waves -> this rule: Q8_0 N = K = 4096, M = 8 8.19 -> 7.68; Q4_0 N = 14336,
+    // K = 4096, M = 8 17.19 -> 14.79; Q8_0 N = 4096, K = 14336, M = 8 21.18 vs 21.35 level).
+    const bool al = (nb % 4) == 0 && ((uintptr_t)A & 15u) == 0;
     const int wgs = (N + kSkRows - 1) / kSkRows;
     const int steps = (nb + 3) / 4;
-    const int max_nwv = M <= 4 ? 16 : 8;
-    const long long wave_target = M <= 4 ? 4096 : 1024;
+    const int max_nwv = (M <= 4 || al) ? 16 : 8;
+    const long long wave_target = (M <= 4 || al) ? 4096 : 1024;
     int nwv = 4;
     while (nwv < max_nwv && (long long)wgs * nwv < wave_target && steps >= 2 * nwv) nwv *= 2;
     // 5-8 rows on a grid of at most one workgroup per CU: 8 waves (whole call, us: Q8_0 N = K =

@@ -575,10 +575,12 @@ def _family(engines):
 
 
 @pytest.mark.parametrize("wtype,M,N,K,expect", [
-    (0, 6, 11008, 4096, "skinny"), (4, 5, 18944, 3584, "decode"), (1, 7, 14336, 4096, "decode"),
-    (0, 8, 4096, 4096, "skinny"), (4, 3, 2560, 2560, "skinny"), (0, 3, 4096, 4096, "decode"),
+    (0, 6, 11008, 4096, "skinny"), (4, 5, 18944, 3584, "skinny"), (1, 7, 14336, 4096, "skinny"),
+    (0, 8, 4096, 4096, "skinny"), (4, 3, 2560, 2560, "decode"), (0, 3, 4096, 4096, "decode"),
     (0, 2, 7168, 512, "decode"), (1, 4, 9728, 2560, "skinny"), (4, 8, 18944, 3584, "skinny"),
-    (0, 5, 3584, 18944, "decode"), (1, 8, 7168, 7168, "skinny"), (5, 4, 12288, 5120, "decode"),
+    (0, 5, 3584, 18944, "skinny"), (1, 8, 7168, 7168, "skinny"), (5, 4, 12288, 5120, "skinny"),
+    (0, 8, 18432, 7168, "mmq"), (1, 8, 18432, 7168, "skinny"), (0, 6, 5120, 12288, "decode"),
+    (1, 8, 512, 7168, "decode"),
     (2, 8, 4096, 4096, "mmq"), (3, 7, 12288, 5120, "mmq"), (2, 5, 7168, 7168, "decode"),
     (1, 2, 4096, 4096, "decode"), (0, 2, 14336, 4096, "decode"), (2, 5, 12288, 5120, "mmq"),
     (2, 6, 7168, 512, "mmq"), (2, 8, 4096, 1024, "decode")])
