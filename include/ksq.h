@@ -303,7 +303,7 @@ KSQ_API void moe_w4a32c8_q4_0_fp32_int8(const uint8_t* weight, const float* acti
 /* Path selection for testing and benchmarking, for calls made from the calling host thread
  * (other threads keep their own setting): 0 = automatic (default), 1 = always the v_dot4 decode
  * kernels, 2 = always the int8 MFMA GEMM where it applies, 3 = the 4x4x4-MFMA small-batch
- * kernel for M <= 8 where it applies. */
+ * kernel where it applies (M <= 8; M <= 32 with K % 128 == 0 and 16-byte aligned activations). */
 KSQ_API int ksq_set_path(int path);
 
 /* MFMA tile configuration for tuning, for calls made from the calling host thread: 0 = chosen

@@ -160,7 +160,7 @@ int check_common(int wtype, int atype, const void* weight, const void* activatio
 bool use_mmq(int wtype, int M, int N, int K, const void* W, bool a_aligned16) {
     if (g_path == 1 || !ksq::mmq_supported(wtype, M, N, K, W, a_aligned16)) return false;
     if (g_path == 2) return true;
-    if (g_path == 3) return M > 8;
+    if (g_path == 3) return M > 32;
     return ksq::mmq_preferred(wtype, M, N, K);
 }
 

@@ -1185,7 +1185,9 @@ static int pick_config(int wtype, int M, int N, int K) {
 // rows of up to 7168 elements once N * K >= 1.5e7 (N = 12288, K = 5120, M = 8: 1.30x; with
 // K = 14336 the decode kernel stays 1.15x faster).
 bool mmq_preferred(int wtype, int M, int N, int K) {
-    if (M > 8) return true;
+    // 9-32 rows: the small-batch kernel where it applies (shared activation pieces: K % 128 == 0)
+    // and measured faster
+    if (M > 8) return !(M <= 32 && (K % 128) == 0 && skinny_preferred(wtype, M, N, K));
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
     const double nk = (double)N * (double)K;
     // Q4_K at M = 5, 6 against the register-direct decode kernel: the MFMA GEMM on rows of up to

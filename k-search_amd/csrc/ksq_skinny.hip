@@ -34,7 +34,7 @@ namespace {
 constexpr uint32_t kSkMagic = 0x4B400000u;  // 12582912.0f
 constexpr float kSkMagicF = 12582912.0f;
 constexpr int kSkRows = 16;                 // weight rows per workgroup
-constexpr int kSkPD = 4;                    // K steps in flight per wave
+constexpr int kSkPD2 = 4;                   // K steps in flight per wave (up to 8 rows)
 
 // Per-lane weight registers of one block: the WD dwords from the 4-byte aligned address at or
 // below the block start (Q4_0 18 B, Q8_0 34 B and Q5_0 22 B blocks are only 2-byte aligned; the
@@ -173,17 +173,12 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
 
     auto compute = [&](const Step& st) {
         // AL: the wave's step pieces into its LDS region, then every lane's activation blocks
-        uint32_t al[AL ? MP : 1][9];
         if constexpr (AL) {
             wave_lds_exchange();   // the previous step's reads come first
 #pragma unroll
             for (int i = 0; i < APL; i++)
                 if (lane + 64 * i < AP) *(u32x4*)&sap[4 * (lane + 64 * i)] = st.ap[i];
-            wave_lds_exchange();   // every lane reads pieces other lanes wrote
-#pragma unroll
-            for (int pp = 0; pp < MP; pp++)
-#pragma unroll
-                for (int i = 0; i < 9; i++) al[pp][i] = sap[(q + 4 * pp) * 36 + kb * 9 + i];
+            wave_lds_exchange();   // every lane reads pieces other lanes wrote (per pass, below)
         }
         // weight scale(s) and the 8 A-operand dwords (elements 4j .. 4j+3)
         float dw, mw = 0.0f;
@@ -228,7 +223,12 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
         for (int pp = 0; pp < MP; pp++) {
             if (pp * 4 >= M) break;  // uniform: no activation rows in this pass
             i32x4 d = bias;
-            const uint32_t* av = AL ? al[AL ? pp : 0] : st.a[AL ? 0 : pp];
+            uint32_t al[9];
+            if constexpr (AL) {
+#pragma unroll
+                for (int i = 0; i < 9; i++) al[i] = sap[(q + 4 * pp) * 36 + kb * 9 + i];
+            }
+            const uint32_t* av = AL ? al : st.a[AL ? 0 : pp];
 #pragma unroll
             for (int j = 0; j < 8; j++)
                 d = __builtin_amdgcn_mfma_i32_4x4x4i8((int)a8[j], (int)av[1 + j], d, 0, 0, 0);
@@ -250,7 +250,8 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
         }
     };
 
-    // kSkPD steps in flight (wave-uniform branches only)
+    // PD steps in flight (wave-uniform branches only)
+    constexpr int kSkPD = MP <= 2 ? kSkPD2 : 2;
     Step buf[kSkPD];
 #pragma unroll
     for (int d = 0; d < kSkPD; d++)
@@ -303,10 +304,12 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
     {
         // 16 waves leave 128 VGPRs per lane: enough for one activation pass, or two with the
         // shared pieces (the 5-8-row launch rule asks for 16 only then)
-        if (nwv == 16 && al) {
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
-                               wbytes, abytes);
-            return hipGetLastError();
+        if constexpr (MP <= 4) {
+            if (nwv == 16 && al) {
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
+                                   wbytes, abytes);
+                return hipGetLastError();
+            }
         }
         if constexpr (MP == 1) {
             if (nwv == 16) {
@@ -316,18 +319,26 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
             }
         }
     }
-    if (nwv >= 8) {
-        if (al)
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
-                               abytes);
-        else
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    if constexpr (MP > 2) {
+        // 9-32 rows: the shared activation pieces only (the per-lane form would not fit)
+        if (!al) return hipErrorNotSupported;
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N,
+                           wbytes, abytes);
+        return hipGetLastError();
     } else {
-        if (al)
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes,
-                               abytes);
-        else
-            hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+        if (nwv >= 8) {
+            if (al)
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
+                                   abytes);
+            else
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+        } else {
+            if (al)
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes,
+                                   abytes);
+            else
+                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+        }
     }
     return hipGetLastError();
 }
@@ -335,17 +346,21 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
 template <int WT, bool AS>
 hipError_t skinny_launch_mp(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
                             hipStream_t s) {
-    return M <= 4 ? skinny_launch_nwv<WT, 1, AS>(nwv, W, A, C, M, N, nb, s)
-                  : skinny_launch_nwv<WT, 2, AS>(nwv, W, A, C, M, N, nb, s);
+    if (M <= 4) return skinny_launch_nwv<WT, 1, AS>(nwv, W, A, C, M, N, nb, s);
+    if (M <= 8) return skinny_launch_nwv<WT, 2, AS>(nwv, W, A, C, M, N, nb, s);
+    if (M <= 16) return skinny_launch_nwv<WT, 4, AS>(nwv, W, A, C, M, N, nb, s);
+    return skinny_launch_nwv<WT, 8, AS>(nwv, W, A, C, M, N, nb, s);
 }
 
 }  // namespace
 
 bool skinny_supported(int wtype, int afmt, int M, int N, int K, const void* W, const void* A) {
     const bool type_ok = wtype == kWQ40 || wtype == kWQ80 || wtype == kWQ41 || wtype == kWQ50 || wtype == kWQ51;
-    if (!type_ok || !(afmt == kAQ81 || (afmt == kAQ8S && wtype == kWQ80)) || M < 1 || M > 8 || N < 1 || K < 32 ||
+    if (!type_ok || !(afmt == kAQ81 || (afmt == kAQ8S && wtype == kWQ80)) || M < 1 || M > 32 || N < 1 || K < 32 ||
         (K % 32) != 0 || (((uintptr_t)W | (uintptr_t)A) & 3u) != 0)
         return false;
+    // 9-32 rows only with the shared activation pieces (whole 4-block steps, 16-byte aligned)
+    if (M > 8 && ((K % 128) != 0 || ((uintptr_t)A & 15u) != 0)) return false;
     // buffer offsets are 32-bit and kOOB (2^31) must lie past both buffers
     const uint64_t wbytes = (uint64_t)N * (K / 32) * block_bytes(wtype) + 4, abytes = (uint64_t)M * (K / 32) * kQ81Bytes;
     return wbytes < (1ull << 31) && abytes < (1ull << 31);
@@ -375,6 +390,17 @@ bool skinny_preferred(int wtype, int M, int N, int K) {
     // N = 512, K = 7168, M = 8 the decode kernel wins by 10-18% and N = 5120, K = 12288, M = 6 by
     // 2-29%.
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
+    if (M > 8) {
+        // 9-32 rows (the shared activation pieces; Q8_1 input, us, against the split MFMA GEMM):
+        // 9-16 rows but on large square-ish matrices (Q8_0 N = K = 4096, M = 16: 9.6 vs 12.8;
+        // Q4_0 7.9 vs 12.4; N = 14336, K = 4096: 27.8 vs 28.3 / 21.8 vs 22.3; the other way
+        // N = K = 7168, Q4_0: 22.9 vs 18.9), 17-32 rows (8 passes, one workgroup per CU) only for
+        // the nibble types up to 4096 x 4096 (Q4_0 M = 32: 12.3 vs 13.5; Q8_0 14.7 vs 14.0; N =
+        // 14336, K = 4096: 41.9 vs 24.3)
+        if (!(nib || wtype == kWQ80)) return false;
+        if (M <= 16) return !(N >= 7168 && K >= 7168);
+        return nib && (long long)N * K <= 16777216ll;
+    }
     if (M == 3) return N >= 2048 && (K <= 1536 || (nib && N >= 100000 && K <= 2560));
     if (M == 4) {
         if (N < 2048) return false;

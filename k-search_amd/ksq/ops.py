@@ -260,8 +260,8 @@ def moe_workspace_size(wtype: int, T: int, N: int, K: int, E: int, top_k: int) -
 
 def set_path(path: int) -> None:
     """Routing override for calls from this thread: 0 automatic, 1 v_dot4 decode kernels only,
-    2 int8 MFMA GEMM where it applies, 3 the 4x4x4-MFMA small-batch kernel for M <= 8 where it
-    applies."""
+    2 int8 MFMA GEMM where it applies, 3 the 4x4x4-MFMA small-batch kernel where it applies
+    (M <= 8; M <= 32 with K % 128 == 0 and 16-byte aligned activations)."""
     check(lib().ksq_set_path(path))
 
 

@@ -225,6 +225,9 @@ def _engine_cases():
         cases.append((f"decf_oddnb_w{wt}", wt, 1, 100, 1056, 0, 1, 0, {"gemv_row_fq"}, 0))
         for M in (1, 3, 8):
             cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1024, 1, 3, 0, {"skinny"}, 0))
+        # 9-32 rows (4 and 8 row passes of 4 over the shared activation pieces), ragged rows
+        for M in (12, 17, 32):
+            cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1152, 1, 3, 0, {"skinny"}, 0))
     # the LDS-DMA GEMM (fp32 activations quantised to planar block_q8_1; Q4_0 / Q4_1): split in
     # two along K, with an even (4) and an odd (5) number of 4-block steps per split; ragged M, N
     for wt in (0, 4):
@@ -233,7 +236,7 @@ def _engine_cases():
         # a single row and a ragged 33 rows in one 128-row tile (rows past M read row M-1)
         for M in (1, 33):
             cases.append((f"mmqp_m{M}_w{wt}", wt, M, 136, 512, 0, 2, 8, {"quantize", "mmq_planar"}, 0))
-    cases.append(("splitk_w0", 0, 32, 1024, 8192, 1, 0, 0, {"mmq5", "splitk"}, 0))
+    cases.append(("splitk_w0", 0, 32, 1024, 8192, 1, 2, 0, {"mmq5", "splitk"}, 0))
     cases.append(("splitk_w1", 1, 32, 1024, 8192, 1, 0, 0, {"mmq3", "splitk"}, 0))
     # the native W8A8C8 operator's block_q8s activations: fp32 (its quantiser) and pre-quantised
     for M, path, eng in ((1, 1, {"gemv_direct_fq"}), (5, 3, {"quantize", "skinny"}),

@@ -536,13 +536,13 @@ SKINNY_WTYPES = [0, 1, 4, 5, 6]          # the 32-element block types of the 4x4
 
 @pytest.mark.parametrize("wtype", SKINNY_WTYPES)
 def test_skinny_small_batch(dev, oracle, wtype):
-    """The 4x4x4-MFMA small-batch kernel (path 3) for M = 1..8 on ragged shapes: N not a multiple
+    """The 4x4x4-MFMA small-batch kernel (path 3) for M = 1..32 on ragged shapes: N not a multiple
     of the 16-row workgroup, K steps with a partial last step (K/32 not a multiple of 4), one K
     step in all, and enough steps for every wave count (4, 8, 16 waves per workgroup)."""
     from ksq import synth
     g = np.random.default_rng(2400 + wtype)
     for M, N, K in ((1, 37, 96), (2, 100, 544), (3, 16, 32), (4, 4096, 4096), (5, 75, 1056), (7, 260, 2048),
-                    (8, 1536, 5120), (6, 4100, 4096)):
+                    (8, 1536, 5120), (6, 4100, 4096), (12, 300, 2048), (20, 1040, 4096), (32, 4096, 1024)):
         w = synth.weights(wtype, g, N, K)
         x = synth.activations(g, M, K)
         y = _gpu_gemm(dev, wtype, w, x, M, N, K, path=3)
@@ -581,11 +581,14 @@ def _family(engines):
     (0, 5, 3584, 18944, "skinny"), (1, 8, 7168, 7168, "skinny"), (5, 4, 12288, 5120, "skinny"),
     (0, 8, 18432, 7168, "mmq"), (1, 8, 18432, 7168, "skinny"), (0, 6, 5120, 12288, "decode"),
     (1, 8, 512, 7168, "decode"),
+    # 9-32 rows: the small-batch kernel where measured faster, else the MFMA GEMM
+    (0, 16, 4096, 4096, "skinny"), (1, 12, 4096, 14336, "skinny"), (0, 16, 7168, 7168, "mmq"),
+    (1, 24, 4096, 4096, "mmq"), (0, 32, 4096, 4096, "skinny"), (5, 16, 4096, 4096, "mmq"),
     (2, 8, 4096, 4096, "mmq"), (3, 7, 12288, 5120, "mmq"), (2, 5, 7168, 7168, "decode"),
     (1, 2, 4096, 4096, "decode"), (0, 2, 14336, 4096, "decode"), (2, 5, 12288, 5120, "mmq"),
     (2, 6, 7168, 512, "mmq"), (2, 8, 4096, 1024, "decode")])
 def test_small_m_default_routing(dev, oracle, wtype, M, N, K, expect):
-    """M = 2..8 by default: large matrices take the MFMA GEMM (the measured crossovers), short
+    """M = 2..32 by default: large matrices take the MFMA GEMM (the measured crossovers), short
     rows on wide matrices the 4x4x4-MFMA small-batch kernel, the rest the decode kernel (the
     engine family each shape takes is asserted); each way the fp32 entry matches the oracle,
     with the library pool and with a caller workspace of exactly ksq_gemm_workspace_size bytes."""
