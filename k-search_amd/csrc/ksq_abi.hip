@@ -634,7 +634,7 @@ namespace {
 bool moe_uses_scratch(int top_k) { return top_k >= KSQ_MOE_SCRATCH_MIN_TOPK; }
 
 struct MoeLayout {
-    size_t aq, ids, wts, rows, eend, ntiles, texp, trow0, scratch, total;
+    size_t aq, ids, wts, rows, inv, eend, ntiles, texp, trow0, scratch, total;
     int max_tiles;
 };
 
@@ -660,6 +660,7 @@ MoeLayout moe_layout(int wtype, int T, int N, int K, int E, int top_k) {
     L.ids = off; off = align256(off + ent * 4);
     L.wts = off; off = align256(off + ent * 4);
     L.rows = off; off = align256(off + ent * 4);
+    L.inv = off; off = align256(off + ent * 4);
     L.eend = off; off = align256(off + (size_t)E * 4);
     L.ntiles = off; off = align256(off + 4);
     L.texp = off; off = align256(off + (size_t)L.max_tiles * 4);
@@ -728,36 +729,42 @@ int moe_run(int wtype, const void* weights, const float* activation, const float
         if (e != hipSuccess) return hip_error(e, "fill launch");
     }
     int32_t* rows = (int32_t*)(base + L.rows);
+    int32_t* inv = planar ? (int32_t*)(base + L.inv) : nullptr;   // the scatter quantiser's map
     int32_t* eend = (int32_t*)(base + L.eend);
     int32_t* ntiles = (int32_t*)(base + L.ntiles);
     int32_t* texp = (int32_t*)(base + L.texp);
     int32_t* trow0 = (int32_t*)(base + L.trow0);
+    // the LDS-DMA form clears the output in the routing launch when routing runs in one
+    // workgroup (the rest of the chip is idle meanwhile), else in the quantiser's launch
+    const bool zero_in_route = planar && zero_fused && logits && moe_route_in_group(T, E);
     if (logits && moe_route_in_group(T, E)) {
-        e = ksq::launch_moe_route_group(logits, T, E, top_k, renorm, ids, wts, tile_rows, rows, eend, ntiles, texp,
-                                        trow0, s);
+        e = ksq::launch_moe_route_group(logits, T, E, top_k, renorm, ids, wts, tile_rows, rows, inv, eend, ntiles,
+                                        texp, trow0, zero_in_route ? output : nullptr, zero_in_route ? nout : 0, s);
         if (e != hipSuccess) return hip_error(e, "route launch");
         g_engines |= KSQ_ENG_MOE_ROUTE;
     } else if (logits) {
         // many tokens: one thread per token over the whole chip, then the grouping workgroup
         e = ksq::launch_moe_route(logits, T, E, top_k, renorm, ids, wts, s);
         if (e != hipSuccess) return hip_error(e, "route launch");
-        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
+        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, inv, eend, ntiles, texp, trow0, s);
         if (e != hipSuccess) return hip_error(e, "group launch");
         g_engines |= KSQ_ENG_MOE_ROUTE;
     } else {
         ids = (int32_t*)ids_in;
         wts = (float*)wts_in;
-        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, eend, ntiles, texp, trow0, s);
+        e = ksq::launch_moe_group(ids, T, top_k, E, tile_rows, rows, inv, eend, ntiles, texp, trow0, s);
         if (e != hipSuccess) return hip_error(e, "group launch");
     }
     g_engines |= KSQ_ENG_QUANTIZE | KSQ_ENG_MOE_GROUP;
     ksq::MoeTilesArgs a{ntiles, texp, trow0, eend, rows, wts, scratch, top_k};
     if (planar) {
-        // the LDS-DMA form: the entries' rows quantised in expert-sorted order (the output zeroed in
-        // the same launch), then 128-row tiles of each expert
+        // the LDS-DMA form: each token quantised once into its entries' places in expert-sorted
+        // order (the output zeroed in the routing launch or in this one), then 128-row tiles of each
+        // expert
         const ksq::PlanarQ81 P = ksq::planar_at(aq, moe_planar_rows(T, top_k), K);
-        e = ksq::launch_quantize_planar_gather(activation, P, T * top_k, K, ksq::planar_da_scale(wtype), rows, top_k,
-                                               zero_fused ? output : nullptr, zero_fused ? nout : 0, s);
+        const bool zero_here = zero_fused && !zero_in_route;
+        e = ksq::launch_quantize_planar_scatter(activation, P, T, K, ksq::planar_da_scale(wtype), inv, top_k,
+                                                zero_here ? output : nullptr, zero_here ? nout : 0, s);
         if (e != hipSuccess) return hip_error(e, "quantize launch");
         e = ksq::launch_mmq_planar_moe(wtype, (const uint8_t*)weights, P, output, N, K, L.max_tiles, a, s);
     } else {

@@ -49,11 +49,11 @@ size_t planar_bytes(int M, int K);
 PlanarQ81 planar_at(void* ws, int M, int K);
 // fp32 [M][K] (16-byte aligned, K % 128 == 0) -> planar block_q8_1.
 hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int K, float da_scale, hipStream_t s);
-// The same for the grouped MoE GEMM: planar row m (m < entries) holds x row rows[m] / top_k; rows
-// entries .. y.mp - 1 hold zero blocks (their quants are not written).  With zero non-null the
-// same launch also clears nzero floats there (16-byte aligned, nzero % 4 == 0).
-hipError_t launch_quantize_planar_gather(const float* x, const PlanarQ81& y, int entries, int K, float da_scale,
-                                         const int32_t* rows, int top_k, float* zero, int64_t nzero, hipStream_t s);
+// The same for the grouped MoE GEMM: x row m (m < T) goes to planar rows inv[m * top_k + s] (s <
+// top_k; -1: none); planar rows no entry maps to are not written.  With zero non-null the same
+// launch also clears nzero floats there (16-byte aligned, nzero % 4 == 0).
+hipError_t launch_quantize_planar_scatter(const float* x, const PlanarQ81& y, int T, int K, float da_scale,
+                                          const int32_t* inv, int top_k, float* zero, int64_t nzero, hipStream_t s);
 // The LDS-DMA GEMM (Q4_0 / Q4_1 weights, K % 256 == 0, W 16-byte aligned) on planar
 // activations quantised with da_scale = planar_da_scale(wtype); whether it is the pick for this
 // shape (fp32 activations); partials as launch_mmq (mmq_splits(...) > 1).
@@ -137,7 +137,7 @@ struct MoeTilesArgs {
 // Rows per grouped-GEMM tile (the MoE tile schedule's granularity) for a routing shape.
 int mmq_moe_tile_rows(int wtype, int T, int E, int top_k);
 // Whether the grouped GEMM runs on the LDS-DMA kernel (128-row tiles over planar activations in
-// expert-sorted order, launch_quantize_planar_gather), and that launch.
+// expert-sorted order, launch_quantize_planar_scatter), and that launch.
 bool mmq_moe_planar(int wtype, int T, int E, int top_k, int K);
 hipError_t launch_mmq_planar_moe(int wtype, const uint8_t* W, const PlanarQ81& A, float* C, int N, int K,
                                  int max_tiles, const MoeTilesArgs& a, hipStream_t s);
@@ -148,12 +148,17 @@ hipError_t launch_mmq_moe(int wtype, const uint8_t* W, const uint8_t* Aq, float*
 hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
                             hipStream_t s);
 // Routing and grouping in one launch (one workgroup): launch_moe_route then launch_moe_group.
+// With zero != nullptr, more workgroups of the same launch clear zero[0, nzero) (nzero % 4 == 0,
+// zero 16-byte aligned) meanwhile.
 hipError_t launch_moe_route_group(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
-                                  int tile_rows, int32_t* rows, int32_t* expert_end, int32_t* num_tiles,
-                                  int32_t* tile_expert, int32_t* tile_row0, hipStream_t s);
+                                  int tile_rows, int32_t* rows, int32_t* inv, int32_t* expert_end, int32_t* num_tiles,
+                                  int32_t* tile_expert, int32_t* tile_row0, float* zero, int64_t nzero,
+                                  hipStream_t s);
 // Stable grouping of the T*top_k (token, slot) entries by expert, plus the tile schedule
 // for tiles of `tile_rows` rows.  max_tiles = T*top_k/tile_rows + E bounds num_tiles.
-hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
+// rows[p] = the entry at place p; inv (if non-null) the inverse: inv[entry] = its place, -1 for an
+// entry with an expert id outside [0, E).
+hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows, int32_t* inv,
                             int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
                             hipStream_t s);
 // out[t][n] = sum_s scratch[t*top_k + s][n] in slot order over the slots whose id is in [0, E)

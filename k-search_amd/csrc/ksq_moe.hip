@@ -19,7 +19,7 @@ namespace ksq {
 
 // Softmax over token t's E logits, then the top_k experts by logit (ties -> lower index).
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int top_k, int renorm,
-                                            int32_t* __restrict__ ids, float* __restrict__ w) {
+                                            int32_t* __restrict__ ids, float* __restrict__ w, int32_t* ids2) {
     const float* l = logits + (size_t)t * E;
     float mx = l[0];
     for (int e = 1; e < E; e++) mx = (l[e] > mx) ? l[e] : mx;
@@ -37,6 +37,7 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
         used[best >> 6] |= 1ull << (best & 63);
         const float p = expf(l[best] - mx) / sum;
         ids[(size_t)t * top_k + s] = best;
+        if (ids2) ids2[t * top_k + s] = best;
         w[(size_t)t * top_k + s] = p;
         wsum += p;
     }
@@ -49,7 +50,8 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
 // comparisons and summation order as route_token, so the same ids and weights bit for bit.
 template <int EMAX>
 __device__ __forceinline__ void route_token_regs(const float* __restrict__ logits, int t, int E, int top_k,
-                                                 int renorm, int32_t* __restrict__ ids, float* __restrict__ w) {
+                                                 int renorm, int32_t* __restrict__ ids, float* __restrict__ w,
+                                                 int32_t* ids2) {
     const float* l = logits + (size_t)t * E;
     float v[EMAX];
 #pragma unroll
@@ -78,6 +80,7 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ logit
         used |= 1ull << best;
         const float p = expf(lb - mx) / sum;
         ids[(size_t)t * top_k + s] = best;
+        if (ids2) ids2[t * top_k + s] = best;
         w[(size_t)t * top_k + s] = p;
         wsum += p;
     }
@@ -85,12 +88,13 @@ __device__ __forceinline__ void route_token_regs(const float* __restrict__ logit
         for (int s = 0; s < top_k; s++) w[(size_t)t * top_k + s] /= wsum;
 }
 
+// ids2 (if non-null): a second copy of the ids (the grouping workgroup's LDS copy)
 __device__ __forceinline__ void route_any(const float* __restrict__ logits, int t, int E, int top_k, int renorm,
-                                          int32_t* __restrict__ ids, float* __restrict__ w) {
-    if (E <= 8) route_token_regs<8>(logits, t, E, top_k, renorm, ids, w);
-    else if (E <= 16) route_token_regs<16>(logits, t, E, top_k, renorm, ids, w);
-    else if (E <= 64) route_token_regs<64>(logits, t, E, top_k, renorm, ids, w);
-    else route_token(logits, t, E, top_k, renorm, ids, w);
+                                          int32_t* __restrict__ ids, float* __restrict__ w, int32_t* ids2 = nullptr) {
+    if (E <= 8) route_token_regs<8>(logits, t, E, top_k, renorm, ids, w, ids2);
+    else if (E <= 16) route_token_regs<16>(logits, t, E, top_k, renorm, ids, w, ids2);
+    else if (E <= 64) route_token_regs<64>(logits, t, E, top_k, renorm, ids, w, ids2);
+    else route_token(logits, t, E, top_k, renorm, ids, w, ids2);
 }
 
 __global__ void moe_route_kernel(const float* __restrict__ logits, int T, int E, int top_k, int renorm,
@@ -111,10 +115,20 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int re
 // the same expert's entries is its rank within its wave (ballot + popcount) plus the
 // counts of the waves before it; cursor[e] carries the total across chunks.
 constexpr int kGroupThreads = 1024;
+
+// Workgroup barrier ordering LDS only: the grouping reads no global memory that its own workgroup
+// wrote (its ids come from LDS or from an earlier launch), so its barriers need not wait for the
+// global stores in flight (a plain __syncthreads waits for all of them at every barrier).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 constexpr int kGroupWaves = kGroupThreads / 64;
 
-__device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, int total, int E, int tile_rows,
-                                              int32_t* __restrict__ rows, int32_t* __restrict__ expert_end,
+__device__ __forceinline__ void group_entries(const int32_t* ids, int total, int E, int tile_rows,
+                                              int32_t* __restrict__ rows, int32_t* __restrict__ inv,
+                                              int32_t* __restrict__ expert_end,
                                               int32_t* __restrict__ num_tiles, int32_t* __restrict__ tile_expert,
                                               int32_t* __restrict__ tile_row0) {
     __shared__ int32_t count[256];
@@ -122,12 +136,12 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
     __shared__ int32_t wcnt[kGroupWaves][256];
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     for (int e = t; e < E; e += kGroupThreads) count[e] = 0;
-    __syncthreads();
+    lds_barrier();
     for (int j = t; j < total; j += kGroupThreads) {
         const int e = ids[j];
         if (e >= 0 && e < E) atomicAdd(&count[e], 1);
     }
-    __syncthreads();
+    lds_barrier();
     if (t == 0) {
         // full tiles first, then each expert's ragged last tile: the cheaper ragged workgroups
         // are dispatched last, where they fill the grid's final partial wave
@@ -151,7 +165,7 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
         }
         num_tiles[0] = nt;
     }
-    __syncthreads();
+    lds_barrier();
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     for (int base = 0; base < total; base += kGroupThreads) {
         const int j = base + t;
@@ -163,19 +177,22 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
             if (lane == 0) wcnt[wave][x] = __popcll(m);
             if (e == x) rank = __popcll(m & lt);
         }
-        __syncthreads();
+        lds_barrier();
         if (valid) {
             int off = cursor[e] + rank;
             for (int w = 0; w < wave; w++) off += wcnt[w][e];
             rows[off] = j;
+            if (inv) inv[j] = off;
+        } else if (inv && j < total) {
+            inv[j] = -1;
         }
-        __syncthreads();
+        lds_barrier();
         for (int x = t; x < E; x += kGroupThreads) {
             int add = 0;
             for (int w = 0; w < kGroupWaves; w++) add += wcnt[w][x];
             cursor[x] += add;
         }
-        __syncthreads();
+        lds_barrier();
     }
     // entries with an expert id outside [0, E) were not placed: the list's tail past the placed
     // ones gets entry 0, so that every rows[j] < total names a real token
@@ -185,37 +202,62 @@ __device__ __forceinline__ void group_entries(const int32_t* __restrict__ ids, i
 
 __global__ __launch_bounds__(kGroupThreads) void moe_group_kernel(const int32_t* __restrict__ ids, int total, int E,
                                                                   int tile_rows, int32_t* __restrict__ rows,
+                                                                  int32_t* __restrict__ inv,
                                                                   int32_t* __restrict__ expert_end,
                                                                   int32_t* __restrict__ num_tiles,
                                                                   int32_t* __restrict__ tile_expert,
                                                                   int32_t* __restrict__ tile_row0) {
-    group_entries(ids, total, E, tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
+    group_entries(ids, total, E, tile_rows, rows, inv, expert_end, num_tiles, tile_expert, tile_row0);
 }
 
 // Routing and grouping in one workgroup: the threads route the tokens (each its share), the
 // barrier makes the ids visible to the whole workgroup, then the same grouping as above.
+// Workgroups 1.. of the same launch clear kZeroBytesPerRG bytes each of `zero` (n4 16-byte groups):
+// the output the grouped GEMM accumulates into is cleared while the one routing workgroup works,
+// instead of by workgroups of the quantiser's launch that follows it.
+constexpr int kZeroBytesPerRG = 64 * 1024;
+constexpr int kRouteGroupMaxEntries = 8192;
 __global__ __launch_bounds__(kGroupThreads) void moe_route_group_kernel(
     const float* __restrict__ logits, int T, int E, int top_k, int renorm, int32_t* __restrict__ ids,
-    float* __restrict__ w, int tile_rows, int32_t* __restrict__ rows, int32_t* __restrict__ expert_end,
-    int32_t* __restrict__ num_tiles, int32_t* __restrict__ tile_expert, int32_t* __restrict__ tile_row0) {
-    for (int t = threadIdx.x; t < T; t += kGroupThreads) route_any(logits, t, E, top_k, renorm, ids, w);
-    __syncthreads();
-    group_entries(ids, T * top_k, E, tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
+    float* __restrict__ w, int tile_rows, int32_t* __restrict__ rows, int32_t* __restrict__ inv,
+    int32_t* __restrict__ expert_end, int32_t* __restrict__ num_tiles, int32_t* __restrict__ tile_expert,
+    int32_t* __restrict__ tile_row0, float* __restrict__ zero, int64_t n4) {
+    if (blockIdx.x > 0) {
+        const int64_t base = (int64_t)(blockIdx.x - 1) * (kZeroBytesPerRG / 16);
+        f32x4* z = (f32x4*)zero;
+#pragma unroll
+        for (int i = 0; i < kZeroBytesPerRG / 16 / kGroupThreads; i++) {
+            const int64_t k = base + i * kGroupThreads + threadIdx.x;
+            if (k < n4) z[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        return;
+    }
+    // the grouping reads the ids from an LDS copy (T * top_k <= T * E < kRouteGroupMaxEntries)
+    __shared__ int32_t sids[kRouteGroupMaxEntries];
+    for (int t = threadIdx.x; t < T; t += kGroupThreads) route_any(logits, t, E, top_k, renorm, ids, w, sids);
+    lds_barrier();
+    group_entries(sids, T * top_k, E, tile_rows, rows, inv, expert_end, num_tiles, tile_expert, tile_row0);
 }
 
-hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows,
+hipError_t launch_moe_group(const int32_t* ids, int T, int top_k, int E, int tile_rows, int32_t* rows, int32_t* inv,
                             int32_t* expert_end, int32_t* num_tiles, int32_t* tile_expert, int32_t* tile_row0,
                             hipStream_t s) {
-    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, ids, T * top_k, E, tile_rows, rows,
+    hipLaunchKernelGGL(moe_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, ids, T * top_k, E, tile_rows, rows, inv,
                        expert_end, num_tiles, tile_expert, tile_row0);
     return hipGetLastError();
 }
 
 hipError_t launch_moe_route_group(const float* logits, int T, int E, int top_k, int renorm, int32_t* ids, float* w,
-                                  int tile_rows, int32_t* rows, int32_t* expert_end, int32_t* num_tiles,
-                                  int32_t* tile_expert, int32_t* tile_row0, hipStream_t s) {
-    hipLaunchKernelGGL(moe_route_group_kernel, dim3(1), dim3(kGroupThreads), 0, s, logits, T, E, top_k, renorm, ids, w,
-                       tile_rows, rows, expert_end, num_tiles, tile_expert, tile_row0);
+                                  int tile_rows, int32_t* rows, int32_t* inv, int32_t* expert_end, int32_t* num_tiles,
+                                  int32_t* tile_expert, int32_t* tile_row0, float* zero, int64_t nzero,
+                                  hipStream_t s) {
+    if ((long long)T * top_k > kRouteGroupMaxEntries) return hipErrorInvalidValue;
+    const int64_t n4 = zero ? nzero / 4 : 0;
+    const int64_t zgrid = (n4 * 16 + kZeroBytesPerRG - 1) / kZeroBytesPerRG;
+    if (zgrid >= (1ll << 30)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_route_group_kernel, dim3((unsigned)(1 + zgrid)), dim3(kGroupThreads), 0, s, logits, T, E,
+                       top_k, renorm, ids, w, tile_rows, rows, inv, expert_end, num_tiles, tile_expert, tile_row0, zero,
+                       n4);
     return hipGetLastError();
 }
 

@@ -175,19 +175,23 @@ hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, i
 // t / 4, so that the 4 lanes of a row write its 128 quant bytes, its (d, nc) pairs and its 4 sa
 // halves side by side.  Rows M .. mp-1 quantise zeros: their dn and sa entries are written,
 // their quants are not.
-// GATHER (the grouped MoE GEMM's input): planar row m holds x row rows[m] / top_k (rows = the
-// expert-sorted (token, slot) entries, M of them), and workgroups from x = mp / 64 on clear 32 KiB
-// each of `zero` (n4 16-byte groups; chunk (x - mp / 64) * gridDim.y + y), so that the output the
-// grouped GEMM accumulates into needs no launch of its own.
-template <bool GATHER>
+// SCATTER (the grouped MoE GEMM's input): the rows are the T tokens, read once each, and token m's
+// blocks go to planar rows inv[m * top_k + s] for each of its top_k entries (inv: each (token,
+// slot) entry's place in the expert-sorted order; -1 for an entry the grouping did not place), so
+// that the planar rows come out in expert-sorted order without a second read of any token.  Planar
+// rows that no entry maps to (the padding past the entries) are left as they are: the grouped GEMM
+// reads them only for tile rows whose outputs it discards.  Workgroups from x = ceil(T / 64) on
+// clear 32 KiB each of `zero` (n4 16-byte groups; chunk (x - ceil(T / 64)) * gridDim.y + y).
+template <bool SCATTER>
 __global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __restrict__ x, PlanarQ81 y, int M, int K,
-                                                              float da_scale, const int32_t* __restrict__ rows,
+                                                              float da_scale, const int32_t* __restrict__ inv,
                                                               int top_k, float* __restrict__ zero, int64_t n4) {
     __shared__ float stage[64 * 4 * kQPitch];
     const int t = threadIdx.x;
-    if constexpr (GATHER) {
-        if ((int)blockIdx.x >= y.mp / 64) {
-            const int64_t chunk = ((int64_t)blockIdx.x - y.mp / 64) * gridDim.y + blockIdx.y;
+    if constexpr (SCATTER) {
+        const int qx = (M + 63) / 64;
+        if ((int)blockIdx.x >= qx) {
+            const int64_t chunk = ((int64_t)blockIdx.x - qx) * gridDim.y + blockIdx.y;
             const int64_t base = chunk * (kZeroBytesPerWG / 16);
             if (base >= n4) return;
             f32x4* z = (f32x4*)zero;
@@ -204,10 +208,7 @@ __global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __res
     for (int p = 0; p < 8; p++) {
         const int idx = p * 256 + t, row = idx >> 5, c = idx & 31;   // c: float4 of the row segment
         f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (r0 + row < M) {
-            const int src = GATHER ? rows[r0 + row] / top_k : r0 + row;
-            v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)src * K + kb0 * 32) + c);
-        }
+        if (r0 + row < M) v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)(r0 + row) * K + kb0 * 32) + c);
         float* dst = stage + (row * 4 + (c >> 3)) * kQPitch + (c & 7) * 4;
         dst[0] = v.x;
         dst[1] = v.y;
@@ -221,14 +222,26 @@ __global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __res
     for (int j = 0; j < 32; j++) v[j] = stage[t * kQPitch + j];
     uint32_t q[9];
     quantize_block_q8_1(v, q);
-    if (m < M) {
-        u32x4* dq = (u32x4*)(y.q + (size_t)m * K + (size_t)kb * 32);
-        dq[0] = u32x4{q[1], q[2], q[3], q[4]};
-        dq[1] = u32x4{q[5], q[6], q[7], q[8]};
-    }
     const float d = f16_to_f32(q[0] & 0xFFFFu) * da_scale;
-    *(f32x2*)(y.dn + 2 * ((size_t)kb * y.mp + m)) = f32x2{d, -12582912.0f * d};
-    y.sa[((size_t)(kb0 >> 2) * y.mp + m) * 4 + blk] = (uint16_t)((q[0] >> 16) ^ 0x8000u);
+    const uint16_t sa = (uint16_t)((q[0] >> 16) ^ 0x8000u);
+    auto put = [&](int pm, bool quants) __attribute__((always_inline)) {
+        if (quants) {
+            u32x4* dq = (u32x4*)(y.q + (size_t)pm * K + (size_t)kb * 32);
+            dq[0] = u32x4{q[1], q[2], q[3], q[4]};
+            dq[1] = u32x4{q[5], q[6], q[7], q[8]};
+        }
+        *(f32x2*)(y.dn + 2 * ((size_t)kb * y.mp + pm)) = f32x2{d, -12582912.0f * d};
+        y.sa[((size_t)(kb0 >> 2) * y.mp + pm) * 4 + blk] = sa;
+    };
+    if constexpr (SCATTER) {
+        if (m < M)
+            for (int s = 0; s < top_k; s++) {
+                const int pm = inv[(size_t)m * top_k + s];
+                if (pm >= 0) put(pm, true);
+            }
+    } else {
+        put(m, m < M);
+    }
 }
 
 size_t planar_bytes(int M, int K) {
@@ -260,16 +273,18 @@ hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_planar_gather(const float* x, const PlanarQ81& y, int entries, int K, float da_scale,
-                                         const int32_t* rows, int top_k, float* zero, int64_t nzero, hipStream_t s) {
+hipError_t launch_quantize_planar_scatter(const float* x, const PlanarQ81& y, int T, int K, float da_scale,
+                                          const int32_t* inv, int top_k, float* zero, int64_t nzero, hipStream_t s) {
     if (K <= 0 || K % 128) return hipErrorInvalidValue;
-    if (entries < 0 || y.mp < entries || y.mp % 64) return hipErrorInvalidValue;
+    if (T < 0 || top_k < 1 || y.mp < T * top_k) return hipErrorInvalidValue;
     const int64_t n4 = zero ? nzero / 4 : 0;
     const int64_t zchunks = (n4 * 16 + kZeroBytesPerWG - 1) / kZeroBytesPerWG;
     const int64_t zgrid = (zchunks + K / 128 - 1) / (K / 128);   // chunks spread over grid y too
-    const dim3 grid((unsigned)(y.mp / 64 + zgrid), (unsigned)(K / 128));
-    hipLaunchKernelGGL(quantize_planar_kernel<true>, grid, dim3(256), 0, s, x, y, entries, K, da_scale, rows, top_k,
-                       zero, n4);
+    const int64_t qx = (T + 63) / 64;
+    if (qx + zgrid == 0) return hipSuccess;
+    const dim3 grid((unsigned)(qx + zgrid), (unsigned)(K / 128));
+    hipLaunchKernelGGL(quantize_planar_kernel<true>, grid, dim3(256), 0, s, x, y, T, K, da_scale, inv, top_k, zero,
+                       n4);
     return hipGetLastError();
 }
 
