@@ -45,7 +45,7 @@ INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, published
 # copy gives the same counters (reads x2.0, writes x1.0; profiles/copy_calibration.md).  Each
 # figure names the committed summary it comes from.
 TRAFFIC = {
-    "gemm": (int((44674.6 * 2.0 + 32768.0) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
+    "gemm": (int((47251.4 * 2.0 + 32768.3) * 1024), "profiles/mmq_q4_0_m2048_n4096_k4096.md"),
     "gemv": (int((4641.9 * 2.0 + 32.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "gemv_f32": (int((4723.9 * 2.0 + 16.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "q8_0_M1": (int((8737.4 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
@@ -53,7 +53,7 @@ TRAFFIC = {
     "q8_0_M32": (int(((9342.9 + 2062.5) * 2.0 + 4096.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q4_K_M128": (int(((19039.5 + 10766.5) * 2.0 + 21504.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
     "q6_K_M128": (int((26591.9 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
-    "moe_q4_0_T512_E8_top2": (int(((201000.5 + 8032.2 + 21.3) * 2.0 + 57344.0 + 34208.0 + 12.2) * 1024),
+    "moe_q4_0_T512_E8_top2": (int(((199520.0 + 4149.3 + 35.1) * 2.0 + 57344.0 + 5641.1 + 28688.2) * 1024),
                               "profiles/moe_q4_0_t512_e8_top2.md"),
     "w4a16_q4_0_M1": (int((4732.8 * 2.0 + 16.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
     "w4a16_q4_0_M2048": (int((53707.2 * 2.0 + 32768.0) * 1024), "profiles/w16_q4_0_m1_m2048_n4096_k4096.md"),
