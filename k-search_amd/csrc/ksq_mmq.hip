@@ -138,6 +138,15 @@ __device__ __forceinline__ void read_words_g(const uint8_t* p, uint32_t* w) {
 // T::PIPE (tiles of 128 x 128 with K steps of 4 blocks; 32-element block types, no MoE): the
 // global loads of K step k+1 are issued into registers before step k computes (threads 0..127
 // hold an activation chunk, 128..255 a weight chunk), so their latency hides behind the MFMAs.
+// Slot of 32-byte block kb (0..7) in a staged row: the second chunk's blocks 4..7 swapped in
+// pairs (4 <-> 6, 5 <-> 7), so that the lane pair staging a row's two chunks writes blocks j and
+// 4 + j 64 bytes apart mod 128, i.e. 16 banks apart, instead of 128 bytes apart on the same banks.
+__device__ __forceinline__ constexpr int kslot(int kb) { return kb ^ ((kb >> 1) & 2); }
+// Half (4 block slots, 8 bytes) h of row r of the side-term planes (16-byte rows): the halves of
+// rows 8..15 of every 16 swapped, so that the side-term MFMA's 8-byte reads (lane: row l % 32,
+// half l / 32) of rows r and r + 8 fall 8 bytes apart instead of on the same banks.
+__device__ __forceinline__ constexpr int shalf(int r, int h) { return h ^ ((r >> 3) & 1); }
+
 template <class T, int WT, bool DUMP, bool MOE, int AF>
 __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __restrict__ W,
                                                           const uint8_t* __restrict__ A, float* __restrict__ C,
@@ -153,9 +162,14 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
     __shared__ __attribute__((aligned(16))) uint8_t sA[BM * T::APitch];
     // Q6_K: one more row, all zeros, that the lanes outside a sub-block read
     __shared__ __attribute__((aligned(16))) uint8_t sW[(BN + (S::SUB == 2 ? 1 : 0)) * S::WPitch];
-    __shared__ __attribute__((aligned(16))) float sDa[KB][BM];     // d_a' (d_a/8 for Q4_0)
-    __shared__ __attribute__((aligned(16))) float sNc[KB][BM];     // -12582912 * d_a'
-    __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN]; // weight scale per (sub-)block
+    // The lane pair staging a row's two chunks of 4 blocks writes blocks j and 4 + j at once.
+    // Unpadded, the scale planes put those 4 rows of BM (BN) floats apart, a multiple of the
+    // 32 banks that serve one write; 4 floats of padding per row put them 16 banks apart.  (The
+    // 32-byte blocks of a staged row are placed by kslot for the same reason.)
+    constexpr int SP = 4;
+    __shared__ __attribute__((aligned(16))) float sDa[KB][BM + SP];     // d_a' (d_a/8 for Q4_0)
+    __shared__ __attribute__((aligned(16))) float sNc[KB][BM + SP];     // -12582912 * d_a'
+    __shared__ __attribute__((aligned(16))) float sDw[KB * S::SUB][BN + SP]; // weight scale per (sub-)block
     __shared__ __attribute__((aligned(16))) uint16_t sSaH[BM][8];  // -s_a, fp16 bits (side term)
     // block_q8f: -s_a as three bf16 parts (hi + mid + lo, exact), d_w as two (hi + lo, exact)
     __shared__ __attribute__((aligned(16))) uint16_t sSaB[SIDE_BF ? 3 : 1][SIDE_BF ? BM : 1][8];
@@ -244,12 +258,15 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
             v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
         }
     };
+    // (each row's four 2-byte side values of a chunk leave as one 8-byte write: 2-byte writes 16
+    // bytes apart were LDS bank conflicts)
     auto store_act = [&](int sr, int g, const uint32_t* v) {
+        uint32_t sah[2] = {0u, 0u}, sab[3][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int kb = 4 * g + j;
             const uint32_t* bv = v + ABW * j;
-            u32x4* dst = (u32x4*)(sA + sr * T::APitch + kb * 32);
+            u32x4* dst = (u32x4*)(sA + sr * T::APitch + kslot(kb) * 32);
             dst[0] = u32x4{bv[AQ], bv[AQ + 1], bv[AQ + 2], bv[AQ + 3]};
             dst[1] = u32x4{bv[AQ + 4], bv[AQ + 5], bv[AQ + 6], bv[AQ + 7]};
             // fp32 scales (block_q8s, block_q8f) with their two lowest mantissa bits cleared (22
@@ -268,12 +285,18 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 const __bf16 h = (__bf16)x;
                 const float r = x - (float)h;
                 const __bf16 m = (__bf16)r;
-                sSaB[0][sr][kb] = __builtin_bit_cast(uint16_t, h);
-                sSaB[1][sr][kb] = __builtin_bit_cast(uint16_t, m);
-                sSaB[2][sr][kb] = __builtin_bit_cast(uint16_t, (__bf16)(r - (float)m));
+                const uint32_t sh = 16 * (j & 1);
+                sab[0][j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, h) << sh;
+                sab[1][j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, m) << sh;
+                sab[2][j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(r - (float)m)) << sh;
             }
-            if constexpr (SIDE_MFMA) sSaH[sr][kb] = (uint16_t)((bv[0] >> 16) ^ 0x8000u);
+            if constexpr (SIDE_MFMA) sah[j >> 1] |= ((bv[0] >> 16) ^ 0x8000u) << (16 * (j & 1));
         }
+        if constexpr (SIDE_BF) {
+#pragma unroll
+            for (int e = 0; e < 3; e++) *(u32x2*)&sSaB[e][sr][4 * g] = u32x2{sab[e][0], sab[e][1]};
+        }
+        if constexpr (SIDE_MFMA) *(u32x2*)&sSaH[sr][4 * shalf(sr, g)] = u32x2{sah[0], sah[1]};
     };
     // weight chunk g (4 blocks: 72 / 136 / 80 / 88 / 96 B, 8-byte aligned) of staged row sr
     constexpr int WNW = is_kquant(WT) ? 2 : S::Chunk / 4;
@@ -291,20 +314,22 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
     };
     auto store_w = [&](int sr, int g, const uint32_t* v) {
         if constexpr (!is_kquant(WT)) {
+            uint32_t dwh[2] = {0u, 0u}, dwbf[2][2] = {{0u, 0u}, {0u, 0u}};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int kb = 4 * g + j, off = j * S::BB;
                 const uint32_t dwb = half_at(v, off);
                 sDw[kb][sr] = f16_to_f32(dwb);
                 // side factor against -s_a: d_w (Q4_0, Q5_0) or -m (Q4_1, Q5_1)
-                if constexpr (WT == kWQ41 || WT == kWQ51) sDwH[sr][kb] = (uint16_t)(half_at(v, off + 2) ^ 0x8000u);
-                else sDwH[sr][kb] = (uint16_t)dwb;
+                const uint32_t sh = 16 * (j & 1);
+                if constexpr (WT == kWQ41 || WT == kWQ51) dwh[j >> 1] |= ((half_at(v, off + 2) ^ 0x8000u) & 0xFFFFu) << sh;
+                else dwh[j >> 1] |= (dwb & 0xFFFFu) << sh;
                 if constexpr (SIDE_BF) {
                     // d_w (11 significant bits) as bf16 hi + lo, exact
                     const float dwf = f16_to_f32(dwb);
                     const __bf16 h = (__bf16)dwf;
-                    sDwB[0][sr][kb] = __builtin_bit_cast(uint16_t, h);
-                    sDwB[1][sr][kb] = __builtin_bit_cast(uint16_t, (__bf16)(dwf - (float)h));
+                    dwbf[0][j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, h) << sh;
+                    dwbf[1][j >> 1] |= (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)(dwf - (float)h)) << sh;
                 }
                 if constexpr (WT == kWQ40 || WT == kWQ41) {
                     constexpr int q = (WT == kWQ40) ? 2 : 4;  // offset of qs
@@ -312,7 +337,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                         u32x4{word_at(v, off + q), word_at(v, off + q + 4), word_at(v, off + q + 8),
                               word_at(v, off + q + 12)};
                 } else if constexpr (WT == kWQ80) {
-                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kslot(kb) * 32);
                     dst[0] = u32x4{word_at(v, off + 2), word_at(v, off + 6), word_at(v, off + 10), word_at(v, off + 14)};
                     dst[1] = u32x4{word_at(v, off + 18), word_at(v, off + 22), word_at(v, off + 26), word_at(v, off + 30)};
                 } else {
@@ -327,10 +352,15 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                         o[i] = (w4 & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * i));
                         o[4 + i] = ((w4 >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * i));
                     }
-                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kb * 32);
+                    u32x4* dst = (u32x4*)(sW + sr * S::WPitch + kslot(kb) * 32);
                     dst[0] = u32x4{o[0], o[1], o[2], o[3]};
                     dst[1] = u32x4{o[4], o[5], o[6], o[7]};
                 }
+            }
+            *(u32x2*)&sDwH[sr][4 * shalf(sr, g)] = u32x2{dwh[0], dwh[1]};
+            if constexpr (SIDE_BF) {
+#pragma unroll
+                for (int e = 0; e < 2; e++) *(u32x2*)&sDwB[e][sr][4 * g] = u32x2{dwbf[e][0], dwbf[e][1]};
             }
         }
     };
@@ -398,8 +428,13 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                     ll[j >> 1] = lb;
                 }
             }
-            *(u32x4*)&sDwH[sr][0] = u32x4{hh[0], hh[1], hh[2], hh[3]};
-            *(u32x4*)&sDwL[sr][0] = u32x4{ll[0], ll[1], ll[2], ll[3]};
+            if (shalf(sr, 0)) {
+                *(u32x4*)&sDwH[sr][0] = u32x4{hh[2], hh[3], hh[0], hh[1]};
+                *(u32x4*)&sDwL[sr][0] = u32x4{ll[2], ll[3], ll[0], ll[1]};
+            } else {
+                *(u32x4*)&sDwH[sr][0] = u32x4{hh[0], hh[1], hh[2], hh[3]};
+                *(u32x4*)&sDwL[sr][0] = u32x4{ll[0], ll[1], ll[2], ll[3]};
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 *(u32x4*)(sW + sr * S::WPitch + 16 * i) =
@@ -505,7 +540,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
         }  // staging without prefetch
 
         auto frag_a = [&](int b, int i) -> i32x4 {
-            return *(const i32x4*)(sA + (wm * 32 * TM + i * 32 + l32) * T::APitch + b * 32 + 16 * hi);
+            return *(const i32x4*)(sA + (wm * 32 * TM + i * 32 + l32) * T::APitch + kslot(b) * 32 + 16 * hi);
         };
         auto frag_b = [&](int b, int j) -> i32x4 {
             if constexpr (WT == kWQ4K) {
@@ -522,7 +557,7 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
                 return i32x4{(int)((x.x >> s4) & 0x0F0F0F0Fu), (int)((x.y >> s4) & 0x0F0F0F0Fu),
                              (int)((x.z >> s4) & 0x0F0F0F0Fu), (int)((x.w >> s4) & 0x0F0F0F0Fu)};
             } else {
-                return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + b * 32 + 16 * hi);
+                return *(const i32x4*)(sW + (wn * 32 * TN + j * 32 + l32) * S::WPitch + kslot(b) * 32 + 16 * hi);
             }
         };
         // Q6_K sub-block h of block b: the lanes holding the other half (hi != h) read the zero
@@ -644,14 +679,15 @@ __global__ __launch_bounds__(T::NT, T::OCC) void mmq_kernel(const uint8_t* __res
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 if (MOE && wave_rows <= 32 * i) continue;   // a row tile without rows (wave-uniform)
-                const f16x4 sa4 = *(const f16x4*)&sSaH[wm * 32 * TM + i * 32 + l32][4 * hi];
+                const int arow = wm * 32 * TM + i * 32 + l32;
+                const f16x4 sa4 = *(const f16x4*)&sSaH[arow][4 * shalf(arow, hi)];
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const int wrow = wn * 32 * TN + j * 32 + l32;
-                    const f16x4 dw4 = *(const f16x4*)&sDwH[wrow][4 * hi];
+                    const f16x4 dw4 = *(const f16x4*)&sDwH[wrow][4 * shalf(wrow, hi)];
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(dw4, sa4, acc[i][j], 0, 0, 0);
                     if constexpr (WT == kWQ4K) {
-                        const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * hi];
+                        const f16x4 dl4 = *(const f16x4*)&sDwL[wrow][4 * shalf(wrow, hi)];
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x8f16(dl4, sa4, acc[i][j], 0, 0, 0);
                     }
                 }
