@@ -143,6 +143,18 @@ KSQ_API int ksq_quantize_q8_1(const float* x, uint8_t* y, int M, int K, void* st
 #define KSQ_Q81_FUSED_F16 3
 KSQ_API int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int K, void* stream);
 
+/* Weight quantisers: fp32 x [k] (k % 32 == 0, 16-byte aligned) -> k/32 blocks of block_q4_0
+ * (wtype KSQ_W_Q4_0, 18 bytes) or block_q8_0 (KSQ_W_Q8_0, 34 bytes) at y (2-byte aligned):
+ *   KSQ_WQ_DEVICE  the reference's device kernels quantize_q4_0_kernel / quantize_q8_0_kernel
+ *                  and their launchers quantize_q4_0_cuda / quantize_q8_0_cuda
+ *                  (include/quantize.h:221-297, 343-359): round half to even, NaN -> 0
+ *   KSQ_WQ_REF     quantize_row_q4_0_ref / quantize_row_q8_0_ref (include/quantize.h:34-68,
+ *                  110-131): roundf, a NaN or out-of-range product converts to INT32_MIN
+ * KSQ_ERR_TYPE for another weight type or rule. */
+#define KSQ_WQ_DEVICE 0
+#define KSQ_WQ_REF 1
+KSQ_API int ksq_quantize_weights(int wtype, int rule, const float* x, uint8_t* y, int64_t k, void* stream);
+
 /* The reference's fused FP16-activation GEMM gemm_q4_0_fp16_fused (kernels/gemm/gemm_fused.cuh:
  * 311-338) in its orientation: Q4_0 weight [M][K/32] (M weight rows), fp16 activations [N][K]
  * (uint16 bits, 16-byte aligned), output fp32 [M][N] (weight-row major).  Activations are

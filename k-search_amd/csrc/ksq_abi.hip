@@ -296,6 +296,20 @@ int ksq_quantize_q8_1_variant(int variant, const void* x, uint8_t* y, int M, int
     return ok();
 }
 
+int ksq_quantize_weights(int wtype, int rule, const float* x, uint8_t* y, int64_t k, void* stream) {
+    if (wtype != KSQ_W_Q4_0 && wtype != KSQ_W_Q8_0)
+        return set_error(KSQ_ERR_TYPE, "weight quantiser for Q4_0 or Q8_0 only (wtype=%d)", wtype);
+    if (rule != KSQ_WQ_DEVICE && rule != KSQ_WQ_REF) return set_error(KSQ_ERR_TYPE, "unknown weight quantiser rule %d", rule);
+    if (k < 0 || k % 32) return set_error(KSQ_ERR_SHAPE, "bad element count k=%lld", (long long)k);
+    if (k == 0) return ok();
+    if (!x || !y) return set_error(KSQ_ERR_NULL, "x or y is NULL");
+    if (((uintptr_t)x & 15u) || ((uintptr_t)y & 1u))
+        return set_error(KSQ_ERR_ALIGN, "x must be 16-byte and y 2-byte aligned");
+    hipError_t e = ksq::launch_quantize_weights(wtype, rule, x, y, k / 32, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_error(e, "weight quantize launch");
+    return ok();
+}
+
 size_t ksq_gemm_q4_0_fp16_fused_workspace_size(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     return align256(ksq_gemm_workspace_size(KSQ_W_Q4_0, KSQ_A_F16, N, M, K)) +

@@ -64,6 +64,9 @@ hipError_t launch_mmq_planar(int wtype, const uint8_t* W, const PlanarQ81& A, fl
                              float* partials, hipStream_t s);
 // variant 0-3 of ksq_quantize_q8_1_variant (x fp32, or fp16 bits for variant 3)
 hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64_t rows, int K, hipStream_t s);
+// fp32 weights -> nblocks block_q4_0 (wtype kWQ40) or block_q8_0 (kWQ80) by the reference's device
+// rule (rule 0) or CPU-reference rule (rule 1); x 16-byte aligned, y 2-byte aligned.
+hipError_t launch_quantize_weights(int wtype, int rule, const float* x, uint8_t* y, int64_t nblocks, hipStream_t s);
 // out [cols][rows] = in [rows][cols], fp32
 hipError_t launch_transpose_f32(const float* in, float* out, int rows, int cols, hipStream_t s);
 // Decode GEMV/GEMM on v_dot4 (mul_mat_vec_q family), any M.

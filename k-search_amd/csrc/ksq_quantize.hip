@@ -403,6 +403,102 @@ hipError_t launch_quantize_variant(int variant, const void* x, uint8_t* y, int64
     return hipGetLastError();
 }
 
+// ---- device weight quantisers (fp32 -> block_q4_0 / block_q8_0), one lane per block --------
+// RULE 0, the reference's device kernels quantize_q4_0_kernel / quantize_q8_0_kernel
+// (include/quantize.h:221-297): amax by fmaxf, d = amax / 7 (Q4_0) or / 127 (Q8_0), stored as
+// half(d); id = 1 / d (0 when d = 0); q = __float2int_rn(x * id) (half to even, NaN -> 0,
+// saturating), then Q4_0 adds 8 (with 32-bit wrap, as the device's add does) and clamps to
+// [0, 15], Q8_0 clamps to [-128, 127].  RULE 1, the CPU references quantize_row_q4_0_ref /
+// quantize_row_q8_0_ref (include/quantize.h:34-68, 110-131): the same with (int)roundf(x * id)
+// (half away from zero; a NaN or out-of-range value converts to INT32_MIN, as on x86).
+// Q4_0 packs element j in the low nibble and element j + 16 in the high nibble of byte j.
+__device__ __forceinline__ int32_t cvt_rn_sat(float r) {   // __float2int_rn of a rounded value
+    if (r != r) return 0;
+    if (r >= 2147483648.0f) return INT32_MAX;
+    if (r < -2147483648.0f) return INT32_MIN;
+    return (int32_t)r;
+}
+__device__ __forceinline__ int32_t cvt_x86(float r) {      // (int) of a rounded value on x86
+    return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
+}
+
+template <int WT, int RULE>
+__global__ __launch_bounds__(256) void quantize_weights_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                               int64_t nblocks) {
+    static_assert(WT == kWQ40 || WT == kWQ80, "Q4_0 or Q8_0 blocks");
+    const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    float v[32];
+    const f32x4* src = (const f32x4*)(x + b * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const f32x4 q = src[i];
+        v[4 * i] = q.x; v[4 * i + 1] = q.y; v[4 * i + 2] = q.z; v[4 * i + 3] = q.w;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 32; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[j]));
+    const float d = amax / (WT == kWQ40 ? 7.0f : 127.0f);
+    const float id = (d > 0.0f) ? 1.0f / d : 0.0f;
+    auto qv = [&](float f) -> int32_t {
+        return RULE == 0 ? cvt_rn_sat(__builtin_rintf(f * id)) : cvt_x86(__builtin_roundf(f * id));
+    };
+    constexpr int NH = block_bytes(WT) / 2;   // 9 or 17 halves
+    uint16_t* dst = y + b * NH;
+    dst[0] = (uint16_t)f32_to_f16(d);
+    if constexpr (WT == kWQ40) {
+#pragma unroll
+        for (int h = 0; h < 8; h++) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const int j = 2 * h + e;
+                int32_t q0 = qv(v[j]), q1 = qv(v[j + 16]);
+                if (RULE == 0) {
+                    q0 = (int32_t)((uint32_t)q0 + 8u);
+                    q1 = (int32_t)((uint32_t)q1 + 8u);
+                } else {
+                    q0 = q0 == INT32_MIN ? q0 : q0 + 8;
+                    q1 = q1 == INT32_MIN ? q1 : q1 + 8;
+                }
+                q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+                q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+                pair |= (uint32_t)((q1 << 4) | q0) << (8 * e);
+            }
+            dst[1 + h] = (uint16_t)pair;
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 16; h++) {
+            uint32_t pair = 0;
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                int32_t q = qv(v[2 * h + e]);
+                q = q < -128 ? -128 : (q > 127 ? 127 : q);
+                pair |= (uint32_t)(q & 0xFF) << (8 * e);
+            }
+            dst[1 + h] = (uint16_t)pair;
+        }
+    }
+}
+
+hipError_t launch_quantize_weights(int wtype, int rule, const float* x, uint8_t* y, int64_t nblocks, hipStream_t s) {
+    if (nblocks <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((nblocks + 255) / 256)), blk(256);
+    uint16_t* out = (uint16_t*)y;
+    if (wtype == kWQ40 && rule == 0)
+        hipLaunchKernelGGL((quantize_weights_kernel<kWQ40, 0>), grid, blk, 0, s, x, out, nblocks);
+    else if (wtype == kWQ40 && rule == 1)
+        hipLaunchKernelGGL((quantize_weights_kernel<kWQ40, 1>), grid, blk, 0, s, x, out, nblocks);
+    else if (wtype == kWQ80 && rule == 0)
+        hipLaunchKernelGGL((quantize_weights_kernel<kWQ80, 0>), grid, blk, 0, s, x, out, nblocks);
+    else if (wtype == kWQ80 && rule == 1)
+        hipLaunchKernelGGL((quantize_weights_kernel<kWQ80, 1>), grid, blk, 0, s, x, out, nblocks);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 // out[c][r] = in[r][c] for in [rows][cols]: 32 x 32 tiles through LDS (33-float pitch, so
 // the column reads are conflict free), 256 threads = 32 columns x 8 row groups.
 __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restrict__ in, float* __restrict__ out,

@@ -18,6 +18,7 @@ W_Q4_0, W_Q8_0, W_Q4_K, W_Q6_K, W_Q4_1, W_Q5_0, W_Q5_1 = 0, 1, 2, 3, 4, 5, 6
 A_F32, A_Q8_1, A_F32_Q8S, A_Q8S, A_F16 = 0, 1, 2, 3, 4
 A_Q8F, A_F32_Q8F_RNE, A_F32_Q8F_LROUND = 5, 6, 7
 Q8F_RNE, Q8F_LROUND = 0, 1   # KSQ_Q8F_* rules of ksq_quantize_q8f
+WQ_DEVICE, WQ_REF = 0, 1      # KSQ_WQ_* rules of ksq_quantize_weights
 NOALLOC_SCRATCH_BYTES = 32 << 20   # KSQ_NOALLOC_SCRATCH_BYTES
 # KSQ_ENG_* bits of ksq_debug_last_engines (include/ksq.h)
 ENG = {"quantize": 1 << 0, "gemv_row": 1 << 1, "gemv_row_fq": 1 << 2, "gemv_direct": 1 << 3,
@@ -60,6 +61,7 @@ SIGNATURES = {
     "ksq_quantize_q8_1": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8s": ([_P, _P, _I, _I, _P], _I),
     "ksq_quantize_q8_1_variant": ([_I, _P, _P, _I, _I, _P], _I),
+    "ksq_quantize_weights": ([_I, _I, _P, _P, ctypes.c_int64, _P], _I),
     "ksq_gemm_q4_0_fp16_fused_workspace_size": ([_I, _I, _I], _SZ),
     "ksq_gemm_q4_0_fp16_fused": ([_P, _P, _P, _I, _I, _I, _P, _SZ, _P], _I),
     "ksq_gemm_workspace_size": ([_I, _I, _I, _I, _I], _SZ),

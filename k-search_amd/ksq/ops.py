@@ -140,6 +140,21 @@ def quantize_q8_1_variant(x: torch.Tensor, variant: int, out: torch.Tensor | Non
     return out
 
 
+def quantize_weights(wtype: int, x: torch.Tensor, rule: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 [..., K] -> uint8 [..., K/32, 18 | 34] block_q4_0 (wtype W_Q4_0) / block_q8_0 (W_Q8_0) on
+    the device: rule WQ_DEVICE the reference's quantize_q4_0_kernel / quantize_q8_0_kernel
+    (half-to-even), WQ_REF its CPU references quantize_row_q4_0_ref / quantize_row_q8_0_ref."""
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise RuntimeError("quantize_weights expects a CUDA float32 tensor")
+    x = x.contiguous()
+    K = x.shape[-1]
+    bpb = 18 if wtype == 0 else 34
+    if out is None:
+        out = torch.empty((*x.shape[:-1], K // 32, bpb), dtype=torch.uint8, device=x.device)
+    check(lib().ksq_quantize_weights(wtype, rule, _ptr(x), _ptr(out), x.numel(), _stream()))
+    return out
+
+
 def quantize_q8s(x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 [..., K] -> uint8 [..., K/32, 36] block_q8s (the native W8A8C8 operator's rules)."""
     if x.dtype != torch.float32 or not x.is_cuda:

@@ -200,6 +200,52 @@ KSQ_API void ksq_ref_quantize_row_q4_0(const float* x, uint8_t* y, int64_t k) {
     }
 }
 
+/* The reference's device weight quantisers quantize_q4_0_kernel / quantize_q8_0_kernel
+ * (include/quantize.h:221-297): amax by fmaxf, d = amax/7 (Q4_0) or amax/127 (Q8_0), half(d);
+ * id = 1/d or 0; q = __float2int_rn(x*id): round half to even (rintf in the default rounding
+ * mode), NaN -> 0, out of range saturating; Q4_0 then adds 8 in 32-bit two's complement (the
+ * device add wraps) and clamps to [0, 15]; Q8_0 clamps to [-128, 127]. */
+static inline int32_t cvt_i32_device(float r);   /* NaN -> 0, saturating (defined below) */
+static int32_t cvt_rn_sat(float v) { return cvt_i32_device(rintf(v)); }
+
+KSQ_API void ksq_ref_quantize_q4_0_device(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK4_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * KSQ_QK4_0;
+        uint8_t* blk = y + i * 18;
+        float amax = 0.0f;
+        for (int j = 0; j < KSQ_QK4_0; j++) amax = fmaxf(amax, fabsf(xs[j]));
+        const float d = amax / 7.0f;
+        wr_f16(blk, d);
+        const float id = (d > 0) ? 1.0f / d : 0.0f;
+        for (int j = 0; j < KSQ_QK4_0 / 2; j++) {
+            int32_t q0 = (int32_t)((uint32_t)cvt_rn_sat(xs[j] * id) + 8u);
+            int32_t q1 = (int32_t)((uint32_t)cvt_rn_sat(xs[j + 16] * id) + 8u);
+            q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+            q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+            blk[2 + j] = (uint8_t)((q1 << 4) | (q0 & 0x0F));
+        }
+    }
+}
+
+KSQ_API void ksq_ref_quantize_q8_0_device(const float* x, uint8_t* y, int64_t k) {
+    const int64_t nb = k / KSQ_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float* xs = x + i * KSQ_QK8_0;
+        uint8_t* blk = y + i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < KSQ_QK8_0; j++) amax = fmaxf(amax, fabsf(xs[j]));
+        const float d = amax / 127.0f;
+        wr_f16(blk, d);
+        const float id = (d > 0) ? 1.0f / d : 0.0f;
+        for (int j = 0; j < KSQ_QK8_0; j++) {
+            int32_t q = cvt_rn_sat(xs[j] * id);
+            q = q < -128 ? -128 : (q > 127 ? 127 : q);
+            blk[2 + j] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
 /* dequantize_row_q4_0 (include/quantize.h:80-100). */
 KSQ_API void ksq_ref_dequantize_row_q4_0(const uint8_t* x, float* y, int64_t k) {
     const int64_t nb = k / KSQ_QK4_0;

@@ -52,7 +52,7 @@ def lib() -> ctypes.CDLL:
         for name in ("quantize_row_q8_1", "quantize_row_q8_0", "quantize_row_q4_0",
                      "quantize_row_q4_1", "quantize_row_q5_0", "quantize_row_q5_1", "quantize_row_q8s",
                      "dequantize_row_q4_0", "dequantize_row_q8_0", "dequantize_row_q8_1",
-                     "dequantize_row_q4_K", "dequantize_row_q6_K"):
+                     "dequantize_row_q4_K", "dequantize_row_q6_K", "quantize_q4_0_device", "quantize_q8_0_device"):
             f = getattr(L, "ksq_ref_" + name)
             f.argtypes = [P, P, i64]
             f.restype = None
@@ -144,6 +144,24 @@ def quantize_q4_0(x: np.ndarray) -> np.ndarray:
     M, K = x.shape
     y = np.empty((M, K // 32, 18), dtype=np.uint8)
     lib().ksq_ref_quantize_row_q4_0(_p(x), _p(y), M * K)
+    return y
+
+
+def quantize_weights(wtype: int, x: np.ndarray, rule: int = 0) -> np.ndarray:
+    """fp32 [N, K] -> block_q4_0 (wtype 0) / block_q8_0 (wtype 1) bytes [N, K/32, 18 | 34]: rule 0
+    the reference's device kernels (include/quantize.h:221-297), rule 1 its CPU references
+    (quantize_row_q4_0_ref / quantize_row_q8_0_ref)."""
+    if rule == 1:
+        return quantize_q4_0(x) if wtype == 0 else quantize_q8_0(x)
+    name = {0: "quantize_q4_0_device", 1: "quantize_q8_0_device"}[wtype]
+    return _quantize_raw(name, x, 18 if wtype == 0 else 34)
+
+
+def _quantize_raw(name: str, x: np.ndarray, bytes_per_block: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    y = np.empty((M, K // 32, bytes_per_block), dtype=np.uint8)
+    getattr(lib(), "ksq_ref_" + name)(_p(x), _p(y), M * K)
     return y
 
 
