@@ -169,7 +169,7 @@ hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, i
 
 // ---- planar block_q8_1 (the LDS-DMA GEMM's input) ---------------------------------------
 // The same blocks as quantize_q8_1_kernel<kQF81> (same device quantiser, bit for bit), written
-// as the planes of PlanarQ81.  A workgroup owns 64 rows x 4 blocks: it reads the 64 row
+// as the planes of PlanarQ81.  A workgroup owns R rows x 4 blocks: it reads the R row
 // segments of 512 bytes with coalesced 16-byte loads into LDS ([row][block] with a 33-float
 // pitch, so the per-lane block reads are conflict free), and lane t quantises block t % 4 of row
 // t / 4, so that the 4 lanes of a row write its 128 quant bytes, its (d, nc) pairs and its 4 sa
@@ -182,11 +182,15 @@ hipError_t launch_quantize_q8_1_zero(const float* x, uint8_t* y, int64_t rows, i
 // rows that no entry maps to (the padding past the entries) are left as they are: the grouped GEMM
 // reads them only for tile rows whose outputs it discards.  Workgroups from x = ceil(T / 64) on
 // clear 32 KiB each of `zero` (n4 16-byte groups; chunk (x - ceil(T / 64)) * gridDim.y + y).
-template <bool SCATTER>
-__global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __restrict__ x, PlanarQ81 y, int M, int K,
+// R rows per workgroup (4 R threads, each loading 8 16-byte pieces): the dense form takes 16 rows
+// (8 KiB per workgroup, the read curve's best shape at this size): 10.47 -> 10.00 us at config 2
+// against 64 rows, three trace pairs.
+template <bool SCATTER, int R = 64>
+__global__ __launch_bounds__(4 * R) void quantize_planar_kernel(const float* __restrict__ x, PlanarQ81 y, int M, int K,
                                                               float da_scale, const int32_t* __restrict__ inv,
                                                               int top_k, float* __restrict__ zero, int64_t n4) {
-    __shared__ float stage[64 * 4 * kQPitch];
+    static_assert(!SCATTER || R == 64, "the scatter form's clearing workgroups are 256 threads");
+    __shared__ float stage[R * 4 * kQPitch];
     const int t = threadIdx.x;
     if constexpr (SCATTER) {
         const int qx = (M + 63) / 64;
@@ -203,10 +207,10 @@ __global__ __launch_bounds__(256) void quantize_planar_kernel(const float* __res
             return;
         }
     }
-    const int r0 = (int)blockIdx.x * 64, kb0 = (int)blockIdx.y * 4;
+    const int r0 = (int)blockIdx.x * R, kb0 = (int)blockIdx.y * 4;
 #pragma unroll
     for (int p = 0; p < 8; p++) {
-        const int idx = p * 256 + t, row = idx >> 5, c = idx & 31;   // c: float4 of the row segment
+        const int idx = p * 4 * R + t, row = idx >> 5, c = idx & 31;   // c: float4 of the row segment
         f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if (r0 + row < M) v = __builtin_nontemporal_load((const f32x4*)(x + (size_t)(r0 + row) * K + kb0 * 32) + c);
         float* dst = stage + (row * 4 + (c >> 3)) * kQPitch + (c & 7) * 4;
@@ -267,8 +271,9 @@ PlanarQ81 planar_at(void* ws, int M, int K) {
 hipError_t launch_quantize_planar(const float* x, const PlanarQ81& y, int M, int K, float da_scale, hipStream_t s) {
     if (M <= 0 || K <= 0) return hipSuccess;
     if (K % 128) return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(y.mp / 64), (unsigned)(K / 128));
-    hipLaunchKernelGGL(quantize_planar_kernel<false>, grid, dim3(256), 0, s, x, y, M, K, da_scale, nullptr, 1,
+    constexpr int R = 16;
+    const dim3 grid((unsigned)(y.mp / R), (unsigned)(K / 128));
+    hipLaunchKernelGGL((quantize_planar_kernel<false, R>), grid, dim3(4 * R), 0, s, x, y, M, K, da_scale, nullptr, 1,
                        nullptr, (int64_t)0);
     return hipGetLastError();
 }
