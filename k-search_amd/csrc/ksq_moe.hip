@@ -116,6 +116,17 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int top_k, int re
 // counts of the waves before it; cursor[e] carries the total across chunks.
 constexpr int kGroupThreads = 1024;
 
+// Inclusive prefix sum of v over the 64 lanes of a wave (all lanes active).
+__device__ __forceinline__ int wave_iscan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
 // Workgroup barrier ordering LDS only: the grouping reads no global memory that its own workgroup
 // wrote (its ids come from LDS or from an earlier launch), so its barriers need not wait for the
 // global stores in flight (a plain __syncthreads waits for all of them at every barrier).
@@ -142,28 +153,42 @@ __device__ __forceinline__ void group_entries(const int32_t* ids, int total, int
         if (e >= 0 && e < E) atomicAdd(&count[e], 1);
     }
     lds_barrier();
-    if (t == 0) {
-        // full tiles first, then each expert's ragged last tile: the cheaper ragged workgroups
-        // are dispatched last, where they fill the grid's final partial wave
-        int acc = 0, nt = 0;
-        for (int e = 0; e < E; e++) {
-            cursor[e] = acc;
-            for (int r = 0; r + tile_rows <= count[e]; r += tile_rows) {
-                tile_expert[nt] = e;
-                tile_row0[nt] = acc + r;
-                nt++;
+    if (t < 64) {
+        // wave 0, 64 experts per pass, lane e - c0 holding expert e: prefix sums over the experts
+        // give each its entry offset and its tile slots.  Full tiles first, then each expert's
+        // ragged last tile: the cheaper ragged workgroups are dispatched last, where they fill the
+        // grid's final partial wave.  (The same schedule as one thread walking the experts in order,
+        // which took 1.8-2.2 us for 8 experts on its chain of dependent reads.)
+        int acc = 0, nfull = 0;
+        for (int c0 = 0; c0 < E; c0 += 64) {
+            const int e = c0 + lane;
+            const int ce = e < E ? count[e] : 0, nf = ce / tile_rows;
+            const int sc = wave_iscan(ce), sf = wave_iscan(nf);
+            const int cur = acc + sc - ce, f0 = nfull + sf - nf;
+            if (e < E) {
+                cursor[e] = cur;
+                expert_end[e] = cur + ce;
+                for (int r = 0; r < nf; r++) {
+                    tile_expert[f0 + r] = e;
+                    tile_row0[f0 + r] = cur + r * tile_rows;
+                }
             }
-            acc += count[e];
-            expert_end[e] = acc;
+            acc += __shfl(sc, 63, 64);
+            nfull += __shfl(sf, 63, 64);
         }
-        for (int e = 0; e < E; e++) {
-            if (count[e] % tile_rows) {
-                tile_expert[nt] = e;
-                tile_row0[nt] = expert_end[e] - count[e] % tile_rows;
-                nt++;
+        int nrag = 0;
+        for (int c0 = 0; c0 < E; c0 += 64) {
+            const int e = c0 + lane;
+            const int ce = e < E ? count[e] : 0, rg = (ce % tile_rows) != 0;
+            const int sr = wave_iscan(rg);
+            if (e < E && rg) {
+                const int slot = nfull + nrag + sr - 1;
+                tile_expert[slot] = e;
+                tile_row0[slot] = cursor[e] + ce - ce % tile_rows;
             }
+            nrag += __shfl(sr, 63, 64);
         }
-        num_tiles[0] = nt;
+        if (lane == 0) num_tiles[0] = nfull + nrag;
     }
     lds_barrier();
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
