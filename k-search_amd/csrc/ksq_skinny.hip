@@ -1,4 +1,5 @@
-// ksq_skinny.hip - small-batch GEMM (M <= 8 activation rows) on the 4x4x4 int8 MFMA.
+// ksq_skinny.hip - small-batch GEMM: up to 8 activation rows on the 4x4x4 int8 MFMA, 9-32 rows on the
+// 16x16x32 int8 MFMA (skinny16_kernel, below).
 //
 // Reference path: the decode GEMVs of kernelevalplus-main/kernels/gemm/gemm_warp_optimized.cuh:108-1212
 // run with batch > 1 (one warp per weight row, DP4A per activation row) and the block formulas of
@@ -68,6 +69,45 @@ __device__ __forceinline__ void buf_load(__amdgpu_buffer_rsrc_t r, uint32_t off,
         typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
         const u32x3 v = __builtin_amdgcn_raw_buffer_load_b96(r, off + 4 * B, 0, 0);
         out[B] = v.x; out[B + 1] = v.y; out[B + 2] = v.z;
+    }
+}
+
+// One weight block from its load window (F::WD dwords from the 4-byte aligned address at or below
+// the block start, sh = the block start's byte offset in the first dword): the fp16 scale (and
+// min), and the 32 quants as int8 in 8 dwords (elements 4j .. 4j+3 in a8[j]; the nibble types'
+// 0..15 / 0..31 codes, whose offsets the block formula carries).
+template <int WT>
+__device__ __forceinline__ void sk_unpack(const uint32_t* w, int sh, uint32_t (&a8)[8], float& dw, float& mw) {
+    using F = SkFmt<WT>;
+    uint32_t pay[F::NP];
+    mw = 0.0f;
+    if constexpr (F::al4) {
+        dw = f16_to_f32(w[0] & 0xFFFFu);
+        mw = f16_to_f32(w[0] >> 16);
+#pragma unroll
+        for (int i = 0; i < F::NP; i++) pay[i] = w[1 + i];
+    } else {
+        // d at byte sh of the window, the payload from byte sh + 2 (2 or 4)
+        dw = f16_to_f32((w[0] >> (8 * sh)) & 0xFFFFu);
+#pragma unroll
+        for (int i = 0; i < F::NP; i++) pay[i] = sh ? w[i + 1] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+    }
+    if constexpr (WT == kWQ80) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) a8[j] = pay[j];
+    } else if constexpr (WT == kWQ40 || WT == kWQ41) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a8[j] = pay[j] & 0x0F0F0F0Fu;
+            a8[4 + j] = (pay[j] >> 4) & 0x0F0F0F0Fu;
+        }
+    } else {
+        const uint32_t h = pay[0];  // qh: bit e = bit 4 of element e
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a8[j] = (pay[1 + j] & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * j));
+            a8[4 + j] = ((pay[1 + j] >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * j));
+        }
     }
 }
 
@@ -181,38 +221,9 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
             wave_lds_exchange();   // every lane reads pieces other lanes wrote (per pass, below)
         }
         // weight scale(s) and the 8 A-operand dwords (elements 4j .. 4j+3)
-        float dw, mw = 0.0f;
-        uint32_t pay[F::NP];
-        if constexpr (F::al4) {
-            dw = f16_to_f32(st.w[0] & 0xFFFFu);
-            mw = f16_to_f32(st.w[0] >> 16);
-#pragma unroll
-            for (int i = 0; i < F::NP; i++) pay[i] = st.w[1 + i];
-        } else {
-            // d at byte sh of the window, the payload from byte sh + 2 (2 or 4)
-            dw = f16_to_f32((st.w[0] >> (8 * sh)) & 0xFFFFu);
-#pragma unroll
-            for (int i = 0; i < F::NP; i++)
-                pay[i] = sh ? st.w[i + 1] : __builtin_amdgcn_alignbyte(st.w[i + 1], st.w[i], 2);
-        }
+        float dw, mw;
         uint32_t a8[8];
-        if constexpr (WT == kWQ80) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) a8[j] = pay[j];
-        } else if constexpr (WT == kWQ40 || WT == kWQ41) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                a8[j] = pay[j] & 0x0F0F0F0Fu;
-                a8[4 + j] = (pay[j] >> 4) & 0x0F0F0F0Fu;
-            }
-        } else {
-            const uint32_t h = pay[0];  // qh: bit e = bit 4 of element e
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                a8[j] = (pay[1 + j] & 0x0F0F0F0Fu) | qh_to_bit4(h >> (4 * j));
-                a8[4 + j] = ((pay[1 + j] >> 4) & 0x0F0F0F0Fu) | qh_to_bit4(h >> (16 + 4 * j));
-            }
-        }
+        sk_unpack<WT>(st.w, sh, a8, dw, mw);
         float dwr[4], mwr[4];
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -293,6 +304,171 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
     }
 }
 
+// 9-32 activation rows on the 16x16x32 int8 MFMA (one issue per block, weight rows x 16
+// activation rows, in place of 4 activation rows per 4x4x4 pass).  Lane l = 16 c + r loads block
+// c of the step for weight row r (the skinny_kernel's loads: 16 contiguous 4-block runs per
+// instruction), and the MFMA wants lane l to hold dwords 2c, 2c+1 of one block for every
+// 16-lane row c: the 4 x 4 lane-row x dword-pair transpose is two swap stages, v_permlane32_swap
+// (the off-diagonal 2 x 2 blocks of lane rows 0-1 / 2-3) and v_permlane16_swap (inside each),
+// 8 swaps per lane and step.  The activation pieces are shared through the wave's LDS region as
+// in skinny_kernel; the MFMA's B operand (activation row r of the half, dwords 2c, 2c+1) and the
+// result rows (weight rows 4c .. 4c+3 x activation row r) read their scales from there and from
+// the wave's weight-scale slots.  MH halves of 16 activation rows.  Requires K % 128 == 0 and a
+// 16-byte aligned A (the shared pieces); every other rule is skinny_kernel's.
+template <int WT, bool AS, int MH, int NWV>
+__global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
+                                                            float* __restrict__ C, int M, int N, int nb, int ldc,
+                                                            uint32_t wbytes, uint32_t abytes) {
+    using F = SkFmt<WT>;
+    constexpr int BB = F::BB;
+    constexpr int AR = 16 * MH;                  // activation rows of the step pieces
+    constexpr int AP = 9 * AR;                   // 16-byte pieces per step (4 blocks of 36 bytes a row)
+    constexpr int APL = (AP + 63) / 64;
+    constexpr bool MIN = (WT == kWQ41 || WT == kWQ51);
+    constexpr int RED = NWV * kSkRows * AR;      // floats of the cross-wave sum
+    __shared__ __attribute__((aligned(16))) uint32_t sact[NWV * 4 * AP > RED ? NWV * 4 * AP : RED];
+    __shared__ __attribute__((aligned(16))) float swd[NWV][MIN ? 2 : 1][4][kSkRows];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int c = lane >> 4, r = lane & 15;
+    const int n0 = blockIdx.x * kSkRows;
+    const int wrow = min(n0 + r, N - 1);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, (int)wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)abytes, 0x00020000);
+    const uint32_t wrow_off = (uint32_t)wrow * (uint32_t)nb * (uint32_t)BB + (uint32_t)c * BB;
+    const int sh = (int)(((uintptr_t)W + wrow_off) & 3u);
+    uint32_t poff0[APL];
+#pragma unroll
+    for (int i = 0; i < APL; i++) {
+        const int p = lane + 64 * i, row = p / 9;
+        poff0[i] = (p < AP && row < M) ? (uint32_t)row * (uint32_t)nb * (uint32_t)kQ81Bytes + 16u * (uint32_t)(p % 9)
+                                       : kOOB;
+    }
+    const int S = nb >> 2;
+    const int s_lo = (int)((long long)S * wave / NWV), s_hi = (int)((long long)S * (wave + 1) / NWV);
+
+    i32x4 bias;
+#pragma unroll
+    for (int q = 0; q < 4; q++) bias[q] = (int)kSkMagic;
+    float acc[MH][4];
+#pragma unroll
+    for (int h = 0; h < MH; h++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) acc[h][q] = 0.0f;
+
+    struct Step {
+        uint32_t w[F::WD];
+        u32x4 ap[APL];
+    };
+    auto load = [&](int s, Step& st) {
+        const bool bok = 4 * s + c < nb;
+        buf_load<F::WD>(rw, bok ? wrow_off + (uint32_t)(4 * s) * BB - (uint32_t)sh : kOOB, st.w);
+#pragma unroll
+        for (int i = 0; i < APL; i++)
+            st.ap[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                ra, poff0[i] == kOOB ? kOOB : poff0[i] + (uint32_t)(4 * s) * kQ81Bytes, 0, 0);
+    };
+    uint32_t* sap = &sact[wave * 4 * AP];
+
+    auto compute = [&](const Step& st) {
+        float dw, mw;
+        uint32_t a8[8];
+        sk_unpack<WT>(st.w, sh, a8, dw, mw);
+        wave_lds_exchange();   // the previous step's reads come first
+#pragma unroll
+        for (int i = 0; i < APL; i++)
+            if (lane + 64 * i < AP) *(u32x4*)&sap[4 * (lane + 64 * i)] = st.ap[i];
+        swd[wave][0][c][r] = dw;
+        if constexpr (MIN) swd[wave][1][c][r] = mw;
+        wave_lds_exchange();
+        // x[j] = dwords 2j, 2j+1 of this lane's block (lane row c = block c): after the transpose
+        // x[k] of lane row c holds dwords 2c, 2c+1 of block k (for this lane's weight row)
+        uint32_t x[4][2];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[j][0] = a8[2 * j];
+            x[j][1] = a8[2 * j + 1];
+        }
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const auto v = __builtin_amdgcn_permlane32_swap(x[j][e], x[j + 2][e], false, false);
+                x[j][e] = v[0];
+                x[j + 2][e] = v[1];
+            }
+#pragma unroll
+        for (int j = 0; j < 4; j += 2)
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const auto v = __builtin_amdgcn_permlane16_swap(x[j][e], x[j + 1][e], false, false);
+                x[j][e] = v[0];
+                x[j + 1][e] = v[1];
+            }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const long wa = (long)(((uint64_t)x[k][1] << 32) | x[k][0]);
+            const f32x4 dwr = *(const f32x4*)&swd[wave][0][k][4 * c];
+            f32x4 mwr;
+            if constexpr (MIN) mwr = *(const f32x4*)&swd[wave][1][k][4 * c];
+#pragma unroll
+            for (int h = 0; h < MH; h++) {
+                const uint32_t* ab = &sap[(16 * h + r) * 36 + 9 * k];
+                const long bv = (long)(((uint64_t)ab[2 + 2 * c] << 32) | ab[1 + 2 * c]);
+                const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(wa, bv, bias, 0, 0, 0);
+                const uint32_t ds = ab[0];
+                const float da = AS ? __builtin_bit_cast(float, ds & ~3u) : f16_to_f32(ds & 0xFFFFu);
+                const float sa = AS ? 0.0f : f16_to_f32(ds >> 16);
+                const float nc = -kSkMagicF * da;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int e = d[q];
+                    const float X = fmaf(__builtin_bit_cast(float, e), da, nc);  // d_a * sumi
+                    if constexpr (WT == kWQ40) acc[h][q] = fmaf(dwr[q], fmaf(-8.0f, sa, X), acc[h][q]);
+                    else if constexpr (WT == kWQ50) acc[h][q] = fmaf(dwr[q], fmaf(-16.0f, sa, X), acc[h][q]);
+                    else if constexpr (WT == kWQ80) acc[h][q] = fmaf(dwr[q], X, acc[h][q]);
+                    else acc[h][q] = fmaf(mwr[q], sa, fmaf(dwr[q], X, acc[h][q]));
+                }
+            }
+        }
+    };
+
+    // one step in flight per wave: a second (loaded under the current step's MFMAs) needs ~30 more
+    // VGPRs per lane, and at 8 waves the kernel was 2-15% slower with it (Q8_0 N = K = 4096, M = 32:
+    // 11.6 vs 11.3 us; Q4_0 M = 24: 8.9 vs 7.2)
+    constexpr int PD = 1;
+    Step buf[PD];
+#pragma unroll
+    for (int d = 0; d < PD; d++)
+        if (s_lo + d < s_hi) load(s_lo + d, buf[d]);
+    for (int s0 = s_lo; s0 < s_hi; s0 += PD) {
+#pragma unroll
+        for (int d = 0; d < PD; d++) {
+            if (s0 + d < s_hi) {
+                compute(buf[d]);
+                if (s0 + d + PD < s_hi) load(s0 + d + PD, buf[d]);
+            }
+        }
+    }
+
+    // result lane (c, r): weight rows 4c .. 4c+3, activation row 16h + r; the waves' K ranges
+    // summed through LDS (the activation regions, free after the K loop)
+    __syncthreads();
+    float* red = (float*)sact;
+#pragma unroll
+    for (int h = 0; h < MH; h++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) red[(wave * kSkRows + 4 * c + q) * AR + 16 * h + r] = acc[h][q];
+    __syncthreads();
+    for (int t = threadIdx.x; t < kSkRows * AR; t += 64 * NWV) {
+        const int row = t % kSkRows, m = t / kSkRows;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NWV; w++) v += red[(w * kSkRows + row) * AR + m];
+        if (m < M && n0 + row < N) C[(size_t)m * ldc + n0 + row] = v;
+    }
+}
+
 template <int WT, int MP, bool AS>
 hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
                              hipStream_t s) {
@@ -304,7 +480,7 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
     {
         // 16 waves leave 128 VGPRs per lane: enough for one activation pass, or two with the
         // shared pieces (the 5-8-row launch rule asks for 16 only then)
-        if constexpr (MP <= 4) {
+        {
             if (nwv == 16 && al) {
                 hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
                                    wbytes, abytes);
@@ -319,13 +495,8 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
             }
         }
     }
-    if constexpr (MP > 2) {
-        // 9-32 rows: the shared activation pieces only (the per-lane form would not fit)
-        if (!al) return hipErrorNotSupported;
-        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N,
-                           wbytes, abytes);
-        return hipGetLastError();
-    } else {
+    static_assert(MP <= 2, "9-32 rows take skinny16_kernel");
+    {
         if (nwv >= 8) {
             if (al)
                 hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
@@ -343,13 +514,30 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
     return hipGetLastError();
 }
 
+// 8 waves per workgroup (4 when the K steps are too few): 16 measured 2-25% slower at 9-32 rows
+// (Q8_0 N = K = 4096, M = 16: 8.8 vs 8.6 us; N = 14336, K = 4096, M = 32: 42.4 vs 34.4), as did
+// 4 on N <= 4096 (M = 32: 12.0 vs 11.3)
+template <int WT, bool AS, int MH>
+hipError_t skinny16_launch(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
+                           hipStream_t s) {
+    const uint32_t wbytes = (uint32_t)(((uint64_t)N * nb * block_bytes(WT) + 3) & ~(uint64_t)3);
+    const uint32_t abytes = (uint32_t)((uint64_t)M * nb * kQ81Bytes);
+    const dim3 grid((unsigned)((N + kSkRows - 1) / kSkRows));
+    if (nwv >= 8)
+        hipLaunchKernelGGL((skinny16_kernel<WT, AS, MH, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else
+        hipLaunchKernelGGL((skinny16_kernel<WT, AS, MH, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    return hipGetLastError();
+}
+
 template <int WT, bool AS>
 hipError_t skinny_launch_mp(int nwv, const uint8_t* W, const uint8_t* A, float* C, int M, int N, int nb,
                             hipStream_t s) {
     if (M <= 4) return skinny_launch_nwv<WT, 1, AS>(nwv, W, A, C, M, N, nb, s);
     if (M <= 8) return skinny_launch_nwv<WT, 2, AS>(nwv, W, A, C, M, N, nb, s);
-    if (M <= 16) return skinny_launch_nwv<WT, 4, AS>(nwv, W, A, C, M, N, nb, s);
-    return skinny_launch_nwv<WT, 8, AS>(nwv, W, A, C, M, N, nb, s);
+    // 9-32 rows: the 16x16x32 MFMA form (skinny_supported has required the shared pieces)
+    if (M <= 16) return skinny16_launch<WT, AS, 1>(nwv, W, A, C, M, N, nb, s);
+    return skinny16_launch<WT, AS, 2>(nwv, W, A, C, M, N, nb, s);
 }
 
 }  // namespace
@@ -391,15 +579,17 @@ bool skinny_preferred(int wtype, int M, int N, int K) {
     // 2-29%.
     const bool nib = (wtype == kWQ40 || wtype == kWQ41);
     if (M > 8) {
-        // 9-32 rows (the shared activation pieces; Q8_1 input, us, against the split MFMA GEMM):
-        // 9-16 rows but on large square-ish matrices (Q8_0 N = K = 4096, M = 16: 9.6 vs 12.8;
-        // Q4_0 7.9 vs 12.4; N = 14336, K = 4096: 27.8 vs 28.3 / 21.8 vs 22.3; the other way
-        // N = K = 7168, Q4_0: 22.9 vs 18.9), 17-32 rows (8 passes, one workgroup per CU) only for
-        // the nibble types up to 4096 x 4096 (Q4_0 M = 32: 12.3 vs 13.5; Q8_0 14.7 vs 14.0; N =
-        // 14336, K = 4096: 41.9 vs 24.3)
-        if (!(nib || wtype == kWQ80)) return false;
+        // 9-32 rows on the 16x16x32-MFMA form (Q8_1 input, graph replays, us, against the split
+        // MFMA GEMM): 9-16 rows but on large square-ish matrices (N = K = 4096, M = 16: Q8_0 8.6
+        // vs 9.3 (the 4x4x4 passes took 9.3), Q4_0 5.9 vs 7.6, Q5_0 6.7 vs 15.6, Q5_1 6.8 vs 15.5;
+        // N = 14336, K = 4096: Q8_0 26.1 vs 27.4, Q4_0 15.9 vs 17.5; the other way N = K = 7168:
+        // Q8_0 25.2 vs 25.0, Q4_0 17.0 vs 16.7), 17-32 rows up to 4096 x 4096 (M = 32: Q8_0 11.3
+        // vs 13.4-16.0, Q4_0 7.9 vs 9.9 (4x4x4 passes 11.4), Q5_0 9.7 vs 16.3; M = 24: Q8_0 10.3
+        // vs 12.7-14.5; larger matrices go to the MFMA GEMM: N = 14336, K = 4096, M = 32: Q8_0
+        // 34.4 vs 30.6, Q4_0 23.2 vs 21.3; N = K = 7168: 28.9 vs 26.7, 19.9 vs 18.4)
+        if (!(nib || wtype == kWQ80 || wtype == kWQ50 || wtype == kWQ51)) return false;  // K-quants
         if (M <= 16) return !(N >= 7168 && K >= 7168);
-        return nib && (long long)N * K <= 16777216ll;
+        return (long long)N * K <= 16777216ll;
     }
     if (M == 3) return N >= 2048 && (K <= 1536 || (nib && N >= 100000 && K <= 2560));
     if (M == 4) {
@@ -442,6 +632,8 @@ hipError_t launch_skinny(int wtype, int afmt, const uint8_t* W, const uint8_t* A
     // 4096, M = 8 14.3 -> 13.6, M = 6 13.8 -> 12.7; Q4_0 M = 8 13.1 -> 12.4); with 448 workgroups
     // 4 stay better (Q8_0 N = K = 7168, M = 8: 27.2 vs 29.6)
     if (M > 4 && wgs <= 256 && nwv < 8 && steps >= 16) nwv = 8;
+    // 9-32 rows: at most 8 (skinny16_launch)
+    if (M > 8) nwv = min(nwv, 8);
     note_engine(KSQ_ENG_SKINNY);
     switch (wtype) {
         case kWQ40: return skinny_launch_mp<kWQ40, false>(nwv, W, A, C, M, N, nb, s);

@@ -123,8 +123,8 @@ CONFIG_CASES = [
     ("c1_q8_0_m1_q81", 1, 1, 4096, 4096, "q81", {"gemv_direct"}),
     ("c1_q8_0_m8_f32", 1, 8, 4096, 4096, "f32", {"quantize", "skinny"}),
     ("c1_q8_0_m8_q81", 1, 8, 4096, 4096, "q81", {"skinny"}),
-    ("c1_q8_0_m32_f32", 1, 32, 4096, 4096, "f32", {"quantize", "mmq3", "splitk"}),
-    ("c1_q8_0_m32_q81", 1, 32, 4096, 4096, "q81", {"mmq3", "splitk"}),
+    ("c1_q8_0_m32_f32", 1, 32, 4096, 4096, "f32", {"quantize", "skinny"}),
+    ("c1_q8_0_m32_q81", 1, 32, 4096, 4096, "q81", {"skinny"}),
     ("c2_q4_0_m2048_f32", 0, 2048, 4096, 4096, "f32", {"quantize", "mmq_planar"}),
     ("c2_q4_0_m2048_q81", 0, 2048, 4096, 4096, "q81", {"mmq1"}),
     ("c3_q4_k_m128_f32", 2, 128, 14336, 4096, "f32", {"quantize", "mmq7", "splitk"}),
@@ -237,7 +237,7 @@ def _engine_cases():
         for M in (1, 33):
             cases.append((f"mmqp_m{M}_w{wt}", wt, M, 136, 512, 0, 2, 8, {"quantize", "mmq_planar"}, 0))
     cases.append(("splitk_w0", 0, 32, 1024, 8192, 1, 2, 0, {"mmq5", "splitk"}, 0))
-    cases.append(("splitk_w1", 1, 32, 1024, 8192, 1, 0, 0, {"mmq3", "splitk"}, 0))
+    cases.append(("splitk_w1", 1, 32, 1024, 8192, 1, 2, 0, {"mmq3", "splitk"}, 0))
     # the native W8A8C8 operator's block_q8s activations: fp32 (its quantiser) and pre-quantised
     for M, path, eng in ((1, 1, {"gemv_direct_fq"}), (5, 3, {"quantize", "skinny"}),
                          (150, 2, {"quantize", "mmq3", "splitk"})):

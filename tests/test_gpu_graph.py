@@ -61,7 +61,8 @@ GEMM_CASES = [
     ("planar_splitk_q4_1", 4, 0, 300, 520, 1280, 8, {"quantize", "mmq_planar", "splitk"}),
     ("tile128_q8_1_input", 0, 1, 512, 2048, 4096, 1, {"mmq1"}),
     ("decode_fused_fp32", 0, 0, 1, 4096, 4096, 0, {"gemv_direct_fq"}),
-    ("q8_0_m32_splitk", 1, 0, 32, 4096, 4096, 0, {"quantize", "splitk"}),
+    ("q8_0_m32_splitk", 1, 0, 32, 4096, 8192, 0, {"quantize", "splitk"}),
+    ("q8_0_m32_small_batch", 1, 0, 32, 4096, 4096, 0, {"quantize", "skinny"}),
     ("q4_k_m128", 2, 0, 128, 2048, 4096, 0, {"quantize"}),
 ]
 

@@ -550,9 +550,10 @@ def test_skinny_small_batch(dev, oracle, wtype):
         assert _rel_err(y, ref) <= TOL, (M, N, K)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("M", [1, 3, 8, 20])
 def test_skinny_q8s_native(dev, oracle, M):
-    """Q8_0 weights with block_q8s activations (the native W8A8C8 operator's blocks) on path 3."""
+    """Q8_0 weights with block_q8s activations (the native W8A8C8 operator's blocks) on path 3
+    (M = 20: the 16x16x32-MFMA form)."""
     from ksq import synth
     g = np.random.default_rng(2500 + M)
     N, K = 530, 2048
@@ -583,7 +584,8 @@ def _family(engines):
     (1, 8, 512, 7168, "decode"),
     # 9-32 rows: the small-batch kernel where measured faster, else the MFMA GEMM
     (0, 16, 4096, 4096, "skinny"), (1, 12, 4096, 14336, "skinny"), (0, 16, 7168, 7168, "mmq"),
-    (1, 24, 4096, 4096, "mmq"), (0, 32, 4096, 4096, "skinny"), (5, 16, 4096, 4096, "mmq"),
+    (1, 24, 4096, 4096, "skinny"), (0, 32, 4096, 4096, "skinny"), (5, 16, 4096, 4096, "skinny"),
+    (6, 32, 4096, 4096, "skinny"), (1, 32, 14336, 4096, "mmq"), (1, 32, 7168, 7168, "mmq"), (2, 20, 4096, 4096, "mmq"),
     (2, 8, 4096, 4096, "mmq"), (3, 7, 12288, 5120, "mmq"), (2, 5, 7168, 7168, "decode"),
     (1, 2, 4096, 4096, "decode"), (0, 2, 14336, 4096, "decode"), (2, 5, 12288, 5120, "mmq"),
     (2, 6, 7168, 512, "mmq"), (2, 8, 4096, 1024, "decode")])
