@@ -315,7 +315,12 @@ __global__ __launch_bounds__(64 * NWV) void skinny_kernel(const uint8_t* __restr
 // result rows (weight rows 4c .. 4c+3 x activation row r) read their scales from there and from
 // the wave's weight-scale slots.  MH halves of 16 activation rows.  Requires K % 128 == 0 and a
 // 16-byte aligned A (the shared pieces); every other rule is skinny_kernel's.
-template <int WT, bool AS, int MH, int NWV>
+// WST (16-byte aligned W): the step's 16 weight-row runs are loaded as 16-byte aligned chunks
+// (one coalesced segment per row, ~2.5x fewer cache lines touched per load instruction than the
+// per-lane block windows) into the wave's LDS region, and each lane reads its block window from
+// there; the loads, not the MFMA or LDS work, bound this kernel (per-wave timestamps: each K
+// step ~1.2-1.4 us, ~4x its compute).
+template <int WT, bool AS, int MH, int NWV, bool WST = false>
 __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __restrict__ W, const uint8_t* __restrict__ A,
                                                             float* __restrict__ C, int M, int N, int nb, int ldc,
                                                             uint32_t wbytes, uint32_t abytes) {
@@ -328,6 +333,9 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
     constexpr int RED = NWV * kSkRows * AR;      // floats of the cross-wave sum
     __shared__ __attribute__((aligned(16))) uint32_t sact[NWV * 4 * AP > RED ? NWV * 4 * AP : RED];
     __shared__ __attribute__((aligned(16))) float swd[NWV][MIN ? 2 : 1][4][kSkRows];
+    // WST: the step's weight rows as 16-byte aligned chunks (RUN bytes of a row at any even offset)
+    constexpr int RUN = 4 * BB, WCH = (RUN + 14 + 15) / 16, WQ = kSkRows * WCH, WQL = (WQ + 63) / 64;
+    __shared__ __attribute__((aligned(16))) uint32_t swc[WST ? NWV : 1][WST ? WQ * 4 : 4];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int c = lane >> 4, r = lane & 15;
@@ -337,6 +345,15 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)abytes, 0x00020000);
     const uint32_t wrow_off = (uint32_t)wrow * (uint32_t)nb * (uint32_t)BB + (uint32_t)c * BB;
     const int sh = (int)(((uintptr_t)W + wrow_off) & 3u);
+    const uint32_t rs_own = (uint32_t)min(n0 + r, N - 1) * (uint32_t)nb * (uint32_t)BB;
+    uint32_t wrs[WQL];
+    int wch[WQL];
+#pragma unroll
+    for (int i = 0; i < WQL; i++) {
+        const int q = lane + 64 * i, row = q / WCH;
+        wrs[i] = (uint32_t)min(n0 + min(row, kSkRows - 1), N - 1) * (uint32_t)nb * (uint32_t)BB;
+        wch[i] = q < WQ ? 16 * (q % WCH) : -1;
+    }
     uint32_t poff0[APL];
 #pragma unroll
     for (int i = 0; i < APL; i++) {
@@ -357,12 +374,20 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
         for (int q = 0; q < 4; q++) acc[h][q] = 0.0f;
 
     struct Step {
-        uint32_t w[F::WD];
+        uint32_t w[WST ? 1 : F::WD];
+        u32x4 wc[WST ? WQL : 1];
         u32x4 ap[APL];
     };
     auto load = [&](int s, Step& st) {
-        const bool bok = 4 * s + c < nb;
-        buf_load<F::WD>(rw, bok ? wrow_off + (uint32_t)(4 * s) * BB - (uint32_t)sh : kOOB, st.w);
+        if constexpr (WST) {
+#pragma unroll
+            for (int i = 0; i < WQL; i++)
+                st.wc[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rw, wch[i] >= 0 ? ((wrs[i] + (uint32_t)(RUN * s)) & ~15u) + (uint32_t)wch[i] : kOOB, 0, 0);
+        } else {
+            const bool bok = 4 * s + c < nb;
+            buf_load<F::WD>(rw, bok ? wrow_off + (uint32_t)(4 * s) * BB - (uint32_t)sh : kOOB, st.w);
+        }
 #pragma unroll
         for (int i = 0; i < APL; i++)
             st.ap[i] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -370,11 +395,24 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
     };
     uint32_t* sap = &sact[wave * 4 * AP];
 
-    auto compute = [&](const Step& st) {
+    auto compute = [&](const Step& st, int s) {
         float dw, mw;
         uint32_t a8[8];
-        sk_unpack<WT>(st.w, sh, a8, dw, mw);
         wave_lds_exchange();   // the previous step's reads come first
+        if constexpr (WST) {
+#pragma unroll
+            for (int i = 0; i < WQL; i++)
+                if (wch[i] >= 0) *(u32x4*)&swc[wave][4 * (lane + 64 * i)] = st.wc[i];
+            wave_lds_exchange();
+            const uint32_t o = ((rs_own + (uint32_t)(RUN * s)) & 15u) + (uint32_t)(BB * c);
+            const uint32_t* wp = &swc[wave][r * WCH * 4 + (o >> 2)];
+            uint32_t wv[F::WD];
+#pragma unroll
+            for (int i = 0; i < F::WD; i++) wv[i] = wp[i];
+            sk_unpack<WT>(wv, (int)(o & 3u), a8, dw, mw);
+        } else {
+            sk_unpack<WT>(st.w, sh, a8, dw, mw);
+        }
 #pragma unroll
         for (int i = 0; i < APL; i++)
             if (lane + 64 * i < AP) *(u32x4*)&sap[4 * (lane + 64 * i)] = st.ap[i];
@@ -445,7 +483,7 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
 #pragma unroll
         for (int d = 0; d < PD; d++) {
             if (s0 + d < s_hi) {
-                compute(buf[d]);
+                compute(buf[d], s0 + d);
                 if (s0 + d + PD < s_hi) load(s0 + d + PD, buf[d]);
             }
         }
@@ -523,6 +561,16 @@ hipError_t skinny16_launch(int nwv, const uint8_t* W, const uint8_t* A, float* C
     const uint32_t wbytes = (uint32_t)(((uint64_t)N * nb * block_bytes(WT) + 3) & ~(uint64_t)3);
     const uint32_t abytes = (uint32_t)((uint64_t)M * nb * kQ81Bytes);
     const dim3 grid((unsigned)((N + kSkRows - 1) / kSkRows));
+    if constexpr (WT == kWQ80) {
+        // Q8_0: the weights staged as aligned row chunks (us, N = K = 4096, M = 32: 11.35 -> 10.74;
+        // M = 16 8.61 -> 8.19; N = 14336, K = 4096, M = 16 26.0 -> 23.6).  The shorter blocks of the
+        // other types lose with it at N = 4096 (Q4_0 M = 32 7.87 -> 8.36).
+        if (nwv >= 8 && ((uintptr_t)W & 15u) == 0) {
+            hipLaunchKernelGGL((skinny16_kernel<WT, AS, MH, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
+                               abytes);
+            return hipGetLastError();
+        }
+    }
     if (nwv >= 8)
         hipLaunchKernelGGL((skinny16_kernel<WT, AS, MH, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
     else

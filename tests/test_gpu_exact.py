@@ -225,9 +225,11 @@ def _engine_cases():
         cases.append((f"decf_oddnb_w{wt}", wt, 1, 100, 1056, 0, 1, 0, {"gemv_row_fq"}, 0))
         for M in (1, 3, 8):
             cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1024, 1, 3, 0, {"skinny"}, 0))
-        # 9-32 rows (4 and 8 row passes of 4 over the shared activation pieces), ragged rows
+        # 9-32 rows (the 16x16x32-MFMA form over the shared activation pieces), ragged rows
         for M in (12, 17, 32):
             cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1152, 1, 3, 0, {"skinny"}, 0))
+        # weights 4-byte aligned only: Q8_0 off its row-chunk staging onto the per-lane windows
+        cases.append((f"skinny_m20_woff4_w{wt}", wt, 20, 130, 1024, 1, 3, 0, {"skinny"}, 4))
     # the LDS-DMA GEMM (fp32 activations quantised to planar block_q8_1; Q4_0 / Q4_1): split in
     # two along K, with an even (4) and an odd (5) number of 4-block steps per split; ragged M, N
     for wt in (0, 4):
