@@ -50,7 +50,7 @@ TRAFFIC = {
     "gemv_f32": (int((4723.9 * 2.0 + 16.0) * 1024), "profiles/gemv_q4_0_m1_n4096_k4096.md"),
     "q8_0_M1": (int((8737.4 * 2.0 + 32.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q8_0_M8": (int((8897.0 * 2.0 + 128.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
-    "q8_0_M32": (int((9307.7 * 2.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
+    "q8_0_M32": (int((9329.1 * 2.0 + 512.0) * 1024), "profiles/q8_0_m1_m8_m32_n4096_k4096.md"),
     "q4_K_M128": (int(((19039.5 + 10766.5) * 2.0 + 21504.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
     "q6_K_M128": (int((26591.9 * 2.0 + 7168.0) * 1024), "profiles/mmq_kquant_m128_n14336_k4096.md"),
     "moe_q4_0_T512_E8_top2": (int(((199520.0 + 4149.3 + 35.1) * 2.0 + 57344.0 + 5641.1 + 28688.2) * 1024),
