@@ -345,14 +345,18 @@ __global__ __launch_bounds__(64 * NWV) void skinny16_kernel(const uint8_t* __res
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, (int)abytes, 0x00020000);
     const uint32_t wrow_off = (uint32_t)wrow * (uint32_t)nb * (uint32_t)BB + (uint32_t)c * BB;
     const int sh = (int)(((uintptr_t)W + wrow_off) & 3u);
-    const uint32_t rs_own = (uint32_t)min(n0 + r, N - 1) * (uint32_t)nb * (uint32_t)BB;
-    uint32_t wrs[WQL];
-    int wch[WQL];
+    // WST: this lane's row start, and the chunk (row q / WCH, byte 16 (q % WCH) of the row's run)
+    // each of its loads brings in, q = lane + 64 i (-1: no chunk)
+    const uint32_t rs_own = (uint32_t)wrow * (uint32_t)nb * (uint32_t)BB;
+    uint32_t wrs[WST ? WQL : 1];
+    int wch[WST ? WQL : 1];
+    if constexpr (WST) {
 #pragma unroll
-    for (int i = 0; i < WQL; i++) {
-        const int q = lane + 64 * i, row = q / WCH;
-        wrs[i] = (uint32_t)min(n0 + min(row, kSkRows - 1), N - 1) * (uint32_t)nb * (uint32_t)BB;
-        wch[i] = q < WQ ? 16 * (q % WCH) : -1;
+        for (int i = 0; i < WQL; i++) {
+            const int q = lane + 64 * i, row = q / WCH;
+            wrs[i] = (uint32_t)min(n0 + min(row, kSkRows - 1), N - 1) * (uint32_t)nb * (uint32_t)BB;
+            wch[i] = q < WQ ? 16 * (q % WCH) : -1;
+        }
     }
     uint32_t poff0[APL];
 #pragma unroll
@@ -515,40 +519,22 @@ hipError_t skinny_launch_nwv(int nwv, const uint8_t* W, const uint8_t* A, float*
     const dim3 grid((unsigned)((N + kSkRows - 1) / kSkRows));
     // the shared activation pieces: whole 4-block steps, 16-byte aligned rows
     const bool al = (nb % 4) == 0 && ((uintptr_t)A & 15u) == 0;
-    {
-        // 16 waves leave 128 VGPRs per lane: enough for one activation pass, or two with the
-        // shared pieces (the 5-8-row launch rule asks for 16 only then)
-        {
-            if (nwv == 16 && al) {
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
-                                   wbytes, abytes);
-                return hipGetLastError();
-            }
-        }
-        if constexpr (MP == 1) {
-            if (nwv == 16) {
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N,
-                                   wbytes, abytes);
-                return hipGetLastError();
-            }
-        }
-    }
     static_assert(MP <= 2, "9-32 rows take skinny16_kernel");
-    {
-        if (nwv >= 8) {
-            if (al)
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes,
-                                   abytes);
-            else
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
-        } else {
-            if (al)
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes,
-                                   abytes);
-            else
-                hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
-        }
-    }
+    // 16 waves leave 128 VGPRs per lane: enough for one activation pass, or two with the shared
+    // pieces (the 5-8-row launch rule asks for 16 only then)
+    if (nwv == 16 && al)
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 16, true>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N, wbytes,
+                           abytes);
+    else if (MP == 1 && nwv == 16)
+        hipLaunchKernelGGL((skinny_kernel<WT, 1, AS, 16>), grid, dim3(1024), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else if (nwv >= 8 && al)
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8, true>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else if (nwv >= 8)
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 8>), grid, dim3(512), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else if (al)
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4, true>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
+    else
+        hipLaunchKernelGGL((skinny_kernel<WT, MP, AS, 4>), grid, dim3(256), 0, s, W, A, C, M, N, nb, N, wbytes, abytes);
     return hipGetLastError();
 }
 
