@@ -57,7 +57,7 @@ KSQ_API const char* ksq_error_string(int status);
 /* Library version string. */
 KSQ_API const char* ksq_version(void);
 
-/* Free the per-device workspace pools the void entries allocate on demand. */
+/* Free the workspace pools (one per device and stream) the void entries allocate on demand. */
 KSQ_API void ksq_release(void);
 
 /* ---- drop-in entries: the reference's quant_gemm signature --------------- */

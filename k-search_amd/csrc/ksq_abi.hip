@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <vector>
 
@@ -45,32 +46,45 @@ int hip_error(hipError_t e, const char* where) {
     return set_error(KSQ_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
 }
 
-// Per-device scratch: the quantised copy of fp32 activations, split-K partial sums and the
-// MoE routing tables when the caller passes no workspace.  A pool that must grow takes a new,
-// larger buffer and keeps the outgrown one until ksq_release(): a graph captured earlier may
-// still read and write it.  Growing is refused while the stream captures a graph.
+// Library scratch: the quantised copy of fp32 activations, split-K partial sums and the MoE
+// routing tables when the caller passes no workspace.  One pool per (device, stream): calls on
+// one stream run in stream order and share it; eager calls on two streams of one GPU get two
+// buffers and cannot race.  A pool that must grow takes a new, larger buffer and keeps the
+// outgrown one until ksq_release(): a graph captured earlier may still read and write it.
+// Growing is refused while the stream captures a graph; a capturing stream whose own pool is too
+// small uses the device's largest pool that is large enough (the usual warm-up-then-capture
+// sequence: the call was made eagerly on another stream first), so such a graph shares that
+// stream's pool and must not run concurrently with its calls.
 struct Pool {
     void* ptr = nullptr;
     size_t size = 0;
     std::vector<void*> retired;
 };
 std::mutex g_pool_mu;
-std::vector<Pool> g_pools;
+std::map<std::pair<int, uintptr_t>, Pool> g_pools;
 
 int pool_get(size_t bytes, hipStream_t s, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_error(e, "hipGetDevice");
     std::lock_guard<std::mutex> lk(g_pool_mu);
-    if ((int)g_pools.size() <= dev) g_pools.resize(dev + 1);
-    Pool& p = g_pools[dev];
+    Pool& p = g_pools[{dev, (uintptr_t)s}];
     if (p.size < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        if (s && hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+            const Pool* big = nullptr;
+            for (const auto& kv : g_pools)
+                if (kv.first.first == dev && kv.second.size >= bytes && (!big || kv.second.size > big->size))
+                    big = &kv.second;
+            if (big) {
+                *out = big->ptr;
+                return KSQ_OK;
+            }
             return set_error(KSQ_ERR_WORKSPACE,
                              "the workspace pool would have to grow to %zu bytes during graph capture; "
                              "pass a workspace",
                              bytes);
+        }
         size_t want = 2 * p.size;
         if (want < bytes) want = bytes;
         if (want < (1u << 20)) want = 1u << 20;
@@ -248,14 +262,15 @@ void ksq_release(void) {
     std::lock_guard<std::mutex> lk(g_pool_mu);
     int cur = 0;
     (void)hipGetDevice(&cur);
-    for (size_t d = 0; d < g_pools.size(); d++) {
-        if (g_pools[d].ptr || !g_pools[d].retired.empty()) {
-            (void)hipSetDevice((int)d);
-            if (g_pools[d].ptr) (void)hipFree(g_pools[d].ptr);
-            for (void* r : g_pools[d].retired) (void)hipFree(r);
+    for (auto& kv : g_pools) {
+        Pool& p = kv.second;
+        if (p.ptr || !p.retired.empty()) {
+            (void)hipSetDevice(kv.first.first);
+            if (p.ptr) (void)hipFree(p.ptr);
+            for (void* r : p.retired) (void)hipFree(r);
         }
-        g_pools[d] = Pool{};
     }
+    g_pools.clear();
     (void)hipSetDevice(cur);
 }
 

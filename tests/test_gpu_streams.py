@@ -1,0 +1,48 @@
+"""Calls on concurrent streams of one GPU without a caller workspace: each (device, stream) has
+its own library pool, so two streams' calls in flight at once do not share scratch.  GPU only."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+    assert torch.cuda.is_available(), "gpu tests need a GPU"
+    from ksq import _lib
+    _lib.lib()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("wtype,M,N,K", [(0, 256, 1024, 4096),    # fp32 rows quantised into the pool, MFMA GEMM
+                                         (1, 64, 1024, 8192),     # split-K partial sums in the pool
+                                         (0, 2048, 512, 2048)])   # planar quantised copy in the pool
+def test_pool_per_stream_concurrent(dev, wtype, M, N, K):
+    """Two streams each run the same call shape on their own inputs, back to back without
+    synchronising, eight times; every output equals the same call made alone on the default
+    stream."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(6200 + wtype + M)
+    ws = [_t(synth.weights(wtype, g, N, K), dev) for _ in range(2)]
+    xs = [_t(synth.activations(g, M, K), dev) for _ in range(2)]
+    want = [ops.gemm(wtype, 0, w, x, M, N, K) for w, x in zip(ws, xs)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.empty((M, N), dtype=torch.float32, device=dev) for _ in range(2)]
+    for rep in range(8):
+        for o in outs:
+            o.fill_(float("nan"))
+        torch.cuda.synchronize()
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                ops.gemm(wtype, 0, ws[i], xs[i], M, N, K, out=outs[i])
+        torch.cuda.synchronize()
+        for i in range(2):
+            assert torch.equal(outs[i], want[i]), (rep, i)
