@@ -230,6 +230,8 @@ def _engine_cases():
             cases.append((f"skinny_m{M}_w{wt}", wt, M, 200, 1152, 1, 3, 0, {"skinny"}, 0))
         # weights 4-byte aligned only: Q8_0 off its row-chunk staging onto the per-lane windows
         cases.append((f"skinny_m20_woff4_w{wt}", wt, 20, 130, 1024, 1, 3, 0, {"skinny"}, 4))
+        # one K step in all (fewer steps than waves: the idle waves add zeros), N below one workgroup
+        cases.append((f"skinny_m20_k128_w{wt}", wt, 20, 12, 128, 1, 3, 0, {"skinny"}, 0))
     # the LDS-DMA GEMM (fp32 activations quantised to planar block_q8_1; Q4_0 / Q4_1): split in
     # two along K, with an even (4) and an odd (5) number of 4-block steps per split; ragged M, N
     for wt in (0, 4):
