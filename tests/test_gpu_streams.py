@@ -46,3 +46,65 @@ def test_pool_per_stream_concurrent(dev, wtype, M, N, K):
         torch.cuda.synchronize()
         for i in range(2):
             assert torch.equal(outs[i], want[i]), (rep, i)
+
+
+def test_capture_borrows_warmed_pool(dev):
+    """An eager call on one stream grows that stream's pool; capturing the same call (no caller
+    workspace) on torch's capture stream then uses that pool, and every replay equals the eager
+    output."""
+    import torch
+    from ksq import ops, synth
+    g = np.random.default_rng(6300)
+    M, N, K = 256, 1024, 4096
+    w = _t(synth.weights(0, g, N, K), dev)
+    x = _t(synth.activations(g, M, K), dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.gemm(0, 0, w, x, M, N, K, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    want = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.gemm(0, 0, w, x, M, N, K, out=out)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+    del graph
+
+
+def test_capture_refuses_to_grow_pool(dev):
+    """With every pool released, a call that needs library scratch is refused during capture
+    (KSQ_ERR_WORKSPACE, nothing launched), and runs once a workspace is passed."""
+    import torch
+    from ksq import _lib, ops, synth
+    g = np.random.default_rng(6301)
+    M, N, K = 256, 1024, 4096
+    w = _t(synth.weights(0, g, N, K), dev)
+    x = _t(synth.activations(g, M, K), dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    _lib.lib().ksq_release()
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(_lib.KsqError) as err:
+        with torch.cuda.graph(graph):
+            ops.gemm(0, 0, w, x, M, N, K, out=out)
+    assert _lib.STATUS[err.value.status] == "KSQ_ERR_WORKSPACE"
+    del graph
+    torch.cuda.synchronize()
+    ws = torch.empty(ops.workspace_size(0, 0, M, N, K), dtype=torch.uint8, device=dev)
+    want = ops.gemm(0, 0, w, x, M, N, K)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.gemm(0, 0, w, x, M, N, K, out=out, workspace=ws)
+    out.fill_(float("nan"))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    del graph
